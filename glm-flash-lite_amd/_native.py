@@ -1,0 +1,173 @@
+"""ctypes binding of libgfl_moe.so (the C ABI declared in include/gfl_moe.h).
+
+The native library is the product: there is no Python or CPU fallback. If the shared object is missing or cannot be
+loaded, every entry point raises NativeUnavailable (build it with `python glm-flash-lite_amd/build.py`).
+Tensor arguments are torch tensors on the context's device; the current torch stream is used.
+"""
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libgfl_moe.so")
+
+# exported symbols of include/gfl_moe.h (checked by tests/test_abi.py against the header)
+SYMBOLS = ("gfl_last_error", "gfl_version", "gfl_ctx_create", "gfl_ctx_destroy", "gfl_register_layer",
+           "gfl_moe_forward", "gfl_dequant", "gfl_split", "gfl_combine", "gfl_grouped_rows", "gfl_synth_trellis",
+           "gfl_stats")
+
+MODE_AUTO, MODE_AFFINE, MODE_EXACT, MODE_I16 = -1, 0, 1, 2
+
+
+class NativeUnavailable(RuntimeError):
+    pass
+
+
+class NativeError(RuntimeError):
+    pass
+
+
+_LIB = None
+_P = C.c_void_p
+
+
+def load(path=LIB_PATH):
+    """Load and type the library once; raise NativeUnavailable when it is absent."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(path):
+        raise NativeUnavailable(f"{path} is missing: build it with `python glm-flash-lite_amd/build.py`")
+    try:
+        L = C.CDLL(path)
+    except OSError as e:
+        raise NativeUnavailable(f"cannot load {path}: {e}") from e
+    L.gfl_last_error.restype = C.c_char_p
+    L.gfl_version.restype = C.c_int
+    L.gfl_ctx_create.argtypes = [C.c_int, C.POINTER(_P)]
+    L.gfl_ctx_destroy.argtypes = [_P]
+    L.gfl_register_layer.argtypes = [_P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _P]
+    L.gfl_moe_forward.argtypes = [_P, C.c_int, _P, _P, _P, C.c_int, C.c_int, C.c_int, _P, C.c_int, C.c_float, _P]
+    L.gfl_dequant.argtypes = [_P, C.c_int, C.c_int, C.c_int, _P, _P]
+    L.gfl_split.argtypes = [_P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P,
+                            C.c_int64, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P]
+    L.gfl_combine.argtypes = [_P, C.c_int, C.c_int, _P, _P, _P, _P, C.c_int64, _P]
+    L.gfl_grouped_rows.argtypes = [_P, _P, C.c_int, C.c_int, _P, C.c_int, _P, _P, _P, _P, C.POINTER(C.c_int)]
+    L.gfl_synth_trellis.argtypes = [_P, C.c_size_t, C.c_uint64, _P]
+    L.gfl_stats.argtypes = [_P, _P, C.c_int]
+    for name in SYMBOLS:
+        if name != "gfl_last_error":
+            getattr(L, name).restype = C.c_int
+    _LIB = L
+    return L
+
+
+def check(rc):
+    if rc != 0:
+        raise NativeError(load().gfl_last_error().decode() or f"gfl error {rc}")
+
+
+def _stream():
+    import torch
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def ptr(t):
+    return C.c_void_p(t.data_ptr()) if t is not None else None
+
+
+class Context:
+    """One gfl_ctx on a device (layer registry + workspace)."""
+
+    def __init__(self, device=0):
+        L = load()
+        h = _P()
+        check(L.gfl_ctx_create(int(device), C.byref(h)))
+        self.h = h
+        self.device = int(device)
+        self._keep = {}
+
+    def close(self):
+        if self.h:
+            load().gfl_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def register_layer(self, li, E, H, I, ks, ptr_table, keep=None):
+        """ptr_table: sequence of E*9 device addresses (see gfl_register_layer)."""
+        arr = (C.c_uint64 * (9 * E))(*[int(p) for p in ptr_table])
+        check(load().gfl_register_layer(self.h, li, E, H, I, int(ks[0]), int(ks[1]), int(ks[2]), arr))
+        if keep is not None:
+            self._keep[li] = keep
+
+    def moe_forward(self, li, x, sel, w, out, mode=MODE_EXACT, act_limit=0.0):
+        """x fp16 [M,H], sel int64 [M,topk], w fp16|fp32 [M,topk], out fp32 [M,H] (all on the context device)."""
+        import torch
+        M, topk = sel.shape
+        assert x.dtype == torch.float16 and x.is_contiguous() and x.shape[0] == M
+        assert sel.dtype == torch.int64 and sel.is_contiguous()
+        assert w.dtype in (torch.float16, torch.float32) and w.is_contiguous() and tuple(w.shape) == (M, topk)
+        assert out.dtype == torch.float32 and out.is_contiguous() and tuple(out.shape) == tuple(x.shape)
+        for t in (x, sel, w, out):
+            assert t.is_cuda and t.device.index == self.device
+        check(load().gfl_moe_forward(self.h, li, ptr(x), ptr(sel), ptr(w), int(w.dtype == torch.float16), M, topk,
+                                     ptr(out), int(mode), float(act_limit), _stream()))
+        return out
+
+    def stats(self):
+        out = (C.c_int64 * 4)()
+        check(load().gfl_stats(self.h, out, 4))
+        return list(out)
+
+
+def dequant(trellis, k, n, K, out):
+    check(load().gfl_dequant(ptr(trellis), k, n, K, ptr(out), _stream()))
+    return out
+
+
+def synth_trellis(dst, seed, nbytes=None):
+    nb = dst.numel() * dst.element_size() if nbytes is None else int(nbytes)
+    check(load().gfl_synth_trellis(ptr(dst), nb, C.c_uint64(seed & 0xFFFFFFFFFFFFFFFF), _stream()))
+    return dst
+
+
+def split(sel, w, z, E, first, slotof, score, pol, ctrl, hx, hpicks, seq, li, keep_ids, sel_out, w_out, dflag,
+          stats, rres):
+    """ft_split with the reference's argument list (ctrl/hx/hpicks as integer addresses)."""
+    bsz, H = z.shape
+    n = sel.numel()
+    check(load().gfl_split(ptr(sel), ptr(w), ptr(z), bsz, n, H, int(E), int(first), ptr(slotof), ptr(score),
+                           ptr(pol), C.c_void_p(int(ctrl)), C.c_void_p(int(hx)), C.c_void_p(int(hpicks)), int(seq),
+                           int(li), int(keep_ids), ptr(sel_out), ptr(w_out), ptr(dflag), ptr(stats),
+                           ptr(rres) if rres is not None and rres.numel() else None, _stream()))
+
+
+def combine(out, dflag, ctrl, hout, stats, timeout_ns):
+    """ft_combine with the reference's argument list (ctrl/hout as integer addresses)."""
+    import torch
+    check(load().gfl_combine(ptr(out), int(out.dtype == torch.float16), out.numel(), ptr(dflag),
+                             C.c_void_p(int(ctrl)), C.c_void_p(int(hout)), ptr(stats), int(timeout_ns), _stream()))
+
+
+def grouped_rows(sel, w, take, E):
+    """Host routine over numpy arrays (tier_lut_build_grouped_rows)."""
+    import numpy as np
+    sel = np.ascontiguousarray(sel, dtype=np.int64)
+    T, K = sel.shape
+    w = np.ascontiguousarray(w, dtype=np.float32).reshape(T, K)
+    take = np.ascontiguousarray(take, dtype=np.uint8)
+    if take.size != E:
+        raise ValueError("grouped take must be contiguous CPU uint8 [E]")
+    ex = np.zeros(E, np.int32); off = np.zeros(E + 1, np.int32)
+    rt = np.zeros(max(1, T * K), np.int32); rw = np.zeros(max(1, T * K), np.float32)
+    rows = C.c_int(0)
+    P = lambda a: a.ctypes.data_as(C.c_void_p)
+    n = load().gfl_grouped_rows(P(sel), P(w), T, K, P(take), int(E), P(ex), P(off), P(rt), P(rw), C.byref(rows))
+    if n < 0:
+        raise ValueError(load().gfl_last_error().decode())
+    r = rows.value
+    return ex[:n].copy(), off[:n + 1].copy(), rt[:r].copy(), rw[:r].copy()

@@ -1,0 +1,300 @@
+// C-ABI host layer of gfl_moe (include/gfl_moe.h): argument checks, layer registry, workspace, kernel dispatch.
+#include "gfl_moe.h"
+#include "gfl_internal.hpp"
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg)
+{
+    g_err = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what)
+{
+    return fail(GFL_ERUNTIME, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define GFL_HIP(call)                                       \
+    do                                                      \
+    {                                                       \
+        hipError_t e_ = (call);                             \
+        if (e_ != hipSuccess) return hip_fail(e_, #call);   \
+    } while (0)
+
+struct Layer
+{
+    int E = 0, H = 0, I = 0, K[3] = { 0, 0, 0 };
+    uint64_t* dptrs = nullptr;  // device copy of the [E][9] table
+};
+
+}  // namespace
+
+struct gfl_ctx
+{
+    int device = 0;
+    std::vector<Layer> layers;
+    std::mutex mu;
+    // workspace (grown on demand, never shrunk)
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    int64_t calls = 0, picks = 0;
+};
+
+namespace {
+
+struct Workspace
+{
+    gfl::PlanView pv;
+    float* ygu;      // [2][cap][I]
+    uint16_t* xtd;   // [cap][I]
+    float* yd;       // [cap][H]
+};
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+int ensure_ws(gfl_ctx* c, int cap, int H, int I, Workspace& w)
+{
+    const size_t ints = align256(sizeof(int) * (size_t)(4 + 6 * cap + 2));
+    const size_t b_ygu = align256(sizeof(float) * 2 * (size_t)cap * I);
+    const size_t b_xtd = align256(sizeof(uint16_t) * (size_t)cap * I);
+    const size_t b_yd = align256(sizeof(float) * (size_t)cap * H);
+    const size_t need = ints + b_ygu + b_xtd + b_yd;
+    if (need > c->ws_bytes)
+    {
+        if (c->ws) GFL_HIP(hipFree(c->ws));
+        c->ws = nullptr;
+        c->ws_bytes = 0;
+        hipError_t e = hipMalloc(&c->ws, need);
+        if (e != hipSuccess) return fail(GFL_ENOMEM, std::string("workspace hipMalloc: ") + hipGetErrorString(e));
+        c->ws_bytes = need;
+    }
+    char* b = static_cast<char*>(c->ws);
+    int* ip = reinterpret_cast<int*>(b);
+    w.pv.hdr = ip;
+    w.pv.uexp = ip + 4;
+    w.pv.uoff = w.pv.uexp + cap;
+    w.pv.slot_pick = w.pv.uoff + cap + 1;
+    w.pv.slot_u = w.pv.slot_pick + cap;
+    w.pv.pick_slot = w.pv.slot_u + cap;
+    w.pv.pick_job = w.pv.pick_slot + cap;
+    w.pv.cap_slots = cap;
+    w.ygu = reinterpret_cast<float*>(b + ints);
+    w.xtd = reinterpret_cast<uint16_t*>(b + ints + b_ygu);
+    w.yd = reinterpret_cast<float*>(b + ints + b_ygu + b_xtd);
+    return GFL_OK;
+}
+
+bool k_ok(int K) { return K >= 2 && K <= 5; }
+
+}  // namespace
+
+extern "C" {
+
+const char* gfl_last_error(void) { return g_err.c_str(); }
+
+int gfl_version(void) { return 100; }
+
+int gfl_ctx_create(int device, gfl_ctx** out)
+{
+    if (!out) return fail(GFL_EINVAL, "gfl_ctx_create: out is NULL");
+    int n = 0;
+    GFL_HIP(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n) return fail(GFL_EINVAL, "gfl_ctx_create: no such device");
+    gfl_ctx* c = new gfl_ctx();
+    c->device = device;
+    *out = c;
+    return GFL_OK;
+}
+
+int gfl_ctx_destroy(gfl_ctx* c)
+{
+    if (!c) return GFL_OK;
+    hipSetDevice(c->device);
+    for (auto& L : c->layers)
+        if (L.dptrs) hipFree(L.dptrs);
+    if (c->ws) hipFree(c->ws);
+    delete c;
+    return GFL_OK;
+}
+
+int gfl_register_layer(gfl_ctx* c, int li, int E, int H, int I, int k_gate, int k_up, int k_down, const uint64_t* ptrs)
+{
+    if (!c || !ptrs) return fail(GFL_EINVAL, "gfl_register_layer: NULL argument");
+    if (li < 0 || li > 4096) return fail(GFL_EINVAL, "gfl_register_layer: layer index out of range");
+    if (E < 1 || E > gfl::MAX_EXPERTS) return fail(GFL_EINVAL, "gfl_register_layer: E must be 1..1024");
+    if (H < 128 || I < 128 || H % 128 || I % 128) return fail(GFL_EINVAL, "gfl_register_layer: H and I must be multiples of 128");
+    if (!k_ok(k_gate) || !k_ok(k_up) || !k_ok(k_down)) return fail(GFL_EINVAL, "gfl_register_layer: K must be 2..5");
+    for (int i = 0; i < E * 9; ++i)
+        if (ptrs[i] == 0 || (ptrs[i] & 3)) return fail(GFL_EINVAL, "gfl_register_layer: NULL or misaligned device pointer");
+    std::lock_guard<std::mutex> g(c->mu);
+    GFL_HIP(hipSetDevice(c->device));
+    if ((int)c->layers.size() <= li) c->layers.resize(li + 1);
+    Layer& L = c->layers[li];
+    if (L.dptrs) GFL_HIP(hipFree(L.dptrs));
+    L.dptrs = nullptr;
+    GFL_HIP(hipMalloc(&L.dptrs, sizeof(uint64_t) * 9 * (size_t)E));
+    GFL_HIP(hipMemcpy(L.dptrs, ptrs, sizeof(uint64_t) * 9 * (size_t)E, hipMemcpyHostToDevice));
+    L.E = E; L.H = H; L.I = I; L.K[0] = k_gate; L.K[1] = k_up; L.K[2] = k_down;
+    return GFL_OK;
+}
+
+int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half, int M,
+                    int topk, float* out, int mode, float act_limit, gfl_stream stream)
+{
+    if (!c || !x || !sel || !w || !out) return fail(GFL_EINVAL, "gfl_moe_forward: NULL argument");
+    if (li < 0 || li >= (int)c->layers.size() || !c->layers[li].dptrs)
+        return fail(GFL_EINVAL, "gfl_moe_forward: layer not registered");
+    if (mode != GFL_MODE_AUTO && mode != GFL_MODE_EXACT)
+        return fail(GFL_EINVAL, "gfl_moe_forward: the device path computes EXACT (mode 1 or -1)");
+    if (M < 1 || topk < 1 || topk > gfl::MAX_TOPK || (int64_t)M * topk > gfl::MAX_PICKS)
+        return fail(GFL_EINVAL, "gfl_moe_forward: need 1 <= topk <= 16 and M*topk <= 1024");
+    if (!std::isfinite(act_limit) || act_limit < 0) return fail(GFL_EINVAL, "gfl_moe_forward: act_limit must be >= 0");
+    std::lock_guard<std::mutex> g(c->mu);
+    const Layer& L = c->layers[li];
+    GFL_HIP(hipSetDevice(c->device));
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const int P = M * topk;
+    Workspace ws;
+    if (int r = ensure_ws(c, P, L.H, L.I, ws)) return r;
+    const int umax = P < L.E ? P : L.E;
+    const int ns = M < 8 ? M : 8;   // slots per pass; an expert holds at most M slots unless a token repeats it
+    gfl::launch_plan(sel, P, topk, L.E, ws.pv, st);
+    if (L.K[0] == L.K[1])
+    {
+        if (gfl::launch_chain(L.K[0], ns, true, L.dptrs, 0, 2, L.H, L.I, ws.pv, topk, umax, x, ws.ygu, st))
+            return fail(GFL_EINVAL, "gfl_moe_forward: unsupported K");
+    }
+    else
+    {
+        if (gfl::launch_chain(L.K[0], ns, true, L.dptrs, 0, 1, L.H, L.I, ws.pv, topk, umax, x, ws.ygu, st) ||
+            gfl::launch_chain(L.K[1], ns, true, L.dptrs, 1, 1, L.H, L.I, ws.pv, topk, umax, x,
+                              ws.ygu + (size_t)P * L.I, st))
+            return fail(GFL_EINVAL, "gfl_moe_forward: unsupported K");
+    }
+    gfl::launch_act(L.dptrs, ws.pv, P, ws.ygu, ws.xtd, L.I, act_limit, st);
+    if (gfl::launch_chain(L.K[2], ns, false, L.dptrs, 2, 1, L.I, L.H, ws.pv, topk, umax, ws.xtd, ws.yd, st))
+        return fail(GFL_EINVAL, "gfl_moe_forward: unsupported K");
+    gfl::launch_final(L.dptrs, ws.pv, w, w_is_half ? 1 : 0, M, topk, ws.yd, out, L.H, st);
+    GFL_HIP(hipGetLastError());
+    c->calls += 1;
+    c->picks += P;
+    return GFL_OK;
+}
+
+int gfl_dequant(const void* trellis, int k, int n, int K, uint16_t* out, gfl_stream stream)
+{
+    if (!trellis || !out) return fail(GFL_EINVAL, "gfl_dequant: NULL argument");
+    if (k < 16 || n < 16 || k % 16 || n % 16) return fail(GFL_EINVAL, "gfl_dequant: k and n must be multiples of 16");
+    if (!k_ok(K)) return fail(GFL_EINVAL, "gfl_dequant: K must be 2..5");
+    if (gfl::launch_dequant(static_cast<const uint8_t*>(trellis), k, n, K, out, reinterpret_cast<hipStream_t>(stream)))
+        return fail(GFL_EINVAL, "gfl_dequant: unsupported K");
+    GFL_HIP(hipGetLastError());
+    return GFL_OK;
+}
+
+int gfl_split(const int64_t* sel, const uint16_t* w, const uint16_t* z, int bsz, int n, int H, int E, int first,
+              const int32_t* slotof, const float* score, const float* pol, int64_t* ctrl, uint16_t* hx,
+              int32_t* hpicks, int64_t seq, int li, int keep_ids, int64_t* sel_out, uint16_t* w_out, int64_t* dflag,
+              int64_t* stats, const int32_t* rres, gfl_stream stream)
+{
+    if (!sel || !w || !z || !slotof || !score || !pol || !ctrl || !hx || !hpicks || !sel_out || !w_out || !dflag || !stats)
+        return fail(GFL_EINVAL, "gfl_split: NULL argument");
+    if (bsz < 1 || n < 1 || n % bsz) return fail(GFL_EINVAL, "gfl_split: n must be a positive multiple of bsz");
+    if (n > gfl::MAX_PICKS) return fail(GFL_EINVAL, "gfl_split: n <= 1024");
+    if (E < 1 || E > gfl::MAX_EXPERTS || H % 8) return fail(GFL_EINVAL, "ft_split: E <= 1024");
+    if ((reinterpret_cast<uintptr_t>(z) | reinterpret_cast<uintptr_t>(hx)) & 15)
+        return fail(GFL_EINVAL, "gfl_split: z and hx must be 16-byte aligned");
+    gfl::launch_split(sel, w, z, n, bsz, n / bsz, H, E, first, slotof, score, pol, ctrl, hx, hpicks, seq, li, keep_ids,
+                      sel_out, w_out, dflag, stats, rres, reinterpret_cast<hipStream_t>(stream));
+    GFL_HIP(hipGetLastError());
+    return GFL_OK;
+}
+
+int gfl_combine(void* out, int out_is_half, int n, const int64_t* dflag, const int64_t* ctrl, const float* hout,
+                int64_t* stats, int64_t timeout_ns, gfl_stream stream)
+{
+    if (!out || !dflag || !ctrl || !hout || !stats) return fail(GFL_EINVAL, "gfl_combine: NULL argument");
+    if (n < 0) return fail(GFL_EINVAL, "gfl_combine: n < 0");
+    if (timeout_ns < 0) return fail(GFL_EINVAL, "gfl_combine: timeout_ns < 0");
+    gfl::launch_combine(out, out_is_half ? 1 : 0, n, dflag, ctrl, hout, stats, timeout_ns,
+                        reinterpret_cast<hipStream_t>(stream));
+    GFL_HIP(hipGetLastError());
+    return GFL_OK;
+}
+
+int gfl_grouped_rows(const int64_t* sel, const float* w, int T, int K, const uint8_t* take, int E, int32_t* experts,
+                     int32_t* offsets, int32_t* row_token, float* row_weight, int* rows)
+{
+    if (!sel || !w || !take || !experts || !offsets || !row_token || !row_weight || !rows)
+        return fail(GFL_EINVAL, "gfl_grouped_rows: NULL argument");
+    if (T < 0 || K < 0 || E < 1) return fail(GFL_EINVAL, "grouped E must fit a positive int32 expert count");
+    std::vector<int32_t> count((size_t)E, 0), last((size_t)E, -1), cursor((size_t)E, 0);
+    for (int e = 0; e < E; ++e)
+        if (take[e] > 1) return -fail(GFL_EINVAL, "grouped take entries must be zero or one");
+    for (int t = 0; t < T; ++t)
+        for (int k = 0; k < K; ++k)
+        {
+            const int64_t at = (int64_t)t * K + k, e = sel[at];
+            const float wv = w[at];
+            if (!std::isfinite(wv)) return -fail(GFL_EINVAL, "grouped routing weight must be finite");
+            if (e < -1 || e >= E) return -fail(GFL_EINVAL, "grouped expert index out of range");
+            if (e == -1)
+            {
+                if (wv != 0.0f) return -fail(GFL_EINVAL, "grouped masked picks require zero weight");
+                continue;
+            }
+            if (!take[e]) continue;
+            if (last[(size_t)e] == t) return -fail(GFL_EINVAL, "grouped duplicate expert for token");
+            last[(size_t)e] = t;
+            ++count[(size_t)e];
+        }
+    int nexp = 0;
+    offsets[0] = 0;
+    for (int e = 0; e < E; ++e)
+        if (count[(size_t)e])
+        {
+            experts[nexp] = e;
+            cursor[(size_t)e] = offsets[nexp];
+            offsets[nexp + 1] = offsets[nexp] + count[(size_t)e];
+            ++nexp;
+        }
+    for (int t = 0; t < T; ++t)
+        for (int k = 0; k < K; ++k)
+        {
+            const int64_t at = (int64_t)t * K + k, e = sel[at];
+            if (e < 0 || !take[e]) continue;
+            const int32_t row = cursor[(size_t)e]++;
+            row_token[row] = t;
+            row_weight[row] = w[at];
+        }
+    *rows = offsets[nexp];
+    return nexp;
+}
+
+int gfl_synth_trellis(void* dst, size_t nbytes, uint64_t seed, gfl_stream stream)
+{
+    if (!dst) return fail(GFL_EINVAL, "gfl_synth_trellis: NULL destination");
+    gfl::launch_synth(static_cast<uint8_t*>(dst), nbytes, seed, reinterpret_cast<hipStream_t>(stream));
+    GFL_HIP(hipGetLastError());
+    return GFL_OK;
+}
+
+int gfl_stats(gfl_ctx* c, int64_t* out, int n)
+{
+    if (!c || !out) return fail(GFL_EINVAL, "gfl_stats: NULL argument");
+    const int64_t v[4] = { c->calls, c->picks, (int64_t)c->layers.size(), (int64_t)c->ws_bytes };
+    for (int i = 0; i < n && i < 4; ++i) out[i] = v[i];
+    return GFL_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,150 @@
+// Device helpers shared by the gfx950 kernels: EXL3 trellis decode, fp16 rounding points, wave-level Hadamard-128.
+//
+// Trellis format (kernels/cpu_avx2/ft_core.h:28-83 of the reference): a 16x16 tile is a circular 256*K-bit stream,
+// MSB-first inside little-endian 32-bit words; weight t takes the 16-bit state ending at bit (t+1)*K, hashes it as
+// bytesum(state * 0x83DCD12D mod 2^32) and maps it to fp16 with one rounding of fma(1024 + sum, KINV, KBIAS).
+// Stream index t*8+j sits at tile row {r0, r0+1, r0+8, r0+9}[j%4] (r0 = 2*(t%4)), column t/4 + 8*(j>=4).
+//
+// Lane layout used everywhere: lane l = 16*q + n decodes the four consecutive stream indices
+// 32*(n%8) + 8*q + 4*(n/8) + {0,1,2,3}, i.e. column n, rows 2q + {0,1,8,9} of the tile. Those four weights are
+// exactly the MFMA 16x16x16 B-operand slice of lane l when the K index is 4q + j.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace gfl {
+
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+constexpr uint32_t MUL1 = 0x83DCD12Du;
+constexpr float HADF = 0.088388347648f;
+constexpr uint16_t KINV_BITS = 0x1eee, KBIAS_BITS = 0xc931;
+
+// Per-lane decode constants: byte offsets of the two words holding the lane's 3K+16-bit window inside a tile, and the
+// funnel shift that puts the window's last bit at bit 0.
+struct LaneDec
+{
+    uint32_t o0, o1, sh;
+};
+
+__host__ __device__ inline LaneDec lane_dec(int lane, int K)
+{
+    const int q = lane >> 4, n = lane & 15;
+    const int S = 32 * (n & 7) + 8 * q + 4 * (n >> 3);  // first stream index of the lane's run
+    const int e = (S + 4) * K;                           // end (exclusive) of the run's window, in stream bits
+    const int words = 8 * K;
+    const int wa = (e - 33) >= 0 ? (e - 33) / 32 : -1;  // floor((e-33)/32): e - 32*wa in [33, 64]
+    LaneDec d;
+    d.sh = (uint32_t)(64 - (e - 32 * wa));
+    d.o0 = (uint32_t)(4 * ((wa + words) % words));
+    d.o1 = (uint32_t)(4 * ((wa + 1 + words) % words));
+    return d;
+}
+
+__device__ inline uint32_t ld_u32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
+
+// four consecutive states -> four fp16 codebook weights, packed {w0,w1}, {w2,w3}
+template <int K>
+__device__ inline half4 decode4(uint32_t hi, uint32_t lo, uint32_t sh)
+{
+    const uint32_t R = __builtin_amdgcn_alignbit(hi, lo, sh);
+    const uint32_t p0 = __builtin_amdgcn_ubfe(R, 3 * K, 16) * MUL1;
+    const uint32_t p1 = __builtin_amdgcn_ubfe(R, 2 * K, 16) * MUL1;
+    const uint32_t p2 = __builtin_amdgcn_ubfe(R, K, 16) * MUL1;
+    const uint32_t p3 = __builtin_amdgcn_ubfe(R, 0, 16) * MUL1;
+    // sum of the product bytes on top of 0x6400 = fp16 bits of (1024 + sum); the hi variant lands in bits 16..31
+    uint32_t s01 = __builtin_amdgcn_sad_u8(p0, 0u, 0x64006400u);
+    uint32_t s23 = __builtin_amdgcn_sad_u8(p2, 0u, 0x64006400u);
+    asm("v_sad_hi_u8 %0, %1, 0, %0" : "+v"(s01) : "v"(p1));
+    asm("v_sad_hi_u8 %0, %1, 0, %0" : "+v"(s23) : "v"(p3));
+    half2v a, b;
+    __builtin_memcpy(&a, &s01, 4);
+    __builtin_memcpy(&b, &s23, 4);
+    _Float16 ki, kb;
+    const uint16_t kib = KINV_BITS, kbb = KBIAS_BITS;
+    __builtin_memcpy(&ki, &kib, 2);
+    __builtin_memcpy(&kb, &kbb, 2);
+    const half2v kinv2 = { ki, ki }, kbias2 = { kb, kb };
+    // one fp16 rounding of an exact product-sum (v_pk_fma_f16): equals round16(fma_f32(1024+s, KINV, KBIAS))
+    const half2v w01 = __builtin_elementwise_fma(a, kinv2, kbias2);
+    const half2v w23 = __builtin_elementwise_fma(b, kinv2, kbias2);
+    half4 r = { w01[0], w01[1], w23[0], w23[1] };
+    return r;
+}
+
+// fp32 -> fp16 (round to nearest even, subnormals kept) as an opaque conversion. The reference rounds every product
+// to fp32 before rounding it to fp16 (e.g. r16(y * HAD), ft_core.h:102,109); left to itself the compiler fuses
+// fptrunc(a*b) into one v_fma_mixlo_f16, which rounds once and differs at fp16 ties.
+__device__ inline uint32_t f2h_bits(float x)
+{
+    uint32_t h;
+    asm("v_cvt_f16_f32 %0, %1" : "=v"(h) : "v"(x));
+    return h & 0xFFFFu;
+}
+
+__device__ inline float r16(float x)
+{
+    uint32_t h;
+    float r;
+    asm("v_cvt_f16_f32 %0, %1" : "=v"(h) : "v"(x));
+    asm("v_cvt_f32_f16 %0, %1" : "=v"(r) : "v"(h));
+    return r;
+}
+
+// Wave-level Hadamard-128 in the reference's butterfly order (had128, ft_core.h:89-94): lane L holds elements L and
+// L+64; stages w = 1..32 cross lanes, w = 64 stays in the lane. Every element sees the same add/sub sequence.
+__device__ inline void fwht128(float& v0, float& v1)
+{
+    const int L = threadIdx.x & 63;
+#pragma unroll
+    for (int w = 1; w < 64; w <<= 1)
+    {
+        const float p0 = __shfl_xor(v0, w), p1 = __shfl_xor(v1, w);
+        if (L & w) { v0 = p0 - v0; v1 = p1 - v1; }
+        else { v0 = v0 + p0; v1 = v1 + p1; }
+    }
+    const float a = v0, c = v1;
+    v0 = a + c;
+    v1 = a - c;
+}
+
+__device__ inline float h2f_bits(uint16_t h) { __half x; __builtin_memcpy(&x, &h, 2); return __half2float(x); }
+
+// prep_block (ft_core.h:97-102) on lane-held elements L, L+64
+__device__ inline void prep_block_wave(float& v0, float& v1, float s0, float s1)
+{
+    v0 = v0 * s0;
+    v1 = v1 * s1;
+    fwht128(v0, v1);
+    v0 = r16(v0 * HADF);
+    v1 = r16(v1 * HADF);
+}
+
+// out_block (ft_core.h:105-110)
+__device__ inline void out_block_wave(float& v0, float& v1, float s0, float s1)
+{
+    v0 = r16(v0);
+    v1 = r16(v1);
+    fwht128(v0, v1);
+    v0 = r16(v0 * HADF * s0);
+    v1 = r16(v1 * HADF * s1);
+}
+
+// silu(g) * u with the exllamav3 clamp (ft_core.h:123-132). exp is taken in fp64 and rounded once, so it equals a
+// correctly rounded expf except in vanishingly rare near-tie cases.
+__device__ inline float act_mul(float g, float u, float limit)
+{
+    const float e = (float)exp(-(double)g);
+    float x = g / (1.0f + e);
+    if (limit != 0.0f)
+    {
+        u = fminf(fmaxf(u, -limit), limit);
+        x = fminf(x, limit);
+    }
+    return x * u;
+}
+
+}  // namespace gfl

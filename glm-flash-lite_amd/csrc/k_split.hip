@@ -1,0 +1,294 @@
+// Token split / combine around the experts, plus the synthetic trellis generator.
+//
+// split   = ft_split (kernels/cpu_avx2/ft_tier_cu.cu:21-157 stock, kernels/k110/ft_split_fast.cu:18-198 fast):
+//           count each local expert's picks (w != 0), hits = slotof[e] >= 0, rank the misses coldest first
+//           (score ascending, id ascending), choose how many go to the host lane with the cost model, publish the host
+//           job (x rows, picks in pick order, control words) and mask those picks out of the selection.
+//           Unique experts are discovered from the picks and ranked in parallel, the cost search stays serial with the
+//           reference's float expressions (uncontracted), and the published pick list is built in pick order from a
+//           wavefront ballot prefix.
+// combine = ft_combine (ft_tier_cu.cu:205-235, trellis build): wait (bounded) for the host done flag, add the fp32
+//           partial into the fp32/fp16 output.
+#include "gfl_device.hpp"
+#include "gfl_internal.hpp"
+
+namespace gfl {
+
+__global__ __launch_bounds__(256) void split_kernel(const int64_t* __restrict__ sel, const uint16_t* __restrict__ w,
+    const uint16_t* __restrict__ z, int n, int bsz, int topk, int H, int E, int first,
+    const int32_t* __restrict__ slotof, const float* __restrict__ score, const float* __restrict__ p, int64_t* ctrl,
+    uint16_t* hx, int32_t* hpicks, int64_t seq, int li, int keep_ids, int64_t* sel_out, uint16_t* w_out,
+    int64_t* dflag, int64_t* stats, const int32_t* __restrict__ rres)
+{
+    __shared__ int cnt[MAX_EXPERTS];
+    __shared__ unsigned char cpu[MAX_EXPERTS];
+    __shared__ int s_le[MAX_PICKS];          // local expert id of pick s, or -1 (out of range)
+    __shared__ unsigned char s_nz[MAX_PICKS];
+    __shared__ int uq[MAX_PICKS], nu;         // unique local experts with a nonzero pick
+    __shared__ int ue[MAX_PICKS];             // unique experts sorted ascending
+    __shared__ int miss[MAX_PICKS], rmiss[MAX_PICKS];
+    __shared__ int s_nm, s_nh, s_nr, s_publish, s_npk;
+    __shared__ float pol[20];
+    const int t = threadIdx.x, lane = t & 63;
+    for (int e = t; e < E; e += blockDim.x) { cnt[e] = 0; cpu[e] = 0; }
+    if (t < 20) pol[t] = p[t];
+    if (t == 0) nu = 0;
+    for (int s = t; s < n; s += blockDim.x)
+    {
+        const int64_t e = sel[s] - first;
+        s_le[s] = (e >= 0 && e < E) ? (int)e : -1;
+        s_nz[s] = (w[s] & 0x7FFFu) != 0;    // __half2float(w) != 0.0f (NaN counts as nonzero)
+    }
+    __syncthreads();
+    for (int s = t; s < n; s += blockDim.x)
+        if (s_nz[s] && s_le[s] >= 0)
+            if (atomicAdd(&cnt[s_le[s]], 1) == 0) uq[atomicAdd(&nu, 1)] = s_le[s];
+    __syncthreads();
+    const int U = nu;
+    for (int i = t; i < U; i += blockDim.x)
+    {
+        int r = 0;
+        for (int k = 0; k < U; ++k) r += uq[k] < uq[i];
+        ue[r] = uq[i];
+    }
+    __syncthreads();
+    const bool tri = pol[8] > 0.5f && rres != nullptr && (int)pol[6] < 0;
+    // misses ranked inside their class (score ascending, ties by ascending id) = the stock insertion order
+    for (int i = t; i < U; i += blockDim.x)
+    {
+        const int e = ue[i];
+        if (slotof[e] >= 0) continue;
+        const int cl = (tri && rres[e]) ? 1 : 0;
+        const float sc = score[e];
+        int r = 0;
+        for (int k = 0; k < U; ++k)
+        {
+            const int e2 = ue[k];
+            if (slotof[e2] >= 0 || ((tri && rres[e2]) ? 1 : 0) != cl) continue;
+            const float s2 = score[e2];
+            if (s2 < sc || (s2 == sc && e2 < e)) ++r;
+        }
+        if (cl) rmiss[r] = e; else miss[r] = e;
+    }
+    if (t == 0)
+    {
+        int nh = 0, nr = 0;
+        for (int i = 0; i < U; ++i)
+        {
+            const int e = ue[i];
+            if (slotof[e] >= 0) ++nh;
+            else if (tri && rres[e]) ++nr;
+        }
+        s_nh = nh; s_nr = nr; s_nm = U - nh - nr;
+    }
+    __syncthreads();
+    if (t == 0)
+    {
+        const int nm = s_nm, nh = s_nh, nr = s_nr;
+        const bool lut = pol[12] > 0.0f;
+        int best = 0, bestr = 0;
+        const int force = (int)pol[6], maxc = min((int)pol[5], nm);
+        if (force >= 0) best = min(force, nm);
+        else if (tri)
+        {
+            float bt = 1e30f, cr = 0.0f;
+            for (int kr = 0; kr <= nr; ++kr)
+            {
+                if (kr) { const float f = pol[4] * (float)(cnt[rmiss[kr - 1]] - 1); const float g = 1.0f + f; cr = cr + pol[10] * g; }
+                const float rem = kr ? pol[9] + cr : 0.0f;
+                float c = 0.0f, cx = 0.0f;
+                for (int k = 0; k <= maxc; ++k)
+                {
+                    if (k)
+                    {
+                        const float f = pol[4] * (float)(cnt[miss[k - 1]] - 1); const float g = 1.0f + f;
+                        c = c + pol[3] * g;
+                        const float f2 = pol[3] * pol[4];
+                        cx = cx + f2 * (float)(cnt[miss[k - 1]] - 1);
+                    }
+                    const int zz = nm - k + nr - kr;
+                    const float gpu = pol[1] * (float)(nh + zz) + pol[0] * (float)zz;
+                    float loc = 0.0f;
+                    if (k) loc = lut ? (pol[11 + (k < 8 ? k : 8)] + (k > 8 ? pol[3] * (float)(k - 8) : 0.0f)) + cx : pol[2] + c;
+                    const float tt = fmaxf(gpu, fmaxf(loc, rem));
+                    if (tt < bt - 1e-6f) { bt = tt; best = k; bestr = kr; }
+                }
+            }
+            for (int k = 0; k < bestr; ++k) cpu[rmiss[k]] = 1;
+        }
+        else
+        {
+            float bt = 1e30f, c = 0.0f, cx = 0.0f;
+            for (int k = 0; k <= maxc; ++k)
+            {
+                if (k)
+                {
+                    const float f = pol[4] * (float)(cnt[miss[k - 1]] - 1); const float g = 1.0f + f;
+                    c = c + pol[3] * g;
+                    const float f2 = pol[3] * pol[4];
+                    cx = cx + f2 * (float)(cnt[miss[k - 1]] - 1);
+                }
+                const float gpu = pol[1] * (float)(nh + nm - k) + pol[0] * (float)(nm - k);
+                float loc = 0.0f;
+                if (k) loc = lut ? (pol[11 + (k < 8 ? k : 8)] + (k > 8 ? pol[3] * (float)(k - 8) : 0.0f)) + cx : pol[2] + c;
+                const float tt = fmaxf(gpu, loc);
+                if (tt < bt - 1e-6f) { bt = tt; best = k; }
+            }
+        }
+        for (int k = 0; k < best; ++k) cpu[miss[k]] = 1;
+        s_publish = best + bestr > 0 || pol[7] > 0.5f;
+        stats[0] += nh; stats[1] += nm + nr; stats[2] += best + bestr; stats[3] += 1;
+    }
+    __syncthreads();
+    const int publish = s_publish;
+    if (publish && t < 64)
+    {
+        int base = 0;
+        for (int s0 = 0; s0 < n; s0 += 64)
+        {
+            const int s = s0 + lane;
+            const bool take = s < n && s_le[s] >= 0 && cpu[s_le[s]] && s_nz[s];
+            const uint64_t m = __ballot(take);
+            if (take)
+            {
+                const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+                const int k = base + __popcll(m & below);
+                const float wf = h2f_bits(w[s]);
+                int wb;
+                __builtin_memcpy(&wb, &wf, 4);
+                hpicks[k * 3] = s / topk;
+                hpicks[k * 3 + 1] = s_le[s];
+                hpicks[k * 3 + 2] = wb;
+            }
+            base += __popcll(m);
+        }
+        if (t == 0) s_npk = base;
+    }
+    for (int s = t; s < n; s += blockDim.x)
+    {
+        const int64_t e = sel[s];
+        const bool c = s_le[s] >= 0 && cpu[s_le[s]];
+        sel_out[s] = (c && !keep_ids) ? -1 : e;
+        w_out[s] = c ? (uint16_t)0 : w[s];
+    }
+    if (publish)
+    {
+        const int nx = bsz * H / 8;
+        for (int i = t; i < nx; i += blockDim.x)
+            reinterpret_cast<uint4*>(hx)[i] = reinterpret_cast<const uint4*>(z)[i];
+        __threadfence_system();
+        __syncthreads();
+        if (t == 0)
+        {
+            ctrl[2] = li; ctrl[3] = bsz; ctrl[4] = s_npk;
+            __threadfence_system();
+            __hip_atomic_store(&ctrl[0], seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+            __threadfence_system();
+            dflag[0] = seq;
+        }
+    }
+    else if (t == 0) dflag[0] = 0;
+}
+
+// timeout_ticks: bounded wait in wall-clock ticks (the caller converts ns with the device's wall clock rate)
+__global__ __launch_bounds__(256) void combine_kernel(void* out, int is_half, int n, const int64_t* __restrict__ dflag,
+                                                      const int64_t* ctrl, const float* hout, int64_t* stats,
+                                                      int64_t timeout_ticks, int64_t ns_per_tick_q16)
+{
+    __shared__ int go;
+    if (threadIdx.x == 0)
+    {
+        const int64_t s = dflag[0];
+        go = s != 0;
+        if (go)
+        {
+            const int64_t* done = ctrl + 1;
+            if (__hip_atomic_load(done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) >= s && blockIdx.x == 0)
+                atomicAdd(reinterpret_cast<unsigned long long*>(&stats[7]), 1ull);
+            const uint64_t t0 = wall_clock64();
+            uint64_t t1 = t0;
+            while (__hip_atomic_load(done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) < s)
+            {
+                t1 = wall_clock64();
+                if ((int64_t)(t1 - t0) > timeout_ticks)
+                {
+                    go = 0;
+                    if (blockIdx.x == 0) atomicAdd(reinterpret_cast<unsigned long long*>(&stats[6]), 1ull);
+                    break;
+                }
+            }
+            if (blockIdx.x == 0)
+            {
+                const unsigned long long waited = (unsigned long long)(((t1 - t0) * (uint64_t)ns_per_tick_q16) >> 16);
+                atomicAdd(reinterpret_cast<unsigned long long*>(&stats[4]), waited);
+                atomicAdd(reinterpret_cast<unsigned long long*>(&stats[5]), 1ull);
+            }
+        }
+    }
+    __syncthreads();
+    if (!go) return;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+    {
+        const float v = __hip_atomic_load(&hout[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        if (is_half)
+        {
+            __half* o = reinterpret_cast<__half*>(out);
+            o[i] = __float2half_rn(__half2float(o[i]) + v);
+        }
+        else reinterpret_cast<float*>(out)[i] += v;
+    }
+}
+
+// splitmix64 in counter form: output i of the sequence seeded with `seed` is mix(seed + (i+1) * golden)
+__device__ inline uint64_t splitmix64_at(uint64_t seed, uint64_t i)
+{
+    uint64_t z = seed + (i + 1) * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__global__ __launch_bounds__(256) void synth_kernel(uint8_t* dst, size_t nbytes, uint64_t seed)
+{
+    const size_t nw = nbytes / 8;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < nw; i += (size_t)gridDim.x * blockDim.x)
+        reinterpret_cast<uint64_t*>(dst)[i] = splitmix64_at(seed, i);
+    if (blockIdx.x == 0 && threadIdx.x == 0)
+    {
+        const uint64_t v = splitmix64_at(seed, nw);
+        for (size_t b = nw * 8; b < nbytes; ++b) dst[b] = (uint8_t)(v >> (8 * (b - nw * 8)));
+    }
+}
+
+int launch_split(const int64_t* sel, const uint16_t* w, const uint16_t* z, int n, int bsz, int topk, int H, int E,
+                 int first, const int32_t* slotof, const float* score, const float* pol, int64_t* ctrl, uint16_t* hx,
+                 int32_t* hpicks, int64_t seq, int li, int keep_ids, int64_t* sel_out, uint16_t* w_out,
+                 int64_t* dflag, int64_t* stats, const int32_t* rres, hipStream_t st)
+{
+    hipLaunchKernelGGL(split_kernel, dim3(1), dim3(256), 0, st, sel, w, z, n, bsz, topk, H, E, first, slotof, score,
+                       pol, ctrl, hx, hpicks, seq, li, keep_ids, sel_out, w_out, dflag, stats, rres);
+    return 0;
+}
+
+void launch_combine(void* out, int is_half, int n, const int64_t* dflag, const int64_t* ctrl, const float* hout,
+                    int64_t* stats, int64_t timeout_ns, hipStream_t st)
+{
+    int dev = 0, khz = 100000;
+    hipGetDevice(&dev);
+    if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || khz <= 0) khz = 100000;
+    const int64_t ticks = (int64_t)((double)timeout_ns * (double)khz / 1e6);
+    const int64_t ns_per_tick_q16 = (int64_t)(65536.0 * 1e6 / (double)khz);
+    hipLaunchKernelGGL(combine_kernel, dim3(16), dim3(256), 0, st, out, is_half, n, dflag, ctrl, hout, stats, ticks,
+                       ns_per_tick_q16);
+}
+
+void launch_synth(uint8_t* dst, size_t nbytes, uint64_t seed, hipStream_t st)
+{
+    const size_t nw = nbytes / 8;
+    size_t blocks = (nw + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks == 0) blocks = 1;
+    hipLaunchKernelGGL(synth_kernel, dim3((unsigned)blocks), dim3(256), 0, st, dst, nbytes, seed);
+}
+
+}  // namespace gfl

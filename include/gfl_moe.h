@@ -1,0 +1,106 @@
+/* gfl_moe -- MI355X (gfx950) routed-MoE expert path behind a C ABI.
+ *
+ * Drop-in for the routed-expert path of glm-flash-lite: the ft_split / ft_combine kernels the k_ftsplit and cpu_tier
+ * monkeypatches call, the expert-call signature of the CPU tier (tier_init / tier_add_layer / tier_forward) and the
+ * expert-residency lookup of expert_cache. With every expert resident in HBM the host tier and the PCIe cache are
+ * gone; what remains is the EXL3 trellis decode + Hadamard SwiGLU expert arithmetic and the split/combine around it.
+ *
+ * Conventions: plain pointers and sizes, no framework types. Device pointers unless stated otherwise. Every call that
+ * launches work takes a stream (a hipStream_t; NULL = the null stream), is stream-ordered and never synchronises the
+ * host. Return value 0 = success; otherwise a GFL_E* code with a message in gfl_last_error() (thread-local).
+ * Citations are paths in the reference repository.
+ */
+#ifndef GFL_MOE_H
+#define GFL_MOE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct gfl_ctx gfl_ctx;
+typedef void* gfl_stream; /* hipStream_t */
+
+enum
+{
+    GFL_OK = 0,
+    GFL_EINVAL = 1,   /* bad argument (shape, dtype code, unregistered layer, unsupported K) */
+    GFL_ERUNTIME = 2, /* HIP runtime error */
+    GFL_ENOMEM = 3,   /* device allocation failed */
+};
+
+/* Expert arithmetic modes, numbered as tier_forward's `mode` (kernels/cpu_avx2/ft_tier_ext.cpp:865-904).
+ * The device path computes EXACT (bit-identical to the reference's EXACT mode); AUTO selects it. */
+enum
+{
+    GFL_MODE_AUTO = -1,
+    GFL_MODE_AFFINE = 0,
+    GFL_MODE_EXACT = 1,
+    GFL_MODE_I16 = 2,
+};
+
+/* Last error message of the calling thread ("" if none). */
+const char* gfl_last_error(void);
+/* ABI version (major*100 + minor). */
+int gfl_version(void);
+
+/* Context on one device: registered layers plus the per-call workspace.
+ * Replaces the global Tier singleton of tier_init (kernels/cpu_avx2/ft_tier_ext.cpp:137-157). */
+int gfl_ctx_create(int device, gfl_ctx** out);
+int gfl_ctx_destroy(gfl_ctx* ctx);
+
+/* Register layer `li`: E experts of a SwiGLU MLP, hidden H, intermediate I; gate/up are [H->I], down [I->H], each an
+ * EXL3 trellis of K bits per weight (k_gate/k_up/k_down in 2..5) in 16x16 tiles stored row-major [k/16][n/16].
+ * ptrs: HOST array [E][9] of DEVICE addresses per expert:
+ *   trellis gate, up, down; suh_gate, svh_gate, suh_up, svh_up, suh_down, svh_down (fp16 sign/scale vectors).
+ * The table is copied; the weights stay where the caller put them (full HBM residency).
+ * Replaces tier_add_layer (ft_tier_ext.cpp:160-211) and the pointer tables expert_cache maintains
+ * (glm53/expert_cache.py:540-635). */
+int gfl_register_layer(gfl_ctx* ctx, int li, int E, int H, int I, int k_gate, int k_up, int k_down,
+                       const uint64_t* ptrs);
+
+/* Routed-expert forward of one layer (the expert call, tier_forward, ft_tier_ext.cpp:865-904):
+ *   out[t] = sum over picks k of w[t,k] * expert_{sel[t,k]}(x[t]), picks with sel < 0 skipped,
+ * summed in the reference's job order (moe_forward, kernels/cpu_avx2/ft_core.h:1338-1407).
+ * x: fp16 [M, H]; sel: int64 [M, topk]; w: [M, topk] fp16 (w_is_half=1) or fp32; out: fp32 [M, H].
+ * act_limit: SwiGLU clamp (tier_set_act_limit, ft_tier_ext.cpp:629-636), 0 = off. M*topk <= 1024, topk <= 16. */
+int gfl_moe_forward(gfl_ctx* ctx, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half, int M,
+                    int topk, float* out, int mode, float act_limit, gfl_stream stream);
+
+/* Dequantize one trellis matrix to fp16 W[k][n] (dense_weights, kernels/cpu_avx2/ft_core.h:1657-1672). */
+int gfl_dequant(const void* trellis, int k, int n, int K, uint16_t* out, gfl_stream stream);
+
+/* ft_split (kernels/cpu_avx2/ft_tier_cu.cu:238-271, kernels/k110/ft_split_fast.cu:200-235), same arguments with
+ * tensors as pointers: sel int64 [n], w fp16 [n], z fp16 [bsz, H], slotof int32 [E], score fp32 [E], pol fp32 [20],
+ * ctrl int64 [>=5] / hx fp16 [bsz*H] / hpicks int32 [n*3] (host-mapped or device memory), sel_out int64 [n],
+ * w_out fp16 [n], dflag int64 [1], stats int64 [8], rres int32 [E] or NULL. n = bsz*topk <= 1024, E <= 1024. */
+int gfl_split(const int64_t* sel, const uint16_t* w, const uint16_t* z, int bsz, int n, int H, int E, int first,
+              const int32_t* slotof, const float* score, const float* pol, int64_t* ctrl, uint16_t* hx,
+              int32_t* hpicks, int64_t seq, int li, int keep_ids, int64_t* sel_out, uint16_t* w_out, int64_t* dflag,
+              int64_t* stats, const int32_t* rres, gfl_stream stream);
+
+/* ft_combine (kernels/cpu_avx2/ft_tier_cu.cu:273-294): when dflag != 0 wait (at most timeout_ns) for the done word
+ * ctrl[1] >= dflag, then out += hout. out fp32 or fp16 (out_is_half) [n]; stats as ft_split's (4 wait ns, 5 waits,
+ * 6 timeouts, 7 already done). */
+int gfl_combine(void* out, int out_is_half, int n, const int64_t* dflag, const int64_t* ctrl, const float* hout,
+                int64_t* stats, int64_t timeout_ns, gfl_stream stream);
+
+/* Expert-major routing rows (tier_lut_build_grouped_rows, ft_tier_ext.cpp:1047-1097), HOST arrays:
+ * sel int64 [T*K], w fp32 [T*K], take uint8 [E] -> experts [<=E], offsets [<=E+1], row_token / row_weight [<=T*K].
+ * Returns the expert count (>= 0) or -GFL_EINVAL on a rejected routing; *rows receives the row count. */
+int gfl_grouped_rows(const int64_t* sel, const float* w, int T, int K, const uint8_t* take, int E, int32_t* experts,
+                     int32_t* offsets, int32_t* row_token, float* row_weight, int* rows);
+
+/* Fill nbytes of device memory with the splitmix64 stream of `seed` (synthetic trellis for tests and benchmarks;
+ * any bit stream is a valid EXL3 tile). Byte b = byte (b % 8) of output b/8. */
+int gfl_synth_trellis(void* dst, size_t nbytes, uint64_t seed, gfl_stream stream);
+
+/* Host-side counters of the context (no device sync): [0] forward calls, [1] picks submitted, [2] registered layers,
+ * [3] workspace bytes. Writes min(n, 4) entries into the host array `out`. */
+int gfl_stats(gfl_ctx* ctx, int64_t* out, int n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,166 @@
+"""HIP path vs the CPU oracle, through the C ABI (libgfl_moe.so).
+
+Bar: dequantized weights bit-exact; expert and layer outputs bit-exact against the reference's EXACT mode (the
+oracle restates it bit-for-bit, see test_oracle.py). Every case also reports max-abs/RMS against the north-star
+tolerance (max|y - y_ref| <= 2e-3 * RMS(y_ref)), which bit-exactness implies.
+"""
+import numpy as np
+import pytest
+
+TOL = 2e-3   # north-star: max-abs error relative to output RMS
+
+
+def _layer(gpu, li, E, H, I, Ks=(3, 3, 3)):
+    import synth
+    L = synth.SynthLayer(li, E, H, I, Ks)
+    L.register(gpu, li)
+    return L
+
+
+def _host_experts(oracle, L):
+    from oracle import Mat
+    ex = []
+    for e in range(L.E):
+        mats = []
+        for p in range(3):
+            tr, suh, svh = L.matrix(e, p)
+            k, n = (L.H, L.I) if p < 2 else (L.I, L.H)
+            mats.append(Mat(tr, suh, svh, k, n, L.Ks[p]))
+        ex.append(tuple(mats))
+    return ex
+
+
+def _forward(gpu, li, x16, sel, w, w_half=False):
+    import torch
+    xd = torch.from_numpy(x16.view(np.int16)).view(torch.float16).cuda()
+    seld = torch.from_numpy(np.ascontiguousarray(sel, dtype=np.int64)).cuda()
+    wd = torch.from_numpy(np.ascontiguousarray(w)).cuda()
+    out = torch.empty(x16.shape, dtype=torch.float32, device="cuda")
+    gpu.moe_forward(li, xd.contiguous(), seld, wd, out)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def _report(name, got, want):
+    rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
+    mx = float(np.abs(got.astype(np.float64) - want).max())
+    nbad = int(np.count_nonzero(got != want))
+    print(f"{name}: max-abs {mx:.3e} rms {rms:.3e} ratio {mx / max(rms, 1e-30):.3e} mismatched {nbad}/{want.size}")
+    return mx, rms, nbad
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("K", [3, 4, 5, 2])
+def test_dequant_bitexact(gpu, oracle, K):
+    import torch
+    import synth
+    import _native
+    for (k, n, s) in [(256, 128, 11), (512, 384, 12), (5120, 1536, 13)]:
+        nb = synth.trellis_bytes(k, n, K)
+        tr = torch.empty(nb, dtype=torch.uint8, device="cuda")
+        _native.synth_trellis(tr, s)
+        W = torch.empty((k, n), dtype=torch.int16, device="cuda")
+        _native.dequant(tr, k, n, K, W)
+        torch.cuda.synchronize()
+        got = W.cpu().numpy().view(np.uint16)
+        want = oracle.dequant(tr.cpu().numpy(), k, n, K)
+        print(f"dequant K={K} {k}x{n}: mismatches {int(np.count_nonzero(got != want))}")
+        assert np.array_equal(got, want)
+
+
+@pytest.mark.gpu
+def test_synth_trellis_matches_checker(gpu, oracle):
+    import torch
+    import _native
+    for nb, s in [(96, 1), (1000, 2), (8847, 0x6A11F1A5)]:
+        t = torch.empty(nb, dtype=torch.uint8, device="cuda")
+        _native.synth_trellis(t, s)
+        torch.cuda.synchronize()
+        assert np.array_equal(t.cpu().numpy(), oracle.synth_trellis(s, nb))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("ntok", [1, 3, 4])
+def test_forward_small_bitexact(gpu, oracle, ntok):
+    """Small shape, the reference harness's routing (t + 2k) % E (duplicate picks of one expert per token)."""
+    H, I, E = 512, 256, 6
+    L = _layer(gpu, 1, E, H, I)
+    ex = _host_experts(oracle, L)
+    rng = np.random.default_rng(777 + ntok)
+    x16 = (rng.standard_normal((ntok, H)) * 0.35).astype(np.float16)
+    sel = np.array([[(t + 2 * k) % E for k in range(4)] for t in range(ntok)], np.int64)
+    w = np.full(sel.shape, 0.25, np.float32)
+    got = _forward(gpu, 1, x16, sel, w)
+    want = oracle.moe_forward(ex, x16.astype(np.float32), sel, w, mode=1)
+    mx, rms, nbad = _report(f"small ntok={ntok}", got, want)
+    assert nbad == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("scale", [0.35, 0.05, 1.0])
+def test_forward_sweep_bitexact(gpu, oracle, scale):
+    """16 tokens x every expert of an 8-expert layer (128 picks, 16 slots per expert): exercises many rounding ties,
+    small activations (fp16 subnormal range after the input Hadamard) and multi-pass slot chunks."""
+    H, I, E = 512, 256, 8
+    L = _layer(gpu, 5, E, H, I)
+    ex = _host_experts(oracle, L)
+    rng = np.random.default_rng(int(scale * 1000))
+    x16 = (rng.standard_normal((16, H)) * scale).astype(np.float16)
+    sel = np.tile(np.arange(E, dtype=np.int64), (16, 1))
+    w = rng.random(sel.shape).astype(np.float32)
+    got = _forward(gpu, 5, x16, sel, w)
+    want = oracle.moe_forward(ex, x16.astype(np.float32), sel, w, mode=1)
+    mx, rms, nbad = _report(f"sweep scale={scale}", got, want)
+    assert nbad == 0
+
+
+@pytest.mark.gpu
+def test_forward_config0_single_expert(gpu, oracle):
+    """Config 0: one routed expert H=5120 I=1536 K=3, M=1, weight 1."""
+    H, I = 5120, 1536
+    L = _layer(gpu, 2, 2, H, I)
+    ex = _host_experts(oracle, L)
+    rng = np.random.default_rng(5)
+    x16 = rng.standard_normal((1, H)).astype(np.float16)
+    sel = np.array([[1]], np.int64)
+    w = np.ones((1, 1), np.float32)
+    got = _forward(gpu, 2, x16, sel, w)
+    want = oracle.expert_forward(ex[1], x16.astype(np.float32), mode=1)
+    mx, rms, nbad = _report("config0", got, want)
+    assert mx <= TOL * rms
+    assert nbad == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M", [1, 2])
+def test_forward_layer_shape_bitexact(gpu, oracle, M):
+    """Config-1 shape (H=5120, I=1536, K=3, top-8) on a 12-expert layer."""
+    import synth
+    H, I, E = 5120, 1536, 12
+    L = _layer(gpu, 3, E, H, I)
+    ex = _host_experts(oracle, L)
+    rng = np.random.default_rng(100 + M)
+    x16 = rng.standard_normal((M, H)).astype(np.float16)
+    (sel, w16), _ = synth.route_uniform(M, E, 8, rng)
+    got = _forward(gpu, 3, x16, sel, w16)
+    want = oracle.moe_forward(ex, x16.astype(np.float32), sel, w16.astype(np.float32), mode=1)
+    mx, rms, nbad = _report(f"layer M={M}", got, want)
+    assert mx <= TOL * rms
+    assert nbad == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("Ks", [(4, 4, 3), (3, 3, 5), (2, 5, 4)])
+def test_forward_mixed_k_bitexact(gpu, oracle, Ks):
+    """Config-2 style mixed bitrates (K-generic decode in one kernel family), small shape."""
+    H, I, E = 512, 256, 5
+    L = _layer(gpu, 4, E, H, I, Ks)
+    ex = _host_experts(oracle, L)
+    rng = np.random.default_rng(sum(Ks))
+    x16 = rng.standard_normal((3, H)).astype(np.float16)
+    sel = np.array([[0, 2, 4], [1, 2, -1], [4, 3, 0]], np.int64)
+    w = rng.random(sel.shape).astype(np.float32)
+    got = _forward(gpu, 4, x16, sel, w)
+    want = oracle.moe_forward(ex, x16.astype(np.float32), sel, w, mode=1)
+    mx, rms, nbad = _report(f"mixed {Ks}", got, want)
+    assert nbad == 0
