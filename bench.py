@@ -1,0 +1,210 @@
+#!/usr/bin/env python3
+"""Routed-MoE decode benchmark on one MI355X.
+
+Workload: one MoE layer of 288 routed experts, top-8, SwiGLU H=5120 I=1536, EXL3 3 bits/weight,
+M = 1..4 decode tokens with fp16 N(0,1) activations and sigmoid top-8 routing of N(0,1) fp32 logits. A step is one
+layer call (split -> 8*M expert GEMVs -> weighted combine) through the C ABI. Steps cycle through `--layers` distinct
+288-expert layers (2.56 GB each) and 32 routings, so expert bytes come from HBM, not the 256 MB Infinity Cache.
+Steps are captured in a HIP graph and replayed; the timed region is bracketed by synchronisation.
+
+value        = microseconds per token at M=1 (lower is better); per_M holds M=1..4.
+roofline     = the gate|up GEMV kernel (the dominant one) at M=1: algorithmic quantized bytes per launch (union of
+               routed experts x (gate+up trellis + their suh/svh)) / its mean launch time, from device events
+               recorded around every launch during a timed eager pass; peak = 8 TB/s HBM.
+cpu_baseline = the reference's own AVX2 expert engine (kernels/cpu_avx2/ft_core.h, built into oracle/_ref) timed on
+               this host: decode calls of 1 token x 8 experts cycling a DRAM-cold pool of 288 experts, I16 mode.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "glm-flash-lite_amd"))
+
+METRIC = "MoE-layer decode µs/token at M=1..4 + % HBM roofline on quantized bytes"
+HBM_PEAK_GBPS = 8000.0
+H, I, E, TOPK, KBITS = 5120, 1536, 288, 8, 3
+
+
+def physical_cpus(skip=2, cap=16):
+    """One logical CPU per physical core among the allowed CPUs, minus the first `skip` (auto_cpus rule of the
+    reference, glm53/cpu_tier.py:114-127), capped at the GPU box's CPU share."""
+    allowed = sorted(os.sched_getaffinity(0))
+    seen, firsts = set(), []
+    for c in allowed:
+        try:
+            core = open(f"/sys/devices/system/cpu/cpu{c}/topology/core_id").read().strip()
+            pkg = open(f"/sys/devices/system/cpu/cpu{c}/topology/physical_package_id").read().strip()
+        except OSError:
+            core, pkg = str(c), "0"
+        if (pkg, core) not in seen:
+            seen.add((pkg, core))
+            firsts.append(c)
+    cpus = firsts[skip:] if len(firsts) > skip + 1 else firsts[-1:]
+    return cpus[:cap]
+
+
+def cpu_baseline(iters, warmup):
+    """Reference AVX2 engine timing; returns the cpu_baseline object or None when the engine is not built."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from oracle import REFLIB, Mat, Oracle, RefEngine
+    if not os.path.exists(REFLIB):
+        return None
+    cpus = physical_cpus()
+    O = Oracle()
+    eng = RefEngine(threads=len(cpus), cpus=cpus)
+    t0 = time.time()
+    pool = []
+    for e in range(E):
+        mats = []
+        for p, (k, n) in enumerate(((H, I), (H, I), (I, H))):
+            s = O.seed(90, e, p)
+            tr = O.synth_trellis(s, (k // 16) * (n // 16) * 32 * KBITS)
+            suh, svh = O.synth_scales(s, k, n, k)
+            mats.append(Mat(tr, suh, svh, k, n, KBITS))
+        pool.append(tuple(mats))
+    gen_s = time.time() - t0
+    rng = np.random.default_rng(4242)
+    x = rng.standard_normal(H).astype(np.float16).astype(np.float32)
+    res = {}
+    for name, mode in (("i16", 2), ("exact", 1)):
+        secs = eng.time_decode(pool, x, TOPK, iters, warmup, mode)
+        res[name] = float(np.median(secs)) * 1e6
+    per_expert = sum(m.tr.size + 2 * (m.k + m.n) for m in pool[0])
+    return {"value": round(res["i16"], 2), "unit": "us/token", "cores": len(cpus), "kind": "reference",
+            "sample": f"{iters} decode calls (after {warmup} warm-up) of 1 token x {TOPK} experts, I16 mode, "
+                      f"cycling a DRAM-cold pool of {E} experts (H={H} I={I} K={KBITS}, {E * per_expert / 1e9:.2f} GB); "
+                      f"median",
+            "exact_mode_us_per_token": round(res["exact"], 2),
+            "GBps_i16": round(TOPK * per_expert / (res["i16"] * 1e-6) / 1e9, 2),
+            "cpus": cpus, "pool_gen_s": round(gen_s, 1)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=320)
+    ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--layers", type=int, default=4)
+    ap.add_argument("--Ms", default="1,2,3,4")
+    ap.add_argument("--graph-steps", type=int, default=32)
+    ap.add_argument("--profile-steps", type=int, default=64)
+    ap.add_argument("--cpu-iters", type=int, default=300)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures the routed-expert path on one GPU; multi-GPU runs are not part of this build "
+              "(run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    import _native
+    import synth
+
+    torch.cuda.set_device(0)
+    ctx = _native.Context(0)
+    t0 = time.time()
+    layers = []
+    for li in range(args.layers):
+        L = synth.SynthLayer(li, E, H, I, (KBITS,) * 3)
+        L.register(ctx, li)
+        layers.append(L)
+    setup_s = time.time() - t0
+    per_expert = layers[0].quant_bytes_per_expert
+    gu_per_expert = layers[0].tbytes[0] + layers[0].tbytes[1] + 2 * 2 * (H + I)
+    G = args.graph_steps
+    reps = max(1, args.steps // G)
+    steps = reps * G
+    per_M = {}
+    roof = None
+    for M in [int(m) for m in args.Ms.split(",")]:
+        rng = np.random.default_rng(1000 + M)
+        NR = 32
+        xs, sels, ws, U = [], [], [], []
+        for r in range(NR):
+            x = rng.standard_normal((M, H)).astype(np.float16)
+            (sel, w16), _ = synth.route_uniform(M, E, TOPK, rng)
+            xs.append(torch.from_numpy(x.view(np.int16)).view(torch.float16).cuda())
+            sels.append(torch.from_numpy(sel).cuda())
+            ws.append(torch.from_numpy(w16.view(np.int16)).view(torch.float16).cuda())
+            U.append(len(np.unique(sel)))
+        out = torch.empty((M, H), dtype=torch.float32, device="cuda")
+
+        def step(i):
+            r = i % NR
+            ctx.moe_forward(i % args.layers, xs[r], sels[r], ws[r], out)
+
+        for i in range(args.warmup):
+            step(i)
+        torch.cuda.synchronize()
+        # graph of G steps (each with its own layer and routing), replayed `reps` times
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for i in range(3):
+                step(i)
+        torch.cuda.current_stream().wait_stream(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(G):
+                step(i)
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        step(G - 1)
+        torch.cuda.synchronize()
+        graph_ok = bool(torch.equal(got, out))
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        step_bytes = float(np.mean([U[i % NR] for i in range(G)])) * per_expert + M * H * 6
+        gbps = step_bytes / (ms * 1e-3) / 1e9
+        per_M[str(M)] = {"us_per_token": round(ms * 1e3 / M, 3), "ms_per_step": round(ms, 5),
+                         "union_experts": round(float(np.mean(U)), 2), "GBps": round(gbps, 1),
+                         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "graph_replay_matches_eager": graph_ok}
+        if M == 1:
+            # live per-kernel timing of the dominant kernel (gate|up GEMV): device events around every launch
+            ctx.profile(True)
+            torch.cuda.synchronize()
+            for i in range(args.profile_steps):
+                step(i)
+            prof = ctx.profile_read()
+            ctx.profile(False)
+            gu_ms, gu_n = prof["gate_up"]
+            gu_bytes = float(np.mean([U[i % NR] for i in range(args.profile_steps)])) * gu_per_expert
+            ach = gu_bytes / (gu_ms / gu_n * 1e-3) / 1e9
+            stage_us = {k: round(v[0] / max(1, v[1]) * 1e3, 2) for k, v in prof.items()}
+            roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                    "frac": round(ach / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": "chain_gemv_kernel (gate|up)",
+                    "algorithmic_bytes_per_launch": round(gu_bytes), "mean_launch_us": round(gu_ms / gu_n * 1e3, 2),
+                    "stage_mean_us": stage_us}
+        del g
+    traffic_file = os.path.join(ROOT, "profiles", "traffic_gate_up_config1_M1.json")
+    if roof is not None and os.path.exists(traffic_file):
+        try:
+            roof["traffic"] = json.load(open(traffic_file)).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            pass
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_iters, 20)
+    m1 = per_M.get("1") or next(iter(per_M.values()))
+    line = {"metric": METRIC, "value": m1["us_per_token"], "unit": "us/token", "n_gpus": 1, "steps": steps,
+            "warmup": args.warmup, "ms_per_step": m1["ms_per_step"], "higher_is_better": False, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f32 (fp16 operands)", "data": "synthetic",
+            "config": {"workload": "config1: one 288-expert top-8 MoE layer decode, M=1, H=5120 I=1536 K=3 bpw",
+                       "experts": E, "topk": TOPK, "hidden": H, "intermediate": I, "bits": KBITS,
+                       "layers_cycled": args.layers, "graph_steps": G},
+            "per_M": per_M, "roofline": roof, "cpu_baseline": cpu, "setup_s": round(setup_s, 1)}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -13,7 +13,7 @@ LIB_PATH = os.path.join(HERE, "libgfl_moe.so")
 # exported symbols of include/gfl_moe.h (checked by tests/test_abi.py against the header)
 SYMBOLS = ("gfl_last_error", "gfl_version", "gfl_ctx_create", "gfl_ctx_destroy", "gfl_register_layer",
            "gfl_moe_forward", "gfl_dequant", "gfl_split", "gfl_combine", "gfl_grouped_rows", "gfl_synth_trellis",
-           "gfl_stats")
+           "gfl_stats", "gfl_profile_enable", "gfl_profile_read")
 
 MODE_AUTO, MODE_AFFINE, MODE_EXACT, MODE_I16 = -1, 0, 1, 2
 
@@ -54,6 +54,8 @@ def load(path=LIB_PATH):
     L.gfl_grouped_rows.argtypes = [_P, _P, C.c_int, C.c_int, _P, C.c_int, _P, _P, _P, _P, C.POINTER(C.c_int)]
     L.gfl_synth_trellis.argtypes = [_P, C.c_size_t, C.c_uint64, _P]
     L.gfl_stats.argtypes = [_P, _P, C.c_int]
+    L.gfl_profile_enable.argtypes = [_P, C.c_int]
+    L.gfl_profile_read.argtypes = [_P, _P, _P]
     for name in SYMBOLS:
         if name != "gfl_last_error":
             getattr(L, name).restype = C.c_int
@@ -117,6 +119,18 @@ class Context:
         check(load().gfl_moe_forward(self.h, li, ptr(x), ptr(sel), ptr(w), int(w.dtype == torch.float16), M, topk,
                                      ptr(out), int(mode), float(act_limit), _stream()))
         return out
+
+    STAGES = ("plan", "gate_up", "act", "down", "combine")
+
+    def profile(self, enable):
+        check(load().gfl_profile_enable(self.h, int(bool(enable))))
+
+    def profile_read(self):
+        """{stage: (total device ms, launches)} since the last read (synchronises the recorded events)."""
+        ms = (C.c_double * 5)()
+        n = (C.c_int64 * 5)()
+        check(load().gfl_profile_read(self.h, ms, n))
+        return {s: (ms[i], n[i]) for i, s in enumerate(self.STAGES)}
 
     def stats(self):
         out = (C.c_int64 * 4)()

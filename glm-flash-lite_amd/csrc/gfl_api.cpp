@@ -48,6 +48,11 @@ struct gfl_ctx
     void* ws = nullptr;
     size_t ws_bytes = 0;
     int64_t calls = 0, picks = 0;
+    // per-stage profiling events (gfl_profile_enable / gfl_profile_read)
+    bool prof = false;
+    std::vector<hipEvent_t> ev_pool;
+    struct Rec { int stage; hipEvent_t a, b; };
+    std::vector<Rec> recs;
 };
 
 namespace {
@@ -96,6 +101,33 @@ int ensure_ws(gfl_ctx* c, int cap, int H, int I, Workspace& w)
 
 bool k_ok(int K) { return K >= 2 && K <= 5; }
 
+hipEvent_t take_event(gfl_ctx* c)
+{
+    if (!c->ev_pool.empty())
+    {
+        hipEvent_t e = c->ev_pool.back();
+        c->ev_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+// runs `launch` bracketed by a pair of events when profiling is on
+template <class F>
+int staged(gfl_ctx* c, int stage, hipStream_t st, F&& launch)
+{
+    if (!c->prof) return launch();
+    hipEvent_t a = take_event(c), b = take_event(c);
+    if (!a || !b) return fail(GFL_ERUNTIME, "profiling: hipEventCreate failed");
+    GFL_HIP(hipEventRecord(a, st));
+    const int r = launch();
+    GFL_HIP(hipEventRecord(b, st));
+    c->recs.push_back({ stage, a, b });
+    return r;
+}
+
 }  // namespace
 
 extern "C" {
@@ -120,6 +152,8 @@ int gfl_ctx_destroy(gfl_ctx* c)
 {
     if (!c) return GFL_OK;
     hipSetDevice(c->device);
+    for (auto& r : c->recs) { hipEventDestroy(r.a); hipEventDestroy(r.b); }
+    for (auto e : c->ev_pool) hipEventDestroy(e);
     for (auto& L : c->layers)
         if (L.dptrs) hipFree(L.dptrs);
     if (c->ws) hipFree(c->ws);
@@ -168,23 +202,27 @@ int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, c
     if (int r = ensure_ws(c, P, L.H, L.I, ws)) return r;
     const int umax = P < L.E ? P : L.E;
     const int ns = M < 8 ? M : 8;   // slots per pass; an expert holds at most M slots unless a token repeats it
-    gfl::launch_plan(sel, P, topk, L.E, ws.pv, st);
-    if (L.K[0] == L.K[1])
-    {
-        if (gfl::launch_chain(L.K[0], ns, true, L.dptrs, 0, 2, L.H, L.I, ws.pv, topk, umax, x, ws.ygu, st))
-            return fail(GFL_EINVAL, "gfl_moe_forward: unsupported K");
-    }
-    else
-    {
-        if (gfl::launch_chain(L.K[0], ns, true, L.dptrs, 0, 1, L.H, L.I, ws.pv, topk, umax, x, ws.ygu, st) ||
-            gfl::launch_chain(L.K[1], ns, true, L.dptrs, 1, 1, L.H, L.I, ws.pv, topk, umax, x,
-                              ws.ygu + (size_t)P * L.I, st))
-            return fail(GFL_EINVAL, "gfl_moe_forward: unsupported K");
-    }
-    gfl::launch_act(L.dptrs, ws.pv, P, ws.ygu, ws.xtd, L.I, act_limit, st);
-    if (gfl::launch_chain(L.K[2], ns, false, L.dptrs, 2, 1, L.I, L.H, ws.pv, topk, umax, ws.xtd, ws.yd, st))
-        return fail(GFL_EINVAL, "gfl_moe_forward: unsupported K");
-    gfl::launch_final(L.dptrs, ws.pv, w, w_is_half ? 1 : 0, M, topk, ws.yd, out, L.H, st);
+    int r = staged(c, 0, st, [&] { gfl::launch_plan(sel, P, topk, L.E, ws.pv, st); return 0; });
+    if (!r)
+        r = staged(c, 1, st, [&] {
+            if (L.K[0] == L.K[1])
+                return gfl::launch_chain(L.K[0], ns, true, L.dptrs, 0, 2, L.H, L.I, ws.pv, topk, umax, x, ws.ygu, st);
+            if (gfl::launch_chain(L.K[0], ns, true, L.dptrs, 0, 1, L.H, L.I, ws.pv, topk, umax, x, ws.ygu, st))
+                return -1;
+            return gfl::launch_chain(L.K[1], ns, true, L.dptrs, 1, 1, L.H, L.I, ws.pv, topk, umax, x,
+                                     ws.ygu + (size_t)P * L.I, st);
+        });
+    if (!r) r = staged(c, 2, st, [&] { gfl::launch_act(L.dptrs, ws.pv, P, ws.ygu, ws.xtd, L.I, act_limit, st); return 0; });
+    if (!r)
+        r = staged(c, 3, st, [&] {
+            return gfl::launch_chain(L.K[2], ns, false, L.dptrs, 2, 1, L.I, L.H, ws.pv, topk, umax, ws.xtd, ws.yd, st);
+        });
+    if (!r)
+        r = staged(c, 4, st, [&] {
+            gfl::launch_final(L.dptrs, ws.pv, w, w_is_half ? 1 : 0, M, topk, ws.yd, out, L.H, st);
+            return 0;
+        });
+    if (r) return r > 0 ? r : fail(GFL_EINVAL, "gfl_moe_forward: unsupported K");
     GFL_HIP(hipGetLastError());
     c->calls += 1;
     c->picks += P;
@@ -286,6 +324,36 @@ int gfl_synth_trellis(void* dst, size_t nbytes, uint64_t seed, gfl_stream stream
     if (!dst) return fail(GFL_EINVAL, "gfl_synth_trellis: NULL destination");
     gfl::launch_synth(static_cast<uint8_t*>(dst), nbytes, seed, reinterpret_cast<hipStream_t>(stream));
     GFL_HIP(hipGetLastError());
+    return GFL_OK;
+}
+
+int gfl_profile_enable(gfl_ctx* c, int enable)
+{
+    if (!c) return fail(GFL_EINVAL, "gfl_profile_enable: NULL context");
+    std::lock_guard<std::mutex> g(c->mu);
+    c->prof = enable != 0;
+    return GFL_OK;
+}
+
+int gfl_profile_read(gfl_ctx* c, double* stage_ms, int64_t* launches)
+{
+    if (!c || !stage_ms || !launches) return fail(GFL_EINVAL, "gfl_profile_read: NULL argument");
+    std::lock_guard<std::mutex> g(c->mu);
+    GFL_HIP(hipSetDevice(c->device));
+    for (auto& r : c->recs)
+    {
+        GFL_HIP(hipEventSynchronize(r.b));
+        float ms = 0.f;
+        GFL_HIP(hipEventElapsedTime(&ms, r.a, r.b));
+        if (r.stage >= 0 && r.stage < 5)
+        {
+            stage_ms[r.stage] += ms;
+            launches[r.stage] += 1;
+        }
+        c->ev_pool.push_back(r.a);
+        c->ev_pool.push_back(r.b);
+    }
+    c->recs.clear();
     return GFL_OK;
 }
 

@@ -124,18 +124,55 @@ __device__ inline int perm_pos(int b, int r)
     return (tk * 4 + j) * 4 + q;
 }
 
-// One workgroup = 8 waves = 8 adjacent tile columns (128 outputs) of one matrix of one routed expert, all tile rows,
-// for up to NS of the expert's slots at a time. Each wave owns one tile column; lane (j = l/16, n = l%16) carries the
-// reference's accumulator j of output column n for every slot.
-//   PREP = true : matrix is gate/up; the WG builds xt = prep_block(x_token, suh) for its slots in LDS
-//   PREP = false: matrix is down; xt (already transformed and permuted) is copied from xin
-template <int K, int NS, bool PREP>
-__global__ __launch_bounds__(512) void chain_gemv_kernel(const uint64_t* __restrict__ ptrs, int mat_base, int kdim,
-                                                         int ndim, PlanView pv, int topk,
-                                                         const uint16_t* __restrict__ xin, float* __restrict__ yout)
+// One workgroup = NW waves = NW adjacent tile columns (16*NW outputs) of one matrix of one routed expert, all tile
+// rows, for up to NS of the expert's slots at a time. Each wave owns one tile column; lane (j = l/16, n = l%16)
+// carries the reference's accumulator j of output column n for every slot.
+// Trellis bytes are streamed in batches of BR tile rows: each thread issues coalesced 16-byte loads into a ring of
+// NRING register batches (so NRING batches are in flight), the batch is written to one of two LDS buffers and the
+// waves decode their tile column from there.
+//   PREP = true : gate/up; the WG builds xt = prep_block(x_token, suh) for its slots in LDS
+//   PREP = false: down; xt (already transformed and permuted) is copied from xin
+//   OUTB = true : apply out_block (ft_core.h:1016) to each 128-output block and write final expert outputs
+//                 (needs NW = 8)
+constexpr int BR = 16;      // tile rows per batch
+
+// Workgroup barrier that only orders LDS traffic: wait for this wave's LDS operations, then s_barrier. Unlike
+// __syncthreads it carries no release fence, so outstanding global loads of the prefetch ring stay in flight.
+__device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// 16-byte load through the global address space (pointers taken from the layer table are generic; a flat load
+// would also count against lgkmcnt and be drained by every LDS wait)
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4 gload16(const uint8_t* p)
 {
-    extern __shared__ uint16_t lds_x[];   // [NS][kdim] fp16, permuted [tk][j][q]
-    const int TN = ndim / 16, TK = kdim / 16, ncb = TN / 8;
+    typedef const __attribute__((address_space(1))) u32x4 gu32x4;
+    return *(gu32x4*)(p);
+}
+constexpr int NRING = 4;    // batches in flight per workgroup
+
+template <int K, int NW>
+struct Stage
+{
+    static constexpr int TB = 32 * K;                   // bytes per tile
+    static constexpr int RB = NW * TB;                  // bytes per tile-row slice of the workgroup
+    static constexpr int BB = BR * RB;                  // bytes per batch
+    static constexpr int NCH = BB / 16;                 // 16-byte chunks per batch
+    static constexpr int CPT = (NCH + NW * 64 - 1) / (NW * 64);   // chunks per thread
+    static constexpr int BBP = CPT * NW * 64 * 16;      // staged bytes per batch incl. the pad the surplus chunks fill
+};
+
+template <int K, int NS, bool PREP, int NW, bool OUTB>
+__global__ __launch_bounds__(NW * 64) void chain_gemv_kernel(const uint64_t* __restrict__ ptrs, int mat_base,
+                                                             int kdim, int ndim, PlanView pv, int topk,
+                                                             const uint16_t* __restrict__ xin,
+                                                             float* __restrict__ yout)
+{
+    using St = Stage<K, NW>;
+    extern __shared__ __align__(16) uint8_t lds_raw[];
+    uint8_t* stage_buf = lds_raw;                                     // [2][BBP]
+    uint16_t* lds_x = reinterpret_cast<uint16_t*>(lds_raw + 2 * St::BBP);  // [NS][kdim] fp16, permuted [tk][j][q]
+    float* lds_y = reinterpret_cast<float*>(lds_raw + 2 * St::BBP + (size_t)NS * kdim * 2);  // [NS][128] (OUTB)
+    const int TN = ndim / 16, TK = kdim / 16, ncb = TN / NW;
     const int u = blockIdx.x / ncb, cb = blockIdx.x % ncb;
     if (u >= pv.hdr[0]) return;
     const int mat = mat_base + blockIdx.y;                 // 0 gate, 1 up, 2 down
@@ -143,28 +180,82 @@ __global__ __launch_bounds__(512) void chain_gemv_kernel(const uint64_t* __restr
     const int e = pv.uexp[u];
     const uint8_t* tr = reinterpret_cast<const uint8_t*>(ptrs[(size_t)e * 9 + mat]);
     const uint16_t* suh = reinterpret_cast<const uint16_t*>(ptrs[(size_t)e * 9 + 3 + 2 * mat]);
+    const uint16_t* svh = reinterpret_cast<const uint16_t*>(ptrs[(size_t)e * 9 + 4 + 2 * mat]);
     const int s_begin = pv.uoff[u], s_end = pv.uoff[u + 1];
-    const int t = cb * 8 + wave;                           // this wave's tile column
     const LaneDec d = lane_dec(lane, K);
     const int j = lane >> 4, n = lane & 15;
     half4 Pm;
 #pragma unroll
     for (int r = 0; r < 4; ++r) Pm[r] = (_Float16)((j == (n & 3) && r == (n >> 2)) ? 1.0f : 0.0f);
     const float4v zero = { 0.f, 0.f, 0.f, 0.f };
-    const size_t rstride = (size_t)TN * 32 * K;
+    const size_t gstride = (size_t)TN * St::TB;            // global bytes between tile rows
+    const uint8_t* gbase = tr + (size_t)cb * St::RB;        // tile row 0 of this workgroup's slice
+    const int nb = (TK + BR - 1) / BR;
     float* ybase = yout + (size_t)blockIdx.y * (size_t)pv.cap_slots * ndim;
+
+    // chunk c of batch b: tile row b*BR + c/(RB/16), byte (c % (RB/16))*16 of the slice; batches past the end reload
+    // the last tile row (in bounds, never consumed) so the ring has no branches
+    // every thread moves exactly CPT chunks; chunks past NCH reload chunk c - NCH into the pad (no branches)
+#define GFL_LOAD_BATCH(BI, REG)                                                                                  \
+    _Pragma("unroll") for (int i_ = 0; i_ < St::CPT; ++i_)                                                       \
+    {                                                                                                            \
+        const int cr_ = threadIdx.x + i_ * NW * 64;                                                              \
+        const int c_ = cr_ < St::NCH ? cr_ : cr_ - St::NCH;                                                      \
+        const int row_ = min((BI) * BR + c_ / (St::RB / 16), TK - 1);                                            \
+        REG[i_] = gload16(gbase + (size_t)row_ * gstride + (c_ % (St::RB / 16)) * 16);                           \
+    }
+#define GFL_STORE_BATCH(BUF, REG)                                                                                \
+    _Pragma("unroll") for (int i_ = 0; i_ < St::CPT; ++i_)                                                       \
+        reinterpret_cast<u32x4*>(stage_buf + (BUF) * St::BBP)[threadIdx.x + i_ * NW * 64] = REG[i_];
+    // one pipeline step: publish batch BI from its ring slot, refill the slot with batch BI + 4, decode batch BI
+#define GFL_STEP(BI, REG)                                                                                        \
+    {                                                                                                            \
+        const int b_ = (BI);                                                                                     \
+        GFL_STORE_BATCH(b_ & 1, REG)                                                                             \
+        lds_barrier();                                                                                           \
+        GFL_LOAD_BATCH(b_ + 4, REG)                                                                              \
+        const uint8_t* sb_ = wl + (b_ & 1) * St::BBP;                                                             \
+        const int rows_ = b_ < nb ? min(BR, TK - b_ * BR) : 0;                                                   \
+        _Pragma("unroll 4") for (int r_ = 0; r_ < rows_; ++r_)                                                   \
+        {                                                                                                        \
+            const uint32_t hi_ = *reinterpret_cast<const uint32_t*>(sb_ + r_ * St::RB + d.o0);                   \
+            const uint32_t lo_ = *reinterpret_cast<const uint32_t*>(sb_ + r_ * St::RB + d.o1);                   \
+            const half4 B_ = decode4<K>(hi_, lo_, d.sh);                                                          \
+            const float4v cw_ = __builtin_amdgcn_mfma_f32_16x16x16f16(Pm, B_, zero, 0, 0, 0);                     \
+            const int tk_ = b_ * BR + r_;                                                                        \
+            _Pragma("unroll") for (int s_ = 0; s_ < NS; ++s_)                                                    \
+            {                                                                                                    \
+                if (s_ < ns)                                                                                     \
+                {                                                                                                \
+                    const half4 xv_ = *reinterpret_cast<const half4*>(xl + ((size_t)s_ * TK + tk_) * 16);          \
+                    float a_ = acc[s_];                                                                          \
+                    a_ = __builtin_fmaf(cw_[0], (float)xv_[0], a_);                                              \
+                    a_ = __builtin_fmaf(cw_[1], (float)xv_[1], a_);                                              \
+                    a_ = __builtin_fmaf(cw_[2], (float)xv_[2], a_);                                              \
+                    a_ = __builtin_fmaf(cw_[3], (float)xv_[3], a_);                                              \
+                    acc[s_] = a_;                                                                                \
+                }                                                                                                \
+            }                                                                                                    \
+        }                                                                                                        \
+    }
 
     for (int c0 = s_begin; c0 < s_end; c0 += NS)
     {
         const int ns = min(NS, s_end - c0);
-        __syncthreads();
+        // prefetch ring: four named register batches in flight
+        u32x4 ring0[St::CPT], ring1[St::CPT], ring2[St::CPT], ring3[St::CPT];
+        static_assert(NRING == 4, "ring of four batches");
+        GFL_LOAD_BATCH(0, ring0)
+        GFL_LOAD_BATCH(1, ring1)
+        GFL_LOAD_BATCH(2, ring2)
+        GFL_LOAD_BATCH(3, ring3)
+        lds_barrier();   // previous pass done with lds_x / lds_y
         if (PREP)
         {
-            // xt = prep_block(x, suh) per 128-block, written permuted
-            const int nb = kdim / 128;
-            for (int it = wave; it < ns * nb; it += 8)
+            const int nblk = kdim / 128;
+            for (int it = wave; it < ns * nblk; it += NW)
             {
-                const int s = it / nb, b = it % nb;
+                const int s = it / nblk, b = it % nblk;
                 const int tok = pv.slot_pick[c0 + s] / topk;
                 const uint16_t* xr = xin + (size_t)tok * kdim + b * 128;
                 float v0 = h2f_bits(xr[lane]), v1 = h2f_bits(xr[lane + 64]);
@@ -181,40 +272,45 @@ __global__ __launch_bounds__(512) void chain_gemv_kernel(const uint64_t* __restr
             uint4* dst = reinterpret_cast<uint4*>(lds_x);
             for (int i = threadIdx.x; i < nvec; i += blockDim.x) dst[i] = src[i];
         }
-        __syncthreads();
 
         float acc[NS];
 #pragma unroll
         for (int s = 0; s < NS; ++s) acc[s] = 0.f;
-        const uint8_t* tp = tr + (size_t)t * 32 * K;
+        const uint8_t* wl = stage_buf + wave * St::TB;      // this wave's tile inside a staged row slice
         const uint16_t* xl = lds_x + j * 4;
-#pragma unroll 4
-        for (int tk = 0; tk < TK; ++tk)
+        for (int b0 = 0; b0 < nb; b0 += NRING)
         {
-            const uint32_t hi = ld_u32(tp + d.o0), lo = ld_u32(tp + d.o1);
-            tp += rstride;
-            const half4 B = decode4<K>(hi, lo, d.sh);
-            const float4v c = __builtin_amdgcn_mfma_f32_16x16x16f16(Pm, B, zero, 0, 0, 0);
-#pragma unroll
-            for (int s = 0; s < NS; ++s)
-            {
-                if (s < ns)
-                {
-                    const half4 xv = *reinterpret_cast<const half4*>(xl + ((size_t)s * TK + tk) * 16);
-                    float a = acc[s];
-                    a = __builtin_fmaf(c[0], (float)xv[0], a);
-                    a = __builtin_fmaf(c[1], (float)xv[1], a);
-                    a = __builtin_fmaf(c[2], (float)xv[2], a);
-                    a = __builtin_fmaf(c[3], (float)xv[3], a);
-                    acc[s] = a;
-                }
-            }
+            GFL_STEP(b0, ring0)
+            GFL_STEP(b0 + 1, ring1)
+            GFL_STEP(b0 + 2, ring2)
+            GFL_STEP(b0 + 3, ring3)
         }
+#undef GFL_STEP
+#undef GFL_STORE_BATCH
+#undef GFL_LOAD_BATCH
+        const int t = cb * NW + wave;                          // this wave's tile column
 #pragma unroll
         for (int s = 0; s < NS; ++s)
         {
             const float a1 = __shfl(acc[s], n + 16), a2 = __shfl(acc[s], n + 32), a3 = __shfl(acc[s], n + 48);
-            if (s < ns && lane < 16) ybase[(size_t)(c0 + s) * ndim + t * 16 + n] = (acc[s] + a1) + (a2 + a3);
+            const float y = (acc[s] + a1) + (a2 + a3);
+            if (s < ns && lane < 16)
+            {
+                if (OUTB) lds_y[s * 128 + wave * 16 + n] = y;
+                else ybase[(size_t)(c0 + s) * ndim + t * 16 + n] = y;
+            }
+        }
+        if (OUTB)
+        {
+            __syncthreads();
+            const int blk = cb;                                // NW == 8: one 128-output block per workgroup
+            for (int s = wave; s < ns; s += NW)
+            {
+                float v0 = lds_y[s * 128 + lane], v1 = lds_y[s * 128 + lane + 64];
+                out_block_wave(v0, v1, h2f_bits(svh[blk * 128 + lane]), h2f_bits(svh[blk * 128 + lane + 64]));
+                ybase[(size_t)(c0 + s) * ndim + blk * 128 + lane] = v0;
+                ybase[(size_t)(c0 + s) * ndim + blk * 128 + lane + 64] = v1;
+            }
         }
     }
 }
@@ -255,11 +351,10 @@ __global__ __launch_bounds__(256) void final_kernel(const uint64_t* __restrict__
                                                     const void* __restrict__ w, int w_half, int M, int topk,
                                                     const float* __restrict__ yd, float* __restrict__ out, int H)
 {
-    const int nb = H / 128;
-    const int item = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int tkn = item / nb, hb = item % nb;
-    if (tkn >= M) return;
-    // this token's picks sorted by (job, pick index): insertion sort of <= MAX_TOPK entries
+    // one thread per output element; picks of the token summed in (job, pick) order from 0 (ft_core.h:1020-1033)
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= M * H) return;
+    const int tkn = idx / H, col = idx % H;
     int ord[MAX_TOPK];
     int cnt = 0;
     for (int k = 0; k < topk; ++k)
@@ -271,20 +366,14 @@ __global__ __launch_bounds__(256) void final_kernel(const uint64_t* __restrict__
         while (b > 0 && pv.pick_job[ord[b - 1]] > jb) { ord[b] = ord[b - 1]; --b; }
         ord[b] = p;
     }
-    float o0 = 0.f, o1 = 0.f;
+    float o = 0.f;
     for (int i = 0; i < cnt; ++i)
     {
-        const int p = ord[i], s = pv.pick_slot[p];
-        const int e = pv.uexp[pv.slot_u[s]];
-        const uint16_t* svh_d = reinterpret_cast<const uint16_t*>(ptrs[(size_t)e * 9 + 8]);
+        const int p = ord[i];
         const float wt = w_half ? h2f_bits(reinterpret_cast<const uint16_t*>(w)[p]) : reinterpret_cast<const float*>(w)[p];
-        float y0 = yd[(size_t)s * H + hb * 128 + lane], y1 = yd[(size_t)s * H + hb * 128 + lane + 64];
-        out_block_wave(y0, y1, h2f_bits(svh_d[hb * 128 + lane]), h2f_bits(svh_d[hb * 128 + lane + 64]));
-        o0 = o0 + wt * y0;
-        o1 = o1 + wt * y1;
+        o = o + wt * yd[(size_t)pv.pick_slot[p] * H + col];
     }
-    out[(size_t)tkn * H + hb * 128 + lane] = o0;
-    out[(size_t)tkn * H + hb * 128 + lane + 64] = o1;
+    out[idx] = o;
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -322,26 +411,35 @@ void launch_plan(const int64_t* sel, int P, int topk, int E, const PlanView& pv,
     hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(256), 0, st, sel, P, topk, E, pv);
 }
 
-template <int K, int NS, bool PREP>
+template <int K, int NS, bool PREP, int NW, bool OUTB>
 static void chain_launch(const uint64_t* ptrs, int mat_base, int nmat, int kdim, int ndim, const PlanView& pv,
                          int topk, int umax, const uint16_t* xin, float* yout, hipStream_t st)
 {
-    const int ncb = ndim / 128;
-    const size_t lds = (size_t)NS * kdim * 2;
-    auto kern = chain_gemv_kernel<K, NS, PREP>;
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    hipLaunchKernelGGL(kern, dim3(umax * ncb, nmat), dim3(512), lds, st, ptrs, mat_base, kdim, ndim, pv, topk, xin,
-                       yout);
+    const int ncb = ndim / (16 * NW);
+    const size_t lds = 2 * (size_t)Stage<K, NW>::BBP + (size_t)NS * kdim * 2 + (OUTB ? (size_t)NS * 128 * 4 : 0);
+    auto kern = chain_gemv_kernel<K, NS, PREP, NW, OUTB>;
+    static int lds_set = 0;   // largest dynamic LDS this instantiation has been opened up to
+    if ((int)lds > lds_set)
+    {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)lds);
+        lds_set = (int)lds;
+    }
+    hipLaunchKernelGGL(kern, dim3(umax * ncb, nmat), dim3(NW * 64), lds, st, ptrs, mat_base, kdim, ndim, pv, topk,
+                       xin, yout);
 }
 
 template <int K, bool PREP>
 static void chain_ns(int ns, const uint64_t* ptrs, int mat_base, int nmat, int kdim, int ndim, const PlanView& pv,
                      int topk, int umax, const uint16_t* xin, float* yout, hipStream_t st)
 {
-    if (ns <= 1) chain_launch<K, 1, PREP>(ptrs, mat_base, nmat, kdim, ndim, pv, topk, umax, xin, yout, st);
-    else if (ns <= 2) chain_launch<K, 2, PREP>(ptrs, mat_base, nmat, kdim, ndim, pv, topk, umax, xin, yout, st);
-    else if (ns <= 4) chain_launch<K, 4, PREP>(ptrs, mat_base, nmat, kdim, ndim, pv, topk, umax, xin, yout, st);
-    else chain_launch<K, 8, PREP>(ptrs, mat_base, nmat, kdim, ndim, pv, topk, umax, xin, yout, st);
+    // gate/up: 4 waves (64 outputs) per workgroup; down: 8 waves = one 128-output block, out_block fused
+    constexpr int NW = PREP ? 4 : 8;
+    constexpr bool OUTB = !PREP;
+    if (ns <= 1) chain_launch<K, 1, PREP, NW, OUTB>(ptrs, mat_base, nmat, kdim, ndim, pv, topk, umax, xin, yout, st);
+    else if (ns <= 2) chain_launch<K, 2, PREP, NW, OUTB>(ptrs, mat_base, nmat, kdim, ndim, pv, topk, umax, xin, yout, st);
+    else if (ns <= 4) chain_launch<K, 4, PREP, NW, OUTB>(ptrs, mat_base, nmat, kdim, ndim, pv, topk, umax, xin, yout, st);
+    else chain_launch<K, 8, PREP, NW, OUTB>(ptrs, mat_base, nmat, kdim, ndim, pv, topk, umax, xin, yout, st);
 }
 
 int launch_chain(int K, int ns, bool prep, const uint64_t* ptrs, int mat_base, int nmat, int kdim, int ndim,
@@ -370,8 +468,8 @@ void launch_act(const uint64_t* ptrs, const PlanView& pv, int smax, const float*
 void launch_final(const uint64_t* ptrs, const PlanView& pv, const void* w, int w_half, int M, int topk,
                   const float* yd, float* out, int H, hipStream_t st)
 {
-    const int items = M * (H / 128);
-    hipLaunchKernelGGL(final_kernel, dim3((items + 3) / 4), dim3(256), 0, st, ptrs, pv, w, w_half, M, topk, yd, out,
+    const int n = M * H;
+    hipLaunchKernelGGL(final_kernel, dim3((n + 255) / 256), dim3(256), 0, st, ptrs, pv, w, w_half, M, topk, yd, out,
                        H);
 }
 

@@ -6,8 +6,8 @@ Rademacher +-1 and svh is +-U(0.5, 1.5)/sqrt(fan_in) rounded to fp16 (generated 
 checker's generator). Seeds: 0x6A11F1A5 ^ (layer << 20 | expert << 4 | proj), proj 0/1/2 = gate/up/down; the
 scale stream uses seed ^ 0x5C41E50000000000.
 
-One layer lives in one device arena: per expert the three trellis blobs then the six scale vectors, each 256-byte
-aligned; `ptr_table` lists the 9 device addresses per expert that gfl_register_layer takes.
+One layer's trellis lives in one device arena (per expert: gate, up, down blobs, each 256-byte aligned) and its sign and
+scale vectors in a second one; `ptr_table` lists the 9 device addresses per expert that gfl_register_layer takes.
 """
 import numpy as np
 
@@ -53,40 +53,45 @@ def _al(x):
 
 
 class SynthLayer:
-    """E synthetic experts of one layer in one HBM arena."""
+    """E synthetic experts of one layer: trellis in one HBM arena (per expert: gate, up, down, each 256-byte aligned),
+    sign/scale vectors in a second, small arena."""
 
     def __init__(self, layer, E, H, I, Ks=(3, 3, 3), device=0):
         import torch
         self.layer, self.E, self.H, self.I, self.Ks = layer, E, H, I, tuple(Ks)
-        dims = [(H, I, Ks[0]), (H, I, Ks[1]), (I, H, Ks[2])]
+        self.dims = dims = [(H, I, Ks[0]), (H, I, Ks[1]), (I, H, Ks[2])]
         self.tbytes = [trellis_bytes(k, n, K) for k, n, K in dims]
-        offs, o = [], 0
+        self.toffs, o = [], 0
         for tb in self.tbytes:
-            offs.append(o)
+            self.toffs.append(o)
             o += _al(tb)
+        self.trec = o
+        self.soffs, o = [], 0
         for k, n, _ in dims:
-            offs.append(o); o += _al(2 * k)
-            offs.append(o); o += _al(2 * n)
-        self.offs = offs            # trellis g,u,d then suh_g, svh_g, suh_u, svh_u, suh_d, svh_d
-        self.rec = _al(o)
+            self.soffs.append(o); o += _al(2 * k)
+            self.soffs.append(o); o += _al(2 * n)
+        self.srec = o
         self.quant_bytes_per_expert = sum(self.tbytes) + 2 * sum(k + n for k, n, _ in dims)
-        self.arena = torch.empty(self.rec * E, dtype=torch.uint8, device=f"cuda:{device}")
-        host = np.zeros((E, self.rec), np.uint8)
+        dev = f"cuda:{device}"
+        self.arena = torch.empty(self.trec * E, dtype=torch.uint8, device=dev)
+        host = np.zeros((E, self.srec), np.uint8)
         for e in range(E):
             for p, (k, n, _) in enumerate(dims):
                 suh, svh = scales(seed(layer, e, p), k, n, k)
-                host[e, offs[3 + 2 * p]: offs[3 + 2 * p] + 2 * k] = suh.view(np.uint8)
-                host[e, offs[4 + 2 * p]: offs[4 + 2 * p] + 2 * n] = svh.view(np.uint8)
-        self.arena.copy_(torch.from_numpy(host.reshape(-1)))
-        del host
+                host[e, self.soffs[2 * p]: self.soffs[2 * p] + 2 * k] = suh.view(np.uint8)
+                host[e, self.soffs[2 * p + 1]: self.soffs[2 * p + 1] + 2 * n] = svh.view(np.uint8)
+        self.sarena = torch.from_numpy(host.reshape(-1)).to(dev)
         for e in range(E):
             for p in range(3):
-                base = e * self.rec + offs[p]
+                base = e * self.trec + self.toffs[p]
                 _native.synth_trellis(self.arena[base: base + self.tbytes[p]], seed(layer, e, p))
         torch.cuda.synchronize(device)
 
     def ptr(self, e, which):
-        return self.arena.data_ptr() + e * self.rec + self.offs[which]
+        """which 0..2: trellis gate/up/down; 3..8: suh_g, svh_g, suh_u, svh_u, suh_d, svh_d"""
+        if which < 3:
+            return self.arena.data_ptr() + e * self.trec + self.toffs[which]
+        return self.sarena.data_ptr() + e * self.srec + self.soffs[which - 3]
 
     @property
     def ptr_table(self):
@@ -97,13 +102,12 @@ class SynthLayer:
 
     def matrix(self, e, p):
         """(trellis uint8, suh uint16, svh uint16) of expert e, proj p, copied to host numpy."""
-        k, n = (self.H, self.I) if p < 2 else (self.I, self.H)
-        base = e * self.rec
-        a = self.arena[base: base + self.rec].cpu().numpy()
-        tr = a[self.offs[p]: self.offs[p] + self.tbytes[p]].copy()
-        suh = a[self.offs[3 + 2 * p]: self.offs[3 + 2 * p] + 2 * k].view(np.uint16).copy()
-        svh = a[self.offs[4 + 2 * p]: self.offs[4 + 2 * p] + 2 * n].view(np.uint16).copy()
-        return tr, suh, svh
+        k, n, _ = self.dims[p]
+        tb = self.arena[e * self.trec + self.toffs[p]: e * self.trec + self.toffs[p] + self.tbytes[p]]
+        sc = self.sarena[e * self.srec: (e + 1) * self.srec].cpu().numpy()
+        suh = sc[self.soffs[2 * p]: self.soffs[2 * p] + 2 * k].view(np.uint16).copy()
+        svh = sc[self.soffs[2 * p + 1]: self.soffs[2 * p + 1] + 2 * n].view(np.uint16).copy()
+        return tb.cpu().numpy().copy(), suh, svh
 
 
 def route_uniform(M, E, topk, rng):

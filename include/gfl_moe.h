@@ -100,6 +100,14 @@ int gfl_synth_trellis(void* dst, size_t nbytes, uint64_t seed, gfl_stream stream
  * [3] workspace bytes. Writes min(n, 4) entries into the host array `out`. */
 int gfl_stats(gfl_ctx* ctx, int64_t* out, int n);
 
+/* Per-stage device timing of gfl_moe_forward, the counterpart of the per-phase wall times tier_stats reports
+ * (ft_tier_ext.cpp:906-914): while enabled, every forward brackets its stages with device events
+ * (0 routing plan, 1 gate|up GEMV, 2 activation + down-input prep, 3 down GEMV, 4 output transform + combine).
+ * gfl_profile_read synchronises the recorded events, adds their elapsed milliseconds into stage_ms[5] and launch
+ * counts into launches[5] (host arrays), and clears the record. */
+int gfl_profile_enable(gfl_ctx* ctx, int enable);
+int gfl_profile_read(gfl_ctx* ctx, double* stage_ms, int64_t* launches);
+
 #ifdef __cplusplus
 }
 #endif
