@@ -1,0 +1,88 @@
+"""The C-ABI library (libgfl_moe.so) loads, exports every entry point include/gfl_moe.h declares, and its host-side
+logic behaves; no GPU needed (device entry points are only called for their argument checks)."""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "gfl_moe.h")
+
+
+def header_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gfl_[a-z_0-9]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    import _native
+    return _native.load()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    import _native
+    syms = header_symbols()
+    assert len(syms) >= 12
+    out = subprocess.run(["nm", "-D", "--defined-only", _native.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\bT (gfl_[a-z_0-9]+)", out))
+    missing = [s for s in syms if s not in exported]
+    assert not missing, missing
+    assert set(syms) == set(_native.SYMBOLS)
+    for s in syms:
+        getattr(lib, s)
+
+
+def test_version_and_error_string(lib):
+    assert lib.gfl_version() == 100
+    assert isinstance(lib.gfl_last_error(), bytes)
+
+
+def test_argument_checks_without_device(lib):
+    import _native
+    # NULL context / NULL pointers are rejected before any device work
+    assert lib.gfl_moe_forward(None, 0, None, None, None, 0, 1, 8, None, 1, 0.0, None) == 1
+    assert b"NULL" in lib.gfl_last_error()
+    assert lib.gfl_dequant(None, 16, 16, 3, None, None) == 1
+    assert lib.gfl_register_layer(None, 0, 1, 128, 128, 3, 3, 3, None) == 1
+    assert lib.gfl_split(*([None] * 3), 1, 8, 8, 8, 0, *([None] * 6), 0, 0, 0, *([None] * 5), None) == 1
+    assert lib.gfl_combine(None, 0, 1, None, None, None, None, 0, None) == 1
+    with pytest.raises(_native.NativeError):
+        _native.check(lib.gfl_stats(None, None, 0))
+
+
+def test_grouped_rows_host_matches_oracle(oracle):
+    import _native
+    rng = np.random.default_rng(12)
+    T, K, E = 17, 8, 48
+    sel = np.stack([rng.choice(E, K, replace=False) for _ in range(T)]).astype(np.int64)
+    sel[3, 2] = -1
+    w = rng.random((T, K)).astype(np.float32)
+    w[3, 2] = 0
+    take = (rng.random(E) < 0.6).astype(np.uint8)
+    a = _native.grouped_rows(sel, w, take, E)
+    b = oracle.grouped_rows(sel, w, take, E)
+    for x, y in zip(a, b):
+        assert np.array_equal(x, y)
+    dup = sel.copy(); dup[0, 1] = dup[0, 0]
+    with pytest.raises(ValueError, match="duplicate"):
+        _native.grouped_rows(dup, w, np.ones(E, np.uint8), E)
+    badt = np.ones(E, np.uint8); badt[3] = 2
+    with pytest.raises(ValueError, match="zero or one"):
+        _native.grouped_rows(sel, w, badt, E)
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    import _native
+    with pytest.raises(_native.NativeUnavailable):
+        saved = _native._LIB
+        _native._LIB = None
+        try:
+            _native.load(str(tmp_path / "absent.so"))
+        finally:
+            _native._LIB = saved
