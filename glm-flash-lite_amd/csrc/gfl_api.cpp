@@ -69,7 +69,7 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 int ensure_ws(gfl_ctx* c, int cap, int H, int I, Workspace& w)
 {
-    const size_t ints = align256(sizeof(int) * (size_t)(4 + 6 * cap + 2));
+    const size_t ints = align256(sizeof(int) * (size_t)(4 + 8 * cap + 2));
     const size_t b_ygu = align256(sizeof(float) * 2 * (size_t)cap * I);
     const size_t b_xtd = align256(sizeof(uint16_t) * (size_t)cap * I);
     const size_t b_yd = align256(sizeof(float) * (size_t)cap * H);
@@ -92,6 +92,8 @@ int ensure_ws(gfl_ctx* c, int cap, int H, int I, Workspace& w)
     w.pv.slot_u = w.pv.slot_pick + cap;
     w.pv.pick_slot = w.pv.slot_u + cap;
     w.pv.pick_job = w.pv.pick_slot + cap;
+    w.pv.tok_slot = w.pv.pick_job + cap;
+    w.pv.tok_w = reinterpret_cast<float*>(w.pv.tok_slot + cap);
     w.pv.cap_slots = cap;
     w.ygu = reinterpret_cast<float*>(b + ints);
     w.xtd = reinterpret_cast<uint16_t*>(b + ints + b_ygu);
@@ -166,7 +168,8 @@ int gfl_register_layer(gfl_ctx* c, int li, int E, int H, int I, int k_gate, int 
     if (!c || !ptrs) return fail(GFL_EINVAL, "gfl_register_layer: NULL argument");
     if (li < 0 || li > 4096) return fail(GFL_EINVAL, "gfl_register_layer: layer index out of range");
     if (E < 1 || E > gfl::MAX_EXPERTS) return fail(GFL_EINVAL, "gfl_register_layer: E must be 1..1024");
-    if (H < 128 || I < 128 || H % 128 || I % 128) return fail(GFL_EINVAL, "gfl_register_layer: H and I must be multiples of 128");
+    if (H < 256 || I < 256 || H % 256 || I % 256)
+        return fail(GFL_EINVAL, "gfl_register_layer: H and I must be multiples of 256");
     if (!k_ok(k_gate) || !k_ok(k_up) || !k_ok(k_down)) return fail(GFL_EINVAL, "gfl_register_layer: K must be 2..5");
     for (int i = 0; i < E * 9; ++i)
         if (ptrs[i] == 0 || (ptrs[i] & 3)) return fail(GFL_EINVAL, "gfl_register_layer: NULL or misaligned device pointer");
@@ -201,8 +204,9 @@ int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, c
     Workspace ws;
     if (int r = ensure_ws(c, P, L.H, L.I, ws)) return r;
     const int umax = P < L.E ? P : L.E;
-    const int ns = M < 8 ? M : 8;   // slots per pass; an expert holds at most M slots unless a token repeats it
-    int r = staged(c, 0, st, [&] { gfl::launch_plan(sel, P, topk, L.E, ws.pv, st); return 0; });
+    // slots per pass of the GEMV (its LDS holds NS transformed inputs); experts with more slots take extra passes
+    const int ns = M == 1 ? 1 : (M < 8 ? 2 : (M < 32 ? 4 : 8));
+    int r = staged(c, 0, st, [&] { gfl::launch_plan(sel, w, w_is_half ? 1 : 0, P, topk, L.E, ws.pv, st); return 0; });
     if (!r)
         r = staged(c, 1, st, [&] {
             if (L.K[0] == L.K[1])

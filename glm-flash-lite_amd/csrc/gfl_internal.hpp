@@ -19,10 +19,13 @@ struct PlanView
     int* slot_u;     // [slots] union entry of each slot
     int* pick_slot;  // [picks] slot of each pick, -1 when skipped
     int* pick_job;   // [picks] reference job index (combine order)
+    int* tok_slot;   // [tokens][topk] slots of each token in combine order, -1 padded
+    float* tok_w;    // [tokens][topk] their routing weights (fp32)
     int cap_slots;
 };
 
-void launch_plan(const int64_t* sel, int P, int topk, int E, const PlanView& pv, hipStream_t st);
+void launch_plan(const int64_t* sel, const void* w, int w_half, int P, int topk, int E, const PlanView& pv,
+                 hipStream_t st);
 int launch_chain(int K, int ns, bool prep, const uint64_t* ptrs, int mat_base, int nmat, int kdim, int ndim,
                  const PlanView& pv, int topk, int umax, const uint16_t* xin, float* yout, hipStream_t st);
 void launch_act(const uint64_t* ptrs, const PlanView& pv, int smax, const float* ygu, uint16_t* xtd, int I,

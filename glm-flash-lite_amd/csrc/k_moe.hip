@@ -24,11 +24,12 @@ namespace gfl {
 //   pick the index of the reference job it lands in (a new job whenever the expert's current job holds 8 tokens),
 //   which fixes the order of the weighted sum.
 // Ids outside [0, E) are skipped (tier_forward drops sel < 0, ft_tier_ext.cpp:896-898) and counted in err.
-__global__ __launch_bounds__(256) void plan_kernel(const int64_t* __restrict__ sel, int P, int topk, int E, PlanView pv)
+__global__ __launch_bounds__(256) void plan_kernel(const int64_t* __restrict__ sel, const void* __restrict__ w,
+                                                   int w_half, int P, int topk, int E, PlanView pv)
 {
     __shared__ int s_e[MAX_PICKS], s_c[MAX_PICKS], s_first[MAX_PICKS], s_crank[MAX_PICKS];
     __shared__ int firstpick[MAX_EXPERTS], ucnt[MAX_PICKS], uoff[MAX_PICKS + 1];
-    __shared__ int s_U, s_bad;
+    __shared__ int s_U, s_bad, s_job[MAX_PICKS], s_slot[MAX_PICKS];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     for (int e = t; e < E; e += blockDim.x) firstpick[e] = 0x7fffffff;
     if (t == 0) { s_U = 0; s_bad = 0; }
@@ -108,6 +109,31 @@ __global__ __launch_bounds__(256) void plan_kernel(const int64_t* __restrict__ s
         for (int q = 0; q <= p; ++q)
             if (s_e[q] == e && s_c[q] == want) { creator = q; break; }
         pv.pick_job[p] = s_crank[creator];
+        s_job[p] = s_crank[creator];
+        s_slot[p] = slot;
+    }
+    __syncthreads();
+    // per token: its picks in (job, pick) order -> the order of the weighted sum (ft_core.h:1020-1033)
+    for (int t0 = t; t0 * topk < P; t0 += blockDim.x)
+    {
+        int ord[MAX_TOPK];
+        int cnt = 0;
+        for (int k = 0; k < topk; ++k)
+        {
+            const int p = t0 * topk + k;
+            if (s_e[p] < 0) continue;
+            int b = cnt++;
+            while (b > 0 && s_job[ord[b - 1]] > s_job[p]) { ord[b] = ord[b - 1]; --b; }
+            ord[b] = p;
+        }
+        for (int k = 0; k < topk; ++k)
+        {
+            const int p = k < cnt ? ord[k] : -1;
+            pv.tok_slot[t0 * topk + k] = p >= 0 ? s_slot[p] : -1;
+            pv.tok_w[t0 * topk + k] = p < 0 ? 0.f
+                                   : (w_half ? h2f_bits(reinterpret_cast<const uint16_t*>(w)[p])
+                                             : reinterpret_cast<const float*>(w)[p]);
+        }
     }
 }
 
@@ -214,26 +240,38 @@ __global__ __launch_bounds__(NW * 64) void chain_gemv_kernel(const uint64_t* __r
         GFL_STORE_BATCH(b_ & 1, REG)                                                                             \
         lds_barrier();                                                                                           \
         GFL_LOAD_BATCH(b_ + 4, REG)                                                                              \
-        const uint8_t* sb_ = wl + (b_ & 1) * St::BBP;                                                             \
-        const int rows_ = b_ < nb ? min(BR, TK - b_ * BR) : 0;                                                   \
-        _Pragma("unroll 4") for (int r_ = 0; r_ < rows_; ++r_)                                                   \
+        const uint8_t* sb_ = wl + (b_ & 1) * St::BBP;                                                            \
+        if (b_ < nb)                                                                                             \
         {                                                                                                        \
-            const uint32_t hi_ = *reinterpret_cast<const uint32_t*>(sb_ + r_ * St::RB + d.o0);                   \
-            const uint32_t lo_ = *reinterpret_cast<const uint32_t*>(sb_ + r_ * St::RB + d.o1);                   \
-            const half4 B_ = decode4<K>(hi_, lo_, d.sh);                                                          \
-            const float4v cw_ = __builtin_amdgcn_mfma_f32_16x16x16f16(Pm, B_, zero, 0, 0, 0);                     \
-            const int tk_ = b_ * BR + r_;                                                                        \
-            _Pragma("unroll") for (int s_ = 0; s_ < NS; ++s_)                                                    \
+            _Pragma("unroll") for (int g_ = 0; g_ < BR; g_ += 4)                                                 \
             {                                                                                                    \
-                if (s_ < ns)                                                                                     \
+                /* four independent tiles: LDS words, decode and MFMA transposition first, then the chains */   \
+                uint32_t hi_[4], lo_[4];                                                                         \
+                _Pragma("unroll") for (int r_ = 0; r_ < 4; ++r_)                                                 \
                 {                                                                                                \
-                    const half4 xv_ = *reinterpret_cast<const half4*>(xl + ((size_t)s_ * TK + tk_) * 16);          \
-                    float a_ = acc[s_];                                                                          \
-                    a_ = __builtin_fmaf(cw_[0], (float)xv_[0], a_);                                              \
-                    a_ = __builtin_fmaf(cw_[1], (float)xv_[1], a_);                                              \
-                    a_ = __builtin_fmaf(cw_[2], (float)xv_[2], a_);                                              \
-                    a_ = __builtin_fmaf(cw_[3], (float)xv_[3], a_);                                              \
-                    acc[s_] = a_;                                                                                \
+                    hi_[r_] = *reinterpret_cast<const uint32_t*>(sb_ + (g_ + r_) * St::RB + d.o0);              \
+                    lo_[r_] = *reinterpret_cast<const uint32_t*>(sb_ + (g_ + r_) * St::RB + d.o1);              \
+                }                                                                                                \
+                float4v cw_[4];                                                                                  \
+                _Pragma("unroll") for (int r_ = 0; r_ < 4; ++r_)                                                 \
+                    cw_[r_] = __builtin_amdgcn_mfma_f32_16x16x16f16(Pm, decode4<K>(hi_[r_], lo_[r_], d.sh), zero, \
+                                                                    0, 0, 0);                                    \
+                _Pragma("unroll") for (int s_ = 0; s_ < NS; ++s_)                                                \
+                {                                                                                                \
+                    if (s_ < ns)                                                                                 \
+                    {                                                                                            \
+                        float a_ = acc[s_];                                                                      \
+                        _Pragma("unroll") for (int r_ = 0; r_ < 4; ++r_)                                         \
+                        {                                                                                        \
+                            const int tk_ = b_ * BR + g_ + r_;                                                   \
+                            const half4 xv_ = *reinterpret_cast<const half4*>(xl + ((size_t)s_ * TK + tk_) * 16); \
+                            a_ = __builtin_fmaf(cw_[r_][0], (float)xv_[0], a_);                                  \
+                            a_ = __builtin_fmaf(cw_[r_][1], (float)xv_[1], a_);                                  \
+                            a_ = __builtin_fmaf(cw_[r_][2], (float)xv_[2], a_);                                  \
+                            a_ = __builtin_fmaf(cw_[r_][3], (float)xv_[3], a_);                                  \
+                        }                                                                                        \
+                        acc[s_] = a_;                                                                            \
+                    }                                                                                            \
                 }                                                                                                \
             }                                                                                                    \
         }                                                                                                        \
@@ -347,31 +385,19 @@ __global__ __launch_bounds__(256) void act_kernel(const uint64_t* __restrict__ p
 // down out_block + weighted sum in job order (fwd_phase phases 2-3, ft_core.h:1014-1033)
 // ---------------------------------------------------------------------------------------------------------------
 
-__global__ __launch_bounds__(256) void final_kernel(const uint64_t* __restrict__ ptrs, PlanView pv,
-                                                    const void* __restrict__ w, int w_half, int M, int topk,
-                                                    const float* __restrict__ yd, float* __restrict__ out, int H)
+__global__ __launch_bounds__(256) void final_kernel(PlanView pv, int M, int topk, const float* __restrict__ yd,
+                                                    float* __restrict__ out, int H)
 {
-    // one thread per output element; picks of the token summed in (job, pick) order from 0 (ft_core.h:1020-1033)
+    // one thread per output element: o = 0, then += w * y over the token's picks in (job, pick) order
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= M * H) return;
     const int tkn = idx / H, col = idx % H;
-    int ord[MAX_TOPK];
-    int cnt = 0;
+    float o = 0.f;
     for (int k = 0; k < topk; ++k)
     {
-        const int p = tkn * topk + k;
-        if (pv.pick_slot[p] < 0) continue;
-        int b = cnt++;
-        const int jb = pv.pick_job[p];
-        while (b > 0 && pv.pick_job[ord[b - 1]] > jb) { ord[b] = ord[b - 1]; --b; }
-        ord[b] = p;
-    }
-    float o = 0.f;
-    for (int i = 0; i < cnt; ++i)
-    {
-        const int p = ord[i];
-        const float wt = w_half ? h2f_bits(reinterpret_cast<const uint16_t*>(w)[p]) : reinterpret_cast<const float*>(w)[p];
-        o = o + wt * yd[(size_t)pv.pick_slot[p] * H + col];
+        const int s = pv.tok_slot[tkn * topk + k];
+        if (s < 0) break;
+        o = o + pv.tok_w[tkn * topk + k] * yd[(size_t)s * H + col];
     }
     out[idx] = o;
 }
@@ -406,9 +432,10 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
 // launchers
 // ---------------------------------------------------------------------------------------------------------------
 
-void launch_plan(const int64_t* sel, int P, int topk, int E, const PlanView& pv, hipStream_t st)
+void launch_plan(const int64_t* sel, const void* w, int w_half, int P, int topk, int E, const PlanView& pv,
+                 hipStream_t st)
 {
-    hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(256), 0, st, sel, P, topk, E, pv);
+    hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(256), 0, st, sel, w, w_half, P, topk, E, pv);
 }
 
 template <int K, int NS, bool PREP, int NW, bool OUTB>
@@ -469,8 +496,7 @@ void launch_final(const uint64_t* ptrs, const PlanView& pv, const void* w, int w
                   const float* yd, float* out, int H, hipStream_t st)
 {
     const int n = M * H;
-    hipLaunchKernelGGL(final_kernel, dim3((n + 255) / 256), dim3(256), 0, st, ptrs, pv, w, w_half, M, topk, yd, out,
-                       H);
+    hipLaunchKernelGGL(final_kernel, dim3((n + 255) / 256), dim3(256), 0, st, pv, M, topk, yd, out, H);
 }
 
 int launch_dequant(const uint8_t* tr, int k, int n, int K, uint16_t* W, hipStream_t st)

@@ -50,8 +50,8 @@ int gfl_version(void);
 int gfl_ctx_create(int device, gfl_ctx** out);
 int gfl_ctx_destroy(gfl_ctx* ctx);
 
-/* Register layer `li`: E experts of a SwiGLU MLP, hidden H, intermediate I; gate/up are [H->I], down [I->H], each an
- * EXL3 trellis of K bits per weight (k_gate/k_up/k_down in 2..5) in 16x16 tiles stored row-major [k/16][n/16].
+/* Register layer `li`: E experts of a SwiGLU MLP, hidden H, intermediate I (multiples of 256); gate/up are [H->I],
+ * down [I->H], each an EXL3 trellis of K bits per weight (k_gate/k_up/k_down in 2..5) in 16x16 tiles stored row-major [k/16][n/16].
  * ptrs: HOST array [E][9] of DEVICE addresses per expert:
  *   trellis gate, up, down; suh_gate, svh_gate, suh_up, svh_up, suh_down, svh_down (fp16 sign/scale vectors).
  * The table is copied; the weights stay where the caller put them (full HBM residency).
