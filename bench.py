@@ -83,6 +83,75 @@ def cpu_baseline(iters, warmup):
             "cpus": cpus, "pool_gen_s": round(gen_s, 1)}
 
 
+COPY_BYTES = 1 << 30
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gate_up_config1_M1.json")
+GATE_UP_KERNEL = "chain_gemv_kernel<3, 1, true, 4, false>"
+
+
+def pmc_probe(ctx, layers, steps=64):
+    """Dispatches whose HBM counters calibrate and measure the gate|up kernel: four launches of an elementwise
+    negation over COPY_BYTES of fp32 (reads COPY_BYTES, writes COPY_BYTES; 4x the 256 MB Infinity Cache), then
+    `steps` eager M=1 layer calls cycling the layers and 32 routings, as the timed benchmark does."""
+    import numpy as np
+    import torch
+    import synth
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+    rng = np.random.default_rng(1001)
+    xs, sels, ws = [], [], []
+    for r in range(32):
+        x = rng.standard_normal((1, H)).astype(np.float16)
+        (sel, w16), _ = synth.route_uniform(1, E, TOPK, rng)
+        xs.append(torch.from_numpy(x.view(np.int16)).view(torch.float16).cuda())
+        sels.append(torch.from_numpy(sel).cuda())
+        ws.append(torch.from_numpy(w16.view(np.int16)).view(torch.float16).cuda())
+    out = torch.empty((1, H), dtype=torch.float32, device="cuda")
+    for i in range(steps):
+        ctx.moe_forward(i % len(layers), xs[i % 32], sels[i % 32], ws[i % 32], out)
+    torch.cuda.synchronize()
+    print(f"pmc probe: {4} copies of {COPY_BYTES} B, {steps} M=1 layer calls", flush=True)
+
+
+def _pmc_rows(folder, counter):
+    import csv
+    import glob
+    files = glob.glob(os.path.join(folder, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {folder}")
+    rows = []
+    for f in files:
+        for r in csv.DictReader(open(f)):
+            if r.get("Counter_Name") == counter:
+                rows.append((r["Kernel_Name"], float(r["Counter_Value"])))
+    return rows
+
+
+def pmc_digest(fetch_dir, write_dir):
+    """HBM bytes per gate|up launch from FETCH_SIZE and WRITE_SIZE (KiB per dispatch), each scaled by the factor
+    that makes the calibration copy read / write exactly COPY_BYTES."""
+    import numpy as np
+    res = {}
+    for name, folder in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        rows = _pmc_rows(folder, name)
+        cal = [v for k, v in rows if "neg" in k.lower()]
+        gu = [v for k, v in rows if GATE_UP_KERNEL in k]
+        if not cal or not gu:
+            raise SystemExit(f"{name}: calibration or gate|up dispatches missing ({len(cal)}, {len(gu)})")
+        factor = COPY_BYTES / (float(np.median(cal)) * 1024.0)
+        res[name] = {"copy_kib_median": float(np.median(cal)), "scale": round(factor, 4),
+                     "gate_up_kib_mean": round(float(np.mean(gu)), 1), "dispatches": len(gu),
+                     "gate_up_bytes_scaled": round(float(np.mean(gu)) * 1024.0 * factor)}
+    total = res["FETCH_SIZE"]["gate_up_bytes_scaled"] + res["WRITE_SIZE"]["gate_up_bytes_scaled"]
+    doc = {"kernel": GATE_UP_KERNEL, "workload": "config1 M=1 decode, eager calls cycling 4 layers",
+           "hbm_bytes_per_launch": total, "counters": res}
+    json.dump(doc, open(TRAFFIC_FILE, "w"), indent=1)
+    print(json.dumps(doc))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -94,7 +163,14 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=64)
     ap.add_argument("--cpu-iters", type=int, default=300)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="counter run: the calibration copy, then eager M=1 steps (run under rocprofv3 --pmc)")
+    ap.add_argument("--pmc-digest", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="turn two rocprofv3 --pmc output folders (FETCH_SIZE, WRITE_SIZE) into the traffic file")
     args = ap.parse_args()
+    if args.pmc_digest:
+        pmc_digest(*args.pmc_digest)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the routed-expert path on one GPU; multi-GPU runs are not part of this build "
               "(run with --gpus 1)", file=sys.stderr)
@@ -114,6 +190,9 @@ def main():
         L.register(ctx, li)
         layers.append(L)
     setup_s = time.time() - t0
+    if args.pmc_probe:
+        pmc_probe(ctx, layers)
+        return
     per_expert = layers[0].quant_bytes_per_expert
     gu_per_expert = layers[0].tbytes[0] + layers[0].tbytes[1] + 2 * 2 * (H + I)
     G = args.graph_steps
@@ -188,10 +267,9 @@ def main():
                     "algorithmic_bytes_per_launch": round(gu_bytes), "mean_launch_us": round(gu_ms / gu_n * 1e3, 2),
                     "stage_mean_us": stage_us}
         del g
-    traffic_file = os.path.join(ROOT, "profiles", "traffic_gate_up_config1_M1.json")
-    if roof is not None and os.path.exists(traffic_file):
+    if roof is not None and os.path.exists(TRAFFIC_FILE):
         try:
-            roof["traffic"] = json.load(open(traffic_file)).get("hbm_bytes_per_launch")
+            roof["traffic"] = json.load(open(TRAFFIC_FILE)).get("hbm_bytes_per_launch")
         except (OSError, ValueError):
             pass
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_iters, 20)
