@@ -190,10 +190,14 @@ __global__ __launch_bounds__(256) void split_kernel(const int64_t* __restrict__ 
     else if (t == 0) dflag[0] = 0;
 }
 
-// timeout_ticks: bounded wait in wall-clock ticks (the caller converts ns with the device's wall clock rate)
-__global__ __launch_bounds__(256) void combine_kernel(void* out, int is_half, int n, const int64_t* __restrict__ dflag,
-                                                      const int64_t* ctrl, const float* hout, int64_t* stats,
-                                                      int64_t timeout_ticks, int64_t ns_per_tick_q16)
+// One workgroup decides once, for every output element, whether the host partial is added: the trellis build of the
+// reference waits in each of its 16 blocks separately (ft_tier_cu.cu:205-235), so a done flag that lands inside the
+// timeout window can be added by some blocks and dropped by others; its LUT build already moved the decision into a
+// single block (ft_tier_cu.cu:162-201). Same counters: stats[4] waited ns, [5] waits, [6] timeouts, [7] already done.
+// timeout_ticks: bounded wait in wall-clock ticks (the caller converts ns with the device's wall clock rate).
+__global__ __launch_bounds__(1024) void combine_kernel(void* out, int is_half, int n, const int64_t* __restrict__ dflag,
+                                                       const int64_t* ctrl, const float* hout, int64_t* stats,
+                                                       int64_t timeout_ticks, int64_t ns_per_tick_q16)
 {
     __shared__ int go;
     if (threadIdx.x == 0)
@@ -203,7 +207,7 @@ __global__ __launch_bounds__(256) void combine_kernel(void* out, int is_half, in
         if (go)
         {
             const int64_t* done = ctrl + 1;
-            if (__hip_atomic_load(done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) >= s && blockIdx.x == 0)
+            if (__hip_atomic_load(done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) >= s)
                 atomicAdd(reinterpret_cast<unsigned long long*>(&stats[7]), 1ull);
             const uint64_t t0 = wall_clock64();
             uint64_t t1 = t0;
@@ -213,27 +217,24 @@ __global__ __launch_bounds__(256) void combine_kernel(void* out, int is_half, in
                 if ((int64_t)(t1 - t0) > timeout_ticks)
                 {
                     go = 0;
-                    if (blockIdx.x == 0) atomicAdd(reinterpret_cast<unsigned long long*>(&stats[6]), 1ull);
+                    atomicAdd(reinterpret_cast<unsigned long long*>(&stats[6]), 1ull);
                     break;
                 }
             }
-            if (blockIdx.x == 0)
-            {
-                const unsigned long long waited = (unsigned long long)(((t1 - t0) * (uint64_t)ns_per_tick_q16) >> 16);
-                atomicAdd(reinterpret_cast<unsigned long long*>(&stats[4]), waited);
-                atomicAdd(reinterpret_cast<unsigned long long*>(&stats[5]), 1ull);
-            }
+            const unsigned long long waited = (unsigned long long)(((t1 - t0) * (uint64_t)ns_per_tick_q16) >> 16);
+            atomicAdd(reinterpret_cast<unsigned long long*>(&stats[4]), waited);
+            atomicAdd(reinterpret_cast<unsigned long long*>(&stats[5]), 1ull);
         }
     }
     __syncthreads();
     if (!go) return;
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+    for (int i = threadIdx.x; i < n; i += blockDim.x)
     {
         const float v = __hip_atomic_load(&hout[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         if (is_half)
         {
-            __half* o = reinterpret_cast<__half*>(out);
-            o[i] = __float2half_rn(__half2float(o[i]) + v);
+            uint16_t* o = reinterpret_cast<uint16_t*>(out);
+            o[i] = (uint16_t)f2h_bits(h2f_bits(o[i]) + v);
         }
         else reinterpret_cast<float*>(out)[i] += v;
     }
@@ -278,7 +279,7 @@ void launch_combine(void* out, int is_half, int n, const int64_t* dflag, const i
     if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || khz <= 0) khz = 100000;
     const int64_t ticks = (int64_t)((double)timeout_ns * (double)khz / 1e6);
     const int64_t ns_per_tick_q16 = (int64_t)(65536.0 * 1e6 / (double)khz);
-    hipLaunchKernelGGL(combine_kernel, dim3(16), dim3(256), 0, st, out, is_half, n, dflag, ctrl, hout, stats, ticks,
+    hipLaunchKernelGGL(combine_kernel, dim3(1), dim3(1024), 0, st, out, is_half, n, dflag, ctrl, hout, stats, ticks,
                        ns_per_tick_q16);
 }
 
