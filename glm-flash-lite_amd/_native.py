@@ -13,7 +13,7 @@ LIB_PATH = os.path.join(HERE, "libgfl_moe.so")
 # exported symbols of include/gfl_moe.h (checked by tests/test_abi.py against the header)
 SYMBOLS = ("gfl_last_error", "gfl_version", "gfl_ctx_create", "gfl_ctx_destroy", "gfl_register_layer",
            "gfl_moe_forward", "gfl_dequant", "gfl_split", "gfl_combine", "gfl_grouped_rows", "gfl_synth_trellis",
-           "gfl_stats", "gfl_profile_enable", "gfl_profile_read")
+           "gfl_stats", "gfl_profile_enable", "gfl_profile_read", "gfl_exp_table")
 
 MODE_AUTO, MODE_AFFINE, MODE_EXACT, MODE_I16 = -1, 0, 1, 2
 
@@ -109,13 +109,20 @@ class Context:
     def moe_forward(self, li, x, sel, w, out, mode=MODE_EXACT, act_limit=0.0):
         """x fp16 [M,H], sel int64 [M,topk], w fp16|fp32 [M,topk], out fp32 [M,H] (all on the context device)."""
         import torch
+        if sel.dim() != 2:
+            raise ValueError("sel must be int64 [M, topk]")
         M, topk = sel.shape
-        assert x.dtype == torch.float16 and x.is_contiguous() and x.shape[0] == M
-        assert sel.dtype == torch.int64 and sel.is_contiguous()
-        assert w.dtype in (torch.float16, torch.float32) and w.is_contiguous() and tuple(w.shape) == (M, topk)
-        assert out.dtype == torch.float32 and out.is_contiguous() and tuple(out.shape) == tuple(x.shape)
+        if not (x.dtype == torch.float16 and x.is_contiguous() and x.dim() == 2 and x.shape[0] == M):
+            raise ValueError("x must be contiguous fp16 [M, H]")
+        if not (sel.dtype == torch.int64 and sel.is_contiguous()):
+            raise ValueError("sel must be contiguous int64 [M, topk]")
+        if not (w.dtype in (torch.float16, torch.float32) and w.is_contiguous() and tuple(w.shape) == (M, topk)):
+            raise ValueError("w must be contiguous fp16 or fp32 [M, topk]")
+        if not (out.dtype == torch.float32 and out.is_contiguous() and tuple(out.shape) == tuple(x.shape)):
+            raise ValueError("out must be contiguous fp32 [M, H]")
         for t in (x, sel, w, out):
-            assert t.is_cuda and t.device.index == self.device
+            if not (t.is_cuda and t.device.index == self.device):
+                raise ValueError(f"all tensors must be on cuda:{self.device}")
         check(load().gfl_moe_forward(self.h, li, ptr(x), ptr(sel), ptr(w), int(w.dtype == torch.float16), M, topk,
                                      ptr(out), int(mode), float(act_limit), _stream()))
         return out
@@ -165,6 +172,14 @@ def combine(out, dflag, ctrl, hout, stats, timeout_ns):
     import torch
     check(load().gfl_combine(ptr(out), int(out.dtype == torch.float16), out.numel(), ptr(dflag),
                              C.c_void_p(int(ctrl)), C.c_void_p(int(hout)), ptr(stats), int(timeout_ns), _stream()))
+
+
+def exp_table():
+    """Host copy of the SwiGLU exponential table: expf(-g) for every fp16 bit pattern of g (float32 [65536])."""
+    import numpy as np
+    out = np.empty(65536, np.float32)
+    check(load().gfl_exp_table(out.ctypes.data_as(C.c_void_p), out.size))
+    return out
 
 
 def grouped_rows(sel, w, take, E):

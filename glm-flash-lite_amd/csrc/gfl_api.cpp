@@ -53,6 +53,8 @@ struct gfl_ctx
     std::vector<hipEvent_t> ev_pool;
     struct Rec { int stage; hipEvent_t a, b; };
     std::vector<Rec> recs;
+    // expf(-g) for every fp16 bit pattern g (the SwiGLU exponential, see build_exp_table)
+    float* exp_tab = nullptr;
 };
 
 namespace {
@@ -138,14 +140,50 @@ const char* gfl_last_error(void) { return g_err.c_str(); }
 
 int gfl_version(void) { return 100; }
 
+// The SwiGLU gate of the reference is silu(g) = g / (1 + std::exp(-g)) in fp32 (ft_core.h:123), i.e. the host C
+// library's expf. g is always fp16-valued (out_block rounds it, ft_core.h:109), so the exponential the device needs
+// is expf over the 65,536 fp16 bit patterns. glibc's expf is not correctly rounded on every one of them (it is
+// within 0.502 ulp), so no device formula reproduces it exactly; the table is evaluated here, by the same library
+// call the reference makes, and the activation kernel looks it up.
+static void build_exp_table(float* tab)
+{
+    for (uint32_t b = 0; b < 65536; ++b)
+    {
+        const uint16_t bits = (uint16_t)b;
+        _Float16 h;
+        std::memcpy(&h, &bits, 2);
+        const float g = (float)h;     // exact
+        tab[b] = std::exp(-g);
+    }
+}
+
+int gfl_exp_table(float* out, int n)
+{
+    if (!out || n < 65536) return fail(GFL_EINVAL, "gfl_exp_table: needs a host array of 65536 floats");
+    build_exp_table(out);
+    return GFL_OK;
+}
+
 int gfl_ctx_create(int device, gfl_ctx** out)
 {
     if (!out) return fail(GFL_EINVAL, "gfl_ctx_create: out is NULL");
     int n = 0;
     GFL_HIP(hipGetDeviceCount(&n));
     if (device < 0 || device >= n) return fail(GFL_EINVAL, "gfl_ctx_create: no such device");
+    GFL_HIP(hipSetDevice(device));
+    std::vector<float> tab(65536);
+    build_exp_table(tab.data());
+    float* dtab = nullptr;
+    if (hipMalloc(&dtab, tab.size() * sizeof(float)) != hipSuccess) return fail(GFL_ENOMEM, "gfl_ctx_create: exp table");
+    const hipError_t e = hipMemcpy(dtab, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice);
+    if (e != hipSuccess)
+    {
+        hipFree(dtab);
+        return fail(GFL_ERUNTIME, std::string("gfl_ctx_create: ") + hipGetErrorString(e));
+    }
     gfl_ctx* c = new gfl_ctx();
     c->device = device;
+    c->exp_tab = dtab;
     *out = c;
     return GFL_OK;
 }
@@ -159,6 +197,7 @@ int gfl_ctx_destroy(gfl_ctx* c)
     for (auto& L : c->layers)
         if (L.dptrs) hipFree(L.dptrs);
     if (c->ws) hipFree(c->ws);
+    if (c->exp_tab) hipFree(c->exp_tab);
     delete c;
     return GFL_OK;
 }
@@ -216,7 +255,7 @@ int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, c
             return gfl::launch_chain(L.K[1], ns, true, L.dptrs, 1, 1, L.H, L.I, ws.pv, topk, umax, x,
                                      ws.ygu + (size_t)P * L.I, st);
         });
-    if (!r) r = staged(c, 2, st, [&] { gfl::launch_act(L.dptrs, ws.pv, P, ws.ygu, ws.xtd, L.I, act_limit, st); return 0; });
+    if (!r) r = staged(c, 2, st, [&] { gfl::launch_act(L.dptrs, ws.pv, P, ws.ygu, ws.xtd, L.I, act_limit, c->exp_tab, st); return 0; });
     if (!r)
         r = staged(c, 3, st, [&] {
             return gfl::launch_chain(L.K[2], ns, false, L.dptrs, 2, 1, L.I, L.H, ws.pv, topk, umax, ws.xtd, ws.yd, st);

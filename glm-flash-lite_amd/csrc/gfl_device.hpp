@@ -133,11 +133,11 @@ __device__ inline void out_block_wave(float& v0, float& v1, float s0, float s1)
     v1 = r16(v1 * HADF * s1);
 }
 
-// silu(g) * u with the exllamav3 clamp (ft_core.h:123-132). exp is taken in fp64 and rounded once, so it equals a
-// correctly rounded expf except in vanishingly rare near-tie cases.
-__device__ inline float act_mul(float g, float u, float limit)
+// silu(g) * u with exllamav3's clamp (act_mul, ft_core.h:123-132); e = expf(-g) comes from the context's table,
+// indexed by the fp16 bits of g (g is fp16-valued)
+__device__ inline float act_mul(float g, float u, float limit, const float* __restrict__ exp_tab)
 {
-    const float e = (float)exp(-(double)g);
+    const float e = exp_tab[f2h_bits(g) & 0xFFFFu];
     float x = g / (1.0f + e);
     if (limit != 0.0f)
     {

@@ -29,7 +29,7 @@ void launch_plan(const int64_t* sel, const void* w, int w_half, int P, int topk,
 int launch_chain(int K, int ns, bool prep, const uint64_t* ptrs, int mat_base, int nmat, int kdim, int ndim,
                  const PlanView& pv, int topk, int umax, const uint16_t* xin, float* yout, hipStream_t st);
 void launch_act(const uint64_t* ptrs, const PlanView& pv, int smax, const float* ygu, uint16_t* xtd, int I,
-                float limit, hipStream_t st);
+                float limit, const float* exp_tab, hipStream_t st);
 void launch_final(const uint64_t* ptrs, const PlanView& pv, const void* w, int w_half, int M, int topk,
                   const float* yd, float* out, int H, hipStream_t st);
 int launch_dequant(const uint8_t* tr, int k, int n, int K, uint16_t* W, hipStream_t st);

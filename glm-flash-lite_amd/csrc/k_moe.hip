@@ -359,7 +359,7 @@ __global__ __launch_bounds__(NW * 64) void chain_gemv_kernel(const uint64_t* __r
 
 __global__ __launch_bounds__(256) void act_kernel(const uint64_t* __restrict__ ptrs, PlanView pv,
                                                   const float* __restrict__ ygu, uint16_t* __restrict__ xtd, int I,
-                                                  float limit)
+                                                  float limit, const float* __restrict__ exp_tab)
 {
     const int nb = I / 128;
     const int item = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -374,7 +374,7 @@ __global__ __launch_bounds__(256) void act_kernel(const uint64_t* __restrict__ p
     float g0 = yg[lane], g1 = yg[lane + 64], u0 = yu[lane], u1 = yu[lane + 64];
     out_block_wave(g0, g1, h2f_bits(svh_g[ib * 128 + lane]), h2f_bits(svh_g[ib * 128 + lane + 64]));
     out_block_wave(u0, u1, h2f_bits(svh_u[ib * 128 + lane]), h2f_bits(svh_u[ib * 128 + lane + 64]));
-    float a0 = r16(act_mul(g0, u0, limit)), a1 = r16(act_mul(g1, u1, limit));
+    float a0 = r16(act_mul(g0, u0, limit, exp_tab)), a1 = r16(act_mul(g1, u1, limit, exp_tab));
     prep_block_wave(a0, a1, h2f_bits(suh_d[ib * 128 + lane]), h2f_bits(suh_d[ib * 128 + lane + 64]));
     uint16_t* dst = xtd + (size_t)s * I;
     dst[perm_pos(ib, lane)] = (uint16_t)f2h_bits(a0);
@@ -486,10 +486,11 @@ int launch_chain(int K, int ns, bool prep, const uint64_t* ptrs, int mat_base, i
 }
 
 void launch_act(const uint64_t* ptrs, const PlanView& pv, int smax, const float* ygu, uint16_t* xtd, int I,
-                float limit, hipStream_t st)
+                float limit, const float* exp_tab, hipStream_t st)
 {
     const int items = smax * (I / 128);
-    hipLaunchKernelGGL(act_kernel, dim3((items + 3) / 4), dim3(256), 0, st, ptrs, pv, ygu, xtd, I, limit);
+    hipLaunchKernelGGL(act_kernel, dim3((items + 3) / 4), dim3(256), 0, st, ptrs, pv, ygu, xtd, I, limit,
+                       exp_tab);
 }
 
 void launch_final(const uint64_t* ptrs, const PlanView& pv, const void* w, int w_half, int M, int topk,

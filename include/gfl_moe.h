@@ -96,6 +96,11 @@ int gfl_grouped_rows(const int64_t* sel, const float* w, int T, int K, const uin
  * any bit stream is a valid EXL3 tile). Byte b = byte (b % 8) of output b/8. */
 int gfl_synth_trellis(void* dst, size_t nbytes, uint64_t seed, gfl_stream stream);
 
+/* The SwiGLU gate exponential, host copy: out[b] = expf(-g) for every fp16 bit pattern b of g (n >= 65536 floats).
+ * silu (kernels/cpu_avx2/ft_core.h:123) calls the host C library's expf; g is always fp16-valued, so this table,
+ * evaluated with that same library call, is what every context uploads and the activation kernel reads. */
+int gfl_exp_table(float* out, int n);
+
 /* Host-side counters of the context (no device sync): [0] forward calls, [1] picks submitted, [2] registered layers,
  * [3] workspace bytes. Writes min(n, 4) entries into the host array `out`. */
 int gfl_stats(gfl_ctx* ctx, int64_t* out, int n);

@@ -8,7 +8,8 @@ regenerated from seeds by the checker's splitmix64 generator, so only seeds and 
   dense_K3_*      dense_weights (ft_core.h:1657-1672) of seeded matrices, fp16 bit patterns
   prep / outb     prep_block / out_block (ft_core.h:97-110) of seeded vectors
   moe_*           moe_forward (ft_core.h:1338-1407) EXACT and AFFINE outputs: H=512 I=256 E=6 with the reference
-                  harness routing ((t + 2k) % E, weight 0.25; kernel-ab-harness.cpp:115-116), ntok 1/3/4
+                  harness routing ((t + 2k) % E, weight 0.25; kernel-ab-harness.cpp:115-116), ntok 1/3/4/16
+                  (16 tokens put 10-11 tokens on each expert: two jobs per expert)
   expert_c0_*     config-0 expert (H=5120 I=1536 K=3) one token: EXACT moe_forward with weight 1, and ref_expert fp64
 
     python tests/golden/make_golden.py
@@ -63,7 +64,7 @@ def main():
     # small MoE layer, harness routing
     H, I, E = 512, 256, 6
     ex = [O.synth_expert(7, e, H, I) for e in range(E)]
-    for nt in (1, 3, 4):
+    for nt in (1, 3, 4, 16):
         r2 = np.random.default_rng(777 + nt)
         x = (r2.standard_normal((nt, H)) * 0.35).astype(np.float16).astype(np.float32)
         sel = np.array([[(t + 2 * k) % E for k in range(4)] for t in range(nt)], np.int32)

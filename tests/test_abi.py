@@ -86,3 +86,22 @@ def test_missing_library_fails_loudly(tmp_path):
             _native.load(str(tmp_path / "absent.so"))
         finally:
             _native._LIB = saved
+
+
+def test_exp_table_is_the_c_library_expf():
+    """The activation's exponential table equals the C library's expf at every fp16 input (what silu calls,
+    ft_core.h:123). It also documents why a table is used: correctly rounded exp disagrees with it on some inputs."""
+    import ctypes as C
+    import math
+    import _native
+    tab = _native.exp_table()
+    libm = C.CDLL("libm.so.6")
+    libm.expf.restype, libm.expf.argtypes = C.c_float, [C.c_float]
+    g = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float32)
+    want = np.array([libm.expf(float(-v)) for v in g], np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(tab), nan)
+    assert np.array_equal(tab[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    fin = np.isfinite(g) & (np.abs(g) < 80)
+    cr = np.array([np.float32(math.exp(float(-v))) for v in g[fin]], np.float32)
+    assert (cr.view(np.uint32) != want[fin].view(np.uint32)).sum() > 0

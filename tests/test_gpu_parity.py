@@ -97,6 +97,24 @@ def test_forward_small_bitexact(gpu, oracle, ntok):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("nt", [1, 3, 4, 16])
+def test_forward_equals_reference_engine_golden(gpu, nt):
+    """Layer output against the reference engine's own EXACT moe_forward (tests/golden, written from
+    kernels/cpu_avx2/ft_core.h), no oracle in between: H=512 I=256 E=6, harness routing (t + 2k) % 6, weight 0.25;
+    16 tokens give every expert two jobs."""
+    import os
+    from conftest import GOLDEN
+    G = np.load(os.path.join(GOLDEN, "ref_vectors.npz"))
+    _layer(gpu, 7, 6, 512, 256)
+    x, sel = G[f"moe_x_{nt}"], G[f"moe_sel_{nt}"].astype(np.int64)
+    w = np.full(sel.shape, 0.25, np.float32)
+    got = _forward(gpu, 7, x.astype(np.float16), sel, w)
+    want = G[f"moe_exact_{nt}"]
+    _report(f"golden nt={nt}", got, want)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("scale", [0.35, 0.05, 1.0])
 def test_forward_sweep_bitexact(gpu, oracle, scale):
     """16 tokens x every expert of an 8-expert layer (128 picks, 16 slots per expert): exercises many rounding ties,

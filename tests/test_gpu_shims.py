@@ -1,0 +1,127 @@
+"""The reference-shaped surface on the GPU: a full-residency expert_cache.Pool over duck-typed MoE modules, the tier
+registered from it as cpu_tier.start does, tier_forward (the reference's expert-call signature: CPU fp32 x, int32 sel
+with -1 skips, fp32 w) bit-identical to the oracle, the SwiGLU clamp through tier_set_act_limit, and the split through
+the handle k_ftsplit.install swaps in."""
+import numpy as np
+import pytest
+import torch
+
+import fake_moe
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def tier(gpu):
+    import expert_cache
+    import ft_tier
+    import synth
+    H, I, E = 512, 256, 6
+    layers = [synth.SynthLayer(40 + li, E, H, I, Ks) for li, Ks in enumerate(((3, 3, 3), (4, 4, 3)))]
+    mods = [fake_moe.from_synth(L, f"model.layers.{li}.mlp") for li, L in enumerate(layers)]
+    pool = expert_cache.Pool(torch.device("cuda", 0), mods)
+    ft_tier.tier_shutdown()
+    ctrl = torch.zeros(16, dtype=torch.int64, device="cuda")
+    ft_tier.tier_init(1, [0], ctrl, None, None, None, -1, H, I, len(mods), 0)
+    ft_tier.add_pool_layers(pool, bits=[L.Ks for L in layers])
+    yield dict(pool=pool, layers=layers, mods=mods, H=H, I=I, E=E)
+    ft_tier.tier_set_act_limit(0.0)
+    ft_tier.tier_shutdown()
+
+
+def _experts(oracle, L):
+    from oracle import Mat
+    out = []
+    for e in range(L.E):
+        mats = []
+        for p in range(3):
+            tr, suh, svh = L.matrix(e, p)
+            k, n = (L.H, L.I) if p < 2 else (L.I, L.H)
+            mats.append(Mat(tr, suh, svh, k, n, L.Ks[p]))
+        out.append(tuple(mats))
+    return out
+
+
+@pytest.mark.parametrize("li", [0, 1])
+def test_tier_forward_reference_signature_bitexact(tier, oracle, li):
+    import ft_tier
+    rng = np.random.default_rng(50 + li)
+    m = 5
+    x = torch.from_numpy((rng.standard_normal((m, tier["H"])) * 0.4).astype(np.float16).astype(np.float32))
+    sel = torch.from_numpy(np.stack([rng.choice(tier["E"], 4, replace=False) for _ in range(m)]).astype(np.int32))
+    sel[1, 2] = -1
+    w = torch.from_numpy(rng.random((m, 4)).astype(np.float32))
+    got = ft_tier.tier_forward(li, x, sel, w, -1)
+    assert got.device.type == "cpu" and got.dtype == torch.float32 and tuple(got.shape) == (m, tier["H"])
+    want = oracle.moe_forward(_experts(oracle, tier["layers"][li]), x.numpy(), sel.numpy(), w.numpy(), mode=1)
+    assert np.array_equal(got.numpy(), want)
+    st = ft_tier.tier_stats()
+    assert len(st) == 12 and st[0] >= 1
+
+
+def test_tier_forward_act_limit(tier, oracle):
+    import ft_tier
+    rng = np.random.default_rng(60)
+    x = torch.from_numpy((rng.standard_normal((3, tier["H"])) * 0.8).astype(np.float16).astype(np.float32))
+    sel = torch.tensor([[0, 1, 2, 3], [2, 3, 4, 5], [5, 0, 1, 4]], dtype=torch.int32)
+    w = torch.full((3, 4), 0.25)
+    lim = 0.05
+    ft_tier.tier_set_act_limit(lim)
+    try:
+        got = ft_tier.tier_forward(0, x, sel, w, 1)
+    finally:
+        ft_tier.tier_set_act_limit(0.0)
+    ex = _experts(oracle, tier["layers"][0])
+    want = oracle.moe_forward(ex, x.numpy(), sel.numpy(), w.numpy(), mode=1, act_limit=lim)
+    free = oracle.moe_forward(ex, x.numpy(), sel.numpy(), w.numpy(), mode=1)
+    assert not np.array_equal(want, free)           # the clamp is active at this limit
+    assert np.array_equal(got.numpy(), want)
+
+
+def test_tier_forward_argument_errors(tier):
+    import ft_tier
+    x = torch.full((1, tier["H"]), 0.1)              # 0.1 is not an fp16 value
+    sel = torch.zeros(1, 4, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="fp16-valued"):
+        ft_tier.tier_forward(0, x, sel, torch.ones(1, 4), 1)
+    with pytest.raises(RuntimeError, match="EXACT"):
+        ft_tier.tier_forward(0, x.half().float(), sel, torch.ones(1, 4), 2)
+    with pytest.raises(RuntimeError, match="out of range"):
+        ft_tier.tier_forward(0, x.half().float(), sel + 99, torch.ones(1, 4), 1)
+    with pytest.raises(RuntimeError, match="already initialised"):
+        ft_tier.tier_init(1, [0], None, None, None, None, -1, tier["H"], tier["I"], 1, 0)
+
+
+def test_pool_on_device_verifies_clean(tier):
+    r = tier["pool"].verify()
+    assert r["bad_slots"] == 0 and r["bad_tables"] == 0 and r["owned"] == 2 * tier["E"]
+    tier["pool"].step(0, torch.tensor([[0, 1, 2, 3]], device="cuda"), True)
+    assert tier["pool"].summary()["hits"] >= 4
+
+
+def test_installed_split_handle_on_device(tier, oracle):
+    """cpu_tier.routed's call, through the handle k_ftsplit.install puts in place, with the pool's own slotof."""
+    import types
+    import k_ftsplit
+    cpu_tier = types.SimpleNamespace(_CU=None)
+    k_ftsplit.install(cpu_tier)
+    pool = tier["pool"]
+    rng = np.random.default_rng(70)
+    bsz, H, E = 2, tier["H"], tier["E"]
+    sel = torch.from_numpy(np.stack([rng.choice(E, 4, replace=False) for _ in range(bsz)]).astype(np.int64)).cuda()
+    w = torch.from_numpy(rng.random((bsz, 4)).astype(np.float16)).cuda()
+    z = torch.from_numpy(rng.standard_normal((bsz, H)).astype(np.float16)).cuda()
+    score = torch.zeros(E, device="cuda")
+    pol = torch.tensor([0.4, 0.023, 0.11, 0.104, 0.2, 32, -1, 0] + [0.0] * 12, device="cuda")
+    ctrl = torch.zeros(16, dtype=torch.int64, device="cuda")
+    hx = torch.zeros(bsz * H, dtype=torch.float16, device="cuda")
+    hp = torch.zeros(bsz * 4 * 3, dtype=torch.int32, device="cuda")
+    so, wo = torch.empty(bsz * 4, dtype=torch.int64, device="cuda"), torch.empty(bsz * 4, dtype=torch.float16, device="cuda")
+    dflag, stats = torch.zeros(1, dtype=torch.int64, device="cuda"), torch.zeros(8, dtype=torch.int64, device="cuda")
+    cpu_tier._CU.ft_split(sel.contiguous(), w.contiguous(), z, pool.E, pool.first, pool.slotof[0], score, pol,
+                          ctrl.data_ptr(), hx.data_ptr(), hp.data_ptr(), 1, 0, 0, so, wo, dflag, stats,
+                          torch.empty(0, dtype=torch.int32, device="cuda"))
+    torch.cuda.synchronize()
+    # full residency: every pick is a hit, the selection passes through, nothing is published
+    assert torch.equal(so.view(bsz, 4), sel) and torch.equal(wo.view(bsz, 4), w)
+    assert int(dflag.item()) == 0 and stats.tolist()[:4] == [len(torch.unique(sel)), 0, 0, 1]

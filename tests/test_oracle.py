@@ -131,7 +131,7 @@ def test_prep_and_out_block_golden(oracle):
 # experts and layers
 # ---------------------------------------------------------------------------------------------------------------
 
-@pytest.mark.parametrize("nt", [1, 3, 4])
+@pytest.mark.parametrize("nt", [1, 3, 4, 16])
 @pytest.mark.parametrize("mode,key", [(1, "exact"), (0, "affine")])
 def test_moe_forward_golden(oracle, nt, mode, key):
     ex = [oracle.synth_expert(7, e, 512, 256) for e in range(6)]
