@@ -85,7 +85,7 @@ def cpu_baseline(iters, warmup):
 
 COPY_BYTES = 1 << 30
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gate_up_config1_M1.json")
-GATE_UP_KERNEL = "chain_gemv_kernel<3, 1, true, 4, false>"
+GATE_UP_KERNEL = "gu_kernel<3, 1>"
 
 
 def pmc_probe(ctx, layers, steps=64):
@@ -263,7 +263,7 @@ def main():
             ach = gu_bytes / (gu_ms / gu_n * 1e-3) / 1e9
             stage_us = {k: round(v[0] / max(1, v[1]) * 1e3, 2) for k, v in prof.items()}
             roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                    "frac": round(ach / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": "chain_gemv_kernel (gate|up)",
+                    "frac": round(ach / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": "gu_kernel<3, 1> (gate|up GEMV + SwiGLU)",
                     "algorithmic_bytes_per_launch": round(gu_bytes), "mean_launch_us": round(gu_ms / gu_n * 1e3, 2),
                     "stage_mean_us": stage_us}
         del g

@@ -22,6 +22,9 @@ SOURCES = ["k_moe.hip", "k_split.hip", "gfl_api.cpp"]
 
 CFLAGS = ["--offload-arch=" + ARCH, "-O3", "-fPIC", "-std=c++17", "-ffp-contract=off",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          # MFMA results straight into VGPRs: the transposing MFMA of the GEMV feeds VALU FMAs, and the AGPR form
+          # costs four v_accvgpr_read per tile
+          "-mllvm", "-amdgpu-mfma-vgpr-form",
           "-Wno-unused-result", "-I" + os.path.join(ROOT, "include"), "-I" + CSRC]
 
 

@@ -2,6 +2,7 @@
 #include "gfl_moe.h"
 #include "gfl_internal.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -46,7 +47,7 @@ struct gfl_ctx
     std::mutex mu;
     // workspace (grown on demand, never shrunk)
     void* ws = nullptr;
-    size_t ws_bytes = 0;
+    size_t ws_bytes = 0, ws_cnt_off = 0;
     int64_t calls = 0, picks = 0;
     // per-stage profiling events (gfl_profile_enable / gfl_profile_read)
     bool prof = false;
@@ -65,24 +66,44 @@ struct Workspace
     float* ygu;      // [2][cap][I]
     uint16_t* xtd;   // [cap][I]
     float* yd;       // [cap][H]
+    int* act_cnt;    // [cap][I/128] last-one counters of the SwiGLU stage (zero between calls)
+    int* out_cnt;    // [cap][H/128] last-one counters of the combine (zero between calls)
 };
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-int ensure_ws(gfl_ctx* c, int cap, int H, int I, Workspace& w)
+// The workspace grows to the largest (picks, H, I) seen and is laid out for the current call. The counter region is
+// zeroed when the buffer is (re)allocated; the kernels leave every counter at zero when they finish.
+int ensure_ws(gfl_ctx* c, int cap, int H, int I, hipStream_t st, Workspace& w)
 {
-    const size_t ints = align256(sizeof(int) * (size_t)(4 + 8 * cap + 2));
+    const size_t ints = align256(sizeof(int) * (size_t)(4 + 9 * cap + 2));
     const size_t b_ygu = align256(sizeof(float) * 2 * (size_t)cap * I);
     const size_t b_xtd = align256(sizeof(uint16_t) * (size_t)cap * I);
     const size_t b_yd = align256(sizeof(float) * (size_t)cap * H);
-    const size_t need = ints + b_ygu + b_xtd + b_yd;
-    if (need > c->ws_bytes)
+    const size_t b_cnt = align256(sizeof(int) * (size_t)cap * (I / 128 + H / 128));
+    const size_t data = ints + b_ygu + b_xtd + b_yd;
+    // data regions from the start, counters in a tail region of their own: grow when either does not fit
+    const size_t old_off = c->ws ? c->ws_cnt_off : 0, old_cnt = c->ws ? c->ws_bytes - c->ws_cnt_off : 0;
+    if (!c->ws || data > old_off || b_cnt > old_cnt)
     {
-        if (c->ws) GFL_HIP(hipFree(c->ws));
+        const size_t off = std::max(data, old_off), need = off + std::max(b_cnt, old_cnt);
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+            return fail(GFL_EINVAL, "gfl_moe_forward: the workspace must be sized before graph capture "
+                                    "(run one forward of this shape first)");
+        if (c->ws)
+        {
+            GFL_HIP(hipDeviceSynchronize());
+            GFL_HIP(hipFree(c->ws));
+        }
         c->ws = nullptr;
         c->ws_bytes = 0;
+        c->ws_cnt_off = 0;
         hipError_t e = hipMalloc(&c->ws, need);
         if (e != hipSuccess) return fail(GFL_ENOMEM, std::string("workspace hipMalloc: ") + hipGetErrorString(e));
+        GFL_HIP(hipMemset(c->ws, 0, need));
+        GFL_HIP(hipDeviceSynchronize());
+        c->ws_cnt_off = off;
         c->ws_bytes = need;
     }
     char* b = static_cast<char*>(c->ws);
@@ -96,10 +117,14 @@ int ensure_ws(gfl_ctx* c, int cap, int H, int I, Workspace& w)
     w.pv.pick_job = w.pv.pick_slot + cap;
     w.pv.tok_slot = w.pv.pick_job + cap;
     w.pv.tok_w = reinterpret_cast<float*>(w.pv.tok_slot + cap);
+    w.pv.tok_npk = reinterpret_cast<int*>(w.pv.tok_w + cap);
     w.pv.cap_slots = cap;
     w.ygu = reinterpret_cast<float*>(b + ints);
     w.xtd = reinterpret_cast<uint16_t*>(b + ints + b_ygu);
     w.yd = reinterpret_cast<float*>(b + ints + b_ygu + b_xtd);
+    // counters live at the fixed tail of the allocation so that a smaller call reuses the same (zeroed) words
+    w.act_cnt = reinterpret_cast<int*>(b + c->ws_cnt_off);
+    w.out_cnt = w.act_cnt + (size_t)cap * (I / 128);
     return GFL_OK;
 }
 
@@ -241,29 +266,28 @@ int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, c
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const int P = M * topk;
     Workspace ws;
-    if (int r = ensure_ws(c, P, L.H, L.I, ws)) return r;
+    if (int r = ensure_ws(c, P, L.H, L.I, st, ws)) return r;
     const int umax = P < L.E ? P : L.E;
     // slots per pass of the GEMV (its LDS holds NS transformed inputs); experts with more slots take extra passes
     const int ns = M == 1 ? 1 : (M < 8 ? 2 : (M < 32 ? 4 : 8));
-    int r = staged(c, 0, st, [&] { gfl::launch_plan(sel, w, w_is_half ? 1 : 0, P, topk, L.E, ws.pv, st); return 0; });
-    if (!r)
-        r = staged(c, 1, st, [&] {
-            if (L.K[0] == L.K[1])
-                return gfl::launch_chain(L.K[0], ns, true, L.dptrs, 0, 2, L.H, L.I, ws.pv, topk, umax, x, ws.ygu, st);
-            if (gfl::launch_chain(L.K[0], ns, true, L.dptrs, 0, 1, L.H, L.I, ws.pv, topk, umax, x, ws.ygu, st))
-                return -1;
-            return gfl::launch_chain(L.K[1], ns, true, L.dptrs, 1, 1, L.H, L.I, ws.pv, topk, umax, x,
-                                     ws.ygu + (size_t)P * L.I, st);
-        });
-    if (!r) r = staged(c, 2, st, [&] { gfl::launch_act(L.dptrs, ws.pv, P, ws.ygu, ws.xtd, L.I, act_limit, c->exp_tab, st); return 0; });
+    if (gfl::gate_up_lds_bytes(L.K[0], ns, L.H, P, L.E) > 163840 || gfl::gate_up_lds_bytes(L.K[1], ns, L.H, P, L.E) > 163840
+        || gfl::down_lds_bytes(L.K[2], ns, L.I) > 163840)
+        return fail(GFL_EINVAL, "gfl_moe_forward: shape needs more than 160 KB of LDS per workgroup");
+    const int wh = w_is_half ? 1 : 0;
+    int r = staged(c, 1, st, [&] {
+        if (L.K[0] == L.K[1])
+            return gfl::launch_gate_up(L.K[0], ns, L.dptrs, 0, 2, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
+                                       ws.xtd, ws.act_cnt, c->exp_tab, act_limit, ws.pv, out, st);
+        if (gfl::launch_gate_up(L.K[0], ns, L.dptrs, 0, 1, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
+                                ws.xtd, ws.act_cnt, c->exp_tab, act_limit, ws.pv, out, st))
+            return -1;
+        return gfl::launch_gate_up(L.K[1], ns, L.dptrs, 1, 1, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
+                                   ws.xtd, ws.act_cnt, c->exp_tab, act_limit, ws.pv, out, st);
+    });
     if (!r)
         r = staged(c, 3, st, [&] {
-            return gfl::launch_chain(L.K[2], ns, false, L.dptrs, 2, 1, L.I, L.H, ws.pv, topk, umax, ws.xtd, ws.yd, st);
-        });
-    if (!r)
-        r = staged(c, 4, st, [&] {
-            gfl::launch_final(L.dptrs, ws.pv, w, w_is_half ? 1 : 0, M, topk, ws.yd, out, L.H, st);
-            return 0;
+            return gfl::launch_down(L.K[2], ns, L.dptrs, topk, L.H, L.I, umax, ws.pv, ws.xtd, ws.yd, ws.out_cnt, out,
+                                    st);
         });
     if (r) return r > 0 ? r : fail(GFL_EINVAL, "gfl_moe_forward: unsupported K");
     GFL_HIP(hipGetLastError());

@@ -21,17 +21,21 @@ struct PlanView
     int* pick_job;   // [picks] reference job index (combine order)
     int* tok_slot;   // [tokens][topk] slots of each token in combine order, -1 padded
     float* tok_w;    // [tokens][topk] their routing weights (fp32)
+    int* tok_npk;    // [tokens] number of valid picks of each token
     int cap_slots;
 };
 
-void launch_plan(const int64_t* sel, const void* w, int w_half, int P, int topk, int E, const PlanView& pv,
-                 hipStream_t st);
-int launch_chain(int K, int ns, bool prep, const uint64_t* ptrs, int mat_base, int nmat, int kdim, int ndim,
-                 const PlanView& pv, int topk, int umax, const uint16_t* xin, float* yout, hipStream_t st);
-void launch_act(const uint64_t* ptrs, const PlanView& pv, int smax, const float* ygu, uint16_t* xtd, int I,
-                float limit, const float* exp_tab, hipStream_t st);
-void launch_final(const uint64_t* ptrs, const PlanView& pv, const void* w, int w_half, int M, int topk,
-                  const float* yd, float* out, int H, hipStream_t st);
+// gate|up launch: routing plan (published to pv by workgroup 0), gate and/or up GEMV, SwiGLU per 128-block by the
+// last workgroup of the block. mat_base/nmat: matrices of this launch (0,2 = both, 0,1 = gate, 1,1 = up).
+int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, const int64_t* sel, const void* w,
+                   int w_half, int P, int topk, int E, int H, int I, int umax, const uint16_t* x, float* ygu,
+                   uint16_t* xtd, int* act_cnt, const float* exp_tab, float act_limit, const PlanView& pv, float* out,
+                   hipStream_t st);
+// down launch: down GEMV + out_block, weighted combine per (token, 128-block) by the token's last expert
+int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int umax, const PlanView& pv,
+                const uint16_t* xtd, float* yd, int* out_cnt, float* out, hipStream_t st);
+size_t gate_up_lds_bytes(int K, int ns, int H, int P, int E);
+size_t down_lds_bytes(int K, int ns, int I);
 int launch_dequant(const uint8_t* tr, int k, int n, int K, uint16_t* W, hipStream_t st);
 
 int launch_split(const int64_t* sel, const uint16_t* w, const uint16_t* z, int n, int bsz, int topk, int H, int E,

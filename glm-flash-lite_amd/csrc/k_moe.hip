@@ -1,139 +1,286 @@
-// Routed-MoE decode path on gfx950: routing plan, bit-exact trellis GEMV, activation, ordered combine.
+// Routed-MoE decode path on gfx950 in two launches: gate|up (with the routing plan and the SwiGLU stage fused in)
+// and down (with the output transform and the weighted combine fused in).
 //
 // Numerics follow the reference's EXACT mode (kernels/cpu_avx2/ft_core.h:313-387, 933-1033) operation for
 // operation, so outputs are bit-identical to it:
 //   * each output column keeps the reference's four fp32 accumulators (AVX lanes j of tile_accum), each a chain of
 //     fused multiply-adds over tile rows, and inside a tile row over the four stream groups q;
 //   * the column result is (a0 + a1) + (a2 + a3);
-//   * Hadamard/rounding points are those of prep_block / out_block / act_mul.
+//   * Hadamard/rounding points are those of prep_block / out_block / act_mul;
+//   * the weighted sum runs over each token's picks in the reference's job order.
 // The chain needs the weights of one (column, accumulator) in q order, while the trellis decodes four consecutive
 // stream indices per lane (fixed q, accumulators 0..3). One MFMA 16x16x16 against a constant 0/1 permutation
 // matrix moves the decoded tile from the first layout to the second as exact fp32 values.
+//
+// Cross-workgroup steps use "last one finishes" counters instead of extra launches: a workgroup publishes its
+// outputs, then bumps a device-scope acquire-release counter; the one that completes the count runs the dependent
+// step (SwiGLU of a 128-block once gate and up of that block are in; the combine of a token's 128-block once all its
+// experts' down outputs are in) and re-arms the counter to zero for the next call. Nothing waits on anything.
 #include "gfl_device.hpp"
 #include "gfl_internal.hpp"
 
 namespace gfl {
 
 // ---------------------------------------------------------------------------------------------------------------
-// routing plan
+// routing plan, built in LDS by every workgroup in O(P + E)
 // ---------------------------------------------------------------------------------------------------------------
 
-// One block. Picks p = t*topk + k are scanned token-major, as the reference builds its jobs
-// (moe_forward, ft_core.h:1343-1349):
-//   union of experts in first-appearance order (uexp), their slots (one per pick, tokens ascending), and for every
-//   pick the index of the reference job it lands in (a new job whenever the expert's current job holds 8 tokens),
-//   which fixes the order of the weighted sum.
-// Ids outside [0, E) are skipped (tier_forward drops sel < 0, ft_tier_ext.cpp:896-898) and counted in err.
-__global__ __launch_bounds__(256) void plan_kernel(const int64_t* __restrict__ sel, const void* __restrict__ w,
-                                                   int w_half, int P, int topk, int E, PlanView pv)
+// Picks p = t*topk + k are scanned token-major, as the reference builds its jobs (moe_forward, ft_core.h:1343-1349):
+//   union of experts in first-appearance order (uexp), one slot per pick grouped by union entry with tokens
+//   ascending (uoff / spick), and the index of the reference job every pick lands in (a new job whenever the
+//   expert's current job holds 8 tokens), which fixes the order of the weighted sum.
+// Ids outside [0, E) are skipped (tier_forward drops sel < 0, ft_tier_ext.cpp:896-898) and counted in bad.
+struct LPlan
 {
-    __shared__ int s_e[MAX_PICKS], s_c[MAX_PICKS], s_first[MAX_PICKS], s_crank[MAX_PICKS];
-    __shared__ int firstpick[MAX_EXPERTS], ucnt[MAX_PICKS], uoff[MAX_PICKS + 1];
-    __shared__ int s_U, s_bad, s_job[MAX_PICKS], s_slot[MAX_PICKS];
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    for (int e = t; e < E; e += blockDim.x) firstpick[e] = 0x7fffffff;
-    if (t == 0) { s_U = 0; s_bad = 0; }
-    for (int p = t; p < P; p += blockDim.x)
+    int* e;       // [P] expert of pick p, -1 if skipped
+    int* c;       // [P] occurrence of pick p among its expert's picks (pick order)
+    int* rank;    // [P] union rank, valid at an expert's first pick
+    int* crank;   // [P] job index, valid at a job's first pick (c % 8 == 0)
+    int* spick;   // [P] pick of slot s
+    int* uoff;    // [P + 1] slot offsets of the union entries
+    int* uexp;    // [P] expert of union entry u
+    int* first;   // [E] first pick of expert e
+    int* cnt;     // [E] running per-expert count during the scan, then the slot count of union entry u
+};
+
+__host__ __device__ constexpr size_t lplan_ints(int P, int E) { return 7 * (size_t)P + 1 + 2 * (size_t)E; }
+
+__device__ inline LPlan lplan_carve(int* base, int P, int E)
+{
+    LPlan L;
+    L.e = base;
+    L.c = L.e + P;
+    L.rank = L.c + P;
+    L.crank = L.rank + P;
+    L.spick = L.crank + P;
+    L.uoff = L.spick + P;
+    L.uexp = L.uoff + P + 1;
+    L.first = L.uexp + P;
+    L.cnt = L.first + E;
+    return L;
+}
+
+// Whole workgroup. On return: hdr[0] = U, hdr[1] = slots, hdr[2] = ids outside [0, E); L filled.
+__device__ void build_plan(const int64_t* __restrict__ sel, int P, int E, const LPlan& L, int* hdr)
+{
+    const int t = threadIdx.x, nt = blockDim.x, lane = t & 63;
+    for (int e = t; e < E; e += nt) { L.first[e] = 0x7fffffff; L.cnt[e] = 0; }
+    if (t == 0) hdr[2] = 0;
+    __syncthreads();
+    for (int p = t; p < P; p += nt)
     {
         const int64_t e = sel[p];
-        s_e[p] = (e >= 0 && e < E) ? (int)e : -1;
-        if (e >= E || e < -1) atomicAdd(&s_bad, 1);
-        ucnt[p] = 0;
+        const bool ok = e >= 0 && e < E;
+        L.e[p] = ok ? (int)e : -1;
+        if (ok) atomicMin(&L.first[(int)e], p);
+        if (e >= E || e < -1) atomicAdd(&hdr[2], 1);
     }
     __syncthreads();
-    for (int p = t; p < P; p += blockDim.x)
-        if (s_e[p] >= 0) atomicMin(&firstpick[s_e[p]], p);
-    // occurrence index of each pick among the picks of its expert
-    for (int p = t; p < P; p += blockDim.x)
+    if (t < 64)
     {
-        const int e = s_e[p];
-        int c = 0;
-        if (e >= 0)
-            for (int q = 0; q < p; ++q) c += s_e[q] == e;
-        s_c[p] = c;
-    }
-    __syncthreads();
-    // wave 0: ballot prefix sums in pick order -> union rank of first picks, rank of job-creating picks
-    if (wave == 0)
-    {
+        // one wave scans the picks in order, 64 at a time: occurrence index from an equal-expert lane mask built with
+        // ten ballots (E <= 1024), union ranks and job ranks as ballot prefix sums
         int base_u = 0, base_j = 0;
+        const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
         for (int p0 = 0; p0 < P; p0 += 64)
         {
             const int p = p0 + lane;
-            const bool ok = p < P && s_e[p] >= 0;
-            const bool first = ok && s_c[p] == 0;
-            const bool creator = ok && (s_c[p] % 8) == 0;
-            const uint64_t mf = __ballot(first), mc = __ballot(creator);
-            const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-            if (first) s_first[p] = base_u + __popcll(mf & below);
-            if (creator) s_crank[p] = base_j + __popcll(mc & below);
+            const int e = p < P ? L.e[p] : -1;
+            const bool ok = e >= 0;
+            uint64_t eq = __ballot(ok);
+#pragma unroll
+            for (int b = 0; b < 10; ++b)
+            {
+                const bool bit = ok && ((e >> b) & 1);
+                const uint64_t m = __ballot(bit);
+                eq &= bit ? m : ~m;
+            }
+            const int cin = __popcll(eq & below);
+            const int base = ok ? L.cnt[e] : 0;
+            const int c = base + cin;
+            const bool firstp = ok && c == 0, creator = ok && (c & 7) == 0;
+            const uint64_t mf = __ballot(firstp), mc = __ballot(creator);
+            if (ok)
+            {
+                L.c[p] = c;
+                if (cin == 0) L.cnt[e] = base + __popcll(eq);   // lowest lane of the group advances the count
+            }
+            if (firstp)
+            {
+                const int r = base_u + __popcll(mf & below);
+                L.rank[p] = r;
+                L.uexp[r] = e;
+            }
+            if (creator) L.crank[p] = base_j + __popcll(mc & below);
             base_u += __popcll(mf);
             base_j += __popcll(mc);
         }
-        if (lane == 0) s_U = base_u;
+        if (lane == 0) hdr[0] = base_u;
     }
     __syncthreads();
-    const int U = s_U;
-    for (int p = t; p < P; p += blockDim.x)
+    const int U = hdr[0];
+    // slot counts per union entry (cnt is indexed by expert until here; U <= E entries are rewritten in place only
+    // after every thread has read its expert's count; U <= P <= 1024 <= 4 * blockDim.x)
+    int mine[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
     {
-        const int e = s_e[p];
+        const int u = t + i * nt;
+        mine[i] = u < U ? L.cnt[L.uexp[u]] : 0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        const int u = t + i * nt;
+        if (u < U) L.cnt[u] = mine[i];
+    }
+    __syncthreads();
+    if (t < 64)
+    {
+        int carry = 0;
+        for (int u0 = 0; u0 < U; u0 += 64)
+        {
+            const int u = u0 + lane;
+            const int v = u < U ? L.cnt[u] : 0;
+            int s = v;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1)
+            {
+                const int o = __shfl_up(s, d);
+                if (lane >= d) s += o;
+            }
+            if (u < U) L.uoff[u] = carry + s - v;
+            carry += __shfl(s, 63);
+        }
+        if (lane == 0) { L.uoff[U] = carry; hdr[1] = carry; }
+    }
+    __syncthreads();
+    for (int p = t; p < P; p += nt)
+    {
+        const int e = L.e[p];
         if (e < 0) continue;
-        const int u = s_first[firstpick[e]];
-        if (s_c[p] == 0) pv.uexp[u] = e;
-        atomicAdd(&ucnt[u], 1);
+        L.spick[L.uoff[L.rank[L.first[e]]] + L.c[p]] = p;
     }
     __syncthreads();
-    if (t == 0)
+}
+
+// The same plan for P <= 64 picks from one wave, without LDS atomics or intermediate barriers (the decode case):
+// lane p holds pick p; all derived quantities are ballot/prefix arithmetic over the wave. first[] is written only for
+// the experts present (the only entries read).
+__device__ void build_plan_wave(const int64_t* __restrict__ sel, int P, int E, const LPlan& L, int* hdr)
+{
+    const int lane = threadIdx.x & 63;
+    if (threadIdx.x < 64)
     {
-        int acc = 0;
-        for (int u = 0; u < U; ++u) { uoff[u] = acc; acc += ucnt[u]; }
-        uoff[U] = acc;
-        pv.hdr[0] = U;
-        pv.hdr[1] = acc;
-        pv.hdr[2] = s_bad;
+        const int64_t e64 = lane < P ? sel[lane] : -1;
+        const bool ok = e64 >= 0 && e64 < E;
+        const int e = ok ? (int)e64 : -1;
+        const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+        const uint64_t bad = __ballot(lane < P && (e64 >= E || e64 < -1));
+        uint64_t eq = __ballot(ok);
+#pragma unroll
+        for (int b = 0; b < 10; ++b)
+        {
+            const bool bit = ok && ((e >> b) & 1);
+            const uint64_t m = __ballot(bit);
+            eq &= bit ? m : ~m;
+        }
+        const int c = __popcll(eq & below);
+        const bool firstp = ok && c == 0, creator = ok && (c & 7) == 0;
+        const uint64_t mf = __ballot(firstp), mc = __ballot(creator);
+        const int r = __popcll(mf & below);
+        // slot offsets: exclusive prefix of the union entries' pick counts, in first-appearance (= lane) order
+        const int v = firstp ? __popcll(eq) : 0;
+        int sc = v;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1)
+        {
+            const int o = __shfl_up(sc, d);
+            if (lane >= d) sc += o;
+        }
+        const int uo = sc - v;
+        const int fl = ok ? __builtin_ctzll(eq) : 0;      // lane of the expert's first pick
+        const int uo_p = __shfl(uo, fl);
+        if (lane < P) L.e[lane] = e;
+        if (ok)
+        {
+            L.c[lane] = c;
+            L.spick[uo_p + c] = lane;
+        }
+        if (firstp)
+        {
+            L.rank[lane] = r;
+            L.uexp[r] = e;
+            L.uoff[r] = uo;
+            L.first[e] = lane;
+        }
+        if (creator) L.crank[lane] = __popcll(mc & below);
+        const int U = __popcll(mf), S = __shfl(sc, 63);
+        if (lane == 0)
+        {
+            L.uoff[U] = S;
+            hdr[0] = U;
+            hdr[1] = S;
+            hdr[2] = __popcll(bad);
+        }
     }
     __syncthreads();
-    for (int u = t; u <= U; u += blockDim.x) pv.uoff[u] = uoff[u];
-    for (int p = t; p < P; p += blockDim.x)
+}
+
+// union entry of pick p's expert and its job index (the job's first pick is the slot 8*floor(c/8) of the entry)
+__device__ inline int plan_u(const LPlan& L, int p) { return L.rank[L.first[L.e[p]]]; }
+__device__ inline int plan_job(const LPlan& L, int p)
+{
+    return L.crank[L.spick[L.uoff[plan_u(L, p)] + (L.c[p] & ~7)]];
+}
+
+// Publish the plan for the down launch (one workgroup): PlanView arrays plus each token's picks in (job, pick) order
+// with their fp32 weights; rows of tokens without a valid pick are written as zeros here (no down workgroup touches
+// them; the reference's sum over an empty route is 0).
+__device__ void publish_plan(const LPlan& L, const int* hdr, int P, int topk, const void* w, int w_half,
+                             const PlanView& pv, float* out, int H)
+{
+    const int t = threadIdx.x, nt = blockDim.x;
+    const int U = hdr[0], S = hdr[1];
+    if (t < 3) pv.hdr[t] = hdr[t];
+    for (int u = t; u < U; u += nt) pv.uexp[u] = L.uexp[u];
+    for (int u = t; u <= U; u += nt) pv.uoff[u] = L.uoff[u];
+    for (int s = t; s < S; s += nt) pv.slot_pick[s] = L.spick[s];
+    for (int p = t; p < P; p += nt)
     {
-        const int e = s_e[p];
-        if (e < 0) { pv.pick_slot[p] = -1; pv.pick_job[p] = 0x7fffffff; continue; }
-        const int u = s_first[firstpick[e]];
-        const int slot = uoff[u] + s_c[p];
-        pv.pick_slot[p] = slot;
-        pv.slot_pick[slot] = p;
-        pv.slot_u[slot] = u;
-        // the job holding this pick was created by the pick of the same expert with occurrence 8*floor(c/8)
-        const int want = (s_c[p] / 8) * 8;
-        int creator = p;
-        for (int q = 0; q <= p; ++q)
-            if (s_e[q] == e && s_c[q] == want) { creator = q; break; }
-        pv.pick_job[p] = s_crank[creator];
-        s_job[p] = s_crank[creator];
-        s_slot[p] = slot;
+        if (L.e[p] < 0) { pv.pick_slot[p] = -1; pv.pick_job[p] = 0x7fffffff; continue; }
+        const int u = plan_u(L, p), s = L.uoff[u] + L.c[p];
+        pv.pick_slot[p] = s;
+        pv.slot_u[s] = u;
+        pv.pick_job[p] = plan_job(L, p);
     }
-    __syncthreads();
-    // per token: its picks in (job, pick) order -> the order of the weighted sum (ft_core.h:1020-1033)
-    for (int t0 = t; t0 * topk < P; t0 += blockDim.x)
+    const int M = P / topk;
+    for (int tk = t; tk < M; tk += nt)
     {
-        int ord[MAX_TOPK];
-        int cnt = 0;
+        int ord[MAX_TOPK], job[MAX_TOPK];
+        int n = 0;
         for (int k = 0; k < topk; ++k)
         {
-            const int p = t0 * topk + k;
-            if (s_e[p] < 0) continue;
-            int b = cnt++;
-            while (b > 0 && s_job[ord[b - 1]] > s_job[p]) { ord[b] = ord[b - 1]; --b; }
+            const int p = tk * topk + k;
+            if (L.e[p] < 0) continue;
+            const int jb = plan_job(L, p);
+            int b = n++;
+            while (b > 0 && job[b - 1] > jb) { ord[b] = ord[b - 1]; job[b] = job[b - 1]; --b; }
             ord[b] = p;
+            job[b] = jb;
         }
         for (int k = 0; k < topk; ++k)
         {
-            const int p = k < cnt ? ord[k] : -1;
-            pv.tok_slot[t0 * topk + k] = p >= 0 ? s_slot[p] : -1;
-            pv.tok_w[t0 * topk + k] = p < 0 ? 0.f
-                                   : (w_half ? h2f_bits(reinterpret_cast<const uint16_t*>(w)[p])
-                                             : reinterpret_cast<const float*>(w)[p]);
+            const int p = k < n ? ord[k] : -1;
+            pv.tok_slot[tk * topk + k] = p >= 0 ? L.uoff[plan_u(L, p)] + L.c[p] : -1;
+            pv.tok_w[tk * topk + k] = p < 0 ? 0.f
+                                    : (w_half ? h2f_bits(reinterpret_cast<const uint16_t*>(w)[p])
+                                              : reinterpret_cast<const float*>(w)[p]);
         }
+        pv.tok_npk[tk] = n;
+        if (n == 0)
+            for (int i = 0; i < H; ++i) out[(size_t)tk * H + i] = 0.f;
     }
 }
 
@@ -150,18 +297,6 @@ __device__ inline int perm_pos(int b, int r)
     return (tk * 4 + j) * 4 + q;
 }
 
-// One workgroup = NW waves = NW adjacent tile columns (16*NW outputs) of one matrix of one routed expert, all tile
-// rows, for up to NS of the expert's slots at a time. Each wave owns one tile column; lane (j = l/16, n = l%16)
-// carries the reference's accumulator j of output column n for every slot.
-// Trellis bytes are streamed in batches of BR tile rows: each thread issues coalesced 16-byte loads into a ring of
-// NRING register batches (so NRING batches are in flight), the batch is written to one of two LDS buffers and the
-// waves decode their tile column from there.
-//   PREP = true : gate/up; the WG builds xt = prep_block(x_token, suh) for its slots in LDS
-//   PREP = false: down; xt (already transformed and permuted) is copied from xin
-//   OUTB = true : apply out_block (ft_core.h:1016) to each 128-output block and write final expert outputs
-//                 (needs NW = 8)
-constexpr int BR = 16;      // tile rows per batch
-
 // Workgroup barrier that only orders LDS traffic: wait for this wave's LDS operations, then s_barrier. Unlike
 // __syncthreads it carries no release fence, so outstanding global loads of the prefetch ring stay in flight.
 __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
@@ -174,6 +309,8 @@ __device__ __forceinline__ u32x4 gload16(const uint8_t* p)
     typedef const __attribute__((address_space(1))) u32x4 gu32x4;
     return *(gu32x4*)(p);
 }
+
+constexpr int BR = 16;      // tile rows per batch
 constexpr int NRING = 4;    // batches in flight per workgroup
 
 template <int K, int NW>
@@ -187,37 +324,24 @@ struct Stage
     static constexpr int BBP = CPT * NW * 64 * 16;      // staged bytes per batch incl. the pad the surplus chunks fill
 };
 
-template <int K, int NS, bool PREP, int NW, bool OUTB>
-__global__ __launch_bounds__(NW * 64) void chain_gemv_kernel(const uint64_t* __restrict__ ptrs, int mat_base,
-                                                             int kdim, int ndim, PlanView pv, int topk,
-                                                             const uint16_t* __restrict__ xin,
-                                                             float* __restrict__ yout)
+// One pass of NW adjacent tile columns over all TK tile rows for up to NS slots whose transformed inputs sit in
+// lds_x ([NS][kdim] fp16 in the permuted [tk][j][q] order). Each wave owns one tile column; lane (j = l/16, n = l%16)
+// carries the reference's accumulator j of output column n. Trellis bytes stream in batches of BR tile rows: every
+// thread issues coalesced 16-byte loads into a ring of NRING register batches, a batch is written to one of two LDS
+// buffers and the waves decode their tile column from there. res[s] = the column results (valid in lanes 0..15).
+template <int K, int NS, int NW>
+__device__ __forceinline__ void chain_pass(const uint8_t* __restrict__ gbase, size_t gstride, int TK, int ns,
+                                           uint8_t* stage_buf, const uint16_t* lds_x, float (&res)[NS])
 {
     using St = Stage<K, NW>;
-    extern __shared__ __align__(16) uint8_t lds_raw[];
-    uint8_t* stage_buf = lds_raw;                                     // [2][BBP]
-    uint16_t* lds_x = reinterpret_cast<uint16_t*>(lds_raw + 2 * St::BBP);  // [NS][kdim] fp16, permuted [tk][j][q]
-    float* lds_y = reinterpret_cast<float*>(lds_raw + 2 * St::BBP + (size_t)NS * kdim * 2);  // [NS][128] (OUTB)
-    const int TN = ndim / 16, TK = kdim / 16, ncb = TN / NW;
-    const int u = blockIdx.x / ncb, cb = blockIdx.x % ncb;
-    if (u >= pv.hdr[0]) return;
-    const int mat = mat_base + blockIdx.y;                 // 0 gate, 1 up, 2 down
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int e = pv.uexp[u];
-    const uint8_t* tr = reinterpret_cast<const uint8_t*>(ptrs[(size_t)e * 9 + mat]);
-    const uint16_t* suh = reinterpret_cast<const uint16_t*>(ptrs[(size_t)e * 9 + 3 + 2 * mat]);
-    const uint16_t* svh = reinterpret_cast<const uint16_t*>(ptrs[(size_t)e * 9 + 4 + 2 * mat]);
-    const int s_begin = pv.uoff[u], s_end = pv.uoff[u + 1];
     const LaneDec d = lane_dec(lane, K);
     const int j = lane >> 4, n = lane & 15;
     half4 Pm;
 #pragma unroll
     for (int r = 0; r < 4; ++r) Pm[r] = (_Float16)((j == (n & 3) && r == (n >> 2)) ? 1.0f : 0.0f);
     const float4v zero = { 0.f, 0.f, 0.f, 0.f };
-    const size_t gstride = (size_t)TN * St::TB;            // global bytes between tile rows
-    const uint8_t* gbase = tr + (size_t)cb * St::RB;        // tile row 0 of this workgroup's slice
     const int nb = (TK + BR - 1) / BR;
-    float* ybase = yout + (size_t)blockIdx.y * (size_t)pv.cap_slots * ndim;
 
     // chunk c of batch b: tile row b*BR + c/(RB/16), byte (c % (RB/16))*16 of the slice; batches past the end reload
     // the last tile row (in bounds, never consumed) so the ring has no branches
@@ -258,7 +382,7 @@ __global__ __launch_bounds__(NW * 64) void chain_gemv_kernel(const uint64_t* __r
                                                                     0, 0, 0);                                    \
                 _Pragma("unroll") for (int s_ = 0; s_ < NS; ++s_)                                                \
                 {                                                                                                \
-                    if (s_ < ns)                                                                                 \
+                    if (s_ == 0 || s_ < ns)     /* a pass always has slot 0 */                                   \
                     {                                                                                            \
                         float a_ = acc[s_];                                                                      \
                         _Pragma("unroll") for (int r_ = 0; r_ < 4; ++r_)                                         \
@@ -277,129 +401,305 @@ __global__ __launch_bounds__(NW * 64) void chain_gemv_kernel(const uint64_t* __r
         }                                                                                                        \
     }
 
-    for (int c0 = s_begin; c0 < s_end; c0 += NS)
-    {
-        const int ns = min(NS, s_end - c0);
-        // prefetch ring: four named register batches in flight
-        u32x4 ring0[St::CPT], ring1[St::CPT], ring2[St::CPT], ring3[St::CPT];
-        static_assert(NRING == 4, "ring of four batches");
-        GFL_LOAD_BATCH(0, ring0)
-        GFL_LOAD_BATCH(1, ring1)
-        GFL_LOAD_BATCH(2, ring2)
-        GFL_LOAD_BATCH(3, ring3)
-        lds_barrier();   // previous pass done with lds_x / lds_y
-        if (PREP)
-        {
-            const int nblk = kdim / 128;
-            for (int it = wave; it < ns * nblk; it += NW)
-            {
-                const int s = it / nblk, b = it % nblk;
-                const int tok = pv.slot_pick[c0 + s] / topk;
-                const uint16_t* xr = xin + (size_t)tok * kdim + b * 128;
-                float v0 = h2f_bits(xr[lane]), v1 = h2f_bits(xr[lane + 64]);
-                prep_block_wave(v0, v1, h2f_bits(suh[b * 128 + lane]), h2f_bits(suh[b * 128 + lane + 64]));
-                uint16_t* dst = lds_x + (size_t)s * kdim;
-                dst[perm_pos(b, lane)] = (uint16_t)f2h_bits(v0);
-                dst[perm_pos(b, lane + 64)] = (uint16_t)f2h_bits(v1);
-            }
-        }
-        else
-        {
-            const int nvec = ns * kdim / 8;
-            const uint4* src = reinterpret_cast<const uint4*>(xin + (size_t)c0 * kdim);
-            uint4* dst = reinterpret_cast<uint4*>(lds_x);
-            for (int i = threadIdx.x; i < nvec; i += blockDim.x) dst[i] = src[i];
-        }
-
-        float acc[NS];
+    // prefetch ring: four named register batches in flight
+    u32x4 ring0[St::CPT], ring1[St::CPT], ring2[St::CPT], ring3[St::CPT];
+    static_assert(NRING == 4, "ring of four batches");
+    GFL_LOAD_BATCH(0, ring0)
+    GFL_LOAD_BATCH(1, ring1)
+    GFL_LOAD_BATCH(2, ring2)
+    GFL_LOAD_BATCH(3, ring3)
+    float acc[NS];
 #pragma unroll
-        for (int s = 0; s < NS; ++s) acc[s] = 0.f;
-        const uint8_t* wl = stage_buf + wave * St::TB;      // this wave's tile inside a staged row slice
-        const uint16_t* xl = lds_x + j * 4;
-        for (int b0 = 0; b0 < nb; b0 += NRING)
-        {
-            GFL_STEP(b0, ring0)
-            GFL_STEP(b0 + 1, ring1)
-            GFL_STEP(b0 + 2, ring2)
-            GFL_STEP(b0 + 3, ring3)
-        }
+    for (int s = 0; s < NS; ++s) acc[s] = 0.f;
+    const uint8_t* wl = stage_buf + wave * St::TB;      // this wave's tile inside a staged row slice
+    const uint16_t* xl = lds_x + j * 4;
+    lds_barrier();                                      // lds_x written by the caller
+    for (int b0 = 0; b0 < nb; b0 += NRING)
+    {
+        GFL_STEP(b0, ring0)
+        GFL_STEP(b0 + 1, ring1)
+        GFL_STEP(b0 + 2, ring2)
+        GFL_STEP(b0 + 3, ring3)
+    }
 #undef GFL_STEP
 #undef GFL_STORE_BATCH
 #undef GFL_LOAD_BATCH
-        const int t = cb * NW + wave;                          // this wave's tile column
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+    {
+        const float a1 = __shfl(acc[s], n + 16), a2 = __shfl(acc[s], n + 32), a3 = __shfl(acc[s], n + 48);
+        res[s] = (acc[s] + a1) + (a2 + a3);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// gate|up launch
+// ---------------------------------------------------------------------------------------------------------------
+
+constexpr int GU_NW = 4;    // waves (tile columns) per gate|up workgroup: 64 outputs
+constexpr int DN_NW = 8;    // waves per down workgroup: one 128-output block, out_block fused
+
+struct GuArgs
+{
+    const uint64_t* ptrs;      // [E][9] layer table
+    const int64_t* sel;
+    const void* w;
+    int w_half, P, topk, E, H, I;
+    int mat_base;              // matrix of blockIdx.y == 0 (0 gate, 1 up)
+    const uint16_t* x;         // [M][H] fp16
+    float* ygu;                // [2][cap][I]
+    uint16_t* xtd;             // [cap][I] down input, permuted
+    int* act_cnt;              // [cap][I/128] last-one counters (zero between calls)
+    const float* exp_tab;
+    float act_limit;
+    PlanView pv;               // written by workgroup (0, 0)
+    float* out;                // [M][H] (rows of tokens without picks zeroed here)
+    int nmat_total;            // gate|up workgroups covering one 128-block
+    int ns_cap;                // slots per pass the LDS allocation holds (<= NS)
+};
+
+__device__ __forceinline__ float ld_agent(const float* p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(float* p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// fwd_phase phase 1 for one 128-block b of union entry u (ft_core.h:974-991): out_block of gate and up,
+// r16(act_mul), down prep_block, stored permuted as the down GEMV input
+__device__ void act_block(const GuArgs& a, int e, int s_begin, int s_end, int b)
+{
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+    const uint16_t* svh_g = reinterpret_cast<const uint16_t*>(a.ptrs[(size_t)e * 9 + 4]);
+    const uint16_t* svh_u = reinterpret_cast<const uint16_t*>(a.ptrs[(size_t)e * 9 + 6]);
+    const uint16_t* suh_d = reinterpret_cast<const uint16_t*>(a.ptrs[(size_t)e * 9 + 7]);
+    const int cap = a.pv.cap_slots;
+    for (int s = s_begin + wave; s < s_end; s += nw)
+    {
+        const float* yg = a.ygu + (size_t)s * a.I + b * 128;
+        const float* yu = a.ygu + (size_t)cap * a.I + (size_t)s * a.I + b * 128;
+        float g0 = ld_agent(&yg[lane]), g1 = ld_agent(&yg[lane + 64]);
+        float u0 = ld_agent(&yu[lane]), u1 = ld_agent(&yu[lane + 64]);
+        out_block_wave(g0, g1, h2f_bits(svh_g[b * 128 + lane]), h2f_bits(svh_g[b * 128 + lane + 64]));
+        out_block_wave(u0, u1, h2f_bits(svh_u[b * 128 + lane]), h2f_bits(svh_u[b * 128 + lane + 64]));
+        float a0 = r16(act_mul(g0, u0, a.act_limit, a.exp_tab)), a1 = r16(act_mul(g1, u1, a.act_limit, a.exp_tab));
+        prep_block_wave(a0, a1, h2f_bits(suh_d[b * 128 + lane]), h2f_bits(suh_d[b * 128 + lane + 64]));
+        uint16_t* dst = a.xtd + (size_t)s * a.I;
+        dst[perm_pos(b, lane)] = (uint16_t)f2h_bits(a0);
+        dst[perm_pos(b, lane + 64)] = (uint16_t)f2h_bits(a1);
+    }
+}
+
+// Grid: (umax * I/64 + 1, nmat). Workgroup = 4 waves = 64 outputs of one matrix of one routed expert, all its
+// slots; the last workgroup of row 0 publishes the plan.
+template <int K, int NS>
+__global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(K == 5 ? 3 : 4))) void gu_kernel(GuArgs a)
+{
+    constexpr int NW = GU_NW;
+    using St = Stage<K, NW>;
+    extern __shared__ __align__(16) uint8_t lds_raw[];
+    __shared__ int hdr[4];
+    __shared__ int s_last;
+    uint8_t* stage_buf = lds_raw;                                                    // [2][BBP]
+    uint16_t* lds_x = reinterpret_cast<uint16_t*>(lds_raw + 2 * St::BBP);           // [ns_cap][H] fp16 permuted
+    int* plan_mem = reinterpret_cast<int*>(lds_raw + 2 * St::BBP + (size_t)a.ns_cap * a.H * 2);
+    const LPlan L = lplan_carve(plan_mem, a.P, a.E);
+    if (a.P <= 64) build_plan_wave(a.sel, a.P, a.E, L, hdr);
+    else build_plan(a.sel, a.P, a.E, L, hdr);
+    const int TN = a.I / 16, TK = a.H / 16, ncb = TN / NW;
+    if (blockIdx.x == gridDim.x - 1)
+    {
+        // the grid's extra workgroup publishes the plan for the down launch (no GEMV work of its own)
+        if (blockIdx.y == 0) publish_plan(L, hdr, a.P, a.topk, a.w, a.w_half, a.pv, a.out, a.H);
+        return;
+    }
+
+    const int u = blockIdx.x / ncb, cb = blockIdx.x % ncb;
+    if (u >= hdr[0]) return;
+    const int mat = a.mat_base + blockIdx.y;              // 0 gate, 1 up
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15;
+    const int e = L.uexp[u];
+    const uint8_t* tr = reinterpret_cast<const uint8_t*>(a.ptrs[(size_t)e * 9 + mat]);
+    const uint16_t* suh = reinterpret_cast<const uint16_t*>(a.ptrs[(size_t)e * 9 + 3 + 2 * mat]);
+    const int s_begin = L.uoff[u], s_end = L.uoff[u + 1];
+    const size_t gstride = (size_t)TN * St::TB;
+    const uint8_t* gbase = tr + (size_t)cb * St::RB;
+    float* ybase = a.ygu + (size_t)mat * a.pv.cap_slots * a.I;
+    const int t = cb * NW + wave;                         // this wave's tile column
+
+    const int nsp = NS == 1 ? 1 : max(1, min(NS, a.ns_cap));
+    for (int c0 = s_begin; c0 < s_end; c0 += nsp)
+    {
+        const int ns = NS == 1 ? 1 : min(nsp, s_end - c0);   // >= 1 (c0 < s_end)
+        lds_barrier();   // previous pass done with lds_x
+        // input transform of the pass's tokens into LDS (prep_block, ft_core.h:97-102)
+        const int nblk = a.H / 128;
+        for (int it = wave; it < ns * nblk; it += NW)
+        {
+            const int s = it / nblk, b = it % nblk;
+            const int tok = L.spick[c0 + s] / a.topk;
+            const uint16_t* xr = a.x + (size_t)tok * a.H + b * 128;
+            float v0 = h2f_bits(xr[lane]), v1 = h2f_bits(xr[lane + 64]);
+            prep_block_wave(v0, v1, h2f_bits(suh[b * 128 + lane]), h2f_bits(suh[b * 128 + lane + 64]));
+            uint16_t* dst = lds_x + (size_t)s * a.H;
+            dst[perm_pos(b, lane)] = (uint16_t)f2h_bits(v0);
+            dst[perm_pos(b, lane + 64)] = (uint16_t)f2h_bits(v1);
+        }
+        float res[NS];
+        chain_pass<K, NS, NW>(gbase, gstride, TK, ns, stage_buf, lds_x, res);
 #pragma unroll
         for (int s = 0; s < NS; ++s)
-        {
-            const float a1 = __shfl(acc[s], n + 16), a2 = __shfl(acc[s], n + 32), a3 = __shfl(acc[s], n + 48);
-            const float y = (acc[s] + a1) + (a2 + a3);
             if (s < ns && lane < 16)
-            {
-                if (OUTB) lds_y[s * 128 + wave * 16 + n] = y;
-                else ybase[(size_t)(c0 + s) * ndim + t * 16 + n] = y;
-            }
-        }
-        if (OUTB)
-        {
-            __syncthreads();
-            const int blk = cb;                                // NW == 8: one 128-output block per workgroup
-            for (int s = wave; s < ns; s += NW)
-            {
-                float v0 = lds_y[s * 128 + lane], v1 = lds_y[s * 128 + lane + 64];
-                out_block_wave(v0, v1, h2f_bits(svh[blk * 128 + lane]), h2f_bits(svh[blk * 128 + lane + 64]));
-                ybase[(size_t)(c0 + s) * ndim + blk * 128 + lane] = v0;
-                ybase[(size_t)(c0 + s) * ndim + blk * 128 + lane + 64] = v1;
-            }
-        }
+                __hip_atomic_store(&ybase[(size_t)(c0 + s) * a.I + t * 16 + n], res[s], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
     }
-}
-
-// ---------------------------------------------------------------------------------------------------------------
-// gate|up -> out_block -> act -> down-input prep (fwd_phase phase 1, ft_core.h:974-991)
-// ---------------------------------------------------------------------------------------------------------------
-
-__global__ __launch_bounds__(256) void act_kernel(const uint64_t* __restrict__ ptrs, PlanView pv,
-                                                  const float* __restrict__ ygu, uint16_t* __restrict__ xtd, int I,
-                                                  float limit, const float* __restrict__ exp_tab)
-{
-    const int nb = I / 128;
-    const int item = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int s = item / nb, ib = item % nb;
-    if (s >= pv.hdr[1]) return;
-    const int e = pv.uexp[pv.slot_u[s]];
-    const uint16_t* svh_g = reinterpret_cast<const uint16_t*>(ptrs[(size_t)e * 9 + 4]);
-    const uint16_t* svh_u = reinterpret_cast<const uint16_t*>(ptrs[(size_t)e * 9 + 6]);
-    const uint16_t* suh_d = reinterpret_cast<const uint16_t*>(ptrs[(size_t)e * 9 + 7]);
-    const float* yg = ygu + (size_t)s * I + ib * 128;
-    const float* yu = ygu + (size_t)pv.cap_slots * I + (size_t)s * I + ib * 128;
-    float g0 = yg[lane], g1 = yg[lane + 64], u0 = yu[lane], u1 = yu[lane + 64];
-    out_block_wave(g0, g1, h2f_bits(svh_g[ib * 128 + lane]), h2f_bits(svh_g[ib * 128 + lane + 64]));
-    out_block_wave(u0, u1, h2f_bits(svh_u[ib * 128 + lane]), h2f_bits(svh_u[ib * 128 + lane + 64]));
-    float a0 = r16(act_mul(g0, u0, limit, exp_tab)), a1 = r16(act_mul(g1, u1, limit, exp_tab));
-    prep_block_wave(a0, a1, h2f_bits(suh_d[ib * 128 + lane]), h2f_bits(suh_d[ib * 128 + lane + 64]));
-    uint16_t* dst = xtd + (size_t)s * I;
-    dst[perm_pos(ib, lane)] = (uint16_t)f2h_bits(a0);
-    dst[perm_pos(ib, lane + 64)] = (uint16_t)f2h_bits(a1);
-}
-
-// ---------------------------------------------------------------------------------------------------------------
-// down out_block + weighted sum in job order (fwd_phase phases 2-3, ft_core.h:1014-1033)
-// ---------------------------------------------------------------------------------------------------------------
-
-__global__ __launch_bounds__(256) void final_kernel(PlanView pv, int M, int topk, const float* __restrict__ yd,
-                                                    float* __restrict__ out, int H)
-{
-    // one thread per output element: o = 0, then += w * y over the token's picks in (job, pick) order
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= M * H) return;
-    const int tkn = idx / H, col = idx % H;
-    float o = 0.f;
-    for (int k = 0; k < topk; ++k)
+    // the last of the workgroups covering this 128-block (its gate and up halves) runs the SwiGLU stage for it.
+    // Outputs went out as agent-scope stores (written through to the device-coherent level, not held in this XCD's
+    // L2); the barrier's wait for outstanding stores orders them before the counter update, and the finisher reads
+    // them back with agent-scope loads. No L2 write-back or invalidate is needed.
+    __syncthreads();
+    const int blk = (cb * NW * 16) / 128;
+    if (threadIdx.x == 0)
     {
-        const int s = pv.tok_slot[tkn * topk + k];
-        if (s < 0) break;
-        o = o + pv.tok_w[tkn * topk + k] * yd[(size_t)s * H + col];
+        int* ctr = a.act_cnt + (size_t)u * (a.I / 128) + blk;
+        const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = old == a.nmat_total - 1;
+        if (s_last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    out[idx] = o;
+    __syncthreads();
+    if (s_last) act_block(a, e, s_begin, s_end, blk);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// down launch
+// ---------------------------------------------------------------------------------------------------------------
+
+struct DnArgs
+{
+    const uint64_t* ptrs;
+    int topk, H, I;
+    PlanView pv;
+    const uint16_t* xtd;       // [cap][I]
+    float* yd;                 // [cap][H] expert outputs after out_block
+    int* out_cnt;              // [tokens][H/128] last-one counters (zero between calls)
+    float* out;                // [M][H]
+    int ns_cap;                // slots per pass the LDS allocation holds (<= NS)
+};
+
+// Grid: umax * H/128. Workgroup = 8 waves = one 128-output block of one routed expert, all its slots.
+template <int K, int NS>
+__global__ __launch_bounds__(DN_NW * 64) __attribute__((amdgpu_waves_per_eu(K == 5 || NS == 8 ? 3 : 4))) void down_kernel(DnArgs a)
+{
+    constexpr int NW = DN_NW;
+    using St = Stage<K, NW>;
+    extern __shared__ __align__(16) uint8_t lds_raw[];
+    __shared__ int s_last[NS];
+    __shared__ int c_tok[NS], c_npk[NS], c_slot[NS][MAX_TOPK];
+    __shared__ float c_w[NS][MAX_TOPK];
+    uint8_t* stage_buf = lds_raw;
+    uint16_t* lds_x = reinterpret_cast<uint16_t*>(lds_raw + 2 * St::BBP);            // [ns_cap][I]
+    float* lds_y = reinterpret_cast<float*>(lds_raw + 2 * St::BBP + (size_t)a.ns_cap * a.I * 2);   // [ns_cap][128]
+    const int TN = a.H / 16, TK = a.I / 16, ncb = TN / NW;
+    const int u = blockIdx.x / ncb, blk = blockIdx.x % ncb;
+    if (u >= a.pv.hdr[0]) return;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15;
+    const int e = a.pv.uexp[u];
+    const uint8_t* tr = reinterpret_cast<const uint8_t*>(a.ptrs[(size_t)e * 9 + 2]);
+    const uint16_t* svh = reinterpret_cast<const uint16_t*>(a.ptrs[(size_t)e * 9 + 8]);
+    const int s_begin = a.pv.uoff[u], s_end = a.pv.uoff[u + 1];
+    const size_t gstride = (size_t)TN * St::TB;
+    const uint8_t* gbase = tr + (size_t)blk * St::RB;
+    const int nbh = a.H / 128;
+
+    const int nsp = NS == 1 ? 1 : max(1, min(NS, a.ns_cap));
+    for (int c0 = s_begin; c0 < s_end; c0 += nsp)
+    {
+        const int ns = NS == 1 ? 1 : min(nsp, s_end - c0);   // >= 1 (c0 < s_end)
+        lds_barrier();   // previous pass done with lds_x / lds_y
+        {
+            const int nvec = ns * a.I / 8;
+            const uint4* src = reinterpret_cast<const uint4*>(a.xtd + (size_t)c0 * a.I);
+            uint4* dst = reinterpret_cast<uint4*>(lds_x);
+            for (int i = threadIdx.x; i < nvec; i += blockDim.x) dst[i] = src[i];
+        }
+        // the pass tokens' combine lists (slots in job order and weights): loads issued before the GEMV, written to
+        // LDS after it (thread i < ns * topk holds entry i)
+        const int ci = threadIdx.x, cs = ci / a.topk, ck = ci % a.topk;
+        int q_tok = 0, q_slot = -1, q_npk = 0;
+        float q_w = 0.f;
+        if (ci < ns * a.topk)
+        {
+            q_tok = a.pv.slot_pick[c0 + cs] / a.topk;
+            q_slot = a.pv.tok_slot[q_tok * a.topk + ck];
+            q_w = a.pv.tok_w[q_tok * a.topk + ck];
+            q_npk = a.pv.tok_npk[q_tok];
+        }
+        float res[NS];
+        chain_pass<K, NS, NW>(gbase, gstride, TK, ns, stage_buf, lds_x, res);
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+            if (s < ns && lane < 16) lds_y[s * 128 + wave * 16 + n] = res[s];
+        if (ci < ns * a.topk)
+        {
+            c_slot[cs][ck] = q_slot;
+            c_w[cs][ck] = q_w;
+            if (ck == 0) { c_tok[cs] = q_tok; c_npk[cs] = q_npk; }
+        }
+        __syncthreads();
+        // out_block (ft_core.h:1016) of the pass's 128-blocks, published as the experts' outputs
+        for (int s = wave; s < ns; s += NW)
+        {
+            float v0 = lds_y[s * 128 + lane], v1 = lds_y[s * 128 + lane + 64];
+            out_block_wave(v0, v1, h2f_bits(svh[blk * 128 + lane]), h2f_bits(svh[blk * 128 + lane + 64]));
+            st_agent(&a.yd[(size_t)(c0 + s) * a.H + blk * 128 + lane], v0);
+            st_agent(&a.yd[(size_t)(c0 + s) * a.H + blk * 128 + lane + 64], v1);
+        }
+        __syncthreads();
+        // count this block of every pass token in (agent-scope stores above, ordered by the barrier's store wait);
+        // the token's last expert sums the block in job order
+        if (threadIdx.x < ns)
+        {
+            const int s = threadIdx.x;
+            const int tok = c_tok[s], npk = c_npk[s];
+            int* ctr = a.out_cnt + (size_t)tok * nbh + blk;
+            const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last[s] = old == npk - 1 ? tok : -1;
+            if (old == npk - 1) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        for (int s = wave; s < ns; s += NW)
+        {
+            const int tok = s_last[s];
+            if (tok < 0) continue;
+            // weighted sum in (job, pick) order (ft_core.h:1020-1033): o = 0, then o += w * y; four experts' blocks
+            // are loaded at a time (independent loads), then added in order
+            const int npk = c_npk[s];
+            float o0 = 0.f, o1 = 0.f;
+            for (int k0 = 0; k0 < npk; k0 += 4)
+            {
+                float y0[4], y1[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (k0 + i < npk)
+                    {
+                        const float* y = a.yd + (size_t)c_slot[s][k0 + i] * a.H + blk * 128;
+                        y0[i] = ld_agent(&y[lane]);
+                        y1[i] = ld_agent(&y[lane + 64]);
+                    }
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (k0 + i < npk)
+                    {
+                        o0 = o0 + c_w[s][k0 + i] * y0[i];
+                        o1 = o1 + c_w[s][k0 + i] * y1[i];
+                    }
+            }
+            a.out[(size_t)tok * a.H + blk * 128 + lane] = o0;
+            a.out[(size_t)tok * a.H + blk * 128 + lane + 64] = o1;
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -432,73 +732,115 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
 // launchers
 // ---------------------------------------------------------------------------------------------------------------
 
-void launch_plan(const int64_t* sel, const void* w, int w_half, int P, int topk, int E, const PlanView& pv,
-                 hipStream_t st)
+template <typename F>
+static void open_lds(F kern, size_t lds, int& lds_set)
 {
-    hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(256), 0, st, sel, w, w_half, P, topk, E, pv);
-}
-
-template <int K, int NS, bool PREP, int NW, bool OUTB>
-static void chain_launch(const uint64_t* ptrs, int mat_base, int nmat, int kdim, int ndim, const PlanView& pv,
-                         int topk, int umax, const uint16_t* xin, float* yout, hipStream_t st)
-{
-    const int ncb = ndim / (16 * NW);
-    const size_t lds = 2 * (size_t)Stage<K, NW>::BBP + (size_t)NS * kdim * 2 + (OUTB ? (size_t)NS * 128 * 4 : 0);
-    auto kern = chain_gemv_kernel<K, NS, PREP, NW, OUTB>;
-    static int lds_set = 0;   // largest dynamic LDS this instantiation has been opened up to
     if ((int)lds > lds_set)
     {
         (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                   (int)lds);
         lds_set = (int)lds;
     }
-    hipLaunchKernelGGL(kern, dim3(umax * ncb, nmat), dim3(NW * 64), lds, st, ptrs, mat_base, kdim, ndim, pv, topk,
-                       xin, yout);
 }
 
-template <int K, bool PREP>
-static void chain_ns(int ns, const uint64_t* ptrs, int mat_base, int nmat, int kdim, int ndim, const PlanView& pv,
-                     int topk, int umax, const uint16_t* xin, float* yout, hipStream_t st)
+template <int K>
+static size_t gu_lds(int ns, int H, int P, int E)
 {
-    // gate/up: 4 waves (64 outputs) per workgroup; down: 8 waves = one 128-output block, out_block fused
-    constexpr int NW = PREP ? 4 : 8;
-    constexpr bool OUTB = !PREP;
-    if (ns <= 1) chain_launch<K, 1, PREP, NW, OUTB>(ptrs, mat_base, nmat, kdim, ndim, pv, topk, umax, xin, yout, st);
-    else if (ns <= 2) chain_launch<K, 2, PREP, NW, OUTB>(ptrs, mat_base, nmat, kdim, ndim, pv, topk, umax, xin, yout, st);
-    else if (ns <= 4) chain_launch<K, 4, PREP, NW, OUTB>(ptrs, mat_base, nmat, kdim, ndim, pv, topk, umax, xin, yout, st);
-    else chain_launch<K, 8, PREP, NW, OUTB>(ptrs, mat_base, nmat, kdim, ndim, pv, topk, umax, xin, yout, st);
+    return 2 * (size_t)Stage<K, GU_NW>::BBP + (size_t)ns * H * 2 + lplan_ints(P, E) * 4;
 }
 
-int launch_chain(int K, int ns, bool prep, const uint64_t* ptrs, int mat_base, int nmat, int kdim, int ndim,
-                 const PlanView& pv, int topk, int umax, const uint16_t* xin, float* yout, hipStream_t st)
+template <int K>
+static size_t dn_lds(int ns, int I)
 {
-#define GFL_K(KK)                                                                                              \
-    case KK:                                                                                                   \
-        if (prep) chain_ns<KK, true>(ns, ptrs, mat_base, nmat, kdim, ndim, pv, topk, umax, xin, yout, st);     \
-        else chain_ns<KK, false>(ns, ptrs, mat_base, nmat, kdim, ndim, pv, topk, umax, xin, yout, st);         \
-        return 0;
-    switch (K)
-    {
-        GFL_K(2) GFL_K(3) GFL_K(4) GFL_K(5)
-        default: return -1;
+    return 2 * (size_t)Stage<K, DN_NW>::BBP + (size_t)ns * I * 2 + (size_t)ns * 128 * 4;
+}
+
+template <int K, int NS>
+static void gu_launch(const GuArgs& a, int umax, int nmat, hipStream_t st)
+{
+    static int lds_set = 0;
+    const size_t lds = gu_lds<K>(a.ns_cap, a.H, a.P, a.E);
+    auto kern = gu_kernel<K, NS>;
+    open_lds(kern, lds, lds_set);
+    hipLaunchKernelGGL(kern, dim3(umax * (a.I / (16 * GU_NW)) + 1, nmat), dim3(GU_NW * 64), lds, st, a);
+}
+
+template <int K, int NS>
+static void dn_launch(const DnArgs& a, int umax, hipStream_t st)
+{
+    static int lds_set = 0;
+    const size_t lds = dn_lds<K>(a.ns_cap, a.I);
+    auto kern = down_kernel<K, NS>;
+    open_lds(kern, lds, lds_set);
+    hipLaunchKernelGGL(kern, dim3(umax * (a.H / (16 * DN_NW))), dim3(DN_NW * 64), lds, st, a);
+}
+
+// slots per pass: 1, 4 or 8 (a 2-slot instantiation does not fit the register budget without spilling; passes with
+// fewer slots than NS skip the unused ones)
+#define GFL_NS_SWITCH(NSV, CALL)                                                                                \
+    if ((NSV) <= 1) { constexpr int NS_ = 1; CALL; }                                                           \
+    else if ((NSV) <= 4) { constexpr int NS_ = 4; CALL; }                                                      \
+    else { constexpr int NS_ = 8; CALL; }
+
+#define GFL_K_SWITCH(KV, CALL)                                                                                  \
+    switch (KV)                                                                                                 \
+    {                                                                                                           \
+        case 2: { constexpr int K_ = 2; CALL; } break;                                                          \
+        case 3: { constexpr int K_ = 3; CALL; } break;                                                          \
+        case 4: { constexpr int K_ = 4; CALL; } break;                                                          \
+        case 5: { constexpr int K_ = 5; CALL; } break;                                                          \
+        default: return -1;                                                                                     \
     }
-#undef GFL_K
+
+size_t gate_up_lds_bytes(int K, int ns, int H, int P, int E)
+{
+    size_t r = 0;
+    auto f = [&]() -> int {
+        GFL_K_SWITCH(K, (r = gu_lds<K_>(ns, H, P, E)))
+        return 0;
+    };
+    f();
+    return r;
 }
 
-void launch_act(const uint64_t* ptrs, const PlanView& pv, int smax, const float* ygu, uint16_t* xtd, int I,
-                float limit, const float* exp_tab, hipStream_t st)
+size_t down_lds_bytes(int K, int ns, int I)
 {
-    const int items = smax * (I / 128);
-    hipLaunchKernelGGL(act_kernel, dim3((items + 3) / 4), dim3(256), 0, st, ptrs, pv, ygu, xtd, I, limit,
-                       exp_tab);
+    size_t r = 0;
+    auto f = [&]() -> int {
+        GFL_K_SWITCH(K, (r = dn_lds<K_>(ns, I)))
+        return 0;
+    };
+    f();
+    return r;
 }
 
-void launch_final(const uint64_t* ptrs, const PlanView& pv, const void* w, int w_half, int M, int topk,
-                  const float* yd, float* out, int H, hipStream_t st)
+int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, const int64_t* sel, const void* w,
+                   int w_half, int P, int topk, int E, int H, int I, int umax, const uint16_t* x, float* ygu,
+                   uint16_t* xtd, int* act_cnt, const float* exp_tab, float act_limit, const PlanView& pv, float* out,
+                   hipStream_t st)
 {
-    const int n = M * H;
-    hipLaunchKernelGGL(final_kernel, dim3((n + 255) / 256), dim3(256), 0, st, pv, M, topk, yd, out, H);
+    GuArgs a;
+    a.ptrs = ptrs; a.sel = sel; a.w = w; a.w_half = w_half; a.P = P; a.topk = topk; a.E = E; a.H = H; a.I = I;
+    a.mat_base = mat_base; a.x = x; a.ygu = ygu; a.xtd = xtd; a.act_cnt = act_cnt; a.exp_tab = exp_tab;
+    a.act_limit = act_limit; a.pv = pv; a.out = out;
+    a.nmat_total = 2 * (128 / (16 * GU_NW));
+    a.ns_cap = ns;
+    GFL_K_SWITCH(K, GFL_NS_SWITCH(ns, (gu_launch<K_, NS_>(a, umax, nmat, st))))
+    return 0;
 }
+
+int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int umax, const PlanView& pv,
+                const uint16_t* xtd, float* yd, int* out_cnt, float* out, hipStream_t st)
+{
+    DnArgs a;
+    a.ptrs = ptrs; a.topk = topk; a.H = H; a.I = I; a.pv = pv; a.xtd = xtd; a.yd = yd; a.out_cnt = out_cnt;
+    a.out = out;
+    a.ns_cap = ns;
+    GFL_K_SWITCH(K, GFL_NS_SWITCH(ns, (dn_launch<K_, NS_>(a, umax, st))))
+    return 0;
+}
+#undef GFL_NS_SWITCH
+#undef GFL_K_SWITCH
 
 int launch_dequant(const uint8_t* tr, int k, int n, int K, uint16_t* W, hipStream_t st)
 {

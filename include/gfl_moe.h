@@ -106,8 +106,9 @@ int gfl_exp_table(float* out, int n);
 int gfl_stats(gfl_ctx* ctx, int64_t* out, int n);
 
 /* Per-stage device timing of gfl_moe_forward, the counterpart of the per-phase wall times tier_stats reports
- * (ft_tier_ext.cpp:906-914): while enabled, every forward brackets its stages with device events
- * (0 routing plan, 1 gate|up GEMV, 2 activation + down-input prep, 3 down GEMV, 4 output transform + combine).
+ * (ft_tier_ext.cpp:906-914): while enabled, every forward brackets its launches with device events. Stage 1 is the
+ * gate|up launch (routing plan, gate|up GEMV, SwiGLU and down-input prep), stage 3 the down launch (down GEMV,
+ * output transform, weighted combine); stages 0, 2 and 4 (plan, activation, combine) run inside those two and stay 0.
  * gfl_profile_read synchronises the recorded events, adds their elapsed milliseconds into stage_ms[5] and launch
  * counts into launches[5] (host arrays), and clears the record. */
 int gfl_profile_enable(gfl_ctx* ctx, int enable);
