@@ -46,6 +46,16 @@ __host__ __device__ inline LaneDec lane_dec(int lane, int K)
 
 __device__ inline uint32_t ld_u32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
 
+// A pointer that is the same in every lane of the wave, moved to scalar registers. __builtin_amdgcn_readfirstlane
+// takes and returns a 32-bit int, so the two halves of the 64-bit address go through it separately.
+__device__ inline const uint8_t* uniform_ptr(const uint8_t* p)
+{
+    const uint64_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
+    return reinterpret_cast<const uint8_t*>(((uint64_t)hi << 32) | lo);
+}
+
 // four consecutive states -> four fp16 codebook weights, packed {w0,w1}, {w2,w3}
 template <int K>
 __device__ inline half4 decode4(uint32_t hi, uint32_t lo, uint32_t sh)

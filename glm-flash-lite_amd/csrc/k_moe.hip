@@ -297,133 +297,114 @@ __device__ inline int perm_pos(int b, int r)
     return (tk * 4 + j) * 4 + q;
 }
 
-// Workgroup barrier that only orders LDS traffic: wait for this wave's LDS operations, then s_barrier. Unlike
-// __syncthreads it carries no release fence, so outstanding global loads of the prefetch ring stay in flight.
+// Workgroup barrier that only orders LDS traffic: wait for this wave's LDS operations, then s_barrier (no release
+// fence, so outstanding global loads stay in flight).
 __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// 16-byte load through the global address space (pointers taken from the layer table are generic; a flat load
-// would also count against lgkmcnt and be drained by every LDS wait)
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ u32x4 gload16(const uint8_t* p)
+constexpr int NGRP = 8;     // groups of 8 tiles in each wave's LDS ring (7 in flight)
+
+// One tile column of one matrix over all TK tile rows for up to NS slots whose transformed inputs sit in lds_x
+// ([ns][kdim] fp16 in the permuted [tk][j][q] order). Lane (j = l/16, n = l%16) carries the reference's accumulator j
+// of output column n.
+//
+// Each wave streams its own column through a private LDS ring of NG groups of 8 tiles with LDS-direct buffer loads
+// (global -> LDS without registers): a group of 8 tiles is 256*K bytes = K dword loads of the 64 lanes, lane l of load
+// i fetching byte i*256 + 4l of the group. Group g + NG - 1 is issued before group g is decoded, so NG - 1 groups are
+// in flight per wave; the waves of a workgroup never wait for each other. Loads address tile rows < TK only.
+// col_base = tile row 0 of the column; tile row r sits at col_base + r * gstride (TK * gstride < 2^31); TK % 8 == 0.
+// ring = this wave's NG * 256 * K bytes of LDS. res[s] = the column results (valid in lanes 0..15).
+typedef __attribute__((address_space(3))) void lds_void;
+
+// s_waitcnt vmcnt(N) (expcnt / lgkmcnt not waited): the LDS-direct loads are not tracked by the compiler, so the
+// wait and its ordering against the LDS reads that follow are explicit
+template <int N>
+__device__ __forceinline__ void wait_vmcnt()
 {
-    typedef const __attribute__((address_space(1))) u32x4 gu32x4;
-    return *(gu32x4*)(p);
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-constexpr int BR = 16;      // tile rows per batch
-constexpr int NRING = 4;    // batches in flight per workgroup
-
-template <int K, int NW>
-struct Stage
+template <int K, int NS, int NG>
+__device__ __forceinline__ void chain_dma(const uint8_t* __restrict__ col_base, size_t gstride, int TK, int ns,
+                                          const uint16_t* lds_x, uint8_t* ring, float (&res)[NS])
 {
-    static constexpr int TB = 32 * K;                   // bytes per tile
-    static constexpr int RB = NW * TB;                  // bytes per tile-row slice of the workgroup
-    static constexpr int BB = BR * RB;                  // bytes per batch
-    static constexpr int NCH = BB / 16;                 // 16-byte chunks per batch
-    static constexpr int CPT = (NCH + NW * 64 - 1) / (NW * 64);   // chunks per thread
-    static constexpr int BBP = CPT * NW * 64 * 16;      // staged bytes per batch incl. the pad the surplus chunks fill
-};
-
-// One pass of NW adjacent tile columns over all TK tile rows for up to NS slots whose transformed inputs sit in
-// lds_x ([NS][kdim] fp16 in the permuted [tk][j][q] order). Each wave owns one tile column; lane (j = l/16, n = l%16)
-// carries the reference's accumulator j of output column n. Trellis bytes stream in batches of BR tile rows: every
-// thread issues coalesced 16-byte loads into a ring of NRING register batches, a batch is written to one of two LDS
-// buffers and the waves decode their tile column from there. res[s] = the column results (valid in lanes 0..15).
-template <int K, int NS, int NW>
-__device__ __forceinline__ void chain_pass(const uint8_t* __restrict__ gbase, size_t gstride, int TK, int ns,
-                                           uint8_t* stage_buf, const uint16_t* lds_x, float (&res)[NS])
-{
-    using St = Stage<K, NW>;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    constexpr int TB = 32 * K, GB = 8 * TB;
+    const int lane = threadIdx.x & 63;
     const LaneDec d = lane_dec(lane, K);
     const int j = lane >> 4, n = lane & 15;
     half4 Pm;
 #pragma unroll
     for (int r = 0; r < 4; ++r) Pm[r] = (_Float16)((j == (n & 3) && r == (n >> 2)) ? 1.0f : 0.0f);
     const float4v zero = { 0.f, 0.f, 0.f, 0.f };
-    const int nb = (TK + BR - 1) / BR;
-
-    // chunk c of batch b: tile row b*BR + c/(RB/16), byte (c % (RB/16))*16 of the slice; batches past the end reload
-    // the last tile row (in bounds, never consumed) so the ring has no branches
-    // every thread moves exactly CPT chunks; chunks past NCH reload chunk c - NCH into the pad (no branches)
-#define GFL_LOAD_BATCH(BI, REG)                                                                                  \
-    _Pragma("unroll") for (int i_ = 0; i_ < St::CPT; ++i_)                                                       \
-    {                                                                                                            \
-        const int cr_ = threadIdx.x + i_ * NW * 64;                                                              \
-        const int c_ = cr_ < St::NCH ? cr_ : cr_ - St::NCH;                                                      \
-        const int row_ = min((BI) * BR + c_ / (St::RB / 16), TK - 1);                                            \
-        REG[i_] = gload16(gbase + (size_t)row_ * gstride + (c_ % (St::RB / 16)) * 16);                           \
+    uint8_t* cb = const_cast<uint8_t*>(uniform_ptr(col_base));
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(cb, (short)0, (int)((size_t)TK * gstride),
+                                                                        0x00020000);
+    const int gs = (int)gstride;
+    int voff[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i)
+    {
+        const int byte = i * 256 + lane * 4;
+        voff[i] = (byte / TB) * gs + (byte % TB);
     }
-#define GFL_STORE_BATCH(BUF, REG)                                                                                \
-    _Pragma("unroll") for (int i_ = 0; i_ < St::CPT; ++i_)                                                       \
-        reinterpret_cast<u32x4*>(stage_buf + (BUF) * St::BBP)[threadIdx.x + i_ * NW * 64] = REG[i_];
-    // one pipeline step: publish batch BI from its ring slot, refill the slot with batch BI + 4, decode batch BI
-#define GFL_STEP(BI, REG)                                                                                        \
-    {                                                                                                            \
-        const int b_ = (BI);                                                                                     \
-        GFL_STORE_BATCH(b_ & 1, REG)                                                                             \
-        lds_barrier();                                                                                           \
-        GFL_LOAD_BATCH(b_ + 4, REG)                                                                              \
-        const uint8_t* sb_ = wl + (b_ & 1) * St::BBP;                                                            \
-        if (b_ < nb)                                                                                             \
-        {                                                                                                        \
-            _Pragma("unroll") for (int g_ = 0; g_ < BR; g_ += 4)                                                 \
-            {                                                                                                    \
-                /* four independent tiles: LDS words, decode and MFMA transposition first, then the chains */   \
-                uint32_t hi_[4], lo_[4];                                                                         \
-                _Pragma("unroll") for (int r_ = 0; r_ < 4; ++r_)                                                 \
-                {                                                                                                \
-                    hi_[r_] = *reinterpret_cast<const uint32_t*>(sb_ + (g_ + r_) * St::RB + d.o0);              \
-                    lo_[r_] = *reinterpret_cast<const uint32_t*>(sb_ + (g_ + r_) * St::RB + d.o1);              \
-                }                                                                                                \
-                float4v cw_[4];                                                                                  \
-                _Pragma("unroll") for (int r_ = 0; r_ < 4; ++r_)                                                 \
-                    cw_[r_] = __builtin_amdgcn_mfma_f32_16x16x16f16(Pm, decode4<K>(hi_[r_], lo_[r_], d.sh), zero, \
-                                                                    0, 0, 0);                                    \
-                _Pragma("unroll") for (int s_ = 0; s_ < NS; ++s_)                                                \
-                {                                                                                                \
-                    if (s_ == 0 || s_ < ns)     /* a pass always has slot 0 */                                   \
-                    {                                                                                            \
-                        float a_ = acc[s_];                                                                      \
-                        _Pragma("unroll") for (int r_ = 0; r_ < 4; ++r_)                                         \
-                        {                                                                                        \
-                            const int tk_ = b_ * BR + g_ + r_;                                                   \
-                            const half4 xv_ = *reinterpret_cast<const half4*>(xl + ((size_t)s_ * TK + tk_) * 16); \
-                            a_ = __builtin_fmaf(cw_[r_][0], (float)xv_[0], a_);                                  \
-                            a_ = __builtin_fmaf(cw_[r_][1], (float)xv_[1], a_);                                  \
-                            a_ = __builtin_fmaf(cw_[r_][2], (float)xv_[2], a_);                                  \
-                            a_ = __builtin_fmaf(cw_[r_][3], (float)xv_[3], a_);                                  \
-                        }                                                                                        \
-                        acc[s_] = a_;                                                                            \
-                    }                                                                                            \
-                }                                                                                                \
-            }                                                                                                    \
-        }                                                                                                        \
-    }
-
-    // prefetch ring: four named register batches in flight
-    u32x4 ring0[St::CPT], ring1[St::CPT], ring2[St::CPT], ring3[St::CPT];
-    static_assert(NRING == 4, "ring of four batches");
-    GFL_LOAD_BATCH(0, ring0)
-    GFL_LOAD_BATCH(1, ring1)
-    GFL_LOAD_BATCH(2, ring2)
-    GFL_LOAD_BATCH(3, ring3)
+    const int ngroups = TK / 8;
+    auto issue = [&](int g) {
+        uint8_t* dst = ring + (g % NG) * GB;
+#pragma unroll
+        for (int i = 0; i < K; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(dst + i * 256), 4, voff[i], g * 8 * gs, 0, 0);
+    };
+#pragma unroll
+    for (int g = 0; g < NG - 1; ++g)
+        if (g < ngroups) issue(g);
     float acc[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) acc[s] = 0.f;
-    const uint8_t* wl = stage_buf + wave * St::TB;      // this wave's tile inside a staged row slice
     const uint16_t* xl = lds_x + j * 4;
-    lds_barrier();                                      // lds_x written by the caller
-    for (int b0 = 0; b0 < nb; b0 += NRING)
+    for (int g = 0; g < ngroups; ++g)
     {
-        GFL_STEP(b0, ring0)
-        GFL_STEP(b0 + 1, ring1)
-        GFL_STEP(b0 + 2, ring2)
-        GFL_STEP(b0 + 3, ring3)
+        if (g + NG - 1 < ngroups)
+        {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // reads of the slot being refilled are done
+            issue(g + NG - 1);
+            wait_vmcnt<(NG - 1) * K>();                          // group g has landed
+        }
+        else
+            wait_vmcnt<0>();
+        const uint8_t* sl = ring + (g % NG) * GB;
+#pragma unroll
+        for (int h = 0; h < 8; h += 4)
+        {
+            float4v cw[4];
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+            {
+                const uint8_t* tp = sl + (h + rr) * TB;
+                const uint32_t hi = *reinterpret_cast<const uint32_t*>(tp + d.o0);
+                const uint32_t lo = *reinterpret_cast<const uint32_t*>(tp + d.o1);
+                cw[rr] = __builtin_amdgcn_mfma_f32_16x16x16f16(Pm, decode4<K>(hi, lo, d.sh), zero, 0, 0, 0);
+            }
+#pragma unroll
+            for (int s = 0; s < NS; ++s)
+            {
+                if (s == 0 || s < ns)
+                {
+                    float a = acc[s];
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr)
+                    {
+                        const int tk = g * 8 + h + rr;
+                        const half4 xv = *reinterpret_cast<const half4*>(xl + ((size_t)s * TK + tk) * 16);
+                        a = __builtin_fmaf(cw[rr][0], (float)xv[0], a);
+                        a = __builtin_fmaf(cw[rr][1], (float)xv[1], a);
+                        a = __builtin_fmaf(cw[rr][2], (float)xv[2], a);
+                        a = __builtin_fmaf(cw[rr][3], (float)xv[3], a);
+                    }
+                    acc[s] = a;
+                }
+            }
+        }
     }
-#undef GFL_STEP
-#undef GFL_STORE_BATCH
-#undef GFL_LOAD_BATCH
 #pragma unroll
     for (int s = 0; s < NS; ++s)
     {
@@ -497,14 +478,14 @@ __device__ void act_block(const GuArgs& a, int e, int s_begin, int s_end, int b)
 template <int K, int NS>
 __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(K == 5 ? 3 : 4))) void gu_kernel(GuArgs a)
 {
-    constexpr int NW = GU_NW;
-    using St = Stage<K, NW>;
+    constexpr int NW = GU_NW, TB = 32 * K;
     extern __shared__ __align__(16) uint8_t lds_raw[];
     __shared__ int hdr[4];
     __shared__ int s_last;
-    uint8_t* stage_buf = lds_raw;                                                    // [2][BBP]
-    uint16_t* lds_x = reinterpret_cast<uint16_t*>(lds_raw + 2 * St::BBP);           // [ns_cap][H] fp16 permuted
-    int* plan_mem = reinterpret_cast<int*>(lds_raw + 2 * St::BBP + (size_t)a.ns_cap * a.H * 2);
+    constexpr int RB = NGRP * 8 * TB;                                                 // ring bytes per wave
+    uint8_t* rings = lds_raw;                                                         // [NW][RB]
+    uint16_t* lds_x = reinterpret_cast<uint16_t*>(lds_raw + NW * RB);                // [ns_cap][H] fp16 permuted
+    int* plan_mem = reinterpret_cast<int*>(lds_raw + NW * RB + (size_t)a.ns_cap * a.H * 2);
     const LPlan L = lplan_carve(plan_mem, a.P, a.E);
     if (a.P <= 64) build_plan_wave(a.sel, a.P, a.E, L, hdr);
     else build_plan(a.sel, a.P, a.E, L, hdr);
@@ -520,14 +501,15 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(K ==
     if (u >= hdr[0]) return;
     const int mat = a.mat_base + blockIdx.y;              // 0 gate, 1 up
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15;
+    const int wid = __builtin_amdgcn_readfirstlane(wave);
     const int e = L.uexp[u];
     const uint8_t* tr = reinterpret_cast<const uint8_t*>(a.ptrs[(size_t)e * 9 + mat]);
     const uint16_t* suh = reinterpret_cast<const uint16_t*>(a.ptrs[(size_t)e * 9 + 3 + 2 * mat]);
     const int s_begin = L.uoff[u], s_end = L.uoff[u + 1];
-    const size_t gstride = (size_t)TN * St::TB;
-    const uint8_t* gbase = tr + (size_t)cb * St::RB;
-    float* ybase = a.ygu + (size_t)mat * a.pv.cap_slots * a.I;
+    const size_t gstride = (size_t)TN * TB;
     const int t = cb * NW + wave;                         // this wave's tile column
+    const uint8_t* col = tr + (size_t)t * TB;
+    float* ybase = a.ygu + (size_t)mat * a.pv.cap_slots * a.I;
 
     const int nsp = NS == 1 ? 1 : max(1, min(NS, a.ns_cap));
     for (int c0 = s_begin; c0 < s_end; c0 += nsp)
@@ -548,7 +530,8 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(K ==
             dst[perm_pos(b, lane + 64)] = (uint16_t)f2h_bits(v1);
         }
         float res[NS];
-        chain_pass<K, NS, NW>(gbase, gstride, TK, ns, stage_buf, lds_x, res);
+        lds_barrier();   // lds_x complete
+        chain_dma<K, NS, NGRP>(col, gstride, TK, ns, lds_x, rings + wid * RB, res);
 #pragma unroll
         for (int s = 0; s < NS; ++s)
             if (s < ns && lane < 16)
@@ -592,25 +575,26 @@ struct DnArgs
 template <int K, int NS>
 __global__ __launch_bounds__(DN_NW * 64) __attribute__((amdgpu_waves_per_eu(K == 5 || NS == 8 ? 3 : 4))) void down_kernel(DnArgs a)
 {
-    constexpr int NW = DN_NW;
-    using St = Stage<K, NW>;
+    constexpr int NW = DN_NW, TB = 32 * K;
     extern __shared__ __align__(16) uint8_t lds_raw[];
     __shared__ int s_last[NS];
     __shared__ int c_tok[NS], c_npk[NS], c_slot[NS][MAX_TOPK];
     __shared__ float c_w[NS][MAX_TOPK];
-    uint8_t* stage_buf = lds_raw;
-    uint16_t* lds_x = reinterpret_cast<uint16_t*>(lds_raw + 2 * St::BBP);            // [ns_cap][I]
-    float* lds_y = reinterpret_cast<float*>(lds_raw + 2 * St::BBP + (size_t)a.ns_cap * a.I * 2);   // [ns_cap][128]
+    constexpr int RB = NGRP * 8 * TB;                                                  // ring bytes per wave
+    uint8_t* rings = lds_raw;                                                          // [NW][RB]
+    uint16_t* lds_x = reinterpret_cast<uint16_t*>(lds_raw + NW * RB);                 // [ns_cap][I]
+    float* lds_y = reinterpret_cast<float*>(lds_raw + NW * RB + (size_t)a.ns_cap * a.I * 2);   // [ns_cap][128]
     const int TN = a.H / 16, TK = a.I / 16, ncb = TN / NW;
     const int u = blockIdx.x / ncb, blk = blockIdx.x % ncb;
     if (u >= a.pv.hdr[0]) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15;
+    const int wid = __builtin_amdgcn_readfirstlane(wave);
     const int e = a.pv.uexp[u];
     const uint8_t* tr = reinterpret_cast<const uint8_t*>(a.ptrs[(size_t)e * 9 + 2]);
     const uint16_t* svh = reinterpret_cast<const uint16_t*>(a.ptrs[(size_t)e * 9 + 8]);
     const int s_begin = a.pv.uoff[u], s_end = a.pv.uoff[u + 1];
-    const size_t gstride = (size_t)TN * St::TB;
-    const uint8_t* gbase = tr + (size_t)blk * St::RB;
+    const size_t gstride = (size_t)TN * TB;
+    const uint8_t* col = tr + (size_t)(blk * NW + wave) * TB;   // this wave's tile column
     const int nbh = a.H / 128;
 
     const int nsp = NS == 1 ? 1 : max(1, min(NS, a.ns_cap));
@@ -637,7 +621,8 @@ __global__ __launch_bounds__(DN_NW * 64) __attribute__((amdgpu_waves_per_eu(K ==
             q_npk = a.pv.tok_npk[q_tok];
         }
         float res[NS];
-        chain_pass<K, NS, NW>(gbase, gstride, TK, ns, stage_buf, lds_x, res);
+        lds_barrier();   // lds_x complete
+        chain_dma<K, NS, NGRP>(col, gstride, TK, ns, lds_x, rings + wid * RB, res);
 #pragma unroll
         for (int s = 0; s < NS; ++s)
             if (s < ns && lane < 16) lds_y[s * 128 + wave * 16 + n] = res[s];
@@ -746,13 +731,13 @@ static void open_lds(F kern, size_t lds, int& lds_set)
 template <int K>
 static size_t gu_lds(int ns, int H, int P, int E)
 {
-    return 2 * (size_t)Stage<K, GU_NW>::BBP + (size_t)ns * H * 2 + lplan_ints(P, E) * 4;
+    return (size_t)GU_NW * NGRP * 8 * 32 * K + (size_t)ns * H * 2 + lplan_ints(P, E) * 4;
 }
 
 template <int K>
 static size_t dn_lds(int ns, int I)
 {
-    return 2 * (size_t)Stage<K, DN_NW>::BBP + (size_t)ns * I * 2 + (size_t)ns * 128 * 4;
+    return (size_t)DN_NW * NGRP * 8 * 32 * K + (size_t)ns * I * 2 + (size_t)ns * 128 * 4;
 }
 
 template <int K, int NS>
