@@ -104,18 +104,57 @@ __device__ inline float r16(float x)
     return r;
 }
 
+// Value of lane L ^ W (W = 1..32) without the LDS crossbar: DPP quad permutes and row mirrors inside 16-lane rows
+// (xor 4 = half-row mirror then xor 3, xor 8 = row mirror then half-row mirror), gfx950's permlane swaps across rows.
+template <int W>
+__device__ __forceinline__ float lane_xor(float v)
+{
+    const int iv = __float_as_int(v);
+    if constexpr (W == 1) return __int_as_float(__builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xF, 0xF, true));
+    if constexpr (W == 2) return __int_as_float(__builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xF, 0xF, true));
+    if constexpr (W == 4)
+    {
+        const int t = __builtin_amdgcn_update_dpp(0, iv, 0x141, 0xF, 0xF, true);   // row_half_mirror: L ^ 7
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, t, 0x1B, 0xF, 0xF, true));   // quad_perm 3210: ^ 3
+    }
+    if constexpr (W == 8)
+    {
+        const int t = __builtin_amdgcn_update_dpp(0, iv, 0x140, 0xF, 0xF, true);   // row_mirror: L ^ 15
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, t, 0x141, 0xF, 0xF, true));  // row_half_mirror: ^ 7
+    }
+    if constexpr (W == 16)
+    {
+        // odd rows of the first operand <-> even rows of the second: {rows 0,0,2,2 ; rows 1,1,3,3}
+        const auto r = __builtin_amdgcn_permlane16_swap(iv, iv, false, false);
+        return __int_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+    }
+    if constexpr (W == 32)
+    {
+        // upper half of the first operand <-> lower half of the second: {lanes 0..31 twice ; 32..63 twice}
+        const auto r = __builtin_amdgcn_permlane32_swap(iv, iv, false, false);
+        return __int_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+    }
+}
+
 // Wave-level Hadamard-128 in the reference's butterfly order (had128, ft_core.h:89-94): lane L holds elements L and
 // L+64; stages w = 1..32 cross lanes, w = 64 stays in the lane. Every element sees the same add/sub sequence.
+template <int W>
+__device__ __forceinline__ void fwht_stage(float& v0, float& v1, int L)
+{
+    const float p0 = lane_xor<W>(v0), p1 = lane_xor<W>(v1);
+    if (L & W) { v0 = p0 - v0; v1 = p1 - v1; }
+    else { v0 = v0 + p0; v1 = v1 + p1; }
+}
+
 __device__ inline void fwht128(float& v0, float& v1)
 {
     const int L = threadIdx.x & 63;
-#pragma unroll
-    for (int w = 1; w < 64; w <<= 1)
-    {
-        const float p0 = __shfl_xor(v0, w), p1 = __shfl_xor(v1, w);
-        if (L & w) { v0 = p0 - v0; v1 = p1 - v1; }
-        else { v0 = v0 + p0; v1 = v1 + p1; }
-    }
+    fwht_stage<1>(v0, v1, L);
+    fwht_stage<2>(v0, v1, L);
+    fwht_stage<4>(v0, v1, L);
+    fwht_stage<8>(v0, v1, L);
+    fwht_stage<16>(v0, v1, L);
+    fwht_stage<32>(v0, v1, L);
     const float a = v0, c = v1;
     v0 = a + c;
     v1 = a - c;
