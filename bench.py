@@ -152,6 +152,127 @@ def pmc_digest(fetch_dir, write_dir):
     print(json.dumps(doc))
 
 
+def make_routes(M, rng, n, kind):
+    """n routings of M tokens: (x fp16 [M,H], sel int64 [M,8], w fp16 [M,8], union size) on the GPU.
+    kind: "uniform" (N(0,1) logits) or "zipf" (Zipf s=1.1 skew over a seeded expert ranking)."""
+    import numpy as np
+    import torch
+    import synth
+    out = []
+    for _ in range(n):
+        x = rng.standard_normal((M, H)).astype(np.float16)
+        if kind == "zipf":
+            sel, w16 = synth.route(synth.zipf_logits(M, E, 1.1, rng), TOPK)
+        else:
+            (sel, w16), _ = synth.route_uniform(M, E, TOPK, rng)
+        out.append((torch.from_numpy(x.view(np.int16)).view(torch.float16).cuda(), torch.from_numpy(sel).cuda(),
+                    torch.from_numpy(w16.view(np.int16)).view(torch.float16).cuda(), len(np.unique(sel))))
+    return out
+
+
+def time_layer_steps(ctx, layer_ids, routes, M, G, reps, warmup, bytes_per_expert, per_step=1):
+    """Graph-timed decode steps. A step is `per_step` consecutive layer calls (layer i of the step = layer_ids[(s *
+    per_step + i) % len]) with routing (s * per_step + i) % len(routes); G steps are captured in one HIP graph and
+    replayed `reps` times between synchronisations. Returns per-token time and bandwidth on the union's bytes."""
+    import numpy as np
+    import torch
+    out = torch.empty((M, H), dtype=torch.float32, device="cuda")
+    NR, NL = len(routes), len(layer_ids)
+
+    def step(s_):
+        for i in range(per_step):
+            c = s_ * per_step + i
+            x, sel, w, _ = routes[c % NR]
+            ctx.moe_forward(layer_ids[c % NL], x, sel, w, out)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        for i in range(2):
+            step(i)
+    torch.cuda.current_stream().wait_stream(st)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(G):
+            step(i)
+    g.replay()
+    torch.cuda.synchronize()
+    got = out.clone()
+    step(G - 1)
+    torch.cuda.synchronize()
+    graph_ok = bool(torch.equal(got, out))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / (reps * G)
+    calls = [(s_ * per_step + i) for s_ in range(G) for i in range(per_step)]
+    step_bytes = sum(routes[c % NR][3] * bytes_per_expert(layer_ids[c % NL]) for c in calls) / G + per_step * M * H * 6
+    gbps = step_bytes / (ms * 1e-3) / 1e9
+    del g
+    return {"us_per_token": round(ms * 1e3 / M, 3), "ms_per_step": round(ms, 5),
+            "union_experts": round(float(np.mean([r[3] for r in routes])), 2), "GBps": round(gbps, 1),
+            "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "graph_replay_matches_eager": graph_ok}
+
+
+def extra_configs(ctx, layers, args, G, reps):
+    """BASELINE configs 2, 3 and the 42-layer resident stack of config 4, timed like config 1."""
+    import numpy as np
+    import synth
+    res = {}
+    t0 = time.time()
+    # config 2: mixed bitrates, Zipf-skewed routing; two layers of each kind cycled (3.1 GB per layer)
+    base = 100
+    mixed = {"A_gate_up4_down3": (4, 4, 3), "B_gate_up3_down5": (3, 3, 5)}
+    for j, (name, ks) in enumerate(mixed.items()):
+        ids = []
+        for r in range(2):
+            li = base + 2 * j + r
+            L = synth.SynthLayer(li, E, H, I, ks)
+            L.register(ctx, li)
+            layers.append(L)
+            ids.append(li)
+        bpe = L.quant_bytes_per_expert
+        per = {}
+        for M in (1, 2, 3, 4):
+            routes = make_routes(M, np.random.default_rng(2000 + 10 * j + M), 32, "zipf")
+            per[str(M)] = time_layer_steps(ctx, ids, routes, M, G, reps, 8, lambda li, b=bpe: b)
+        res["config2_" + name] = per
+        print(f"bench: config 2 {name} done ({time.time() - t0:.0f} s)", file=sys.stderr, flush=True)
+    # config 3: batched decode across conversations on the config-1 layers
+    per = {}
+    for M in (16, 32, 64):
+        routes = make_routes(M, np.random.default_rng(3000 + M), 16, "uniform")
+        per[str(M)] = time_layer_steps(ctx, list(range(args.layers)), routes, M, 16, max(1, reps // 2), 4,
+                                       lambda li: layers[0].quant_bytes_per_expert)
+    res["config3_batched"] = per
+    print(f"bench: config 3 done ({time.time() - t0:.0f} s)", file=sys.stderr, flush=True)
+    # config 4 (decode half): a stack of 42 config-1 layers resident at once, one token through all of them per step
+    nst = args.stack_layers
+    ids = []
+    for r in range(nst):
+        li = 200 + r
+        L = synth.SynthLayer(li, E, H, I, (KBITS,) * 3)
+        L.register(ctx, li)
+        layers.append(L)
+        ids.append(li)
+    print(f"bench: {nst}-layer stack resident ({time.time() - t0:.0f} s)", file=sys.stderr, flush=True)
+    routes = make_routes(1, np.random.default_rng(4000), nst, "uniform")
+    r = time_layer_steps(ctx, ids, routes, 1, 2, max(2, reps // 4), 1, lambda li: layers[0].quant_bytes_per_expert,
+                         per_step=nst)
+    r["layers"] = nst
+    r["resident_GB"] = round(nst * E * layers[0].quant_bytes_per_expert / 1e9, 1)
+    res["config4_stack_decode"] = r
+    res["setup_and_time_s"] = round(time.time() - t0, 1)
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -163,6 +284,9 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=64)
     ap.add_argument("--cpu-iters", type=int, default=300)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the config 2 / 3 / 42-layer-stack measurements (config 1 only)")
+    ap.add_argument("--stack-layers", type=int, default=42)
     ap.add_argument("--pmc-probe", action="store_true",
                     help="counter run: the calibration copy, then eager M=1 steps (run under rocprofv3 --pmc)")
     ap.add_argument("--pmc-digest", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -202,71 +326,32 @@ def main():
     roof = None
     for M in [int(m) for m in args.Ms.split(",")]:
         rng = np.random.default_rng(1000 + M)
-        NR = 32
-        xs, sels, ws, U = [], [], [], []
-        for r in range(NR):
-            x = rng.standard_normal((M, H)).astype(np.float16)
-            (sel, w16), _ = synth.route_uniform(M, E, TOPK, rng)
-            xs.append(torch.from_numpy(x.view(np.int16)).view(torch.float16).cuda())
-            sels.append(torch.from_numpy(sel).cuda())
-            ws.append(torch.from_numpy(w16.view(np.int16)).view(torch.float16).cuda())
-            U.append(len(np.unique(sel)))
-        out = torch.empty((M, H), dtype=torch.float32, device="cuda")
-
-        def step(i):
-            r = i % NR
-            ctx.moe_forward(i % args.layers, xs[r], sels[r], ws[r], out)
-
-        for i in range(args.warmup):
-            step(i)
-        torch.cuda.synchronize()
-        # graph of G steps (each with its own layer and routing), replayed `reps` times
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            for i in range(3):
-                step(i)
-        torch.cuda.current_stream().wait_stream(s)
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for i in range(G):
-                step(i)
-        g.replay()
-        torch.cuda.synchronize()
-        got = out.clone()
-        step(G - 1)
-        torch.cuda.synchronize()
-        graph_ok = bool(torch.equal(got, out))
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        e0.record()
-        for _ in range(reps):
-            g.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / steps
-        step_bytes = float(np.mean([U[i % NR] for i in range(G)])) * per_expert + M * H * 6
-        gbps = step_bytes / (ms * 1e-3) / 1e9
-        per_M[str(M)] = {"us_per_token": round(ms * 1e3 / M, 3), "ms_per_step": round(ms, 5),
-                         "union_experts": round(float(np.mean(U)), 2), "GBps": round(gbps, 1),
-                         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "graph_replay_matches_eager": graph_ok}
+        routes = make_routes(M, rng, 32, "uniform")
+        r = time_layer_steps(ctx, list(range(args.layers)), routes, M, G, reps, args.warmup,
+                             lambda li: layers[li].quant_bytes_per_expert)
+        per_M[str(M)] = r
         if M == 1:
             # live per-kernel timing of the dominant kernel (gate|up GEMV): device events around every launch
+            out = torch.empty((1, H), dtype=torch.float32, device="cuda")
+            NR = len(routes)
             ctx.profile(True)
             torch.cuda.synchronize()
             for i in range(args.profile_steps):
-                step(i)
+                x, sel, w, _ = routes[i % NR]
+                ctx.moe_forward(i % args.layers, x, sel, w, out)
             prof = ctx.profile_read()
             ctx.profile(False)
             gu_ms, gu_n = prof["gate_up"]
-            gu_bytes = float(np.mean([U[i % NR] for i in range(args.profile_steps)])) * gu_per_expert
+            gu_bytes = float(np.mean([routes[i % NR][3] for i in range(args.profile_steps)])) * gu_per_expert
             ach = gu_bytes / (gu_ms / gu_n * 1e-3) / 1e9
             stage_us = {k: round(v[0] / max(1, v[1]) * 1e3, 2) for k, v in prof.items()}
             roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                     "frac": round(ach / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": "gu_kernel<3, 1> (gate|up GEMV + SwiGLU)",
                     "algorithmic_bytes_per_launch": round(gu_bytes), "mean_launch_us": round(gu_ms / gu_n * 1e3, 2),
                     "stage_mean_us": stage_us}
-        del g
+    configs = {}
+    if not args.no_extra:
+        configs = extra_configs(ctx, layers, args, G, reps)
     if roof is not None and os.path.exists(TRAFFIC_FILE):
         try:
             roof["traffic"] = json.load(open(TRAFFIC_FILE)).get("hbm_bytes_per_launch")
@@ -280,7 +365,7 @@ def main():
             "config": {"workload": "config1: one 288-expert top-8 MoE layer decode, M=1, H=5120 I=1536 K=3 bpw",
                        "experts": E, "topk": TOPK, "hidden": H, "intermediate": I, "bits": KBITS,
                        "layers_cycled": args.layers, "graph_steps": G},
-            "per_M": per_M, "roofline": roof, "cpu_baseline": cpu, "setup_s": round(setup_s, 1)}
+            "per_M": per_M, "configs": configs, "roofline": roof, "cpu_baseline": cpu, "setup_s": round(setup_s, 1)}
     print(json.dumps(line), flush=True)
 
 

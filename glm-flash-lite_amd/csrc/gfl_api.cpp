@@ -4,6 +4,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -56,6 +57,8 @@ struct gfl_ctx
     std::vector<Rec> recs;
     // expf(-g) for every fp16 bit pattern g (the SwiGLU exponential, see build_exp_table)
     float* exp_tab = nullptr;
+    // slots per GEMV pass forced by GFL_SLOTS_PER_PASS (1, 2, 4 or 8; 0 = chosen from M)
+    int ns_override = 0;
 };
 
 namespace {
@@ -209,6 +212,11 @@ int gfl_ctx_create(int device, gfl_ctx** out)
     gfl_ctx* c = new gfl_ctx();
     c->device = device;
     c->exp_tab = dtab;
+    if (const char* e = std::getenv("GFL_SLOTS_PER_PASS"))
+    {
+        const int v = std::atoi(e);
+        if (v == 1 || v == 2 || v == 4 || v == 8) c->ns_override = v;
+    }
     *out = c;
     return GFL_OK;
 }
@@ -268,8 +276,11 @@ int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, c
     Workspace ws;
     if (int r = ensure_ws(c, P, L.H, L.I, st, ws)) return r;
     const int umax = P < L.E ? P : L.E;
-    // slots per pass of the GEMV (its LDS holds NS transformed inputs); experts with more slots take extra passes
-    const int ns = M == 1 ? 1 : (M < 8 ? 2 : (M < 32 ? 4 : 8));
+    // slots per pass of the GEMV (its LDS holds NS transformed inputs); experts with more slots take extra passes,
+    // each re-streaming the expert's weights. Measured on MI355X for M = 3..64 (uniform top-8 of 288): two slots per
+    // pass beat four or eight, whose larger LDS footprint costs more occupancy than the extra passes cost bandwidth.
+    int ns = M == 1 ? 1 : 2;
+    if (c->ns_override > 0) ns = std::min(c->ns_override, M);
     if (gfl::gate_up_lds_bytes(L.K[0], ns, L.H, P, L.E) > 163840 || gfl::gate_up_lds_bytes(L.K[1], ns, L.H, P, L.E) > 163840
         || gfl::down_lds_bytes(L.K[2], ns, L.I) > 163840)
         return fail(GFL_EINVAL, "gfl_moe_forward: shape needs more than 160 KB of LDS per workgroup");

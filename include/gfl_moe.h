@@ -68,6 +68,10 @@ int gfl_register_layer(gfl_ctx* ctx, int li, int E, int H, int I, int k_gate, in
 int gfl_moe_forward(gfl_ctx* ctx, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half, int M,
                     int topk, float* out, int mode, float act_limit, gfl_stream stream);
 
+/* Environment: GFL_SLOTS_PER_PASS = 1, 2, 4 or 8 forces the number of (token, expert) slots one GEMV pass of
+ * gfl_moe_forward accumulates (default: 1 at M = 1, else 2; an expert with more slots takes more passes). Read once
+ * by gfl_ctx_create. */
+
 /* Dequantize one trellis matrix to fp16 W[k][n] (dense_weights, kernels/cpu_avx2/ft_core.h:1657-1672). */
 int gfl_dequant(const void* trellis, int k, int n, int K, uint16_t* out, gfl_stream stream);
 
