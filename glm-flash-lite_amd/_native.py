@@ -12,7 +12,8 @@ LIB_PATH = os.path.join(HERE, "libgfl_moe.so")
 
 # exported symbols of include/gfl_moe.h (checked by tests/test_abi.py against the header)
 SYMBOLS = ("gfl_last_error", "gfl_version", "gfl_ctx_create", "gfl_ctx_destroy", "gfl_register_layer",
-           "gfl_moe_forward", "gfl_dequant", "gfl_split", "gfl_combine", "gfl_grouped_rows", "gfl_synth_trellis",
+           "gfl_moe_forward", "gfl_grouped_forward", "gfl_dequant", "gfl_split", "gfl_combine", "gfl_grouped_rows",
+           "gfl_synth_trellis",
            "gfl_stats", "gfl_profile_enable", "gfl_profile_read", "gfl_exp_table")
 
 MODE_AUTO, MODE_AFFINE, MODE_EXACT, MODE_I16 = -1, 0, 1, 2
@@ -47,6 +48,7 @@ def load(path=LIB_PATH):
     L.gfl_ctx_destroy.argtypes = [_P]
     L.gfl_register_layer.argtypes = [_P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _P]
     L.gfl_moe_forward.argtypes = [_P, C.c_int, _P, _P, _P, C.c_int, C.c_int, C.c_int, _P, C.c_int, C.c_float, _P]
+    L.gfl_grouped_forward.argtypes = [_P, C.c_int, _P, _P, _P, C.c_int, C.c_int, C.c_int, _P, C.c_float, _P]
     L.gfl_dequant.argtypes = [_P, C.c_int, C.c_int, C.c_int, _P, _P]
     L.gfl_split.argtypes = [_P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P,
                             C.c_int64, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P]
@@ -127,7 +129,28 @@ class Context:
                                      ptr(out), int(mode), float(act_limit), _stream()))
         return out
 
-    STAGES = ("plan", "gate_up", "act", "down", "combine")
+    def grouped_forward(self, li, x, sel, w, out, act_limit=0.0):
+        """Prefill-sized forward (MFMA grouped GEMMs): same tensors as moe_forward, M*topk <= 65536."""
+        import torch
+        if sel.dim() != 2:
+            raise ValueError("sel must be int64 [M, topk]")
+        M, topk = sel.shape
+        if not (x.dtype == torch.float16 and x.is_contiguous() and x.dim() == 2 and x.shape[0] == M):
+            raise ValueError("x must be contiguous fp16 [M, H]")
+        if not (sel.dtype == torch.int64 and sel.is_contiguous()):
+            raise ValueError("sel must be contiguous int64 [M, topk]")
+        if not (w.dtype in (torch.float16, torch.float32) and w.is_contiguous() and tuple(w.shape) == (M, topk)):
+            raise ValueError("w must be contiguous fp16 or fp32 [M, topk]")
+        if not (out.dtype == torch.float32 and out.is_contiguous() and tuple(out.shape) == tuple(x.shape)):
+            raise ValueError("out must be contiguous fp32 [M, H]")
+        for t in (x, sel, w, out):
+            if not (t.is_cuda and t.device.index == self.device):
+                raise ValueError(f"all tensors must be on cuda:{self.device}")
+        check(load().gfl_grouped_forward(self.h, li, ptr(x), ptr(sel), ptr(w), int(w.dtype == torch.float16), M, topk,
+                                         ptr(out), float(act_limit), _stream()))
+        return out
+
+    STAGES = ("plan", "gate_up", "grouped", "down", "combine")
 
     def profile(self, enable):
         check(load().gfl_profile_enable(self.h, int(bool(enable))))

@@ -18,7 +18,7 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libgfl_moe.so")
 ARCH = os.environ.get("GFL_ARCH", "gfx950")
 
-SOURCES = ["k_moe.hip", "k_split.hip", "gfl_api.cpp"]
+SOURCES = ["k_moe.hip", "k_split.hip", "k_prefill.hip", "gfl_api.cpp"]
 
 CFLAGS = ["--offload-arch=" + ARCH, "-O3", "-fPIC", "-std=c++17", "-ffp-contract=off",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -59,6 +59,9 @@ struct gfl_ctx
     float* exp_tab = nullptr;
     // slots per GEMV pass forced by GFL_SLOTS_PER_PASS (1, 2, 4 or 8; 0 = chosen from M)
     int ns_override = 0;
+    // workspace of the prefill path (gfl_grouped_forward), grown on demand
+    void* gws = nullptr;
+    size_t gws_bytes = 0;
 };
 
 namespace {
@@ -230,6 +233,7 @@ int gfl_ctx_destroy(gfl_ctx* c)
     for (auto& L : c->layers)
         if (L.dptrs) hipFree(L.dptrs);
     if (c->ws) hipFree(c->ws);
+    if (c->gws) hipFree(c->gws);
     if (c->exp_tab) hipFree(c->exp_tab);
     delete c;
     return GFL_OK;
@@ -301,6 +305,74 @@ int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, c
                                     st);
         });
     if (r) return r > 0 ? r : fail(GFL_EINVAL, "gfl_moe_forward: unsupported K");
+    GFL_HIP(hipGetLastError());
+    c->calls += 1;
+    c->picks += P;
+    return GFL_OK;
+}
+
+int gfl_grouped_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half,
+                        int M, int topk, float* out, float act_limit, gfl_stream stream)
+{
+    if (!c || !x || !sel || !w || !out) return fail(GFL_EINVAL, "gfl_grouped_forward: NULL argument");
+    if (li < 0 || li >= (int)c->layers.size() || !c->layers[li].dptrs)
+        return fail(GFL_EINVAL, "gfl_grouped_forward: layer not registered");
+    if (M < 1 || topk < 1 || topk > gfl::MAX_TOPK || (int64_t)M * topk > gfl::MAX_GROUPED_PICKS)
+        return fail(GFL_EINVAL, "gfl_grouped_forward: need 1 <= topk <= 16 and M*topk <= 65536");
+    if (!std::isfinite(act_limit) || act_limit < 0)
+        return fail(GFL_EINVAL, "gfl_grouped_forward: act_limit must be >= 0");
+    std::lock_guard<std::mutex> g(c->mu);
+    const Layer& L = c->layers[li];
+    if (L.H % 256 || L.I % 256) return fail(GFL_EINVAL, "gfl_grouped_forward: H and I must be multiples of 256");
+    GFL_HIP(hipSetDevice(c->device));
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const int P = M * topk, E = L.E, H = L.H, I = L.I;
+    // layout: plan ints, then xt [2][P][H] fp16, ygu [2][P][I] fp32, xd [P][I] fp16, yraw [P][H] fp32
+    const size_t n_int = 4 + (size_t)E + (E + 1) + 7 * (size_t)P + (size_t)M + (size_t)P;
+    const size_t b_int = align256(sizeof(int) * n_int);
+    const size_t b_xt = align256(2 * 2 * (size_t)P * H), b_ygu = align256(4 * 2 * (size_t)P * I);
+    const size_t b_xd = align256(2 * (size_t)P * I), b_yr = align256(4 * (size_t)P * H);
+    const size_t need = b_int + b_xt + b_ygu + b_xd + b_yr;
+    if (need > c->gws_bytes)
+    {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+            return fail(GFL_EINVAL, "gfl_grouped_forward: the workspace must be sized before graph capture "
+                                    "(run one forward of this shape first)");
+        if (c->gws)
+        {
+            GFL_HIP(hipDeviceSynchronize());
+            GFL_HIP(hipFree(c->gws));
+        }
+        c->gws = nullptr;
+        c->gws_bytes = 0;
+        hipError_t e = hipMalloc(&c->gws, need);
+        if (e != hipSuccess) return fail(GFL_ENOMEM, std::string("grouped workspace hipMalloc: ") + hipGetErrorString(e));
+        c->gws_bytes = need;
+    }
+    char* b = static_cast<char*>(c->gws);
+    int* ip = reinterpret_cast<int*>(b);
+    gfl::GPlan gp;
+    gp.hdr = ip;
+    gp.cnt = gp.hdr + 4;
+    gp.off = gp.cnt + E;
+    gp.slot_pick = gp.off + E + 1;
+    gp.slot_e = gp.slot_pick + P;
+    gp.pick_slot = gp.slot_e + P;
+    gp.pick_c = gp.pick_slot + P;
+    gp.pick_job = gp.pick_c + P;
+    gp.tok_slot = gp.pick_job + P;
+    gp.tok_w = reinterpret_cast<float*>(gp.tok_slot + P);
+    gp.tok_npk = reinterpret_cast<int*>(gp.tok_w + P);
+    uint16_t* xt = reinterpret_cast<uint16_t*>(b + b_int);
+    float* ygu = reinterpret_cast<float*>(b + b_int + b_xt);
+    uint16_t* xd = reinterpret_cast<uint16_t*>(b + b_int + b_xt + b_ygu);
+    float* yraw = reinterpret_cast<float*>(b + b_int + b_xt + b_ygu + b_xd);
+    const int r = staged(c, 2, st, [&] {
+        return gfl::launch_grouped(L.dptrs, sel, w, w_is_half ? 1 : 0, P, topk, E, H, I, L.K[0], L.K[1], L.K[2], x, gp,
+                                   P, xt, ygu, xd, yraw, c->exp_tab, act_limit, out, st);
+    });
+    if (r) return fail(GFL_ERUNTIME, "gfl_grouped_forward: launch set-up failed");
     GFL_HIP(hipGetLastError());
     c->calls += 1;
     c->picks += P;

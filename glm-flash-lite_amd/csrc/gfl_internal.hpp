@@ -8,6 +8,7 @@ namespace gfl {
 constexpr int MAX_PICKS = 1024;    // tokens * topk per forward call
 constexpr int MAX_EXPERTS = 1024;  // experts per layer (ft_split's own limit, ft_tier_cu.cu:260)
 constexpr int MAX_TOPK = 16;
+constexpr int MAX_GROUPED_PICKS = 65536;  // tokens * topk per prefill (grouped) call
 
 // Device-side routing plan of one forward call (all arrays in device memory, capacity cap_slots picks).
 struct PlanView
@@ -37,6 +38,29 @@ int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int
 size_t gate_up_lds_bytes(int K, int ns, int H, int P, int E);
 size_t down_lds_bytes(int K, int ns, int I);
 int launch_dequant(const uint8_t* tr, int k, int n, int K, uint16_t* W, hipStream_t st);
+
+// Grouped-rows plan of the prefill path (device arrays; P picks, E experts, M tokens).
+struct GPlan
+{
+    int* hdr;        // [0] slots S, [1] ids outside [-1, E)
+    int* cnt;        // [E] slots of each expert
+    int* off;        // [E + 1] slot offsets (experts ascending)
+    int* slot_pick;  // [P] pick of each slot (picks ascending within an expert)
+    int* slot_e;     // [P] expert of each slot
+    int* pick_slot;  // [P] slot of each pick, -1 when skipped
+    int* pick_c;     // [P] occurrence of the pick among its expert's picks
+    int* pick_job;   // [P] reference job number of the pick (combine order)
+    int* tok_slot;   // [M][topk] slots of each token in combine order
+    float* tok_w;    // [M][topk] their routing weights (fp32)
+    int* tok_npk;    // [M] valid picks of each token
+};
+
+// Prefill-sized layer forward with MFMA grouped GEMMs (k_prefill.hip): xt [2][cap][H] fp16, ygu [2][cap][I] fp32,
+// xd [cap][I] fp16, yraw [cap][H] fp32 workspace, cap >= P.
+int launch_grouped(const uint64_t* ptrs, const int64_t* sel, const void* w, int w_half, int P, int topk, int E, int H,
+                   int I, int Kg, int Ku, int Kd, const uint16_t* x, const GPlan& g, int cap, uint16_t* xt, float* ygu,
+                   uint16_t* xd, float* yraw, const float* exp_tab, float act_limit, float* out, hipStream_t st);
+size_t grouped_gemm_lds_bytes(int K);
 
 int launch_split(const int64_t* sel, const uint16_t* w, const uint16_t* z, int n, int bsz, int topk, int H, int E,
                  int first, const int32_t* slotof, const float* score, const float* pol, int64_t* ctrl, uint16_t* hx,

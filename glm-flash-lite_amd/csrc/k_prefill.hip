@@ -1,0 +1,506 @@
+// Prefill-sized routed-MoE layer on gfx950: grouped rows, the input transforms, two MFMA grouped GEMMs on trellis
+// tiles decoded into registers, SwiGLU, output transform and weighted combine.
+//
+// The decode path (k_moe.hip) reproduces the reference's EXACT accumulation order, which keeps every product in a
+// sequential fp32 chain; at prefill sizes (thousands of tokens) that order is an MFMA-free GEMM. This path instead
+// accumulates with v_mfma_f32_16x16x16_f16: dequantized weights are the same bit-exact fp16 values, every rounding
+// point of the reference's transforms is kept (prep_block, out_block, act_mul; ft_core.h:96-132), but the sums over
+// the hidden dimension are formed in MFMA order. Its outputs therefore differ from EXACT by accumulation rounding
+// only, the same way the reference's own fp64 expert does (ref_expert, ft_core.h:1674-1691).
+//
+// Operand layout: the trellis decode leaves lane l = 16q + n holding the four weights of column n at tile rows
+// 2q + {0, 1, 8, 9}. That is exactly the B slice of lane l in v_mfma_f32_16x16x16_f16 when the k index 4q + jj stands
+// for tile row 2q + {0, 1, 8, 9}[jj]; the inputs are stored with the same row permutation ([tk][q][jj] per tile row),
+// so each decoded tile feeds the MFMA directly, with no transpose.
+#include "gfl_device.hpp"
+#include "gfl_internal.hpp"
+
+namespace gfl {
+
+// ---------------------------------------------------------------------------------------------------------------
+// grouped rows (tier_lut_build_grouped_rows semantics, ft_tier_ext.cpp:1047-1097) and the combine order
+// ---------------------------------------------------------------------------------------------------------------
+
+// Element r (0..127) of a 128-block -> its position in the GEMM input layout [tk][q][jj] (16 per tile row).
+__device__ inline int gp_perm_pos(int b, int r)
+{
+    const int tk = b * 8 + (r >> 4), rho = r & 15;
+    const int jj = (rho & 1) + 2 * (rho >> 3), q = (rho & 7) >> 1;
+    return (tk * 4 + q) * 4 + jj;
+}
+
+constexpr int GP_PLAN_THREADS = 1024;
+
+// One workgroup of 1024 threads. Slots are expert-major, experts ascending, picks (hence tokens) ascending within an
+// expert; picks with ids outside [0, E) are skipped (counted in hdr[1]). The combine order of a token's picks is the
+// reference's job order: moe_forward (ft_core.h:1343-1349) scans picks token-major and opens a job for an expert at
+// its first pick and after every 8 of its picks, so pick p (the c-th of its expert) lands in the job opened by that
+// expert's pick number c - c % 8, and jobs are numbered in the order their opening picks appear.
+__global__ __launch_bounds__(GP_PLAN_THREADS) void gp_plan_kernel(const int64_t* __restrict__ sel, const void* w,
+                                                                  int w_half, int P, int topk, int E, GPlan g)
+{
+    __shared__ int s_cnt[MAX_EXPERTS];      // per-expert count during the scan, then running rank
+    __shared__ int s_off[MAX_EXPERTS + 1];
+    __shared__ unsigned char s_wcnt[GP_PLAN_THREADS / 64][MAX_EXPERTS];   // per-wave group sizes (<= 64)
+    __shared__ int s_scan[GP_PLAN_THREADS];
+    __shared__ int s_bad, s_carry;
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6, NWV = GP_PLAN_THREADS / 64;
+    for (int e = t; e < E; e += GP_PLAN_THREADS) s_cnt[e] = 0;
+    if (t == 0) { s_bad = 0; s_carry = 0; }
+    __syncthreads();
+    // counts
+    for (int p = t; p < P; p += GP_PLAN_THREADS)
+    {
+        const int64_t e = sel[p];
+        if (e >= 0 && e < E) atomicAdd(&s_cnt[(int)e], 1);
+        else if (e != -1) atomicAdd(&s_bad, 1);
+    }
+    __syncthreads();
+    // exclusive scan of the counts (E <= 1024 = blockDim)
+    {
+        const int v = t < E ? s_cnt[t] : 0;
+        s_scan[t] = v;
+        __syncthreads();
+        for (int d = 1; d < GP_PLAN_THREADS; d <<= 1)
+        {
+            const int o = t >= d ? s_scan[t - d] : 0;
+            __syncthreads();
+            s_scan[t] += o;
+            __syncthreads();
+        }
+        if (t < E)
+        {
+            s_off[t] = s_scan[t] - v;
+            g.off[t] = s_scan[t] - v;
+            g.cnt[t] = v;
+            s_cnt[t] = 0;   // becomes the running rank
+        }
+        if (t == 0)
+        {
+            s_off[E] = s_scan[E - 1];
+            g.off[E] = s_scan[E - 1];
+            g.hdr[0] = s_scan[E - 1];
+            g.hdr[1] = s_bad;
+        }
+    }
+    for (int i = t; i < NWV * E; i += GP_PLAN_THREADS) (&s_wcnt[0][0])[(i / E) * MAX_EXPERTS + i % E] = 0;
+    __syncthreads();
+    // stable placement, 1024 picks per round: rank = running count + same-expert picks of earlier waves in the round
+    // + same-expert lanes below in the wave (ten ballots on the id bits, E <= 1024)
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    for (int p0 = 0; p0 < P; p0 += GP_PLAN_THREADS)
+    {
+        const int p = p0 + t;
+        const int64_t e64 = p < P ? sel[p] : -1;
+        const bool ok = e64 >= 0 && e64 < E;
+        const int e = ok ? (int)e64 : 0;
+        uint64_t eq = __ballot(ok);
+#pragma unroll
+        for (int b = 0; b < 10; ++b)
+        {
+            const bool bit = ok && ((e >> b) & 1);
+            const uint64_t m = __ballot(bit);
+            eq &= bit ? m : ~m;
+        }
+        const int cin = __popcll(eq & below);
+        if (ok && cin == 0) s_wcnt[wv][e] = (unsigned char)__popcll(eq);   // lowest lane of the group
+        __syncthreads();
+        int r = -1;
+        if (ok)
+        {
+            r = s_cnt[e] + cin;
+            for (int v = 0; v < wv; ++v) r += s_wcnt[v][e];
+        }
+        __syncthreads();
+        if (ok && cin == 0)
+        {
+            atomicAdd(&s_cnt[e], __popcll(eq));
+        }
+        __syncthreads();
+        if (ok && cin == 0) s_wcnt[wv][e] = 0;
+        if (p < P)
+        {
+            if (ok)
+            {
+                const int s = s_off[e] + r;
+                g.slot_pick[s] = p;
+                g.slot_e[s] = e;
+                g.pick_slot[p] = s;
+                g.pick_c[p] = r;
+            }
+            else g.pick_slot[p] = -1;
+        }
+        __syncthreads();
+    }
+    __threadfence_block();
+    __syncthreads();
+    // job numbers: exclusive prefix count of job-opening picks (c % 8 == 0) in pick order
+    for (int p0 = 0; p0 < P; p0 += GP_PLAN_THREADS)
+    {
+        const int p = p0 + t;
+        const int opener = (p < P && g.pick_slot[p] >= 0 && (g.pick_c[p] & 7) == 0) ? 1 : 0;
+        s_scan[t] = opener;
+        __syncthreads();
+        for (int d = 1; d < GP_PLAN_THREADS; d <<= 1)
+        {
+            const int o = t >= d ? s_scan[t - d] : 0;
+            __syncthreads();
+            s_scan[t] += o;
+            __syncthreads();
+        }
+        if (opener) g.pick_job[p] = s_carry + s_scan[t] - 1;
+        __syncthreads();
+        if (t == GP_PLAN_THREADS - 1) s_carry += s_scan[t];
+        __syncthreads();
+    }
+    __threadfence_block();
+    __syncthreads();
+    // every pick inherits its job from the pick that opened it
+    for (int p = t; p < P; p += GP_PLAN_THREADS)
+    {
+        const int s = g.pick_slot[p];
+        if (s < 0) continue;
+        const int e = g.slot_e[s], c = g.pick_c[p];
+        const int opener = g.slot_pick[s_off[e] + (c & ~7)];
+        if (opener != p) g.pick_job[p] = g.pick_job[opener];
+    }
+    __threadfence_block();
+    __syncthreads();
+    // each token's picks in (job, pick) order with their fp32 weights
+    const int M = P / topk;
+    for (int tk = t; tk < M; tk += GP_PLAN_THREADS)
+    {
+        int n = 0;
+        for (int k = 0; k < topk; ++k) n += g.pick_slot[tk * topk + k] >= 0;
+        g.tok_npk[tk] = n;
+        for (int k = 0; k < topk; ++k)
+        {
+            const int p = tk * topk + k;
+            const int s = g.pick_slot[p];
+            if (s < 0) continue;
+            const int jb = g.pick_job[p];
+            int r = 0;
+            for (int k2 = 0; k2 < topk; ++k2)
+            {
+                const int q = tk * topk + k2;
+                if (g.pick_slot[q] < 0) continue;
+                const int jq = g.pick_job[q];
+                r += (jq < jb) || (jq == jb && q < p);
+            }
+            g.tok_slot[tk * topk + r] = s;
+            g.tok_w[tk * topk + r] = w_half ? h2f_bits(reinterpret_cast<const uint16_t*>(w)[p])
+                                            : reinterpret_cast<const float*>(w)[p];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// transforms, one wave per (slot, 128-block), exact rounding points
+// ---------------------------------------------------------------------------------------------------------------
+
+constexpr int GP_TW = 4;   // waves per transform workgroup
+
+// prep_block (ft_core.h:97-102) of the gate and up inputs of every slot: item = (slot, block, matrix)
+__global__ __launch_bounds__(GP_TW * 64) void gp_prep_kernel(const uint64_t* __restrict__ ptrs,
+                                                             const uint16_t* __restrict__ x, int H, int topk, int cap,
+                                                             GPlan g, uint16_t* __restrict__ xt)
+{
+    const int lane = threadIdx.x & 63;
+    const int nblk = H / 128;
+    const int item = blockIdx.x * GP_TW + (threadIdx.x >> 6);
+    const int mat = item & 1, rest = item >> 1, s = rest / nblk, b = rest % nblk;
+    if (s >= g.hdr[0]) return;
+    const int e = g.slot_e[s], tok = g.slot_pick[s] / topk;
+    const uint16_t* suh = reinterpret_cast<const uint16_t*>(ptrs[(size_t)e * 9 + 3 + 2 * mat]);
+    const uint16_t* xr = x + (size_t)tok * H + b * 128;
+    float v0 = h2f_bits(xr[lane]), v1 = h2f_bits(xr[lane + 64]);
+    prep_block_wave(v0, v1, h2f_bits(suh[b * 128 + lane]), h2f_bits(suh[b * 128 + lane + 64]));
+    uint16_t* dst = xt + ((size_t)mat * cap + s) * H;
+    dst[gp_perm_pos(b, lane)] = (uint16_t)f2h_bits(v0);
+    dst[gp_perm_pos(b, lane + 64)] = (uint16_t)f2h_bits(v1);
+}
+
+// fwd_phase phase 1 (ft_core.h:974-991) per (slot, 128-block of I): out_block of gate and up, r16(act_mul), down
+// prep_block, stored in the GEMM input layout
+__global__ __launch_bounds__(GP_TW * 64) void gp_act_kernel(const uint64_t* __restrict__ ptrs, int I, int cap, GPlan g,
+                                                            const float* __restrict__ ygu, const float* exp_tab,
+                                                            float act_limit, uint16_t* __restrict__ xd)
+{
+    const int lane = threadIdx.x & 63;
+    const int nbi = I / 128;
+    const int item = blockIdx.x * GP_TW + (threadIdx.x >> 6);
+    const int s = item / nbi, b = item % nbi;
+    if (s >= g.hdr[0]) return;
+    const int e = g.slot_e[s];
+    const uint16_t* svh_g = reinterpret_cast<const uint16_t*>(ptrs[(size_t)e * 9 + 4]);
+    const uint16_t* svh_u = reinterpret_cast<const uint16_t*>(ptrs[(size_t)e * 9 + 6]);
+    const uint16_t* suh_d = reinterpret_cast<const uint16_t*>(ptrs[(size_t)e * 9 + 7]);
+    const float* yg = ygu + (size_t)s * I + b * 128;
+    const float* yu = ygu + ((size_t)cap + s) * I + b * 128;
+    float g0 = yg[lane], g1 = yg[lane + 64], u0 = yu[lane], u1 = yu[lane + 64];
+    out_block_wave(g0, g1, h2f_bits(svh_g[b * 128 + lane]), h2f_bits(svh_g[b * 128 + lane + 64]));
+    out_block_wave(u0, u1, h2f_bits(svh_u[b * 128 + lane]), h2f_bits(svh_u[b * 128 + lane + 64]));
+    float a0 = r16(act_mul(g0, u0, act_limit, exp_tab)), a1 = r16(act_mul(g1, u1, act_limit, exp_tab));
+    prep_block_wave(a0, a1, h2f_bits(suh_d[b * 128 + lane]), h2f_bits(suh_d[b * 128 + lane + 64]));
+    uint16_t* dst = xd + (size_t)s * I;
+    dst[gp_perm_pos(b, lane)] = (uint16_t)f2h_bits(a0);
+    dst[gp_perm_pos(b, lane + 64)] = (uint16_t)f2h_bits(a1);
+}
+
+// out_block (ft_core.h:1016) of every expert output block and the weighted sum in job order (ft_core.h:1020-1033),
+// per (token, 128-block of H); rows of tokens without a valid pick become 0
+__global__ __launch_bounds__(GP_TW * 64) void gp_comb_kernel(const uint64_t* __restrict__ ptrs, int H, int M, int topk,
+                                                             GPlan g, const float* __restrict__ yraw,
+                                                             float* __restrict__ out)
+{
+    const int lane = threadIdx.x & 63;
+    const int nbh = H / 128;
+    const int item = blockIdx.x * GP_TW + (threadIdx.x >> 6);
+    const int tok = item / nbh, b = item % nbh;
+    if (tok >= M) return;
+    const int npk = g.tok_npk[tok];
+    float o0 = 0.f, o1 = 0.f;
+    for (int k = 0; k < npk; ++k)
+    {
+        const int s = g.tok_slot[tok * topk + k];
+        const float wk = g.tok_w[tok * topk + k];
+        const uint16_t* svh = reinterpret_cast<const uint16_t*>(ptrs[(size_t)g.slot_e[s] * 9 + 8]);
+        const float* yr = yraw + (size_t)s * H + b * 128;
+        float v0 = yr[lane], v1 = yr[lane + 64];
+        out_block_wave(v0, v1, h2f_bits(svh[b * 128 + lane]), h2f_bits(svh[b * 128 + lane + 64]));
+        o0 = o0 + wk * v0;
+        o1 = o1 + wk * v1;
+    }
+    out[(size_t)tok * H + b * 128 + lane] = o0;
+    out[(size_t)tok * H + b * 128 + lane + 64] = o1;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// MFMA grouped GEMM: y[slot][n] = sum_k x[slot][k] W_e[k][n] for every slot of every expert
+// ---------------------------------------------------------------------------------------------------------------
+
+constexpr int GP_NW = 16;          // waves per GEMM workgroup, one tile column each: 256 output columns
+constexpr int GP_MT = 64;          // slots per pass (4 MFMA row blocks)
+constexpr int GP_NG = 4;           // ring depth (groups of 8 tile rows) of the trellis and input rings
+constexpr int GP_XS = 132;         // fp16 stride of one slot's group chunk in LDS (128 + 4: spreads the banks)
+
+typedef __attribute__((address_space(3))) void gp_lds_void;
+
+template <int N>
+__device__ __forceinline__ void gp_wait_vmcnt()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+struct GemmArgs
+{
+    const uint64_t* ptrs;
+    int mat_base;              // matrix of blockIdx.y == 0 (0 gate, 1 up, 2 down)
+    int kdim, ndim, cap, E;
+    GPlan g;
+    const uint16_t* xin;       // [mats][cap][kdim] fp16, GEMM input layout
+    float* yout;               // [mats][cap][ndim] fp32
+};
+
+// Grid: (E * ndim / 256, matrices). Workgroup = 16 waves = 256 output columns of one matrix of one expert; the
+// expert's slots go through in passes of 64. Per group of 8 tile rows every wave decodes its tile column's 8 tiles
+// and runs 4 MFMAs per tile (one per 16 slots). The tiles stream through per-wave LDS rings and the slots' inputs
+// through a shared ring, both filled by LDS-direct loads GP_NG - 1 groups ahead; two workgroup barriers per group
+// (inputs landed / inputs consumed).
+template <int K>
+__global__ __launch_bounds__(GP_NW * 64) void gp_gemm_kernel(GemmArgs a)
+{
+    constexpr int TB = 32 * K, GB = 8 * TB, NG = GP_NG;
+    extern __shared__ __align__(16) uint8_t gp_lds[];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nch = a.ndim / (16 * GP_NW);
+    const int e = blockIdx.x / nch, nc = blockIdx.x % nch;
+    const int mat = a.mat_base + blockIdx.y;
+    const int s_begin = a.g.off[e], s_end = a.g.off[e + 1];
+    if (s_begin >= s_end) return;
+    const int TN = a.ndim / 16, TK = a.kdim / 16, ngroups = TK / 8;
+    const int t = nc * GP_NW + wave;                                  // this wave's tile column
+    uint8_t* ring = gp_lds + wave * NG * GB;                          // [NG][8 tiles]
+    uint16_t* xring = reinterpret_cast<uint16_t*>(gp_lds + GP_NW * NG * GB);   // [NG][64 slots][GP_XS]
+    const uint8_t* tr = reinterpret_cast<const uint8_t*>(a.ptrs[(size_t)e * 9 + mat]);
+    const size_t gstride = (size_t)TN * TB;
+    uint8_t* cb = const_cast<uint8_t*>(uniform_ptr(tr + (size_t)t * TB));
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(cb, (short)0, (int)((size_t)TK * gstride),
+                                                                        0x00020000);
+    const int gs = (int)gstride;
+    int voff[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i)
+    {
+        const int byte = i * 256 + lane * 4;
+        voff[i] = (byte / TB) * gs + (byte % TB);
+    }
+    const LaneDec d = lane_dec(lane, K);
+    const uint16_t* xin = a.xin + (size_t)(mat - a.mat_base) * a.cap * a.kdim;
+    float* yout = a.yout + (size_t)(mat - a.mat_base) * a.cap * a.ndim;
+    const int q = lane >> 4, i16 = lane & 15;
+
+    for (int c0 = s_begin; c0 < s_end; c0 += GP_MT)
+    {
+        const int T = min(GP_MT, s_end - c0);
+        // the input chunk of group g for this wave's 4 slots (slots past the pass read the pass's last slot)
+        const uint8_t* xbase[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+        {
+            const int sl = min(wave * 4 + j, T - 1);
+            xbase[j] = reinterpret_cast<const uint8_t*>(xin + (size_t)(c0 + sl) * a.kdim);
+        }
+        auto issue = [&](int g) {
+            uint8_t* dst = ring + (g % NG) * GB;
+#pragma unroll
+            for (int i = 0; i < K; ++i)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (gp_lds_void*)(dst + i * 256), 4, voff[i], g * 8 * gs, 0,
+                                                         0);
+            uint16_t* xd = xring + (size_t)(g % NG) * GP_MT * GP_XS;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(xbase[j] + g * 256 + lane * 4),
+                                                 (gp_lds_void*)(xd + (wave * 4 + j) * GP_XS), 4, 0, 0);
+        };
+        float4v acc[4];
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) acc[mb] = float4v{ 0.f, 0.f, 0.f, 0.f };
+        __syncthreads();   // previous pass done with the rings
+#pragma unroll
+        for (int g = 0; g < NG - 1; ++g)
+            if (g < ngroups) issue(g);
+        for (int g = 0; g < ngroups; ++g)
+        {
+            if (g + NG - 1 < ngroups)
+            {
+                issue(g + NG - 1);
+                gp_wait_vmcnt<(NG - 1) * (K + 4)>();   // this wave's loads of group g landed
+            }
+            else gp_wait_vmcnt<0>();
+            __syncthreads();   // every wave's loads of group g landed
+            const uint8_t* sl = ring + (g % NG) * GB;
+            const uint16_t* xs = xring + (size_t)(g % NG) * GP_MT * GP_XS;
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+            {
+                const uint8_t* tp = sl + r * TB;
+                const half4 B = decode4<K>(*reinterpret_cast<const uint32_t*>(tp + d.o0),
+                                           *reinterpret_cast<const uint32_t*>(tp + d.o1), d.sh);
+#pragma unroll
+                for (int mb = 0; mb < 4; ++mb)
+                {
+                    const half4 A = *reinterpret_cast<const half4*>(xs + (mb * 16 + i16) * GP_XS + r * 16 + q * 4);
+                    acc[mb] = __builtin_amdgcn_mfma_f32_16x16x16f16(A, B, acc[mb], 0, 0, 0);
+                }
+            }
+            __syncthreads();   // every wave is done with group g's input slot and its own ring slot
+        }
+        // D[i][n]: lane holds rows 4q + rr of each 16-slot block, column t*16 + i16
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+            {
+                const int sl = mb * 16 + q * 4 + rr;
+                if (sl < T) yout[(size_t)(c0 + sl) * a.ndim + t * 16 + i16] = acc[mb][rr];
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------------------------------------------
+
+template <int K>
+static size_t gp_gemm_lds()
+{
+    return (size_t)GP_NW * GP_NG * 8 * 32 * K + (size_t)GP_NG * GP_MT * GP_XS * 2;
+}
+
+template <int K>
+static int gp_gemm_launch(const GemmArgs& a, int nmat, hipStream_t st)
+{
+    static int lds_set = 0;
+    const size_t lds = gp_gemm_lds<K>();
+    if ((int)lds > lds_set)
+    {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(gp_gemm_kernel<K>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+            return -1;
+        lds_set = (int)lds;
+    }
+    hipLaunchKernelGGL(gp_gemm_kernel<K>, dim3(a.E * (a.ndim / (16 * GP_NW)), nmat), dim3(GP_NW * 64), lds, st, a);
+    return 0;
+}
+
+static int gp_gemm(int K, const GemmArgs& a, int nmat, hipStream_t st)
+{
+    switch (K)
+    {
+        case 2: return gp_gemm_launch<2>(a, nmat, st);
+        case 3: return gp_gemm_launch<3>(a, nmat, st);
+        case 4: return gp_gemm_launch<4>(a, nmat, st);
+        case 5: return gp_gemm_launch<5>(a, nmat, st);
+        default: return -1;
+    }
+}
+
+int launch_grouped(const uint64_t* ptrs, const int64_t* sel, const void* w, int w_half, int P, int topk, int E, int H,
+                   int I, int Kg, int Ku, int Kd, const uint16_t* x, const GPlan& g, int cap, uint16_t* xt, float* ygu,
+                   uint16_t* xd, float* yraw, const float* exp_tab, float act_limit, float* out, hipStream_t st)
+{
+    const int M = P / topk;
+    hipLaunchKernelGGL(gp_plan_kernel, dim3(1), dim3(GP_PLAN_THREADS), 0, st, sel, w, w_half, P, topk, E, g);
+    {
+        const long items = (long)P * (H / 128) * 2;
+        hipLaunchKernelGGL(gp_prep_kernel, dim3((unsigned)((items + GP_TW - 1) / GP_TW)), dim3(GP_TW * 64), 0, st, ptrs,
+                           x, H, topk, cap, g, xt);
+    }
+    GemmArgs a;
+    a.ptrs = ptrs; a.kdim = H; a.ndim = I; a.cap = cap; a.E = E; a.g = g; a.xin = xt; a.yout = ygu;
+    if (Kg == Ku)
+    {
+        a.mat_base = 0;
+        if (gp_gemm(Kg, a, 2, st)) return -1;
+    }
+    else
+    {
+        a.mat_base = 0;
+        if (gp_gemm(Kg, a, 1, st)) return -1;
+        GemmArgs b = a;
+        b.mat_base = 1;
+        b.xin = xt + (size_t)cap * H;
+        b.yout = ygu + (size_t)cap * I;
+        if (gp_gemm(Ku, b, 1, st)) return -1;
+    }
+    {
+        const long items = (long)P * (I / 128);
+        hipLaunchKernelGGL(gp_act_kernel, dim3((unsigned)((items + GP_TW - 1) / GP_TW)), dim3(GP_TW * 64), 0, st, ptrs,
+                           I, cap, g, ygu, exp_tab, act_limit, xd);
+    }
+    GemmArgs c = a;
+    c.mat_base = 2; c.kdim = I; c.ndim = H; c.xin = xd; c.yout = yraw;
+    if (gp_gemm(Kd, c, 1, st)) return -1;
+    {
+        const long items = (long)M * (H / 128);
+        hipLaunchKernelGGL(gp_comb_kernel, dim3((unsigned)((items + GP_TW - 1) / GP_TW)), dim3(GP_TW * 64), 0, st, ptrs,
+                           H, M, topk, g, yraw, out);
+    }
+    return 0;
+}
+
+size_t grouped_gemm_lds_bytes(int K)
+{
+    switch (K)
+    {
+        case 2: return gp_gemm_lds<2>();
+        case 3: return gp_gemm_lds<3>();
+        case 4: return gp_gemm_lds<4>();
+        case 5: return gp_gemm_lds<5>();
+        default: return 0;
+    }
+}
+
+}  // namespace gfl

@@ -72,6 +72,17 @@ int gfl_moe_forward(gfl_ctx* ctx, int li, const uint16_t* x, const int64_t* sel,
  * gfl_moe_forward accumulates (default: 1 at M = 1, else 2; an expert with more slots takes more passes). Read once
  * by gfl_ctx_create. */
 
+/* Routed-expert forward of one layer for prefill-sized M (the north star's MFMA grouped GEMM), same arguments and
+ * result layout as gfl_moe_forward: x fp16 [M, H], sel int64 [M, topk] (ids outside [0, E) skipped), w fp16 or fp32
+ * [M, topk], out fp32 [M, H]; M*topk <= 65536. Rows are grouped expert-major (tier_lut_build_grouped_rows,
+ * kernels/cpu_avx2/ft_tier_ext.cpp:1047-1097), gate|up and down run as v_mfma_f32_16x16x16_f16 grouped GEMMs on the
+ * bit-exact dequantized fp16 weights, the transforms keep the reference's fp16 rounding points and the combine its job
+ * order (kernels/cpu_avx2/ft_core.h:933-1033). The hidden-dimension sums are formed in MFMA order, so results differ
+ * from the EXACT mode of gfl_moe_forward by fp32 accumulation rounding (as the reference's own fp64 expert,
+ * ref_expert, ft_core.h:1674-1691, does). Profiling stage 2. */
+int gfl_grouped_forward(gfl_ctx* ctx, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half,
+                        int M, int topk, float* out, float act_limit, gfl_stream stream);
+
 /* Dequantize one trellis matrix to fp16 W[k][n] (dense_weights, kernels/cpu_avx2/ft_core.h:1657-1672). */
 int gfl_dequant(const void* trellis, int k, int n, int K, uint16_t* out, gfl_stream stream);
 
