@@ -360,8 +360,8 @@ int gfl_grouped_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* se
     gp.slot_e = gp.slot_pick + P;
     gp.pick_slot = gp.slot_e + P;
     gp.pick_c = gp.pick_slot + P;
-    gp.pick_job = gp.pick_c + P;
-    gp.tok_slot = gp.pick_job + P;
+    gp.slot_job = gp.pick_c + P;
+    gp.tok_slot = gp.slot_job + P;
     gp.tok_w = reinterpret_cast<float*>(gp.tok_slot + P);
     gp.tok_npk = reinterpret_cast<int*>(gp.tok_w + P);
     uint16_t* xt = reinterpret_cast<uint16_t*>(b + b_int);

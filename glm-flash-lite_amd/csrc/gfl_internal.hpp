@@ -49,7 +49,7 @@ struct GPlan
     int* slot_e;     // [P] expert of each slot
     int* pick_slot;  // [P] slot of each pick, -1 when skipped
     int* pick_c;     // [P] occurrence of the pick among its expert's picks
-    int* pick_job;   // [P] reference job number of the pick (combine order)
+    int* slot_job;   // [P] reference job number (combine order), set at the slots of job-opening picks
     int* tok_slot;   // [M][topk] slots of each token in combine order
     float* tok_w;    // [M][topk] their routing weights (fp32)
     int* tok_npk;    // [M] valid picks of each token

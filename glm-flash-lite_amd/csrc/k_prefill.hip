@@ -3,7 +3,7 @@
 //
 // The decode path (k_moe.hip) reproduces the reference's EXACT accumulation order, which keeps every product in a
 // sequential fp32 chain; at prefill sizes (thousands of tokens) that order is an MFMA-free GEMM. This path instead
-// accumulates with v_mfma_f32_16x16x16_f16: dequantized weights are the same bit-exact fp16 values, every rounding
+// accumulates with v_mfma_f32_16x16x32_f16: dequantized weights are the same bit-exact fp16 values, every rounding
 // point of the reference's transforms is kept (prep_block, out_block, act_mul; ft_core.h:96-132), but the sums over
 // the hidden dimension are formed in MFMA order. Its outputs therefore differ from EXACT by accumulation rounding
 // only, the same way the reference's own fp64 expert does (ref_expert, ft_core.h:1674-1691).
@@ -11,7 +11,8 @@
 // Operand layout: the trellis decode leaves lane l = 16q + n holding the four weights of column n at tile rows
 // 2q + {0, 1, 8, 9}. That is exactly the B slice of lane l in v_mfma_f32_16x16x16_f16 when the k index 4q + jj stands
 // for tile row 2q + {0, 1, 8, 9}[jj]; the inputs are stored with the same row permutation ([tk][q][jj] per tile row),
-// so each decoded tile feeds the MFMA directly, with no transpose.
+// so each decoded tile feeds the MFMA directly, with no transpose. gfx950's v_mfma_f32_16x16x32_f16 takes two such
+// slices (tile rows r and r + 1) per lane as its 8 k-values.
 #include "gfl_device.hpp"
 #include "gfl_internal.hpp"
 
@@ -21,39 +22,55 @@ namespace gfl {
 // grouped rows (tier_lut_build_grouped_rows semantics, ft_tier_ext.cpp:1047-1097) and the combine order
 // ---------------------------------------------------------------------------------------------------------------
 
-// Element r (0..127) of a 128-block -> its position in the GEMM input layout [tk][q][jj] (16 per tile row).
+// Element r (0..127) of a 128-block (= one group of 8 tile rows) -> its position in the GEMM input layout
+// [block][q][tile row][jj]: row rho = r % 16 of tile row r / 16 is MFMA k-slot jj = (rho&1) + 2*(rho>>3) of lane group
+// q = (rho&7)>>1, so the 4 k-slots of two consecutive tile rows of one q are 8 contiguous fp16.
 __device__ inline int gp_perm_pos(int b, int r)
 {
-    const int tk = b * 8 + (r >> 4), rho = r & 15;
+    const int tr = r >> 4, rho = r & 15;
     const int jj = (rho & 1) + 2 * (rho >> 3), q = (rho & 7) >> 1;
-    return (tk * 4 + q) * 4 + jj;
+    return b * 128 + q * 32 + tr * 4 + jj;
 }
 
 constexpr int GP_PLAN_THREADS = 1024;
+constexpr int GP_PLAN_WAVES = GP_PLAN_THREADS / 64;
 
 // One workgroup of 1024 threads. Slots are expert-major, experts ascending, picks (hence tokens) ascending within an
-// expert; picks with ids outside [0, E) are skipped (counted in hdr[1]). The combine order of a token's picks is the
-// reference's job order: moe_forward (ft_core.h:1343-1349) scans picks token-major and opens a job for an expert at
-// its first pick and after every 8 of its picks, so pick p (the c-th of its expert) lands in the job opened by that
-// expert's pick number c - c % 8, and jobs are numbered in the order their opening picks appear.
+// expert; picks with ids outside [0, E) are skipped (ids other than -1 are counted in hdr[1]). The combine order of a
+// token's picks is the reference's job order: moe_forward (ft_core.h:1343-1349) scans picks token-major and opens a
+// job for an expert at its first pick and after every 8 of its picks, so pick p (the c-th of its expert) lands in the
+// job opened by that expert's pick number c - c % 8, and jobs are numbered in the order their opening picks appear.
+// Picks are placed 1024 per round in pick order, so the job numbers of the opening picks are a running count over the
+// rounds; the other picks read theirs from the opening pick's slot, which sits c % 8 slots before their own.
 __global__ __launch_bounds__(GP_PLAN_THREADS) void gp_plan_kernel(const int64_t* __restrict__ sel, const void* w,
                                                                   int w_half, int P, int topk, int E, GPlan g)
 {
     __shared__ int s_cnt[MAX_EXPERTS];      // per-expert count during the scan, then running rank
     __shared__ int s_off[MAX_EXPERTS + 1];
-    __shared__ unsigned char s_wcnt[GP_PLAN_THREADS / 64][MAX_EXPERTS];   // per-wave group sizes (<= 64)
+    __shared__ unsigned char s_wcnt[GP_PLAN_WAVES][MAX_EXPERTS];   // per-wave group sizes (<= 64)
     __shared__ int s_scan[GP_PLAN_THREADS];
-    __shared__ int s_bad, s_carry;
-    const int t = threadIdx.x, lane = t & 63, wv = t >> 6, NWV = GP_PLAN_THREADS / 64;
+    __shared__ int s_wop[GP_PLAN_WAVES];    // job-opening picks of each wave in the current round
+    __shared__ int s_bad, s_jobs;
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     for (int e = t; e < E; e += GP_PLAN_THREADS) s_cnt[e] = 0;
-    if (t == 0) { s_bad = 0; s_carry = 0; }
+    if (t == 0) { s_bad = 0; s_jobs = 0; }
     __syncthreads();
-    // counts
-    for (int p = t; p < P; p += GP_PLAN_THREADS)
+    // counts (four independent loads in flight per thread)
+    for (int p0 = 0; p0 < P; p0 += 4 * GP_PLAN_THREADS)
     {
-        const int64_t e = sel[p];
-        if (e >= 0 && e < E) atomicAdd(&s_cnt[(int)e], 1);
-        else if (e != -1) atomicAdd(&s_bad, 1);
+        int64_t ev[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+        {
+            const int p = p0 + j * GP_PLAN_THREADS + t;
+            ev[j] = p < P ? sel[p] : -1;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+        {
+            if (ev[j] >= 0 && ev[j] < E) atomicAdd(&s_cnt[(int)ev[j]], 1);
+            else if (ev[j] != -1) atomicAdd(&s_bad, 1);
+        }
     }
     __syncthreads();
     // exclusive scan of the counts (E <= 1024 = blockDim)
@@ -83,15 +100,17 @@ __global__ __launch_bounds__(GP_PLAN_THREADS) void gp_plan_kernel(const int64_t*
             g.hdr[1] = s_bad;
         }
     }
-    for (int i = t; i < NWV * E; i += GP_PLAN_THREADS) (&s_wcnt[0][0])[(i / E) * MAX_EXPERTS + i % E] = 0;
+    for (int i = t; i < GP_PLAN_WAVES * E; i += GP_PLAN_THREADS) (&s_wcnt[0][0])[(i / E) * MAX_EXPERTS + i % E] = 0;
     __syncthreads();
     // stable placement, 1024 picks per round: rank = running count + same-expert picks of earlier waves in the round
     // + same-expert lanes below in the wave (ten ballots on the id bits, E <= 1024)
     const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    int64_t e_next = t < P ? sel[t] : -1;
     for (int p0 = 0; p0 < P; p0 += GP_PLAN_THREADS)
     {
         const int p = p0 + t;
-        const int64_t e64 = p < P ? sel[p] : -1;
+        const int64_t e64 = e_next;
+        e_next = p + GP_PLAN_THREADS < P ? sel[p + GP_PLAN_THREADS] : -1;   // next round's id, loaded under this one
         const bool ok = e64 >= 0 && e64 < E;
         const int e = ok ? (int)e64 : 0;
         uint64_t eq = __ballot(ok);
@@ -111,13 +130,21 @@ __global__ __launch_bounds__(GP_PLAN_THREADS) void gp_plan_kernel(const int64_t*
             r = s_cnt[e] + cin;
             for (int v = 0; v < wv; ++v) r += s_wcnt[v][e];
         }
+        const bool opener = ok && (r & 7) == 0;
+        const uint64_t om = __ballot(opener);
+        if (lane == 0) s_wop[wv] = __popcll(om);
         __syncthreads();
-        if (ok && cin == 0)
-        {
-            atomicAdd(&s_cnt[e], __popcll(eq));
-        }
+        if (ok && cin == 0) atomicAdd(&s_cnt[e], __popcll(eq));
+        int job = s_jobs + __popcll(om & below);
+        for (int v = 0; v < wv; ++v) job += s_wop[v];
         __syncthreads();
         if (ok && cin == 0) s_wcnt[wv][e] = 0;
+        if (t == 0)
+        {
+            int n = 0;
+            for (int v = 0; v < GP_PLAN_WAVES; ++v) n += s_wop[v];
+            s_jobs += n;
+        }
         if (p < P)
         {
             if (ok)
@@ -125,6 +152,7 @@ __global__ __launch_bounds__(GP_PLAN_THREADS) void gp_plan_kernel(const int64_t*
                 const int s = s_off[e] + r;
                 g.slot_pick[s] = p;
                 g.slot_e[s] = e;
+                if (opener) g.slot_job[s] = job;
                 g.pick_slot[p] = s;
                 g.pick_c[p] = r;
             }
@@ -134,60 +162,33 @@ __global__ __launch_bounds__(GP_PLAN_THREADS) void gp_plan_kernel(const int64_t*
     }
     __threadfence_block();
     __syncthreads();
-    // job numbers: exclusive prefix count of job-opening picks (c % 8 == 0) in pick order
-    for (int p0 = 0; p0 < P; p0 += GP_PLAN_THREADS)
-    {
-        const int p = p0 + t;
-        const int opener = (p < P && g.pick_slot[p] >= 0 && (g.pick_c[p] & 7) == 0) ? 1 : 0;
-        s_scan[t] = opener;
-        __syncthreads();
-        for (int d = 1; d < GP_PLAN_THREADS; d <<= 1)
-        {
-            const int o = t >= d ? s_scan[t - d] : 0;
-            __syncthreads();
-            s_scan[t] += o;
-            __syncthreads();
-        }
-        if (opener) g.pick_job[p] = s_carry + s_scan[t] - 1;
-        __syncthreads();
-        if (t == GP_PLAN_THREADS - 1) s_carry += s_scan[t];
-        __syncthreads();
-    }
-    __threadfence_block();
-    __syncthreads();
-    // every pick inherits its job from the pick that opened it
-    for (int p = t; p < P; p += GP_PLAN_THREADS)
-    {
-        const int s = g.pick_slot[p];
-        if (s < 0) continue;
-        const int e = g.slot_e[s], c = g.pick_c[p];
-        const int opener = g.slot_pick[s_off[e] + (c & ~7)];
-        if (opener != p) g.pick_job[p] = g.pick_job[opener];
-    }
-    __threadfence_block();
-    __syncthreads();
     // each token's picks in (job, pick) order with their fp32 weights
     const int M = P / topk;
     for (int tk = t; tk < M; tk += GP_PLAN_THREADS)
     {
+        // loops unrolled to MAX_TOPK with k < topk guards, so the per-pick arrays stay in registers
+        int ps[MAX_TOPK], jb[MAX_TOPK];
         int n = 0;
-        for (int k = 0; k < topk; ++k) n += g.pick_slot[tk * topk + k] >= 0;
-        g.tok_npk[tk] = n;
-        for (int k = 0; k < topk; ++k)
+#pragma unroll
+        for (int k = 0; k < MAX_TOPK; ++k)
         {
             const int p = tk * topk + k;
-            const int s = g.pick_slot[p];
-            if (s < 0) continue;
-            const int jb = g.pick_job[p];
+            const int s = k < topk ? g.pick_slot[p] : -1;
+            ps[k] = s;
+            jb[k] = s >= 0 ? g.slot_job[s - (g.pick_c[p] & 7)] : 0;
+            n += s >= 0;
+        }
+        g.tok_npk[tk] = n;
+#pragma unroll
+        for (int k = 0; k < MAX_TOPK; ++k)
+        {
+            if (ps[k] < 0) continue;
             int r = 0;
-            for (int k2 = 0; k2 < topk; ++k2)
-            {
-                const int q = tk * topk + k2;
-                if (g.pick_slot[q] < 0) continue;
-                const int jq = g.pick_job[q];
-                r += (jq < jb) || (jq == jb && q < p);
-            }
-            g.tok_slot[tk * topk + r] = s;
+#pragma unroll
+            for (int k2 = 0; k2 < MAX_TOPK; ++k2)
+                r += ps[k2] >= 0 && (jb[k2] < jb[k] || (jb[k2] == jb[k] && k2 < k));
+            const int p = tk * topk + k;
+            g.tok_slot[tk * topk + r] = ps[k];
             g.tok_w[tk * topk + r] = w_half ? h2f_bits(reinterpret_cast<const uint16_t*>(w)[p])
                                             : reinterpret_cast<const float*>(w)[p];
         }
@@ -195,84 +196,163 @@ __global__ __launch_bounds__(GP_PLAN_THREADS) void gp_plan_kernel(const int64_t*
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// transforms, one wave per (slot, 128-block), exact rounding points
+// transforms: one wave per slot (or token) walking its 128-blocks, GP_TU blocks' loads in flight; exact rounding points
 // ---------------------------------------------------------------------------------------------------------------
 
 constexpr int GP_TW = 4;   // waves per transform workgroup
+constexpr int GP_TU = 4;   // 128-blocks per step of a transform wave
 
-// prep_block (ft_core.h:97-102) of the gate and up inputs of every slot: item = (slot, block, matrix)
+// prep_block (ft_core.h:97-102) of the gate and up inputs of slot s (one wave per slot)
 __global__ __launch_bounds__(GP_TW * 64) void gp_prep_kernel(const uint64_t* __restrict__ ptrs,
                                                              const uint16_t* __restrict__ x, int H, int topk, int cap,
                                                              GPlan g, uint16_t* __restrict__ xt)
 {
     const int lane = threadIdx.x & 63;
-    const int nblk = H / 128;
-    const int item = blockIdx.x * GP_TW + (threadIdx.x >> 6);
-    const int mat = item & 1, rest = item >> 1, s = rest / nblk, b = rest % nblk;
+    const int s = blockIdx.x * GP_TW + (threadIdx.x >> 6);
     if (s >= g.hdr[0]) return;
+    const int nblk = H / 128;
     const int e = g.slot_e[s], tok = g.slot_pick[s] / topk;
-    const uint16_t* suh = reinterpret_cast<const uint16_t*>(ptrs[(size_t)e * 9 + 3 + 2 * mat]);
-    const uint16_t* xr = x + (size_t)tok * H + b * 128;
-    float v0 = h2f_bits(xr[lane]), v1 = h2f_bits(xr[lane + 64]);
-    prep_block_wave(v0, v1, h2f_bits(suh[b * 128 + lane]), h2f_bits(suh[b * 128 + lane + 64]));
-    uint16_t* dst = xt + ((size_t)mat * cap + s) * H;
-    dst[gp_perm_pos(b, lane)] = (uint16_t)f2h_bits(v0);
-    dst[gp_perm_pos(b, lane + 64)] = (uint16_t)f2h_bits(v1);
+    const uint16_t* su0 = reinterpret_cast<const uint16_t*>(ptrs[(size_t)e * 9 + 3]);
+    const uint16_t* su1 = reinterpret_cast<const uint16_t*>(ptrs[(size_t)e * 9 + 5]);
+    const uint16_t* xr = x + (size_t)tok * H;
+    uint16_t* d0 = xt + (size_t)s * H;
+    uint16_t* d1 = xt + ((size_t)cap + s) * H;
+    for (int b0 = 0; b0 < nblk; b0 += GP_TU)
+    {
+        uint16_t xv[GP_TU][2], g0[GP_TU][2], g1[GP_TU][2];
+#pragma unroll
+        for (int j = 0; j < GP_TU; ++j)
+        {
+            const int o = min(b0 + j, nblk - 1) * 128 + lane;
+            xv[j][0] = xr[o]; xv[j][1] = xr[o + 64];
+            g0[j][0] = su0[o]; g0[j][1] = su0[o + 64];
+            g1[j][0] = su1[o]; g1[j][1] = su1[o + 64];
+        }
+#pragma unroll
+        for (int j = 0; j < GP_TU; ++j)
+        {
+            const int b = b0 + j;
+            if (b >= nblk) break;
+            float u0 = h2f_bits(xv[j][0]), u1 = h2f_bits(xv[j][1]);
+            float v0 = u0, v1 = u1;
+            prep_block_wave(u0, u1, h2f_bits(g0[j][0]), h2f_bits(g0[j][1]));
+            prep_block_wave(v0, v1, h2f_bits(g1[j][0]), h2f_bits(g1[j][1]));
+            d0[gp_perm_pos(b, lane)] = (uint16_t)f2h_bits(u0);
+            d0[gp_perm_pos(b, lane + 64)] = (uint16_t)f2h_bits(u1);
+            d1[gp_perm_pos(b, lane)] = (uint16_t)f2h_bits(v0);
+            d1[gp_perm_pos(b, lane + 64)] = (uint16_t)f2h_bits(v1);
+        }
+    }
 }
 
-// fwd_phase phase 1 (ft_core.h:974-991) per (slot, 128-block of I): out_block of gate and up, r16(act_mul), down
-// prep_block, stored in the GEMM input layout
+// fwd_phase phase 1 (ft_core.h:974-991) of slot s (one wave per slot): per 128-block of I, out_block of gate and up,
+// r16(act_mul), down prep_block, stored in the GEMM input layout
 __global__ __launch_bounds__(GP_TW * 64) void gp_act_kernel(const uint64_t* __restrict__ ptrs, int I, int cap, GPlan g,
                                                             const float* __restrict__ ygu, const float* exp_tab,
                                                             float act_limit, uint16_t* __restrict__ xd)
 {
     const int lane = threadIdx.x & 63;
-    const int nbi = I / 128;
-    const int item = blockIdx.x * GP_TW + (threadIdx.x >> 6);
-    const int s = item / nbi, b = item % nbi;
+    const int s = blockIdx.x * GP_TW + (threadIdx.x >> 6);
     if (s >= g.hdr[0]) return;
+    const int nbi = I / 128;
     const int e = g.slot_e[s];
     const uint16_t* svh_g = reinterpret_cast<const uint16_t*>(ptrs[(size_t)e * 9 + 4]);
     const uint16_t* svh_u = reinterpret_cast<const uint16_t*>(ptrs[(size_t)e * 9 + 6]);
     const uint16_t* suh_d = reinterpret_cast<const uint16_t*>(ptrs[(size_t)e * 9 + 7]);
-    const float* yg = ygu + (size_t)s * I + b * 128;
-    const float* yu = ygu + ((size_t)cap + s) * I + b * 128;
-    float g0 = yg[lane], g1 = yg[lane + 64], u0 = yu[lane], u1 = yu[lane + 64];
-    out_block_wave(g0, g1, h2f_bits(svh_g[b * 128 + lane]), h2f_bits(svh_g[b * 128 + lane + 64]));
-    out_block_wave(u0, u1, h2f_bits(svh_u[b * 128 + lane]), h2f_bits(svh_u[b * 128 + lane + 64]));
-    float a0 = r16(act_mul(g0, u0, act_limit, exp_tab)), a1 = r16(act_mul(g1, u1, act_limit, exp_tab));
-    prep_block_wave(a0, a1, h2f_bits(suh_d[b * 128 + lane]), h2f_bits(suh_d[b * 128 + lane + 64]));
+    const float* yg = ygu + (size_t)s * I;
+    const float* yu = ygu + ((size_t)cap + s) * I;
     uint16_t* dst = xd + (size_t)s * I;
-    dst[gp_perm_pos(b, lane)] = (uint16_t)f2h_bits(a0);
-    dst[gp_perm_pos(b, lane + 64)] = (uint16_t)f2h_bits(a1);
+    for (int b0 = 0; b0 < nbi; b0 += GP_TU)
+    {
+        float gv[GP_TU][2], uv[GP_TU][2];
+        uint16_t sg[GP_TU][2], su[GP_TU][2], sd[GP_TU][2];
+#pragma unroll
+        for (int j = 0; j < GP_TU; ++j)
+        {
+            const int o = min(b0 + j, nbi - 1) * 128 + lane;
+            gv[j][0] = yg[o]; gv[j][1] = yg[o + 64];
+            uv[j][0] = yu[o]; uv[j][1] = yu[o + 64];
+            sg[j][0] = svh_g[o]; sg[j][1] = svh_g[o + 64];
+            su[j][0] = svh_u[o]; su[j][1] = svh_u[o + 64];
+            sd[j][0] = suh_d[o]; sd[j][1] = suh_d[o + 64];
+        }
+#pragma unroll
+        for (int j = 0; j < GP_TU; ++j)
+        {
+            const int b = b0 + j;
+            if (b >= nbi) break;
+            float g0 = gv[j][0], g1 = gv[j][1], u0 = uv[j][0], u1 = uv[j][1];
+            out_block_wave(g0, g1, h2f_bits(sg[j][0]), h2f_bits(sg[j][1]));
+            out_block_wave(u0, u1, h2f_bits(su[j][0]), h2f_bits(su[j][1]));
+            float a0 = r16(act_mul(g0, u0, act_limit, exp_tab)), a1 = r16(act_mul(g1, u1, act_limit, exp_tab));
+            prep_block_wave(a0, a1, h2f_bits(sd[j][0]), h2f_bits(sd[j][1]));
+            dst[gp_perm_pos(b, lane)] = (uint16_t)f2h_bits(a0);
+            dst[gp_perm_pos(b, lane + 64)] = (uint16_t)f2h_bits(a1);
+        }
+    }
 }
 
 // out_block (ft_core.h:1016) of every expert output block and the weighted sum in job order (ft_core.h:1020-1033),
-// per (token, 128-block of H); rows of tokens without a valid pick become 0
+// one wave per token; lane k < npk holds the token's k-th pick (slot, weight, output scales), read back per pick with
+// readlane. Rows of tokens without a valid pick become 0.
 __global__ __launch_bounds__(GP_TW * 64) void gp_comb_kernel(const uint64_t* __restrict__ ptrs, int H, int M, int topk,
                                                              GPlan g, const float* __restrict__ yraw,
                                                              float* __restrict__ out)
 {
     const int lane = threadIdx.x & 63;
-    const int nbh = H / 128;
-    const int item = blockIdx.x * GP_TW + (threadIdx.x >> 6);
-    const int tok = item / nbh, b = item % nbh;
+    const int tok = blockIdx.x * GP_TW + (threadIdx.x >> 6);
     if (tok >= M) return;
+    const int nbh = H / 128;
     const int npk = g.tok_npk[tok];
-    float o0 = 0.f, o1 = 0.f;
-    for (int k = 0; k < npk; ++k)
+    int my_s = 0;
+    float my_w = 0.f;
+    uint64_t my_p = 0;
+    if (lane < npk)
     {
-        const int s = g.tok_slot[tok * topk + k];
-        const float wk = g.tok_w[tok * topk + k];
-        const uint16_t* svh = reinterpret_cast<const uint16_t*>(ptrs[(size_t)g.slot_e[s] * 9 + 8]);
-        const float* yr = yraw + (size_t)s * H + b * 128;
-        float v0 = yr[lane], v1 = yr[lane + 64];
-        out_block_wave(v0, v1, h2f_bits(svh[b * 128 + lane]), h2f_bits(svh[b * 128 + lane + 64]));
-        o0 = o0 + wk * v0;
-        o1 = o1 + wk * v1;
+        my_s = g.tok_slot[tok * topk + lane];
+        my_w = g.tok_w[tok * topk + lane];
+        my_p = ptrs[(size_t)g.slot_e[my_s] * 9 + 8];
     }
-    out[(size_t)tok * H + b * 128 + lane] = o0;
-    out[(size_t)tok * H + b * 128 + lane + 64] = o1;
+    float* orow = out + (size_t)tok * H;
+    for (int b0 = 0; b0 < nbh; b0 += GP_TU)
+    {
+        float o[GP_TU][2];
+#pragma unroll
+        for (int j = 0; j < GP_TU; ++j) o[j][0] = o[j][1] = 0.f;
+        for (int k = 0; k < npk; ++k)
+        {
+            const int s = __builtin_amdgcn_readlane(my_s, k);
+            const float wk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), k));
+            const uint64_t pa = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(my_p >> 32), k) << 32) |
+                                (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)my_p, k);
+            const uint16_t* svh = reinterpret_cast<const uint16_t*>(pa);
+            const float* yr = yraw + (size_t)s * H;
+            float v[GP_TU][2];
+            uint16_t sv[GP_TU][2];
+#pragma unroll
+            for (int j = 0; j < GP_TU; ++j)
+            {
+                const int oo = min(b0 + j, nbh - 1) * 128 + lane;
+                v[j][0] = yr[oo]; v[j][1] = yr[oo + 64];
+                sv[j][0] = svh[oo]; sv[j][1] = svh[oo + 64];
+            }
+#pragma unroll
+            for (int j = 0; j < GP_TU; ++j)
+            {
+                out_block_wave(v[j][0], v[j][1], h2f_bits(sv[j][0]), h2f_bits(sv[j][1]));
+                o[j][0] = o[j][0] + wk * v[j][0];
+                o[j][1] = o[j][1] + wk * v[j][1];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < GP_TU; ++j)
+        {
+            const int b = b0 + j;
+            if (b >= nbh) break;
+            orow[b * 128 + lane] = o[j][0];
+            orow[b * 128 + lane + 64] = o[j][1];
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -282,7 +362,7 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_comb_kernel(const uint64_t* __r
 constexpr int GP_NW = 16;          // waves per GEMM workgroup, one tile column each: 256 output columns
 constexpr int GP_MT = 64;          // slots per pass (4 MFMA row blocks)
 constexpr int GP_NG = 4;           // ring depth (groups of 8 tile rows) of the trellis and input rings
-constexpr int GP_XS = 132;         // fp16 stride of one slot's group chunk in LDS (128 + 4: spreads the banks)
+constexpr int GP_XS = 136;         // fp16 stride of one slot's group chunk in LDS (128 + 8: conflict-free reads)
 
 typedef __attribute__((address_space(3))) void gp_lds_void;
 
@@ -292,6 +372,12 @@ __device__ __forceinline__ void gp_wait_vmcnt()
     static_assert(N >= 0 && N < 64, "vmcnt range");
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
+
+// Workgroup barrier without __syncthreads' release fence: that fence waits for vmcnt(0), i.e. for every LDS-direct
+// load still in flight, which would drain the prefetch ring at every group. Each wave has already waited for its own
+// loads of the group it is about to read; the barrier only has to order those waits (and the previous group's LDS
+// reads) across the waves. The "memory" clobber keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void gp_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 struct GemmArgs
 {
@@ -304,10 +390,10 @@ struct GemmArgs
 };
 
 // Grid: (E * ndim / 256, matrices). Workgroup = 16 waves = 256 output columns of one matrix of one expert; the
-// expert's slots go through in passes of 64. Per group of 8 tile rows every wave decodes its tile column's 8 tiles
-// and runs 4 MFMAs per tile (one per 16 slots). The tiles stream through per-wave LDS rings and the slots' inputs
-// through a shared ring, both filled by LDS-direct loads GP_NG - 1 groups ahead; two workgroup barriers per group
-// (inputs landed / inputs consumed).
+// expert's slots go through in passes of 64. Per group of 8 tile rows every wave decodes its tile column's 8 tiles and
+// runs 4 MFMAs (16x16x32) per pair of tile rows (one per 16 slots). The tiles stream through per-wave LDS rings and the
+// slots' inputs through a shared ring, both filled by LDS-direct loads GP_NG - 1 groups ahead; one workgroup barrier
+// per group (group g landed for every wave; every wave is past group g - 1, whose slots are refilled after it).
 template <int K>
 __global__ __launch_bounds__(GP_NW * 64) void gp_gemm_kernel(GemmArgs a)
 {
@@ -373,29 +459,29 @@ __global__ __launch_bounds__(GP_NW * 64) void gp_gemm_kernel(GemmArgs a)
             if (g < ngroups) issue(g);
         for (int g = 0; g < ngroups; ++g)
         {
-            if (g + NG - 1 < ngroups)
-            {
-                issue(g + NG - 1);
-                gp_wait_vmcnt<(NG - 1) * (K + 4)>();   // this wave's loads of group g landed
-            }
+            if (g + NG - 2 < ngroups) gp_wait_vmcnt<(NG - 2) * (K + 4)>();   // this wave's loads of group g landed
             else gp_wait_vmcnt<0>();
-            __syncthreads();   // every wave's loads of group g landed
+            gp_barrier();   // every wave's loads of group g landed; every wave is done with group g - 1
+            if (g + NG - 1 < ngroups) issue(g + NG - 1);   // into the slots of group g - 1
             const uint8_t* sl = ring + (g % NG) * GB;
             const uint16_t* xs = xring + (size_t)(g % NG) * GP_MT * GP_XS;
 #pragma unroll
-            for (int r = 0; r < 8; ++r)
+            for (int r = 0; r < 8; r += 2)
             {
-                const uint8_t* tp = sl + r * TB;
-                const half4 B = decode4<K>(*reinterpret_cast<const uint32_t*>(tp + d.o0),
-                                           *reinterpret_cast<const uint32_t*>(tp + d.o1), d.sh);
+                const uint8_t* tp0 = sl + r * TB;
+                const uint8_t* tp1 = tp0 + TB;
+                const half4 B0 = decode4<K>(*reinterpret_cast<const uint32_t*>(tp0 + d.o0),
+                                            *reinterpret_cast<const uint32_t*>(tp0 + d.o1), d.sh);
+                const half4 B1 = decode4<K>(*reinterpret_cast<const uint32_t*>(tp1 + d.o0),
+                                            *reinterpret_cast<const uint32_t*>(tp1 + d.o1), d.sh);
+                const half8 B = { B0[0], B0[1], B0[2], B0[3], B1[0], B1[1], B1[2], B1[3] };
 #pragma unroll
                 for (int mb = 0; mb < 4; ++mb)
                 {
-                    const half4 A = *reinterpret_cast<const half4*>(xs + (mb * 16 + i16) * GP_XS + r * 16 + q * 4);
-                    acc[mb] = __builtin_amdgcn_mfma_f32_16x16x16f16(A, B, acc[mb], 0, 0, 0);
+                    const half8 A = *reinterpret_cast<const half8*>(xs + (mb * 16 + i16) * GP_XS + q * 32 + r * 4);
+                    acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, acc[mb], 0, 0, 0);
                 }
             }
-            __syncthreads();   // every wave is done with group g's input slot and its own ring slot
         }
         // D[i][n]: lane holds rows 4q + rr of each 16-slot block, column t*16 + i16
 #pragma unroll
@@ -453,11 +539,8 @@ int launch_grouped(const uint64_t* ptrs, const int64_t* sel, const void* w, int 
 {
     const int M = P / topk;
     hipLaunchKernelGGL(gp_plan_kernel, dim3(1), dim3(GP_PLAN_THREADS), 0, st, sel, w, w_half, P, topk, E, g);
-    {
-        const long items = (long)P * (H / 128) * 2;
-        hipLaunchKernelGGL(gp_prep_kernel, dim3((unsigned)((items + GP_TW - 1) / GP_TW)), dim3(GP_TW * 64), 0, st, ptrs,
-                           x, H, topk, cap, g, xt);
-    }
+    const unsigned slot_wgs = (unsigned)((P + GP_TW - 1) / GP_TW);
+    hipLaunchKernelGGL(gp_prep_kernel, dim3(slot_wgs), dim3(GP_TW * 64), 0, st, ptrs, x, H, topk, cap, g, xt);
     GemmArgs a;
     a.ptrs = ptrs; a.kdim = H; a.ndim = I; a.cap = cap; a.E = E; a.g = g; a.xin = xt; a.yout = ygu;
     if (Kg == Ku)
@@ -475,19 +558,13 @@ int launch_grouped(const uint64_t* ptrs, const int64_t* sel, const void* w, int 
         b.yout = ygu + (size_t)cap * I;
         if (gp_gemm(Ku, b, 1, st)) return -1;
     }
-    {
-        const long items = (long)P * (I / 128);
-        hipLaunchKernelGGL(gp_act_kernel, dim3((unsigned)((items + GP_TW - 1) / GP_TW)), dim3(GP_TW * 64), 0, st, ptrs,
-                           I, cap, g, ygu, exp_tab, act_limit, xd);
-    }
+    hipLaunchKernelGGL(gp_act_kernel, dim3(slot_wgs), dim3(GP_TW * 64), 0, st, ptrs, I, cap, g, ygu, exp_tab,
+                       act_limit, xd);
     GemmArgs c = a;
     c.mat_base = 2; c.kdim = I; c.ndim = H; c.xin = xd; c.yout = yraw;
     if (gp_gemm(Kd, c, 1, st)) return -1;
-    {
-        const long items = (long)M * (H / 128);
-        hipLaunchKernelGGL(gp_comb_kernel, dim3((unsigned)((items + GP_TW - 1) / GP_TW)), dim3(GP_TW * 64), 0, st, ptrs,
-                           H, M, topk, g, yraw, out);
-    }
+    hipLaunchKernelGGL(gp_comb_kernel, dim3((unsigned)((M + GP_TW - 1) / GP_TW)), dim3(GP_TW * 64), 0, st, ptrs, H, M,
+                       topk, g, yraw, out);
     return 0;
 }
 
