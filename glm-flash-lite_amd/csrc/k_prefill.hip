@@ -359,9 +359,12 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_comb_kernel(const uint64_t* __r
 // MFMA grouped GEMM: y[slot][n] = sum_k x[slot][k] W_e[k][n] for every slot of every expert
 // ---------------------------------------------------------------------------------------------------------------
 
-constexpr int GP_NW = 16;          // waves per GEMM workgroup, one tile column each: 256 output columns
+constexpr int GP_NW = 8;           // waves per GEMM workgroup
+constexpr int GP_CPW = 2;          // tile columns per wave (each A fragment read from LDS feeds GP_CPW MFMAs)
 constexpr int GP_MT = 64;          // slots per pass (4 MFMA row blocks)
-constexpr int GP_NG = 4;           // ring depth (groups of 8 tile rows) of the trellis and input rings
+constexpr int GP_WCOLS = 16 * GP_NW * GP_CPW;   // output columns per workgroup (256)
+constexpr int GP_XPW = GP_MT / GP_NW;           // slots whose input chunk each wave loads per group
+constexpr int GP_NG = 2;           // ring depth (groups of 8 tile rows): 2 keeps two workgroups per CU
 constexpr int GP_XS = 136;         // fp16 stride of one slot's group chunk in LDS (128 + 8: conflict-free reads)
 
 typedef __attribute__((address_space(3))) void gp_lds_void;
@@ -382,45 +385,54 @@ __device__ __forceinline__ void gp_barrier() { asm volatile("s_barrier" ::: "mem
 struct GemmArgs
 {
     const uint64_t* ptrs;
-    int mat_base;              // matrix of blockIdx.y == 0 (0 gate, 1 up, 2 down)
+    int mat_base, nmat;        // first matrix of the launch (0 gate, 1 up, 2 down) and how many
     int kdim, ndim, cap, E;
     GPlan g;
     const uint16_t* xin;       // [mats][cap][kdim] fp16, GEMM input layout
     float* yout;               // [mats][cap][ndim] fp32
 };
 
-// Grid: (E * ndim / 256, matrices). Workgroup = 16 waves = 256 output columns of one matrix of one expert; the
-// expert's slots go through in passes of 64. Per group of 8 tile rows every wave decodes its tile column's 8 tiles and
-// runs 4 MFMAs (16x16x32) per pair of tile rows (one per 16 slots). The tiles stream through per-wave LDS rings and the
-// slots' inputs through a shared ring, both filled by LDS-direct loads GP_NG - 1 groups ahead; one workgroup barrier
-// per group (group g landed for every wave; every wave is past group g - 1, whose slots are refilled after it).
+// Grid: 8 * ceil(E / 8) * (ndim / 256) * matrices, XCD-major. Workgroup = 8 waves x 2 tile columns = 256 output columns of one matrix of one
+// expert; the expert's slots go through in passes of 64. Per group of 8 tile rows every wave decodes its 16 tiles and,
+// per pair of tile rows, reads 4 A fragments (16 slots x 32 k) and runs 8 MFMAs (16x16x32), each fragment feeding both
+// columns. The tiles stream through per-wave LDS rings and the slots' inputs through a shared ring, both filled by
+// LDS-direct loads GP_NG - 1 groups ahead; one workgroup barrier per group (group g landed for every wave; every wave
+// is past group g - 1, whose slots are refilled after it).
 template <int K>
 __global__ __launch_bounds__(GP_NW * 64) void gp_gemm_kernel(GemmArgs a)
 {
-    constexpr int TB = 32 * K, GB = 8 * TB, NG = GP_NG;
+    constexpr int TB = 32 * K, RB = GP_CPW * TB, GB = 8 * RB, NG = GP_NG;
+    constexpr int NLD = GB / 256;                 // trellis dword loads per lane per group
+    constexpr int NV = NLD + GP_XPW;              // vector memory instructions per wave per group
+    static_assert(GB % 256 == 0, "group of tiles must split into whole wave loads");
     extern __shared__ __align__(16) uint8_t gp_lds[];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int nch = a.ndim / (16 * GP_NW);
-    const int e = blockIdx.x / nch, nc = blockIdx.x % nch;
-    const int mat = a.mat_base + blockIdx.y;
+    // XCD-aware order: workgroups are dispatched round-robin over the 8 XCDs (XCD = linear id % 8), so every
+    // workgroup of expert e gets a linear id = e % 8 (mod 8) and the expert's slot inputs are fetched into one L2
+    const int nch = a.ndim / GP_WCOLS, per = nch * a.nmat;
+    const int xcd = blockIdx.x % 8, j = blockIdx.x / 8;
+    const int e = (j / per) * 8 + xcd, rr0 = j % per;
+    if (e >= a.E) return;
+    const int nc = rr0 % nch;
+    const int mat = a.mat_base + rr0 / nch;
     const int s_begin = a.g.off[e], s_end = a.g.off[e + 1];
     if (s_begin >= s_end) return;
     const int TN = a.ndim / 16, TK = a.kdim / 16, ngroups = TK / 8;
-    const int t = nc * GP_NW + wave;                                  // this wave's tile column
-    uint8_t* ring = gp_lds + wave * NG * GB;                          // [NG][8 tiles]
+    const int t0 = (nc * GP_NW + wave) * GP_CPW;                     // this wave's first tile column
+    uint8_t* ring = gp_lds + wave * NG * GB;                          // [NG][8 tile rows][GP_CPW columns][TB]
     uint16_t* xring = reinterpret_cast<uint16_t*>(gp_lds + GP_NW * NG * GB);   // [NG][64 slots][GP_XS]
     const uint8_t* tr = reinterpret_cast<const uint8_t*>(a.ptrs[(size_t)e * 9 + mat]);
-    const size_t gstride = (size_t)TN * TB;
-    uint8_t* cb = const_cast<uint8_t*>(uniform_ptr(tr + (size_t)t * TB));
+    const size_t gstride = (size_t)TN * TB;                           // bytes per tile row of the matrix
+    uint8_t* cb = const_cast<uint8_t*>(uniform_ptr(tr + (size_t)t0 * TB));
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(cb, (short)0, (int)((size_t)TK * gstride),
                                                                         0x00020000);
     const int gs = (int)gstride;
-    int voff[K];
+    int voff[NLD];
 #pragma unroll
-    for (int i = 0; i < K; ++i)
+    for (int i = 0; i < NLD; ++i)
     {
-        const int byte = i * 256 + lane * 4;
-        voff[i] = (byte / TB) * gs + (byte % TB);
+        const int byte = i * 256 + lane * 4;   // within the group's [8][GP_CPW][TB] block
+        voff[i] = (byte / RB) * gs + (byte % RB);
     }
     const LaneDec d = lane_dec(lane, K);
     const uint16_t* xin = a.xin + (size_t)(mat - a.mat_base) * a.cap * a.kdim;
@@ -430,68 +442,89 @@ __global__ __launch_bounds__(GP_NW * 64) void gp_gemm_kernel(GemmArgs a)
     for (int c0 = s_begin; c0 < s_end; c0 += GP_MT)
     {
         const int T = min(GP_MT, s_end - c0);
-        // the input chunk of group g for this wave's 4 slots (slots past the pass read the pass's last slot)
-        const uint8_t* xbase[4];
+        // the input chunk of group g for this wave's slots (slots past the pass read the pass's last slot)
+        const uint8_t* xbase[GP_XPW];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < GP_XPW; ++j)
         {
-            const int sl = min(wave * 4 + j, T - 1);
+            const int sl = min(wave * GP_XPW + j, T - 1);
             xbase[j] = reinterpret_cast<const uint8_t*>(xin + (size_t)(c0 + sl) * a.kdim);
         }
         auto issue = [&](int g) {
             uint8_t* dst = ring + (g % NG) * GB;
 #pragma unroll
-            for (int i = 0; i < K; ++i)
+            for (int i = 0; i < NLD; ++i)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (gp_lds_void*)(dst + i * 256), 4, voff[i], g * 8 * gs, 0,
                                                          0);
             uint16_t* xd = xring + (size_t)(g % NG) * GP_MT * GP_XS;
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < GP_XPW; ++j)
                 __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(xbase[j] + g * 256 + lane * 4),
-                                                 (gp_lds_void*)(xd + (wave * 4 + j) * GP_XS), 4, 0, 0);
+                                                 (gp_lds_void*)(xd + (wave * GP_XPW + j) * GP_XS), 4, 0, 0);
         };
-        float4v acc[4];
+        float4v acc[GP_CPW][4];
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) acc[mb] = float4v{ 0.f, 0.f, 0.f, 0.f };
+        for (int c = 0; c < GP_CPW; ++c)
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb) acc[c][mb] = float4v{ 0.f, 0.f, 0.f, 0.f };
         __syncthreads();   // previous pass done with the rings
 #pragma unroll
         for (int g = 0; g < NG - 1; ++g)
             if (g < ngroups) issue(g);
         for (int g = 0; g < ngroups; ++g)
         {
-            if (g + NG - 2 < ngroups) gp_wait_vmcnt<(NG - 2) * (K + 4)>();   // this wave's loads of group g landed
+            if (g + NG - 2 < ngroups) gp_wait_vmcnt<(NG - 2) * NV>();   // this wave's loads of group g landed
             else gp_wait_vmcnt<0>();
             gp_barrier();   // every wave's loads of group g landed; every wave is done with group g - 1
             if (g + NG - 1 < ngroups) issue(g + NG - 1);   // into the slots of group g - 1
             const uint8_t* sl = ring + (g % NG) * GB;
             const uint16_t* xs = xring + (size_t)(g % NG) * GP_MT * GP_XS;
+            // all trellis words of the group first (in-order LDS returns let each decode wait only for its own)
+            uint32_t wd[4][GP_CPW][2][2];
 #pragma unroll
-            for (int r = 0; r < 8; r += 2)
+            for (int rp = 0; rp < 4; ++rp)
+#pragma unroll
+                for (int c = 0; c < GP_CPW; ++c)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+                    {
+                        const uint8_t* tp = sl + (2 * rp + h) * RB + c * TB;
+                        wd[rp][c][h][0] = *reinterpret_cast<const uint32_t*>(tp + d.o0);
+                        wd[rp][c][h][1] = *reinterpret_cast<const uint32_t*>(tp + d.o1);
+                    }
+#pragma unroll
+            for (int rp = 0; rp < 4; ++rp)
             {
-                const uint8_t* tp0 = sl + r * TB;
-                const uint8_t* tp1 = tp0 + TB;
-                const half4 B0 = decode4<K>(*reinterpret_cast<const uint32_t*>(tp0 + d.o0),
-                                            *reinterpret_cast<const uint32_t*>(tp0 + d.o1), d.sh);
-                const half4 B1 = decode4<K>(*reinterpret_cast<const uint32_t*>(tp1 + d.o0),
-                                            *reinterpret_cast<const uint32_t*>(tp1 + d.o1), d.sh);
-                const half8 B = { B0[0], B0[1], B0[2], B0[3], B1[0], B1[1], B1[2], B1[3] };
+                half8 A[4];
 #pragma unroll
                 for (int mb = 0; mb < 4; ++mb)
+                    A[mb] = *reinterpret_cast<const half8*>(xs + (mb * 16 + i16) * GP_XS + q * 32 + rp * 8);
+                half8 B[GP_CPW];
+#pragma unroll
+                for (int c = 0; c < GP_CPW; ++c)
                 {
-                    const half8 A = *reinterpret_cast<const half8*>(xs + (mb * 16 + i16) * GP_XS + q * 32 + r * 4);
-                    acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, acc[mb], 0, 0, 0);
+                    const half4 B0 = decode4<K>(wd[rp][c][0][0], wd[rp][c][0][1], d.sh);
+                    const half4 B1 = decode4<K>(wd[rp][c][1][0], wd[rp][c][1][1], d.sh);
+                    B[c] = half8{ B0[0], B0[1], B0[2], B0[3], B1[0], B1[1], B1[2], B1[3] };
                 }
+#pragma unroll
+                for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+                    for (int c = 0; c < GP_CPW; ++c)
+                        acc[c][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mb], B[c], acc[c][mb], 0, 0, 0);
             }
         }
-        // D[i][n]: lane holds rows 4q + rr of each 16-slot block, column t*16 + i16
+        // D[i][n]: lane holds rows 4q + rr of each 16-slot block, column (t0 + c) * 16 + i16
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
+        for (int c = 0; c < GP_CPW; ++c)
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr)
-            {
-                const int sl = mb * 16 + q * 4 + rr;
-                if (sl < T) yout[(size_t)(c0 + sl) * a.ndim + t * 16 + i16] = acc[mb][rr];
-            }
+            for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr)
+                {
+                    const int sl = mb * 16 + q * 4 + rr;
+                    if (sl < T) yout[(size_t)(c0 + sl) * a.ndim + (t0 + c) * 16 + i16] = acc[c][mb][rr];
+                }
     }
 }
 
@@ -502,7 +535,7 @@ __global__ __launch_bounds__(GP_NW * 64) void gp_gemm_kernel(GemmArgs a)
 template <int K>
 static size_t gp_gemm_lds()
 {
-    return (size_t)GP_NW * GP_NG * 8 * 32 * K + (size_t)GP_NG * GP_MT * GP_XS * 2;
+    return (size_t)GP_NW * GP_NG * 8 * GP_CPW * 32 * K + (size_t)GP_NG * GP_MT * GP_XS * 2;
 }
 
 template <int K>
@@ -517,7 +550,10 @@ static int gp_gemm_launch(const GemmArgs& a, int nmat, hipStream_t st)
             return -1;
         lds_set = (int)lds;
     }
-    hipLaunchKernelGGL(gp_gemm_kernel<K>, dim3(a.E * (a.ndim / (16 * GP_NW)), nmat), dim3(GP_NW * 64), lds, st, a);
+    GemmArgs b = a;
+    b.nmat = nmat;
+    const unsigned grid = (unsigned)(((a.E + 7) / 8) * 8 * (a.ndim / GP_WCOLS) * nmat);
+    hipLaunchKernelGGL(gp_gemm_kernel<K>, dim3(grid), dim3(GP_NW * 64), lds, st, b);
     return 0;
 }
 
