@@ -11,6 +11,8 @@ value        = microseconds per token at M=1 (lower is better); per_M holds M=1.
 roofline     = the gate|up GEMV kernel (the dominant one) at M=1: algorithmic quantized bytes per launch (union of
                routed experts x (gate+up trellis + their suh/svh)) / its mean launch time, from device events
                recorded around every launch during a timed eager pass; peak = 8 TB/s HBM.
+configs      = BASELINE configs 2 (mixed bitrates, Zipf routing), 3 (M=16/32/64) and 4 (42 resident layers decoded
+               at M=1; prefill of M=2048 tokens through the MFMA grouped path, as TFLOP/s against 2.5 PF dense fp16).
 cpu_baseline = the reference's own AVX2 expert engine (kernels/cpu_avx2/ft_core.h, built into oracle/_ref) timed on
                this host: decode calls of 1 token x 8 experts cycling a DRAM-cold pool of 288 experts, I16 mode.
 """
@@ -25,6 +27,7 @@ sys.path.insert(0, os.path.join(ROOT, "glm-flash-lite_amd"))
 
 METRIC = "MoE-layer decode µs/token at M=1..4 + % HBM roofline on quantized bytes"
 HBM_PEAK_GBPS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0   # dense fp16 MFMA
 H, I, E, TOPK, KBITS = 5120, 1536, 288, 8, 3
 
 
@@ -269,8 +272,63 @@ def extra_configs(ctx, layers, args, G, reps):
     r["layers"] = nst
     r["resident_GB"] = round(nst * E * layers[0].quant_bytes_per_expert / 1e9, 1)
     res["config4_stack_decode"] = r
+    print(f"bench: config 4 stack done ({time.time() - t0:.0f} s)", file=sys.stderr, flush=True)
+    res["config4_prefill"] = time_prefill(ctx, list(range(args.layers)), layers[0].quant_bytes_per_expert, 2048,
+                                          max(4, reps // 2))
+    print(f"bench: config 4 prefill done ({time.time() - t0:.0f} s)", file=sys.stderr, flush=True)
     res["setup_and_time_s"] = round(time.time() - t0, 1)
     return res
+
+
+def time_prefill(ctx, layer_ids, bytes_per_expert, M, reps, G=4):
+    """Config 4 prefill: M tokens, uniform top-8 routing, through gfl_grouped_forward (MFMA grouped GEMMs). G layer
+    calls (layers cycled) are captured in one HIP graph and replayed `reps` times. Algorithmic work per call:
+    2 * picks * 3 * H * I flops (gate, up, down GEMMs) and the union's quantized expert bytes."""
+    import numpy as np
+    import torch
+    routes = make_routes(M, np.random.default_rng(5000 + M), 2, "uniform")
+    out = torch.empty((M, H), dtype=torch.float32, device="cuda")
+    NL = len(layer_ids)
+
+    def call(i):
+        x, sel, w, _ = routes[i % 2]
+        ctx.grouped_forward(layer_ids[i % NL], x, sel, w, out)
+
+    for i in range(3):
+        call(i)
+    torch.cuda.synchronize()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        call(0)
+    torch.cuda.current_stream().wait_stream(st)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(G):
+            call(i)
+    g.replay()
+    torch.cuda.synchronize()
+    got = out.clone()
+    call(G - 1)
+    torch.cuda.synchronize()
+    graph_ok = bool(torch.equal(got, out))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / (reps * G)
+    del g
+    picks = M * TOPK
+    flops = 2.0 * picks * 3 * H * I
+    tflops = flops / (ms * 1e-3) / 1e12
+    union = float(np.mean([r[3] for r in routes]))
+    gbps = (union * bytes_per_expert + M * H * 6) / (ms * 1e-3) / 1e9
+    return {"tokens": M, "ms_per_layer": round(ms, 4), "us_per_token": round(ms * 1e3 / M, 4),
+            "TFLOPs": round(tflops, 1), "mfma_peak_TFLOPs": MFMA_PEAK_TFLOPS,
+            "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "GBps": round(gbps, 1), "union_experts": union,
+            "graph_replay_matches_eager": graph_ok}
 
 
 def main():
@@ -287,6 +345,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the config 2 / 3 / 42-layer-stack measurements (config 1 only)")
     ap.add_argument("--stack-layers", type=int, default=42)
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the config-4 prefill measurement (M=2048 through the grouped path), one JSON line")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="counter run: the calibration copy, then eager M=1 steps (run under rocprofv3 --pmc)")
     ap.add_argument("--pmc-digest", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -316,6 +376,11 @@ def main():
     setup_s = time.time() - t0
     if args.pmc_probe:
         pmc_probe(ctx, layers)
+        return
+    if args.prefill_only:
+        r = time_prefill(ctx, list(range(args.layers)), layers[0].quant_bytes_per_expert, 2048,
+                         max(4, args.steps // 64))
+        print(json.dumps({"config4_prefill": r}), flush=True)
         return
     per_expert = layers[0].quant_bytes_per_expert
     gu_per_expert = layers[0].tbytes[0] + layers[0].tbytes[1] + 2 * 2 * (H + I)

@@ -324,9 +324,11 @@ __device__ __forceinline__ void wait_vmcnt()
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int K, int NS, int NG>
+// pre() runs after the first NG - 1 groups are requested and before the first is read: the caller fills lds_x there
+// (and ends with a workgroup barrier), so the input transform overlaps the trellis fetch latency.
+template <int K, int NS, int NG, class Pre>
 __device__ __forceinline__ void chain_dma(const uint8_t* __restrict__ col_base, size_t gstride, int TK, int ns,
-                                          const uint16_t* lds_x, uint8_t* ring, float (&res)[NS])
+                                          const uint16_t* lds_x, uint8_t* ring, float (&res)[NS], Pre&& pre)
 {
     constexpr int TB = 32 * K, GB = 8 * TB;
     const int lane = threadIdx.x & 63;
@@ -357,6 +359,7 @@ __device__ __forceinline__ void chain_dma(const uint8_t* __restrict__ col_base, 
 #pragma unroll
     for (int g = 0; g < NG - 1; ++g)
         if (g < ngroups) issue(g);
+    pre();
     float acc[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) acc[s] = 0.f;
@@ -418,6 +421,7 @@ __device__ __forceinline__ void chain_dma(const uint8_t* __restrict__ col_base, 
 // ---------------------------------------------------------------------------------------------------------------
 
 constexpr int GU_NW = 4;    // waves (tile columns) per gate|up workgroup: 64 outputs
+constexpr int GU_PU = 10;   // input-transform blocks whose loads a gate|up wave keeps in flight (H = 5120: all of them)
 constexpr int DN_NW = 8;    // waves per down workgroup: one 128-output block, out_block fused
 
 struct GuArgs
@@ -516,22 +520,38 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(K ==
     {
         const int ns = NS == 1 ? 1 : min(nsp, s_end - c0);   // >= 1 (c0 < s_end)
         lds_barrier();   // previous pass done with lds_x
-        // input transform of the pass's tokens into LDS (prep_block, ft_core.h:97-102)
-        const int nblk = a.H / 128;
-        for (int it = wave; it < ns * nblk; it += NW)
-        {
-            const int s = it / nblk, b = it % nblk;
-            const int tok = L.spick[c0 + s] / a.topk;
-            const uint16_t* xr = a.x + (size_t)tok * a.H + b * 128;
-            float v0 = h2f_bits(xr[lane]), v1 = h2f_bits(xr[lane + 64]);
-            prep_block_wave(v0, v1, h2f_bits(suh[b * 128 + lane]), h2f_bits(suh[b * 128 + lane + 64]));
-            uint16_t* dst = lds_x + (size_t)s * a.H;
-            dst[perm_pos(b, lane)] = (uint16_t)f2h_bits(v0);
-            dst[perm_pos(b, lane + 64)] = (uint16_t)f2h_bits(v1);
-        }
         float res[NS];
-        lds_barrier();   // lds_x complete
-        chain_dma<K, NS, NGRP>(col, gstride, TK, ns, lds_x, rings + wid * RB, res);
+        chain_dma<K, NS, NGRP>(col, gstride, TK, ns, lds_x, rings + wid * RB, res, [&] {
+            // input transform of the pass's tokens into LDS (prep_block, ft_core.h:97-102), GU_PU blocks' loads in
+            // flight per wave
+            const int nblk = a.H / 128, nit = ns * nblk;
+            for (int it0 = wave; it0 < nit; it0 += NW * GU_PU)
+            {
+                uint16_t xv[GU_PU][2], sv[GU_PU][2];
+#pragma unroll
+                for (int k = 0; k < GU_PU; ++k)
+                {
+                    const int it = min(it0 + k * NW, nit - 1);
+                    const int s = it / nblk, b = it % nblk;
+                    const uint16_t* xr = a.x + (size_t)(L.spick[c0 + s] / a.topk) * a.H + b * 128;
+                    xv[k][0] = xr[lane]; xv[k][1] = xr[lane + 64];
+                    sv[k][0] = suh[b * 128 + lane]; sv[k][1] = suh[b * 128 + lane + 64];
+                }
+#pragma unroll
+                for (int k = 0; k < GU_PU; ++k)
+                {
+                    const int it = it0 + k * NW;
+                    if (it >= nit) break;
+                    const int s = it / nblk, b = it % nblk;
+                    float v0 = h2f_bits(xv[k][0]), v1 = h2f_bits(xv[k][1]);
+                    prep_block_wave(v0, v1, h2f_bits(sv[k][0]), h2f_bits(sv[k][1]));
+                    uint16_t* dst = lds_x + (size_t)s * a.H;
+                    dst[perm_pos(b, lane)] = (uint16_t)f2h_bits(v0);
+                    dst[perm_pos(b, lane + 64)] = (uint16_t)f2h_bits(v1);
+                }
+            }
+            lds_barrier();   // lds_x complete
+        });
 #pragma unroll
         for (int s = 0; s < NS; ++s)
             if (s < ns && lane < 16)
@@ -602,12 +622,6 @@ __global__ __launch_bounds__(DN_NW * 64) __attribute__((amdgpu_waves_per_eu(K ==
     {
         const int ns = NS == 1 ? 1 : min(nsp, s_end - c0);   // >= 1 (c0 < s_end)
         lds_barrier();   // previous pass done with lds_x / lds_y
-        {
-            const int nvec = ns * a.I / 8;
-            const uint4* src = reinterpret_cast<const uint4*>(a.xtd + (size_t)c0 * a.I);
-            uint4* dst = reinterpret_cast<uint4*>(lds_x);
-            for (int i = threadIdx.x; i < nvec; i += blockDim.x) dst[i] = src[i];
-        }
         // the pass tokens' combine lists (slots in job order and weights): loads issued before the GEMV, written to
         // LDS after it (thread i < ns * topk holds entry i)
         const int ci = threadIdx.x, cs = ci / a.topk, ck = ci % a.topk;
@@ -621,8 +635,13 @@ __global__ __launch_bounds__(DN_NW * 64) __attribute__((amdgpu_waves_per_eu(K ==
             q_npk = a.pv.tok_npk[q_tok];
         }
         float res[NS];
-        lds_barrier();   // lds_x complete
-        chain_dma<K, NS, NGRP>(col, gstride, TK, ns, lds_x, rings + wid * RB, res);
+        chain_dma<K, NS, NGRP>(col, gstride, TK, ns, lds_x, rings + wid * RB, res, [&] {
+            const int nvec = ns * a.I / 8;
+            const uint4* src = reinterpret_cast<const uint4*>(a.xtd + (size_t)c0 * a.I);
+            uint4* dst = reinterpret_cast<uint4*>(lds_x);
+            for (int i = threadIdx.x; i < nvec; i += blockDim.x) dst[i] = src[i];
+            lds_barrier();   // lds_x complete
+        });
 #pragma unroll
         for (int s = 0; s < NS; ++s)
             if (s < ns && lane < 16) lds_y[s * 128 + wave * 16 + n] = res[s];

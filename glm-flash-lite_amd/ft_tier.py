@@ -113,8 +113,13 @@ def tier_set_act_limit(limit):
 def tier_forward(li, x, sel, w, mode):
     """ft_tier_ext.cpp:865-904: x fp32 [m, H], sel int32 [m, k] (sel < 0 skipped), w fp32 [m, k] -> fp32 [m, H],
     sum over picks of w * expert(x) in the reference's job order. Tensors may live on the CPU (as the reference's)
-    or on the device; the result is on x's device. mode -1 (auto) and 1 (EXACT) compute EXACT; the reference's CPU
-    speed modes 0 (AFFINE) and 2 (I16) are outside the expert-output tolerance and are rejected."""
+    or on the device; the result is on x's device.
+
+    mode 1 (EXACT) computes EXACT, bit-identical to the reference's, for m * k <= 1024 picks. mode -1 (auto) does the
+    same up to 1024 picks and, above that (prefill-sized batches, up to 65536 picks), takes the MFMA grouped path,
+    which keeps the exact weights, rounding points and combine order but sums in MFMA order; the reference's auto
+    mode likewise leaves EXACT for its speed modes on large batches (ft_tier_ext.cpp:396). The reference's CPU speed
+    modes 0 (AFFINE) and 2 (I16) are outside the expert-output tolerance and are rejected."""
     import torch
     _check(T is not None and not T.running, "tier_forward: worker running")
     _check(0 <= li < len(T.layers) and T.layers[li] is not None, "tier_forward: layer not registered")
@@ -123,7 +128,9 @@ def tier_forward(li, x, sel, w, mode):
     _check(sel.dtype in (torch.int32, torch.int64) and sel.dim() == 2 and sel.size(0) == x.size(0), "sel: int32 [m, k]")
     _check(w.dtype == torch.float32 and tuple(w.shape) == tuple(sel.shape), "w: float32 [m, k]")
     m, k = sel.shape
-    _check(m * k <= 1024 and k <= 16, "tier_forward: m * k <= 1024 picks, k <= 16")
+    grouped = int(mode) == -1 and m * k > 1024
+    _check(k <= 16 and (m * k <= 1024 or (grouped and m * k <= 65536)),
+           "tier_forward: k <= 16 and m * k <= 1024 picks (EXACT) or <= 65536 (auto)")
     dev = torch.device("cuda", T.ctx.device)
     x16 = x.to(dev).half()
     _check(bool(torch.equal(x16.float(), x.to(dev))), "tier_forward: x must be fp16-valued (the expert input is fp16)")
@@ -133,8 +140,11 @@ def tier_forward(li, x, sel, w, mode):
     seld = torch.where(seld < 0, torch.full_like(seld, -1), seld).contiguous()
     out = torch.empty((m, T.H), dtype=torch.float32, device=dev)
     try:
-        T.ctx.moe_forward(int(li), x16.contiguous(), seld, w.to(dev).contiguous(), out, mode=_native.MODE_EXACT,
-                          act_limit=T.act_limit)
+        if grouped:
+            T.ctx.grouped_forward(int(li), x16.contiguous(), seld, w.to(dev).contiguous(), out, act_limit=T.act_limit)
+        else:
+            T.ctx.moe_forward(int(li), x16.contiguous(), seld, w.to(dev).contiguous(), out,
+                              mode=_native.MODE_EXACT, act_limit=T.act_limit)
     except _native.NativeError as err:
         raise RuntimeError(str(err)) from None
     valid = int((sel >= 0).sum())

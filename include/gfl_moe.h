@@ -75,7 +75,7 @@ int gfl_moe_forward(gfl_ctx* ctx, int li, const uint16_t* x, const int64_t* sel,
 /* Routed-expert forward of one layer for prefill-sized M (the north star's MFMA grouped GEMM), same arguments and
  * result layout as gfl_moe_forward: x fp16 [M, H], sel int64 [M, topk] (ids outside [0, E) skipped), w fp16 or fp32
  * [M, topk], out fp32 [M, H]; M*topk <= 65536. Rows are grouped expert-major (tier_lut_build_grouped_rows,
- * kernels/cpu_avx2/ft_tier_ext.cpp:1047-1097), gate|up and down run as v_mfma_f32_16x16x16_f16 grouped GEMMs on the
+ * kernels/cpu_avx2/ft_tier_ext.cpp:1047-1097), gate|up and down run as v_mfma_f32_16x16x32_f16 grouped GEMMs on the
  * bit-exact dequantized fp16 weights, the transforms keep the reference's fp16 rounding points and the combine its job
  * order (kernels/cpu_avx2/ft_core.h:933-1033). The hidden-dimension sums are formed in MFMA order, so results differ
  * from the EXACT mode of gfl_moe_forward by fp32 accumulation rounding (as the reference's own fp64 expert,
@@ -123,7 +123,8 @@ int gfl_stats(gfl_ctx* ctx, int64_t* out, int n);
 /* Per-stage device timing of gfl_moe_forward, the counterpart of the per-phase wall times tier_stats reports
  * (ft_tier_ext.cpp:906-914): while enabled, every forward brackets its launches with device events. Stage 1 is the
  * gate|up launch (routing plan, gate|up GEMV, SwiGLU and down-input prep), stage 3 the down launch (down GEMV,
- * output transform, weighted combine); stages 0, 2 and 4 (plan, activation, combine) run inside those two and stay 0.
+ * output transform, weighted combine); stage 2 is a whole gfl_grouped_forward call (its six launches); stages 0 and
+ * 4 (plan, combine) run inside the other launches and stay 0.
  * gfl_profile_read synchronises the recorded events, adds their elapsed milliseconds into stage_ms[5] and launch
  * counts into launches[5] (host arrays), and clears the record. */
 int gfl_profile_enable(gfl_ctx* ctx, int enable);

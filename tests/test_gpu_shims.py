@@ -59,6 +59,25 @@ def test_tier_forward_reference_signature_bitexact(tier, oracle, li):
     assert len(st) == 12 and st[0] >= 1
 
 
+def test_tier_forward_auto_prefill_takes_grouped_path(tier, oracle):
+    """m * k > 1024 in auto mode: the MFMA grouped path, within its bars of the oracle's EXACT result (RMS of the
+    difference <= 1e-3, max-abs <= 1e-2 of the output RMS); EXACT mode refuses the size."""
+    import ft_tier
+    rng = np.random.default_rng(70)
+    m = 300
+    x = torch.from_numpy((rng.standard_normal((m, tier["H"])) * 0.5).astype(np.float16).astype(np.float32))
+    sel = torch.from_numpy(np.stack([rng.choice(tier["E"], 4, replace=False) for _ in range(m)]).astype(np.int32))
+    sel[7, 1] = -1
+    w = torch.from_numpy(rng.random((m, 4)).astype(np.float32))
+    got = ft_tier.tier_forward(1, x, sel, w, -1).numpy().astype(np.float64)
+    want = oracle.moe_forward(_experts(oracle, tier["layers"][1]), x.numpy(), sel.numpy(), w.numpy(), mode=1)
+    rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
+    d = got - want
+    assert float(np.sqrt(np.mean(d ** 2))) <= 1e-3 * rms and float(np.abs(d).max()) <= 1e-2 * rms
+    with pytest.raises(RuntimeError, match="1024 picks"):
+        ft_tier.tier_forward(1, x, sel, w, 1)
+
+
 def test_tier_forward_act_limit(tier, oracle):
     import ft_tier
     rng = np.random.default_rng(60)
