@@ -247,8 +247,11 @@ int gfl_register_layer(gfl_ctx* c, int li, int E, int H, int I, int k_gate, int 
     if (H < 256 || I < 256 || H % 256 || I % 256)
         return fail(GFL_EINVAL, "gfl_register_layer: H and I must be multiples of 256");
     if (!k_ok(k_gate) || !k_ok(k_up) || !k_ok(k_down)) return fail(GFL_EINVAL, "gfl_register_layer: K must be 2..5");
+    // trellis words are read 4 bytes at a time, suh/svh 16 bytes at a time
     for (int i = 0; i < E * 9; ++i)
-        if (ptrs[i] == 0 || (ptrs[i] & 3)) return fail(GFL_EINVAL, "gfl_register_layer: NULL or misaligned device pointer");
+        if (ptrs[i] == 0 || (ptrs[i] & (i % 9 < 3 ? 3 : 15)))
+            return fail(GFL_EINVAL, "gfl_register_layer: NULL or misaligned device pointer (trellis 4-byte, suh/svh "
+                                    "16-byte alignment)");
     std::lock_guard<std::mutex> g(c->mu);
     GFL_HIP(hipSetDevice(c->device));
     if ((int)c->layers.size() <= li) c->layers.resize(li + 1);
@@ -272,6 +275,7 @@ int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, c
     if (M < 1 || topk < 1 || topk > gfl::MAX_TOPK || (int64_t)M * topk > gfl::MAX_PICKS)
         return fail(GFL_EINVAL, "gfl_moe_forward: need 1 <= topk <= 16 and M*topk <= 1024");
     if (!std::isfinite(act_limit) || act_limit < 0) return fail(GFL_EINVAL, "gfl_moe_forward: act_limit must be >= 0");
+    if (reinterpret_cast<uintptr_t>(x) & 15) return fail(GFL_EINVAL, "gfl_moe_forward: x must be 16-byte aligned");
     std::lock_guard<std::mutex> g(c->mu);
     const Layer& L = c->layers[li];
     GFL_HIP(hipSetDevice(c->device));

@@ -163,6 +163,51 @@ __device__ inline void fwht128(float& v0, float& v1)
 
 __device__ inline float h2f_bits(uint16_t h) { __half x; __builtin_memcpy(&x, &h, 2); return __half2float(x); }
 
+// Hadamard-128 on one 16-lane row of the wave, 8 elements per lane: lane i of the row holds elements 8i..8i+7.
+// Stages h = 1, 2, 4 pair elements inside the lane, h = 8..64 pair lane i with i ^ (h / 8); every element sees the
+// same add/sub sequence as had128 (ft_core.h:89-94): the lower element of a pair becomes a + b, the upper a - b.
+template <int W>
+__device__ __forceinline__ void fwht_row_stage(float (&v)[8], int L)
+{
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+    {
+        const float p = lane_xor<W>(v[k]);
+        v[k] = (L & W) ? p - v[k] : v[k] + p;
+    }
+}
+
+__device__ inline void fwht128_row(float (&v)[8])
+{
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1)
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (!(k & h))
+            {
+                const float a = v[k], b = v[k + h];
+                v[k] = a + b;
+                v[k + h] = a - b;
+            }
+    const int L = threadIdx.x & 15;
+    fwht_row_stage<1>(v, L);
+    fwht_row_stage<2>(v, L);
+    fwht_row_stage<4>(v, L);
+    fwht_row_stage<8>(v, L);
+}
+
+// prep_block (ft_core.h:97-102) on a 16-lane row: x and suh are the lane's 8 fp16 inputs and scales (16 bytes each)
+__device__ inline void prep_block_row(float (&v)[8], uint4 x, uint4 sc)
+{
+    const uint32_t xw[4] = { x.x, x.y, x.z, x.w }, sw[4] = { sc.x, sc.y, sc.z, sc.w };
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+        v[k] = h2f_bits((uint16_t)(xw[k >> 1] >> (16 * (k & 1)))) * h2f_bits((uint16_t)(sw[k >> 1] >> (16 * (k & 1))));
+    fwht128_row(v);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = r16(v[k] * HADF);
+}
+
 // prep_block (ft_core.h:97-102) on lane-held elements L, L+64
 __device__ inline void prep_block_wave(float& v0, float& v1, float s0, float s1)
 {

@@ -324,11 +324,13 @@ __device__ __forceinline__ void wait_vmcnt()
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// pre() runs after the first NG - 1 groups are requested and before the first is read: the caller fills lds_x there
-// (and ends with a workgroup barrier), so the input transform overlaps the trellis fetch latency.
-template <int K, int NS, int NG, class Pre>
+// pre_load() runs before the first NG - 1 groups are requested, pre() after them and before the first is read: the
+// caller issues its input loads in pre_load (so waiting for them does not wait for the trellis groups queued behind)
+// and fills lds_x in pre (ending with a workgroup barrier), so the input transform overlaps the trellis fetch.
+template <int K, int NS, int NG, class PreLoad, class Pre>
 __device__ __forceinline__ void chain_dma(const uint8_t* __restrict__ col_base, size_t gstride, int TK, int ns,
-                                          const uint16_t* lds_x, uint8_t* ring, float (&res)[NS], Pre&& pre)
+                                          const uint16_t* lds_x, uint8_t* ring, float (&res)[NS], PreLoad&& pre_load,
+                                          Pre&& pre)
 {
     constexpr int TB = 32 * K, GB = 8 * TB;
     const int lane = threadIdx.x & 63;
@@ -356,6 +358,7 @@ __device__ __forceinline__ void chain_dma(const uint8_t* __restrict__ col_base, 
         for (int i = 0; i < K; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(dst + i * 256), 4, voff[i], g * 8 * gs, 0, 0);
     };
+    pre_load();
 #pragma unroll
     for (int g = 0; g < NG - 1; ++g)
         if (g < ngroups) issue(g);
@@ -421,7 +424,7 @@ __device__ __forceinline__ void chain_dma(const uint8_t* __restrict__ col_base, 
 // ---------------------------------------------------------------------------------------------------------------
 
 constexpr int GU_NW = 4;    // waves (tile columns) per gate|up workgroup: 64 outputs
-constexpr int GU_PU = 10;   // input-transform blocks whose loads a gate|up wave keeps in flight (H = 5120: all of them)
+constexpr int GU_PR = 3;    // input-transform rounds (4 blocks per wave each) whose loads a gate|up wave keeps in flight
 constexpr int DN_NW = 8;    // waves per down workgroup: one 128-output block, out_block fused
 
 struct GuArgs
@@ -521,34 +524,52 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(K ==
         const int ns = NS == 1 ? 1 : min(nsp, s_end - c0);   // >= 1 (c0 < s_end)
         lds_barrier();   // previous pass done with lds_x
         float res[NS];
-        chain_dma<K, NS, NGRP>(col, gstride, TK, ns, lds_x, rings + wid * RB, res, [&] {
-            // input transform of the pass's tokens into LDS (prep_block, ft_core.h:97-102), GU_PU blocks' loads in
-            // flight per wave
-            const int nblk = a.H / 128, nit = ns * nblk;
-            for (int it0 = wave; it0 < nit; it0 += NW * GU_PU)
+        // input transform of the pass's tokens into LDS (prep_block, ft_core.h:97-102): each 16-lane row of a wave
+        // takes one (slot, 128-block) item, 8 elements per lane; the first GU_PR rounds of items are loaded before the
+        // trellis groups are requested
+        const int nblk = a.H / 128, nit = ns * nblk, rl = lane >> 4, li = lane & 15;
+        uint4 xv[GU_PR], sv[GU_PR];
+        auto load_round = [&](int r, int k) {
+            const int it = min((r * NW + wave) * 4 + rl, nit - 1);
+            const int s = it / nblk, b = it % nblk;
+            xv[k] = *reinterpret_cast<const uint4*>(a.x + (size_t)(L.spick[c0 + s] / a.topk) * a.H + b * 128 + li * 8);
+            sv[k] = *reinterpret_cast<const uint4*>(suh + b * 128 + li * 8);
+        };
+        auto prep_round = [&](int r, int k) {
+            const int it = (r * NW + wave) * 4 + rl;
+            float v[8];
+            prep_block_row(v, xv[k], sv[k]);
+            if (it < nit)
             {
-                uint16_t xv[GU_PU][2], sv[GU_PU][2];
+                // elements 8li..8li+7 of block b: tile row li/2, accumulators j0 = 2(li&1) and j0 + 1, q = k/2
+                const int s = it / nblk, b = it % nblk, tk = b * 8 + (li >> 1), j0 = 2 * (li & 1);
+                uint16_t* dst = lds_x + (size_t)s * a.H + (tk * 4 + j0) * 4;
+                uint2 e0, e1;
+                e0.x = f2h_bits(v[0]) | (f2h_bits(v[2]) << 16);
+                e0.y = f2h_bits(v[4]) | (f2h_bits(v[6]) << 16);
+                e1.x = f2h_bits(v[1]) | (f2h_bits(v[3]) << 16);
+                e1.y = f2h_bits(v[5]) | (f2h_bits(v[7]) << 16);
+                *reinterpret_cast<uint2*>(dst) = e0;
+                *reinterpret_cast<uint2*>(dst + 4) = e1;
+            }
+        };
+        const int nr = (nit + 4 * NW - 1) / (4 * NW);   // rounds of 4 * NW items
+        chain_dma<K, NS, NGRP>(col, gstride, TK, ns, lds_x, rings + wid * RB, res, [&] {
 #pragma unroll
-                for (int k = 0; k < GU_PU; ++k)
+            for (int k = 0; k < GU_PR; ++k)
+                if (k < nr) load_round(k, k);
+        }, [&] {
+            for (int r0 = 0; r0 < nr; r0 += GU_PR)
+            {
+                if (r0 > 0)
                 {
-                    const int it = min(it0 + k * NW, nit - 1);
-                    const int s = it / nblk, b = it % nblk;
-                    const uint16_t* xr = a.x + (size_t)(L.spick[c0 + s] / a.topk) * a.H + b * 128;
-                    xv[k][0] = xr[lane]; xv[k][1] = xr[lane + 64];
-                    sv[k][0] = suh[b * 128 + lane]; sv[k][1] = suh[b * 128 + lane + 64];
+#pragma unroll
+                    for (int k = 0; k < GU_PR; ++k)
+                        if (r0 + k < nr) load_round(r0 + k, k);
                 }
 #pragma unroll
-                for (int k = 0; k < GU_PU; ++k)
-                {
-                    const int it = it0 + k * NW;
-                    if (it >= nit) break;
-                    const int s = it / nblk, b = it % nblk;
-                    float v0 = h2f_bits(xv[k][0]), v1 = h2f_bits(xv[k][1]);
-                    prep_block_wave(v0, v1, h2f_bits(sv[k][0]), h2f_bits(sv[k][1]));
-                    uint16_t* dst = lds_x + (size_t)s * a.H;
-                    dst[perm_pos(b, lane)] = (uint16_t)f2h_bits(v0);
-                    dst[perm_pos(b, lane + 64)] = (uint16_t)f2h_bits(v1);
-                }
+                for (int k = 0; k < GU_PR; ++k)
+                    if (r0 + k < nr) prep_round(r0 + k, k);
             }
             lds_barrier();   // lds_x complete
         });
@@ -635,11 +656,20 @@ __global__ __launch_bounds__(DN_NW * 64) __attribute__((amdgpu_waves_per_eu(K ==
             q_npk = a.pv.tok_npk[q_tok];
         }
         float res[NS];
+        // the pass's down inputs (ns * I fp16) into LDS; each thread's first two 16-byte loads are issued before the
+        // trellis groups are requested
+        const int nvec = ns * a.I / 8;
+        const uint4* xsrc = reinterpret_cast<const uint4*>(a.xtd + (size_t)c0 * a.I);
+        uint4* xdst = reinterpret_cast<uint4*>(lds_x);
+        const int i0 = threadIdx.x, i1 = threadIdx.x + DN_NW * 64;
+        uint4 xc0 = {}, xc1 = {};
         chain_dma<K, NS, NGRP>(col, gstride, TK, ns, lds_x, rings + wid * RB, res, [&] {
-            const int nvec = ns * a.I / 8;
-            const uint4* src = reinterpret_cast<const uint4*>(a.xtd + (size_t)c0 * a.I);
-            uint4* dst = reinterpret_cast<uint4*>(lds_x);
-            for (int i = threadIdx.x; i < nvec; i += blockDim.x) dst[i] = src[i];
+            if (i0 < nvec) xc0 = xsrc[i0];
+            if (i1 < nvec) xc1 = xsrc[i1];
+        }, [&] {
+            if (i0 < nvec) xdst[i0] = xc0;
+            if (i1 < nvec) xdst[i1] = xc1;
+            for (int i = threadIdx.x + 2 * DN_NW * 64; i < nvec; i += DN_NW * 64) xdst[i] = xsrc[i];
             lds_barrier();   // lds_x complete
         });
 #pragma unroll

@@ -54,6 +54,7 @@ int gfl_ctx_destroy(gfl_ctx* ctx);
  * down [I->H], each an EXL3 trellis of K bits per weight (k_gate/k_up/k_down in 2..5) in 16x16 tiles stored row-major [k/16][n/16].
  * ptrs: HOST array [E][9] of DEVICE addresses per expert:
  *   trellis gate, up, down; suh_gate, svh_gate, suh_up, svh_up, suh_down, svh_down (fp16 sign/scale vectors).
+ * Trellis addresses must be 4-byte aligned, suh/svh addresses 16-byte aligned (both hold for torch allocations).
  * The table is copied; the weights stay where the caller put them (full HBM residency).
  * Replaces tier_add_layer (ft_tier_ext.cpp:160-211) and the pointer tables expert_cache maintains
  * (glm53/expert_cache.py:540-635). */
@@ -64,7 +65,8 @@ int gfl_register_layer(gfl_ctx* ctx, int li, int E, int H, int I, int k_gate, in
  *   out[t] = sum over picks k of w[t,k] * expert_{sel[t,k]}(x[t]), picks with sel < 0 skipped,
  * summed in the reference's job order (moe_forward, kernels/cpu_avx2/ft_core.h:1338-1407).
  * x: fp16 [M, H]; sel: int64 [M, topk]; w: [M, topk] fp16 (w_is_half=1) or fp32; out: fp32 [M, H].
- * act_limit: SwiGLU clamp (tier_set_act_limit, ft_tier_ext.cpp:629-636), 0 = off. M*topk <= 1024, topk <= 16. */
+ * act_limit: SwiGLU clamp (tier_set_act_limit, ft_tier_ext.cpp:629-636), 0 = off. M*topk <= 1024, topk <= 16;
+ * x 16-byte aligned. */
 int gfl_moe_forward(gfl_ctx* ctx, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half, int M,
                     int topk, float* out, int mode, float act_limit, gfl_stream stream);
 

@@ -182,3 +182,22 @@ def test_forward_mixed_k_bitexact(gpu, oracle, Ks):
     want = oracle.moe_forward(ex, x16.astype(np.float32), sel, w, mode=1)
     mx, rms, nbad = _report(f"mixed {Ks}", got, want)
     assert nbad == 0
+
+
+@pytest.mark.gpu
+def test_alignment_errors(gpu):
+    """The gate|up input transform reads x and suh 16 bytes per lane: misaligned addresses are refused, not read."""
+    import torch
+    import _native
+    L = _layer(gpu, 6, 2, 512, 256)
+    bad = list(L.ptr_table)
+    bad[3] += 2                       # suh_gate of expert 0, off its 16-byte alignment
+    with pytest.raises(_native.NativeError, match="misaligned"):
+        gpu.register_layer(7, 2, 512, 256, (3, 3, 3), bad)
+    buf = torch.zeros(512 + 8, dtype=torch.float16, device="cuda")
+    x = buf[1:513].view(1, 512)       # contiguous, 2 bytes off
+    sel = torch.tensor([[0, 1]], dtype=torch.int64, device="cuda")
+    w = torch.ones((1, 2), dtype=torch.float32, device="cuda")
+    out = torch.empty((1, 512), dtype=torch.float32, device="cuda")
+    with pytest.raises(_native.NativeError, match="16-byte aligned"):
+        gpu.moe_forward(6, x, sel, w, out)
