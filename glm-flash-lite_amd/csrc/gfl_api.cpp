@@ -82,7 +82,8 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 // zeroed when the buffer is (re)allocated; the kernels leave every counter at zero when they finish.
 int ensure_ws(gfl_ctx* c, int cap, int H, int I, hipStream_t st, Workspace& w)
 {
-    const size_t ints = align256(sizeof(int) * (size_t)(4 + 9 * cap + 2));
+    // plan ints, then the 8-byte aligned [cap][2] address table
+    const size_t ints = align256(sizeof(int) * (size_t)(4 + 9 * cap + 4) + sizeof(uint64_t) * 2 * (size_t)cap);
     const size_t b_ygu = align256(sizeof(float) * 2 * (size_t)cap * I);
     const size_t b_xtd = align256(sizeof(uint16_t) * (size_t)cap * I);
     const size_t b_yd = align256(sizeof(float) * (size_t)cap * H);
@@ -124,6 +125,7 @@ int ensure_ws(gfl_ctx* c, int cap, int H, int I, hipStream_t st, Workspace& w)
     w.pv.tok_slot = w.pv.pick_job + cap;
     w.pv.tok_w = reinterpret_cast<float*>(w.pv.tok_slot + cap);
     w.pv.tok_npk = reinterpret_cast<int*>(w.pv.tok_w + cap);
+    w.pv.uptr = reinterpret_cast<uint64_t*>(ip + ((4 + 9 * (size_t)cap + 2 + 1) & ~size_t(1)));
     w.pv.cap_slots = cap;
     w.ygu = reinterpret_cast<float*>(b + ints);
     w.xtd = reinterpret_cast<uint16_t*>(b + ints + b_ygu);
@@ -325,6 +327,8 @@ int gfl_grouped_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* se
         return fail(GFL_EINVAL, "gfl_grouped_forward: need 1 <= topk <= 16 and M*topk <= 65536");
     if (!std::isfinite(act_limit) || act_limit < 0)
         return fail(GFL_EINVAL, "gfl_grouped_forward: act_limit must be >= 0");
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out)) & 15)
+        return fail(GFL_EINVAL, "gfl_grouped_forward: x and out must be 16-byte aligned");
     std::lock_guard<std::mutex> g(c->mu);
     const Layer& L = c->layers[li];
     if (L.H % 256 || L.I % 256) return fail(GFL_EINVAL, "gfl_grouped_forward: H and I must be multiples of 256");

@@ -196,7 +196,32 @@ __device__ inline void fwht128_row(float (&v)[8])
     fwht_row_stage<8>(v, L);
 }
 
+__device__ __forceinline__ float h2f_lane(uint4 v, int k)
+{
+    const uint32_t w = k < 2 ? v.x : k < 4 ? v.y : k < 6 ? v.z : v.w;
+    return h2f_bits((uint16_t)(w >> (16 * (k & 1))));
+}
+
+// out_block (ft_core.h:105-110) on a 16-lane row: v = the lane's 8 fp32 outputs, sc its 8 fp16 scales
+__device__ inline void out_block_row(float (&v)[8], uint4 sc)
+{
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = r16(v[k]);
+    fwht128_row(v);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = r16(v[k] * HADF * h2f_lane(sc, k));
+}
+
 // prep_block (ft_core.h:97-102) on a 16-lane row: x and suh are the lane's 8 fp16 inputs and scales (16 bytes each)
+__device__ inline void prep_block_row_f(float (&v)[8], uint4 sc)
+{
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = v[k] * h2f_lane(sc, k);
+    fwht128_row(v);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = r16(v[k] * HADF);
+}
+
 __device__ inline void prep_block_row(float (&v)[8], uint4 x, uint4 sc)
 {
     const uint32_t xw[4] = { x.x, x.y, x.z, x.w }, sw[4] = { sc.x, sc.y, sc.z, sc.w };

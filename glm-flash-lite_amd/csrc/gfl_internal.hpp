@@ -23,6 +23,7 @@ struct PlanView
     int* tok_slot;   // [tokens][topk] slots of each token in combine order, -1 padded
     float* tok_w;    // [tokens][topk] their routing weights (fp32)
     int* tok_npk;    // [tokens] number of valid picks of each token
+    uint64_t* uptr;  // [U][2] down trellis and svh_down addresses of union entry u (one load for the down launch)
     int cap_slots;
 };
 

@@ -239,12 +239,18 @@ __device__ inline int plan_job(const LPlan& L, int p)
 // with their fp32 weights; rows of tokens without a valid pick are written as zeros here (no down workgroup touches
 // them; the reference's sum over an empty route is 0).
 __device__ void publish_plan(const LPlan& L, const int* hdr, int P, int topk, const void* w, int w_half,
-                             const PlanView& pv, float* out, int H)
+                             const PlanView& pv, float* out, int H, const uint64_t* ptrs)
 {
     const int t = threadIdx.x, nt = blockDim.x;
     const int U = hdr[0], S = hdr[1];
     if (t < 3) pv.hdr[t] = hdr[t];
-    for (int u = t; u < U; u += nt) pv.uexp[u] = L.uexp[u];
+    for (int u = t; u < U; u += nt)
+    {
+        const int e = L.uexp[u];
+        pv.uexp[u] = e;
+        pv.uptr[2 * u] = ptrs[(size_t)e * 9 + 2];
+        pv.uptr[2 * u + 1] = ptrs[(size_t)e * 9 + 8];
+    }
     for (int u = t; u <= U; u += nt) pv.uoff[u] = L.uoff[u];
     for (int s = t; s < S; s += nt) pv.slot_pick[s] = L.spick[s];
     for (int p = t; p < P; p += nt)
@@ -500,7 +506,7 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(K ==
     if (blockIdx.x == gridDim.x - 1)
     {
         // the grid's extra workgroup publishes the plan for the down launch (no GEMV work of its own)
-        if (blockIdx.y == 0) publish_plan(L, hdr, a.P, a.topk, a.w, a.w_half, a.pv, a.out, a.H);
+        if (blockIdx.y == 0) publish_plan(L, hdr, a.P, a.topk, a.w, a.w_half, a.pv, a.out, a.H, a.ptrs);
         return;
     }
 
@@ -627,13 +633,15 @@ __global__ __launch_bounds__(DN_NW * 64) __attribute__((amdgpu_waves_per_eu(K ==
     float* lds_y = reinterpret_cast<float*>(lds_raw + NW * RB + (size_t)a.ns_cap * a.I * 2);   // [ns_cap][128]
     const int TN = a.H / 16, TK = a.I / 16, ncb = TN / NW;
     const int u = blockIdx.x / ncb, blk = blockIdx.x % ncb;
-    if (u >= a.pv.hdr[0]) return;
+    // one round of independent loads: the union size, this entry's slot range and its expert's addresses (entries
+    // at u >= U hold stale values and are not used)
+    const int U = a.pv.hdr[0];
+    const int s_begin = a.pv.uoff[u], s_end = a.pv.uoff[u + 1];
+    const uint8_t* tr = reinterpret_cast<const uint8_t*>(a.pv.uptr[2 * u]);
+    const uint16_t* svh = reinterpret_cast<const uint16_t*>(a.pv.uptr[2 * u + 1]);
+    if (u >= U) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15;
     const int wid = __builtin_amdgcn_readfirstlane(wave);
-    const int e = a.pv.uexp[u];
-    const uint8_t* tr = reinterpret_cast<const uint8_t*>(a.ptrs[(size_t)e * 9 + 2]);
-    const uint16_t* svh = reinterpret_cast<const uint16_t*>(a.ptrs[(size_t)e * 9 + 8]);
-    const int s_begin = a.pv.uoff[u], s_end = a.pv.uoff[u + 1];
     const size_t gstride = (size_t)TN * TB;
     const uint8_t* col = tr + (size_t)(blk * NW + wave) * TB;   // this wave's tile column
     const int nbh = a.H / 128;

@@ -196,18 +196,29 @@ __global__ __launch_bounds__(GP_PLAN_THREADS) void gp_plan_kernel(const int64_t*
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// transforms: one wave per slot (or token) walking its 128-blocks, GP_TU blocks' loads in flight; exact rounding points
+// transforms: one wave per slot (or token); each 16-lane row of the wave takes one 128-block, 8 elements per lane
+// (16-byte loads), so a wave works through 4 blocks at a time; exact rounding points
 // ---------------------------------------------------------------------------------------------------------------
 
 constexpr int GP_TW = 4;   // waves per transform workgroup
-constexpr int GP_TU = 4;   // 128-blocks per step of a transform wave
+constexpr int GP_TU = 2;   // rounds of 4 blocks whose loads a transform wave keeps in flight
+
+// Elements 8li..8li+7 of block b in the GEMM input layout gp_perm_pos: pairs (2q, 2q + 1) are adjacent, at
+// b * 128 + q * 32 + (li >> 1) * 4 + 2 * (li & 1)
+__device__ __forceinline__ void gp_store_row(uint16_t* dst, int b, int li, const float (&v)[8])
+{
+    uint16_t* d0 = dst + b * 128 + (li >> 1) * 4 + 2 * (li & 1);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<uint32_t*>(d0 + q * 32) = f2h_bits(v[2 * q]) | (f2h_bits(v[2 * q + 1]) << 16);
+}
 
 // prep_block (ft_core.h:97-102) of the gate and up inputs of slot s (one wave per slot)
 __global__ __launch_bounds__(GP_TW * 64) void gp_prep_kernel(const uint64_t* __restrict__ ptrs,
                                                              const uint16_t* __restrict__ x, int H, int topk, int cap,
                                                              GPlan g, uint16_t* __restrict__ xt)
 {
-    const int lane = threadIdx.x & 63;
+    const int lane = threadIdx.x & 63, rl = lane >> 4, li = lane & 15;
     const int s = blockIdx.x * GP_TW + (threadIdx.x >> 6);
     if (s >= g.hdr[0]) return;
     const int nblk = H / 128;
@@ -217,30 +228,29 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_prep_kernel(const uint64_t* __r
     const uint16_t* xr = x + (size_t)tok * H;
     uint16_t* d0 = xt + (size_t)s * H;
     uint16_t* d1 = xt + ((size_t)cap + s) * H;
-    for (int b0 = 0; b0 < nblk; b0 += GP_TU)
+    for (int b0 = 0; b0 < nblk; b0 += 4 * GP_TU)
     {
-        uint16_t xv[GP_TU][2], g0[GP_TU][2], g1[GP_TU][2];
+        uint4 xv[GP_TU], g0[GP_TU], g1[GP_TU];
 #pragma unroll
-        for (int j = 0; j < GP_TU; ++j)
+        for (int k = 0; k < GP_TU; ++k)
         {
-            const int o = min(b0 + j, nblk - 1) * 128 + lane;
-            xv[j][0] = xr[o]; xv[j][1] = xr[o + 64];
-            g0[j][0] = su0[o]; g0[j][1] = su0[o + 64];
-            g1[j][0] = su1[o]; g1[j][1] = su1[o + 64];
+            const int o = min(b0 + 4 * k + rl, nblk - 1) * 128 + li * 8;
+            xv[k] = *reinterpret_cast<const uint4*>(xr + o);
+            g0[k] = *reinterpret_cast<const uint4*>(su0 + o);
+            g1[k] = *reinterpret_cast<const uint4*>(su1 + o);
         }
 #pragma unroll
-        for (int j = 0; j < GP_TU; ++j)
+        for (int k = 0; k < GP_TU; ++k)
         {
-            const int b = b0 + j;
-            if (b >= nblk) break;
-            float u0 = h2f_bits(xv[j][0]), u1 = h2f_bits(xv[j][1]);
-            float v0 = u0, v1 = u1;
-            prep_block_wave(u0, u1, h2f_bits(g0[j][0]), h2f_bits(g0[j][1]));
-            prep_block_wave(v0, v1, h2f_bits(g1[j][0]), h2f_bits(g1[j][1]));
-            d0[gp_perm_pos(b, lane)] = (uint16_t)f2h_bits(u0);
-            d0[gp_perm_pos(b, lane + 64)] = (uint16_t)f2h_bits(u1);
-            d1[gp_perm_pos(b, lane)] = (uint16_t)f2h_bits(v0);
-            d1[gp_perm_pos(b, lane + 64)] = (uint16_t)f2h_bits(v1);
+            const int b = b0 + 4 * k + rl;
+            float u[8], v[8];
+            prep_block_row(u, xv[k], g0[k]);
+            prep_block_row(v, xv[k], g1[k]);
+            if (b < nblk)
+            {
+                gp_store_row(d0, b, li, u);
+                gp_store_row(d1, b, li, v);
+            }
         }
     }
 }
@@ -251,7 +261,7 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_act_kernel(const uint64_t* __re
                                                             const float* __restrict__ ygu, const float* exp_tab,
                                                             float act_limit, uint16_t* __restrict__ xd)
 {
-    const int lane = threadIdx.x & 63;
+    const int lane = threadIdx.x & 63, rl = lane >> 4, li = lane & 15;
     const int s = blockIdx.x * GP_TW + (threadIdx.x >> 6);
     if (s >= g.hdr[0]) return;
     const int nbi = I / 128;
@@ -262,33 +272,23 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_act_kernel(const uint64_t* __re
     const float* yg = ygu + (size_t)s * I;
     const float* yu = ygu + ((size_t)cap + s) * I;
     uint16_t* dst = xd + (size_t)s * I;
-    for (int b0 = 0; b0 < nbi; b0 += GP_TU)
+    for (int b0 = 0; b0 < nbi; b0 += 4)
     {
-        float gv[GP_TU][2], uv[GP_TU][2];
-        uint16_t sg[GP_TU][2], su[GP_TU][2], sd[GP_TU][2];
+        const int b = b0 + rl, o = min(b, nbi - 1) * 128 + li * 8;
+        const float4 ga = *reinterpret_cast<const float4*>(yg + o), gb = *reinterpret_cast<const float4*>(yg + o + 4);
+        const float4 ua = *reinterpret_cast<const float4*>(yu + o), ub = *reinterpret_cast<const float4*>(yu + o + 4);
+        const uint4 sg = *reinterpret_cast<const uint4*>(svh_g + o);
+        const uint4 su = *reinterpret_cast<const uint4*>(svh_u + o);
+        const uint4 sd = *reinterpret_cast<const uint4*>(suh_d + o);
+        float gv[8] = { ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w };
+        float uv[8] = { ua.x, ua.y, ua.z, ua.w, ub.x, ub.y, ub.z, ub.w };
+        out_block_row(gv, sg);
+        out_block_row(uv, su);
+        float av[8];
 #pragma unroll
-        for (int j = 0; j < GP_TU; ++j)
-        {
-            const int o = min(b0 + j, nbi - 1) * 128 + lane;
-            gv[j][0] = yg[o]; gv[j][1] = yg[o + 64];
-            uv[j][0] = yu[o]; uv[j][1] = yu[o + 64];
-            sg[j][0] = svh_g[o]; sg[j][1] = svh_g[o + 64];
-            su[j][0] = svh_u[o]; su[j][1] = svh_u[o + 64];
-            sd[j][0] = suh_d[o]; sd[j][1] = suh_d[o + 64];
-        }
-#pragma unroll
-        for (int j = 0; j < GP_TU; ++j)
-        {
-            const int b = b0 + j;
-            if (b >= nbi) break;
-            float g0 = gv[j][0], g1 = gv[j][1], u0 = uv[j][0], u1 = uv[j][1];
-            out_block_wave(g0, g1, h2f_bits(sg[j][0]), h2f_bits(sg[j][1]));
-            out_block_wave(u0, u1, h2f_bits(su[j][0]), h2f_bits(su[j][1]));
-            float a0 = r16(act_mul(g0, u0, act_limit, exp_tab)), a1 = r16(act_mul(g1, u1, act_limit, exp_tab));
-            prep_block_wave(a0, a1, h2f_bits(sd[j][0]), h2f_bits(sd[j][1]));
-            dst[gp_perm_pos(b, lane)] = (uint16_t)f2h_bits(a0);
-            dst[gp_perm_pos(b, lane + 64)] = (uint16_t)f2h_bits(a1);
-        }
+        for (int k = 0; k < 8; ++k) av[k] = r16(act_mul(gv[k], uv[k], act_limit, exp_tab));
+        prep_block_row_f(av, sd);
+        if (b < nbi) gp_store_row(dst, b, li, av);
     }
 }
 
@@ -299,7 +299,7 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_comb_kernel(const uint64_t* __r
                                                              GPlan g, const float* __restrict__ yraw,
                                                              float* __restrict__ out)
 {
-    const int lane = threadIdx.x & 63;
+    const int lane = threadIdx.x & 63, rl = lane >> 4, li = lane & 15;
     const int tok = blockIdx.x * GP_TW + (threadIdx.x >> 6);
     if (tok >= M) return;
     const int nbh = H / 128;
@@ -314,43 +314,30 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_comb_kernel(const uint64_t* __r
         my_p = ptrs[(size_t)g.slot_e[my_s] * 9 + 8];
     }
     float* orow = out + (size_t)tok * H;
-    for (int b0 = 0; b0 < nbh; b0 += GP_TU)
+    for (int b0 = 0; b0 < nbh; b0 += 4)
     {
-        float o[GP_TU][2];
+        const int b = b0 + rl, o = min(b, nbh - 1) * 128 + li * 8;
+        float acc[8];
 #pragma unroll
-        for (int j = 0; j < GP_TU; ++j) o[j][0] = o[j][1] = 0.f;
+        for (int k = 0; k < 8; ++k) acc[k] = 0.f;
         for (int k = 0; k < npk; ++k)
         {
             const int s = __builtin_amdgcn_readlane(my_s, k);
             const float wk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), k));
             const uint64_t pa = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(my_p >> 32), k) << 32) |
                                 (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)my_p, k);
-            const uint16_t* svh = reinterpret_cast<const uint16_t*>(pa);
-            const float* yr = yraw + (size_t)s * H;
-            float v[GP_TU][2];
-            uint16_t sv[GP_TU][2];
+            const float* yr = yraw + (size_t)s * H + o;
+            const float4 ya = *reinterpret_cast<const float4*>(yr), yb = *reinterpret_cast<const float4*>(yr + 4);
+            const uint4 sv = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(pa) + o);
+            float v[8] = { ya.x, ya.y, ya.z, ya.w, yb.x, yb.y, yb.z, yb.w };
+            out_block_row(v, sv);
 #pragma unroll
-            for (int j = 0; j < GP_TU; ++j)
-            {
-                const int oo = min(b0 + j, nbh - 1) * 128 + lane;
-                v[j][0] = yr[oo]; v[j][1] = yr[oo + 64];
-                sv[j][0] = svh[oo]; sv[j][1] = svh[oo + 64];
-            }
-#pragma unroll
-            for (int j = 0; j < GP_TU; ++j)
-            {
-                out_block_wave(v[j][0], v[j][1], h2f_bits(sv[j][0]), h2f_bits(sv[j][1]));
-                o[j][0] = o[j][0] + wk * v[j][0];
-                o[j][1] = o[j][1] + wk * v[j][1];
-            }
+            for (int j = 0; j < 8; ++j) acc[j] = acc[j] + wk * v[j];
         }
-#pragma unroll
-        for (int j = 0; j < GP_TU; ++j)
+        if (b < nbh)
         {
-            const int b = b0 + j;
-            if (b >= nbh) break;
-            orow[b * 128 + lane] = o[j][0];
-            orow[b * 128 + lane + 64] = o[j][1];
+            *reinterpret_cast<float4*>(orow + b * 128 + li * 8) = float4{ acc[0], acc[1], acc[2], acc[3] };
+            *reinterpret_cast<float4*>(orow + b * 128 + li * 8 + 4) = float4{ acc[4], acc[5], acc[6], acc[7] };
         }
     }
 }

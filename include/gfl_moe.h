@@ -76,7 +76,7 @@ int gfl_moe_forward(gfl_ctx* ctx, int li, const uint16_t* x, const int64_t* sel,
 
 /* Routed-expert forward of one layer for prefill-sized M (the north star's MFMA grouped GEMM), same arguments and
  * result layout as gfl_moe_forward: x fp16 [M, H], sel int64 [M, topk] (ids outside [0, E) skipped), w fp16 or fp32
- * [M, topk], out fp32 [M, H]; M*topk <= 65536. Rows are grouped expert-major (tier_lut_build_grouped_rows,
+ * [M, topk], out fp32 [M, H]; M*topk <= 65536; x and out 16-byte aligned. Rows are grouped expert-major (tier_lut_build_grouped_rows,
  * kernels/cpu_avx2/ft_tier_ext.cpp:1047-1097), gate|up and down run as v_mfma_f32_16x16x32_f16 grouped GEMMs on the
  * bit-exact dequantized fp16 weights, the transforms keep the reference's fp16 rounding points and the combine its job
  * order (kernels/cpu_avx2/ft_core.h:933-1033). The hidden-dimension sums are formed in MFMA order, so results differ
