@@ -276,8 +276,37 @@ def extra_configs(ctx, layers, args, G, reps):
     res["config4_prefill"] = time_prefill(ctx, list(range(args.layers)), layers[0].quant_bytes_per_expert, 2048,
                                           max(4, reps // 2))
     print(f"bench: config 4 prefill done ({time.time() - t0:.0f} s)", file=sys.stderr, flush=True)
+    res["router"] = {f"M{M}": time_router(M) for M in (1, 4, 64, 2048)}
     res["setup_and_time_s"] = round(time.time() - t0, 1)
     return res
+
+
+def time_router(M, reps=8, G=32):
+    """gfl_route on fp32 N(0,1) logits [M, 288] -> top-8 sel / fp16 w: mean µs per call, G calls captured in a HIP
+    graph replayed `reps` times (device events around the replays)."""
+    import numpy as np
+    import torch
+    import _native
+    lg = torch.from_numpy(np.random.default_rng(6000 + M).standard_normal((M, E)).astype(np.float32)).cuda()
+    sel = torch.empty((M, TOPK), dtype=torch.int64, device="cuda")
+    w = torch.empty((M, TOPK), dtype=torch.float16, device="cuda")
+    for _ in range(3):
+        _native.route(lg, TOPK, sel, w)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(G):
+            _native.route(lg, TOPK, sel, w)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    del g
+    return {"us_per_call": round(e0.elapsed_time(e1) * 1e3 / (reps * G), 2), "tokens": M, "experts": E, "topk": TOPK}
 
 
 def time_prefill(ctx, layer_ids, bytes_per_expert, M, reps, G=4):

@@ -13,7 +13,7 @@ LIB_PATH = os.path.join(HERE, "libgfl_moe.so")
 # exported symbols of include/gfl_moe.h (checked by tests/test_abi.py against the header)
 SYMBOLS = ("gfl_last_error", "gfl_version", "gfl_ctx_create", "gfl_ctx_destroy", "gfl_register_layer",
            "gfl_moe_forward", "gfl_grouped_forward", "gfl_dequant", "gfl_split", "gfl_combine", "gfl_grouped_rows",
-           "gfl_synth_trellis",
+           "gfl_synth_trellis", "gfl_route",
            "gfl_stats", "gfl_profile_enable", "gfl_profile_read", "gfl_exp_table")
 
 MODE_AUTO, MODE_AFFINE, MODE_EXACT, MODE_I16 = -1, 0, 1, 2
@@ -55,6 +55,7 @@ def load(path=LIB_PATH):
     L.gfl_combine.argtypes = [_P, C.c_int, C.c_int, _P, _P, _P, _P, C.c_int64, _P]
     L.gfl_grouped_rows.argtypes = [_P, _P, C.c_int, C.c_int, _P, C.c_int, _P, _P, _P, _P, C.POINTER(C.c_int)]
     L.gfl_synth_trellis.argtypes = [_P, C.c_size_t, C.c_uint64, _P]
+    L.gfl_route.argtypes = [_P, C.c_int, C.c_int, C.c_int, _P, _P, _P]
     L.gfl_stats.argtypes = [_P, _P, C.c_int]
     L.gfl_profile_enable.argtypes = [_P, C.c_int]
     L.gfl_profile_read.argtypes = [_P, _P, _P]
@@ -177,6 +178,25 @@ def synth_trellis(dst, seed, nbytes=None):
     nb = dst.numel() * dst.element_size() if nbytes is None else int(nbytes)
     check(load().gfl_synth_trellis(ptr(dst), nb, C.c_uint64(seed & 0xFFFFFFFFFFFFFFFF), _stream()))
     return dst
+
+
+def route(logits, topk=8, sel=None, w=None):
+    """Router (gfl_route): logits fp32 [M, E] on the device -> (sel int64 [M, topk], w fp16 [M, topk]), the routing_fn
+    contract ft_split consumes. sel / w may be given (contiguous, on the device) to write in place."""
+    import torch
+    if not (logits.dtype == torch.float32 and logits.dim() == 2 and logits.is_contiguous() and logits.is_cuda):
+        raise ValueError("logits must be contiguous fp32 [M, E] on the device")
+    M, E = logits.shape
+    if sel is None:
+        sel = torch.empty((M, topk), dtype=torch.int64, device=logits.device)
+    if w is None:
+        w = torch.empty((M, topk), dtype=torch.float16, device=logits.device)
+    if not (sel.dtype == torch.int64 and sel.is_contiguous() and tuple(sel.shape) == (M, topk)):
+        raise ValueError("sel must be contiguous int64 [M, topk]")
+    if not (w.dtype == torch.float16 and w.is_contiguous() and tuple(w.shape) == (M, topk)):
+        raise ValueError("w must be contiguous fp16 [M, topk]")
+    check(load().gfl_route(ptr(logits), M, E, int(topk), ptr(sel), ptr(w), _stream()))
+    return sel, w
 
 
 def split(sel, w, z, E, first, slotof, score, pol, ctrl, hx, hpicks, seq, li, keep_ids, sel_out, w_out, dflag,

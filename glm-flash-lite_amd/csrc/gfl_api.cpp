@@ -477,6 +477,19 @@ int gfl_grouped_rows(const int64_t* sel, const float* w, int T, int K, const uin
     return nexp;
 }
 
+int gfl_route(const float* logits, int M, int E, int topk, int64_t* sel, uint16_t* w, gfl_stream stream)
+{
+    if (M < 0) return fail(GFL_EINVAL, "gfl_route: M < 0");
+    if (E < 1 || E > gfl::MAX_EXPERTS || topk < 1 || topk > E || topk > 64)
+        return fail(GFL_EINVAL, "gfl_route: need 1 <= E <= 1024 and 1 <= topk <= min(E, 64)");
+    if (M == 0) return GFL_OK;   // an empty batch (whose buffers may be NULL) routes nothing
+    if (!logits || !sel || !w) return fail(GFL_EINVAL, "gfl_route: NULL argument");
+    if (gfl::launch_route(logits, M, E, topk, sel, w, reinterpret_cast<hipStream_t>(stream)))
+        return fail(GFL_EINVAL, "gfl_route: unsupported shape");
+    GFL_HIP(hipGetLastError());
+    return GFL_OK;
+}
+
 int gfl_synth_trellis(void* dst, size_t nbytes, uint64_t seed, gfl_stream stream)
 {
     if (!dst) return fail(GFL_EINVAL, "gfl_synth_trellis: NULL destination");

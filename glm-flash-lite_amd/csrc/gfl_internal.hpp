@@ -70,5 +70,6 @@ int launch_split(const int64_t* sel, const uint16_t* w, const uint16_t* z, int n
 void launch_combine(void* out, int is_half, int n, const int64_t* dflag, const int64_t* ctrl, const float* hout,
                     int64_t* stats, int64_t timeout_ns, hipStream_t st);
 void launch_synth(uint8_t* dst, size_t nbytes, uint64_t seed, hipStream_t st);
+int launch_route(const float* logits, int M, int E, int topk, int64_t* sel, uint16_t* w, hipStream_t st);
 
 }  // namespace gfl

@@ -240,6 +240,91 @@ __global__ __launch_bounds__(1024) void combine_kernel(void* out, int is_half, i
     }
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// router: sigmoid scores, top-k (lower index on ties), weights renormalised over the picks and rounded to fp16
+// ---------------------------------------------------------------------------------------------------------------
+
+// The router feeding ft_split (cpu_tier.py:305-307 calls the model's routing_fn, exllamav3's, which returns sel int64
+// [bsz, 8] and w fp16 [bsz, 8]). One wave per token. The score is s = 1 / (1 + e) in fp32 with e = exp(-x) rounded once
+// to fp32 (evaluated in double, so it is the correctly rounded value). k rounds of a wave arg-max over the unused
+// experts, ordered by (score descending, index ascending); the picks' scores are summed in pick order and w_j = s_j / sum
+// is rounded to fp16 (round to nearest even). Logits must be finite.
+constexpr int ROUTE_WAVES = 4;
+constexpr int ROUTE_MAXE = 1024;   // experts per token: up to 16 per lane
+
+__global__ __launch_bounds__(ROUTE_WAVES * 64) void route_kernel(const float* __restrict__ logits, int M, int E, int topk,
+                                                                 int64_t* __restrict__ sel, uint16_t* __restrict__ w)
+{
+    const int lane = threadIdx.x & 63;
+    const int m = blockIdx.x * ROUTE_WAVES + (threadIdx.x >> 6);
+    if (m >= M) return;
+    const float* lg = logits + (size_t)m * E;
+    float sc[ROUTE_MAXE / 64];
+#pragma unroll
+    for (int i = 0; i < ROUTE_MAXE / 64; ++i)
+    {
+        const int e = lane + 64 * i;
+        float v = -INFINITY;
+        if (e < E)
+        {
+            const float ex = (float)exp(-(double)lg[e]);
+            v = 1.0f / (1.0f + ex);
+        }
+        sc[i] = v;
+    }
+    uint32_t used = 0;
+    float tot = 0.0f, mine = 0.0f;
+    int myidx = 0;
+    for (int j = 0; j < topk; ++j)
+    {
+        // this lane's best unused (score descending, index ascending: the first strict maximum in index order)
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int i = 0; i < ROUTE_MAXE / 64; ++i)
+        {
+            const int e = lane + 64 * i;
+            if (e < E && !((used >> i) & 1) && (sc[i] > bv || bi == 0x7fffffff))
+            {
+                bv = sc[i];
+                bi = e;
+            }
+        }
+        // wave arg-max with the same order
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1)
+        {
+            const float ov = __shfl_xor(bv, d);
+            const int oi = __shfl_xor(bi, d);
+            if (oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi)))
+            {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if ((bi & 63) == lane) used |= 1u << (bi >> 6);
+        tot = tot + bv;               // pick order, as the reference's renormalisation loop
+        if (lane == j)
+        {
+            mine = bv;
+            myidx = bi;
+        }
+    }
+    if (lane < topk)
+    {
+        sel[(size_t)m * topk + lane] = myidx;
+        w[(size_t)m * topk + lane] = (uint16_t)f2h_bits(mine / tot);
+    }
+}
+
+int launch_route(const float* logits, int M, int E, int topk, int64_t* sel, uint16_t* w, hipStream_t st)
+{
+    if (E < 1 || E > ROUTE_MAXE || topk < 1 || topk > E || topk > 64) return -1;
+    hipLaunchKernelGGL(route_kernel, dim3((M + ROUTE_WAVES - 1) / ROUTE_WAVES), dim3(ROUTE_WAVES * 64), 0, st, logits,
+                       M, E, topk, sel, w);
+    return 0;
+}
+
 // splitmix64 in counter form: output i of the sequence seeded with `seed` is mix(seed + (i+1) * golden)
 __device__ inline uint64_t splitmix64_at(uint64_t seed, uint64_t i)
 {

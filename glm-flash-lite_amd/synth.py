@@ -117,9 +117,11 @@ def route_uniform(M, E, topk, rng):
 
 
 def route(logits, topk):
-    """Sigmoid scores, top-k (lower index on ties), w = s / sum(s) rounded to fp16. Returns (sel int64, w fp16)."""
+    """Sigmoid scores s = 1 / (1 + e), e = exp(-x) correctly rounded to fp32, top-k (lower index on ties),
+    w = s / sum(s) (summed in pick order) rounded to fp16. Returns (sel int64, w fp16)."""
     logits = np.asarray(logits, dtype=np.float32)
-    s = (1.0 / (1.0 + np.exp(-logits.astype(np.float32)))).astype(np.float32)
+    ex = np.exp(-logits.astype(np.float64)).astype(np.float32)      # correctly rounded fp32 exp(-x)
+    s = (np.float32(1.0) / (np.float32(1.0) + ex)).astype(np.float32)
     order = np.argsort(-s, axis=1, kind="stable")[:, :topk]
     picked = np.take_along_axis(s, order, axis=1).astype(np.float32)
     tot = np.zeros(picked.shape[0], np.float32)

@@ -109,6 +109,13 @@ int gfl_combine(void* out, int out_is_half, int n, const int64_t* dflag, const i
 int gfl_grouped_rows(const int64_t* sel, const float* w, int T, int K, const uint8_t* take, int E, int32_t* experts,
                      int32_t* offsets, int32_t* row_token, float* row_weight, int* rows);
 
+/* Router for the split (the model's routing_fn that cpu_tier.routed calls first, glm53/cpu_tier.py:305-307; exllamav3's
+ * own router is not in the reference tree): logits fp32 [M, E] (finite) -> sel int64 [M, topk], w fp16 [M, topk], all
+ * device memory. Scores s = 1 / (1 + e) in fp32 with e = exp(-x) correctly rounded to fp32; the topk largest scores in
+ * order (lower expert index on ties); w = s / (sum of the picked scores, added in pick order) rounded to fp16.
+ * E <= 1024, topk <= min(E, 64). One wave per token, stream-ordered. */
+int gfl_route(const float* logits, int M, int E, int topk, int64_t* sel, uint16_t* w, gfl_stream stream);
+
 /* Fill nbytes of device memory with the splitmix64 stream of `seed` (synthetic trellis for tests and benchmarks;
  * any bit stream is a valid EXL3 tile). Byte b = byte (b % 8) of output b/8. */
 int gfl_synth_trellis(void* dst, size_t nbytes, uint64_t seed, gfl_stream stream);

@@ -599,7 +599,14 @@ void gflo_route(const float* logits, int M, int E, int topk, int64_t* sel, uint1
     unsigned char* used = (unsigned char*)malloc((size_t)E);
     for (int m = 0; m < M; ++m)
     {
-        for (int e = 0; e < E; ++e) { s[e] = 1.0f / (1.0f + expf(-logits[(size_t)m * E + e])); used[e] = 0; }
+        for (int e = 0; e < E; ++e)
+        {
+            /* exp evaluated in double and rounded once: the correctly rounded fp32 exp(-x), which the device router
+               reproduces exactly (exllamav3's router is not in the reference tree: parity unpinned against it) */
+            const float ex = (float)exp(-(double)logits[(size_t)m * E + e]);
+            s[e] = 1.0f / (1.0f + ex);
+            used[e] = 0;
+        }
         float tot = 0.0f;
         float pick[64];
         for (int j = 0; j < topk; ++j)
