@@ -12,7 +12,8 @@ roofline     = the gate|up GEMV kernel (the dominant one) at M=1: algorithmic qu
                routed experts x (gate+up trellis + their suh/svh)) / its mean launch time, from device events
                recorded around every launch during a timed eager pass; peak = 8 TB/s HBM.
 configs      = BASELINE configs 2 (mixed bitrates, Zipf routing), 3 (M=16/32/64) and 4 (42 resident layers decoded
-               at M=1; prefill of M=2048 tokens through the MFMA grouped path, as TFLOP/s against 2.5 PF dense fp16).
+               at M=1; prefill of M=2048 tokens through the MFMA grouped path, as TFLOP/s against 2.5 PF dense fp16);
+               the router (gfl_route) per call; routed layer + shared expert, sequential vs overlapped on a side stream.
 cpu_baseline = the reference's own AVX2 expert engine (kernels/cpu_avx2/ft_core.h, built into oracle/_ref) timed on
                this host: decode calls of 1 token x 8 experts cycling a DRAM-cold pool of 288 experts, I16 mode.
 """
@@ -277,7 +278,62 @@ def extra_configs(ctx, layers, args, G, reps):
                                           max(4, reps // 2))
     print(f"bench: config 4 prefill done ({time.time() - t0:.0f} s)", file=sys.stderr, flush=True)
     res["router"] = {f"M{M}": time_router(M) for M in (1, 4, 64, 2048)}
+    res["shared_overlap"] = time_shared(ctx, list(range(args.layers)), G, reps)
+    print(f"bench: shared-expert overlap done ({time.time() - t0:.0f} s)", file=sys.stderr, flush=True)
     res["setup_and_time_s"] = round(time.time() - t0, 1)
+    return res
+
+
+def time_shared(ctx, layer_ids, G, reps):
+    """Routed layer + the layer's shared expert (one more config-0-shaped expert at 3 bpw), per token: the shared
+    expert after the routed call on one stream ("sequential", the stock order) and on a side stream overlapped with
+    it (k_overlap.SharedOverlap, "overlapped"). Graph-timed like the decode steps."""
+    import numpy as np
+    import torch
+    import k_overlap
+    import synth
+    so = k_overlap.SharedOverlap(0)
+    keep = []
+    for li in layer_ids:
+        S = synth.SynthLayer(300 + li, 1, H, I, (KBITS,) * 3)
+        so.register(li, H, I, S.Ks, S.ptr_table, keep=S)
+        keep.append(S)
+    res = {}
+    for M in (1, 4):
+        routes = make_routes(M, np.random.default_rng(7000 + M), 32, "uniform")
+        out = torch.empty((M, H), dtype=torch.float32, device="cuda")
+        r = {}
+        for mode in ("sequential", "overlapped"):
+            ov = mode == "overlapped"
+
+            def step(i):
+                x, sel, w, _ = routes[i % len(routes)]
+                so.forward(ctx, layer_ids[i % len(layer_ids)], x, sel, w, out, overlap=ov)
+
+            for i in range(8):
+                step(i)
+            torch.cuda.synchronize()
+            st = torch.cuda.Stream()
+            st.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(st):
+                step(0)
+            torch.cuda.current_stream().wait_stream(st)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for i in range(G):
+                    step(i)
+            g.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            del g
+            r[mode] = round(e0.elapsed_time(e1) * 1e3 / (reps * G) / M, 3)
+        r["overlap_gain"] = round(r["sequential"] / r["overlapped"], 3)
+        res[f"M{M}_us_per_token"] = r
     return res
 
 

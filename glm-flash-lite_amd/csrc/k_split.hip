@@ -249,6 +249,19 @@ __global__ __launch_bounds__(1024) void combine_kernel(void* out, int is_half, i
 // to fp32 (evaluated in double, so it is the correctly rounded value). k rounds of a wave arg-max over the unused
 // experts, ordered by (score descending, index ascending); the picks' scores are summed in pick order and w_j = s_j / sum
 // is rounded to fp16 (round to nearest even). Logits must be finite.
+// one butterfly step of the (score descending, index ascending) arg-max: combine with lane ^ W
+template <int W>
+__device__ __forceinline__ void route_argmax_step(float& bv, int& bi)
+{
+    const float ov = lane_xor<W>(bv);
+    const int oi = __float_as_int(lane_xor<W>(__int_as_float(bi)));
+    if (oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi)))
+    {
+        bv = ov;
+        bi = oi;
+    }
+}
+
 constexpr int ROUTE_WAVES = 4;
 constexpr int ROUTE_MAXE = 1024;   // experts per token: up to 16 per lane
 
@@ -259,18 +272,20 @@ __global__ __launch_bounds__(ROUTE_WAVES * 64) void route_kernel(const float* __
     const int m = blockIdx.x * ROUTE_WAVES + (threadIdx.x >> 6);
     if (m >= M) return;
     const float* lg = logits + (size_t)m * E;
+    // every load first (uniform guards, clamped addresses), so the token's logits arrive in one round trip
     float sc[ROUTE_MAXE / 64];
 #pragma unroll
     for (int i = 0; i < ROUTE_MAXE / 64; ++i)
+        if (64 * i < E) sc[i] = lg[min(lane + 64 * i, E - 1)];
+#pragma unroll
+    for (int i = 0; i < ROUTE_MAXE / 64; ++i)
     {
-        const int e = lane + 64 * i;
-        float v = -INFINITY;
-        if (e < E)
+        if (64 * i < E)
         {
-            const float ex = (float)exp(-(double)lg[e]);
-            v = 1.0f / (1.0f + ex);
+            const float ex = (float)exp(-(double)sc[i]);
+            sc[i] = lane + 64 * i < E ? 1.0f / (1.0f + ex) : -INFINITY;
         }
-        sc[i] = v;
+        else sc[i] = -INFINITY;
     }
     uint32_t used = 0;
     float tot = 0.0f, mine = 0.0f;
@@ -290,18 +305,13 @@ __global__ __launch_bounds__(ROUTE_WAVES * 64) void route_kernel(const float* __
                 bi = e;
             }
         }
-        // wave arg-max with the same order
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1)
-        {
-            const float ov = __shfl_xor(bv, d);
-            const int oi = __shfl_xor(bi, d);
-            if (oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi)))
-            {
-                bv = ov;
-                bi = oi;
-            }
-        }
+        // wave arg-max with the same order, through DPP / permlane exchanges (no LDS round trips)
+        route_argmax_step<1>(bv, bi);
+        route_argmax_step<2>(bv, bi);
+        route_argmax_step<4>(bv, bi);
+        route_argmax_step<8>(bv, bi);
+        route_argmax_step<16>(bv, bi);
+        route_argmax_step<32>(bv, bi);
         if ((bi & 63) == lane) used |= 1u << (bi >> 6);
         tot = tot + bv;               // pick order, as the reference's renormalisation loop
         if (lane == j)
