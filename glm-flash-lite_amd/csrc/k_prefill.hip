@@ -393,7 +393,8 @@ __global__ __launch_bounds__(GP_NW * 64) void gp_gemm_kernel(GemmArgs a)
     constexpr int NV = NLD + GP_XPW;              // vector memory instructions per wave per group
     static_assert(GB % 256 == 0, "group of tiles must split into whole wave loads");
     extern __shared__ __align__(16) uint8_t gp_lds[];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // the wave index in a scalar register, so every LDS-DMA destination (M0) is scalar arithmetic
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     // XCD-aware order: workgroups are dispatched round-robin over the 8 XCDs (XCD = linear id % 8), so every
     // workgroup of expert e gets a linear id = e % 8 (mod 8) and the expert's slot inputs are fetched into one L2
     const int nch = a.ndim / GP_WCOLS, per = nch * a.nmat;
@@ -423,6 +424,10 @@ __global__ __launch_bounds__(GP_NW * 64) void gp_gemm_kernel(GemmArgs a)
     }
     const LaneDec d = lane_dec(lane, K);
     const uint16_t* xin = a.xin + (size_t)(mat - a.mat_base) * a.cap * a.kdim;
+    // the slots' inputs through a buffer resource too: per-lane offsets fixed for a pass, the group in the scalar offset
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(uniform_ptr(reinterpret_cast<const uint8_t*>(xin))), (short)0,
+        (int)((size_t)a.cap * a.kdim * 2), 0x00020000);
     float* yout = a.yout + (size_t)(mat - a.mat_base) * a.cap * a.ndim;
     const int q = lane >> 4, i16 = lane & 15;
 
@@ -430,12 +435,12 @@ __global__ __launch_bounds__(GP_NW * 64) void gp_gemm_kernel(GemmArgs a)
     {
         const int T = min(GP_MT, s_end - c0);
         // the input chunk of group g for this wave's slots (slots past the pass read the pass's last slot)
-        const uint8_t* xbase[GP_XPW];
+        int xoff[GP_XPW];
 #pragma unroll
         for (int j = 0; j < GP_XPW; ++j)
         {
             const int sl = min(wave * GP_XPW + j, T - 1);
-            xbase[j] = reinterpret_cast<const uint8_t*>(xin + (size_t)(c0 + sl) * a.kdim);
+            xoff[j] = (c0 + sl) * a.kdim * 2 + lane * 4;
         }
         auto issue = [&](int g) {
             uint8_t* dst = ring + (g % NG) * GB;
@@ -446,8 +451,8 @@ __global__ __launch_bounds__(GP_NW * 64) void gp_gemm_kernel(GemmArgs a)
             uint16_t* xd = xring + (size_t)(g % NG) * GP_MT * GP_XS;
 #pragma unroll
             for (int j = 0; j < GP_XPW; ++j)
-                __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(xbase[j] + g * 256 + lane * 4),
-                                                 (gp_lds_void*)(xd + (wave * GP_XPW + j) * GP_XS), 4, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (gp_lds_void*)(xd + (wave * GP_XPW + j) * GP_XS), 4, xoff[j],
+                                                         g * 256, 0, 0);
         };
         float4v acc[GP_CPW][4];
 #pragma unroll
