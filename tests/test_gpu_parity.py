@@ -201,3 +201,52 @@ def test_alignment_errors(gpu):
     out = torch.empty((1, 512), dtype=torch.float32, device="cuda")
     with pytest.raises(_native.NativeError, match="16-byte aligned"):
         gpu.moe_forward(6, x, sel, w, out)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("ns", [1, 2, 4, 8])
+def test_forward_slots_per_pass_bitexact(oracle, ns):
+    """Every slots-per-pass instantiation (GFL_SLOTS_PER_PASS, read at context creation): 12 tokens over 6 experts, so
+    experts hold up to 12 slots and take several passes over their weights."""
+    import os
+    import _native
+    import synth
+    old = os.environ.get("GFL_SLOTS_PER_PASS")
+    os.environ["GFL_SLOTS_PER_PASS"] = str(ns)
+    try:
+        ctx = _native.Context(0)
+    finally:
+        if old is None:
+            os.environ.pop("GFL_SLOTS_PER_PASS", None)
+        else:
+            os.environ["GFL_SLOTS_PER_PASS"] = old
+    H, I, E = 512, 256, 6
+    L = synth.SynthLayer(8, E, H, I, (3, 3, 3))
+    L.register(ctx, 8)
+    ex = _host_experts(oracle, L)
+    rng = np.random.default_rng(100 + ns)
+    M = 12
+    x16 = rng.standard_normal((M, H)).astype(np.float16)
+    sel = np.stack([rng.permutation(E)[:4] for _ in range(M)]).astype(np.int64)
+    w = rng.random(sel.shape).astype(np.float32)
+    got = _forward(ctx, 8, x16, sel, w)
+    want = oracle.moe_forward(ex, x16.astype(np.float32), sel, w, mode=1)
+    mx, rms, nbad = _report(f"slots per pass {ns}", got, want)
+    assert nbad == 0
+
+
+@pytest.mark.gpu
+def test_forward_max_picks_bitexact(gpu, oracle):
+    """The largest decode call: 128 tokens x top-8 = 1024 picks over 32 experts (every expert in several jobs)."""
+    H, I, E = 512, 256, 32
+    L = _layer(gpu, 9, E, H, I)
+    ex = _host_experts(oracle, L)
+    rng = np.random.default_rng(128)
+    M = 128
+    x16 = (rng.standard_normal((M, H)) * 0.5).astype(np.float16)
+    sel = np.stack([rng.permutation(E)[:8] for _ in range(M)]).astype(np.int64)
+    w = rng.random(sel.shape).astype(np.float32)
+    got = _forward(gpu, 9, x16, sel, w)
+    want = oracle.moe_forward(ex, x16.astype(np.float32), sel, w, mode=1)
+    mx, rms, nbad = _report("max picks", got, want)
+    assert nbad == 0
