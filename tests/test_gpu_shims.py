@@ -144,3 +144,21 @@ def test_installed_split_handle_on_device(tier, oracle):
     # full residency: every pick is a hit, the selection passes through, nothing is published
     assert torch.equal(so.view(bsz, 4), sel) and torch.equal(wo.view(bsz, 4), w)
     assert int(dflag.item()) == 0 and stats.tolist()[:4] == [len(torch.unique(sel)), 0, 0, 1]
+
+
+def test_serve_stats_after_forward(tier):
+    """/stats and /ec_verify over the live tier and pool (serve_stats, glm53/serve.py:571-629)."""
+    from fastapi import FastAPI
+    from fastapi.testclient import TestClient
+    import ft_tier
+    import serve_stats
+    x = torch.zeros((1, tier["H"]), dtype=torch.float32)
+    sel = torch.tensor([[0, 1, 2, 3]], dtype=torch.int32)
+    ft_tier.tier_forward(0, x, sel, torch.full((1, 4), 0.25), 1)
+    c = TestClient(serve_stats.mount(FastAPI(), contexts=[ft_tier.T.ctx], pools=[tier["pool"]]))
+    r = c.get("/stats").json()
+    assert r["tier"]["jobs"] >= 1 and r["tier"]["layers"] == 2
+    assert r["contexts"][0]["forward_calls"] >= 1 and r["contexts"][0]["layers"] >= 2
+    assert r["expert_cache"] and r["expert_cache"][0]["residency"] == "full"
+    v = c.get("/ec_verify").json()["verify"]
+    assert all(p["bad_slots"] == 0 and p["bad_tables"] == 0 for p in v)
