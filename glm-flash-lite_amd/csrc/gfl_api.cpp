@@ -291,8 +291,9 @@ int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, c
     // pass beat four or eight, whose larger LDS footprint costs more occupancy than the extra passes cost bandwidth.
     int ns = M == 1 ? 1 : 2;
     if (c->ns_override > 0) ns = std::min(c->ns_override, M);
-    if (gfl::gate_up_lds_bytes(L.K[0], ns, L.H, P, L.E) > 163840 || gfl::gate_up_lds_bytes(L.K[1], ns, L.H, P, L.E) > 163840
-        || gfl::down_lds_bytes(L.K[2], ns, L.I) > 163840)
+    if (gfl::gate_up_lds_bytes(L.K[0], ns, L.H, P, L.E) > gfl::LDS_LIMIT ||
+        gfl::gate_up_lds_bytes(L.K[1], ns, L.H, P, L.E) > gfl::LDS_LIMIT
+        || gfl::down_lds_bytes(L.K[2], ns, L.I) > gfl::LDS_LIMIT)
         return fail(GFL_EINVAL, "gfl_moe_forward: shape needs more than 160 KB of LDS per workgroup");
     const int wh = w_is_half ? 1 : 0;
     int r = staged(c, 1, st, [&] {

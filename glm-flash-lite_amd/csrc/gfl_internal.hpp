@@ -9,6 +9,7 @@ constexpr int MAX_PICKS = 1024;    // tokens * topk per forward call
 constexpr int MAX_EXPERTS = 1024;  // experts per layer (ft_split's own limit, ft_tier_cu.cu:260)
 constexpr int MAX_TOPK = 16;
 constexpr int MAX_GROUPED_PICKS = 65536;  // tokens * topk per prefill (grouped) call
+constexpr int LDS_LIMIT = 163840;         // bytes of LDS one workgroup may use on gfx950
 
 // Device-side routing plan of one forward call (all arrays in device memory, capacity cap_slots picks).
 struct PlanView

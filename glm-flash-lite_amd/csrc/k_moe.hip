@@ -774,15 +774,15 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
 // launchers
 // ---------------------------------------------------------------------------------------------------------------
 
+// Every kernel with dynamic LDS is opened once per process (thread-safe static initialisation) to the 160 KB of a
+// workgroup minus its own static LDS; the launch itself asks for what it needs. Returns false when the runtime refuses.
 template <typename F>
-static void open_lds(F kern, size_t lds, int& lds_set)
+static bool open_lds(F kern)
 {
-    if ((int)lds > lds_set)
-    {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)lds);
-        lds_set = (int)lds;
-    }
+    hipFuncAttributes at;
+    if (hipFuncGetAttributes(&at, reinterpret_cast<const void*>(kern)) != hipSuccess) return false;
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               LDS_LIMIT - (int)at.sharedSizeBytes) == hipSuccess;
 }
 
 template <int K>
@@ -800,20 +800,20 @@ static size_t dn_lds(int ns, int I)
 template <int K, int NS>
 static void gu_launch(const GuArgs& a, int umax, int nmat, hipStream_t st)
 {
-    static int lds_set = 0;
     const size_t lds = gu_lds<K>(a.ns_cap, a.H, a.P, a.E);
     auto kern = gu_kernel<K, NS>;
-    open_lds(kern, lds, lds_set);
+    static const bool opened = open_lds(kern);
+    (void)opened;
     hipLaunchKernelGGL(kern, dim3(umax * (a.I / (16 * GU_NW)) + 1, nmat), dim3(GU_NW * 64), lds, st, a);
 }
 
 template <int K, int NS>
 static void dn_launch(const DnArgs& a, int umax, hipStream_t st)
 {
-    static int lds_set = 0;
     const size_t lds = dn_lds<K>(a.ns_cap, a.I);
     auto kern = down_kernel<K, NS>;
-    open_lds(kern, lds, lds_set);
+    static const bool opened = open_lds(kern);
+    (void)opened;
     hipLaunchKernelGGL(kern, dim3(umax * (a.H / (16 * DN_NW))), dim3(DN_NW * 64), lds, st, a);
 }
 

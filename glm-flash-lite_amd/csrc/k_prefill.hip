@@ -533,15 +533,11 @@ static size_t gp_gemm_lds()
 template <int K>
 static int gp_gemm_launch(const GemmArgs& a, int nmat, hipStream_t st)
 {
-    static int lds_set = 0;
     const size_t lds = gp_gemm_lds<K>();
-    if ((int)lds > lds_set)
-    {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(gp_gemm_kernel<K>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-            return -1;
-        lds_set = (int)lds;
-    }
+    // opened to what the kernel needs once per process (thread-safe static initialisation)
+    static const bool opened = hipFuncSetAttribute(reinterpret_cast<const void*>(gp_gemm_kernel<K>),
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess;
+    if (!opened) return -1;
     GemmArgs b = a;
     b.nmat = nmat;
     const unsigned grid = (unsigned)(((a.E + 7) / 8) * 8 * (a.ndim / GP_WCOLS) * nmat);
