@@ -144,3 +144,20 @@ def test_grouped_single_expert_vs_fp64(gpu, oracle):
     _stats("grouped vs EXACT", got, exact)
     assert rel_g <= 2 * rel_e + 1e-5
     assert mx_g <= 2 * mx_e + 1e-5
+
+
+@pytest.mark.gpu
+def test_grouped_duplicate_picks(gpu, oracle):
+    """Tokens that pick one expert twice, through the grouped path (fp16 weights)."""
+    H, I, E = 512, 256, 4
+    L = _layer(gpu, 26, E, H, I)
+    ex = _host_experts(L)
+    rng = np.random.default_rng(26)
+    M = 40
+    x16 = rng.standard_normal((M, H)).astype(np.float16)
+    sel = rng.integers(0, E, size=(M, 3)).astype(np.int64)       # duplicates within a token are common
+    w = rng.random(sel.shape).astype(np.float16)
+    got = _run(gpu, 26, x16, sel, w)
+    want = oracle.moe_forward(ex, x16.astype(np.float32), sel, w.astype(np.float32), mode=1)
+    rel, mx = _stats("grouped duplicates", got, want)
+    assert rel <= REL_RMS and mx <= MAX_ABS

@@ -250,3 +250,20 @@ def test_forward_max_picks_bitexact(gpu, oracle):
     want = oracle.moe_forward(ex, x16.astype(np.float32), sel, w, mode=1)
     mx, rms, nbad = _report("max picks", got, want)
     assert nbad == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("w_half", [False, True])
+def test_forward_duplicate_picks_bitexact(gpu, oracle, w_half):
+    """A token may pick one expert twice (two slots, two weighted terms in job order); fp16 and fp32 weights."""
+    H, I, E = 512, 256, 4
+    L = _layer(gpu, 10, E, H, I)
+    ex = _host_experts(oracle, L)
+    rng = np.random.default_rng(11 + int(w_half))
+    x16 = rng.standard_normal((3, H)).astype(np.float16)
+    sel = np.array([[1, 1, 2], [3, 0, 3], [2, 2, 2]], np.int64)
+    w = rng.random(sel.shape).astype(np.float16 if w_half else np.float32)
+    got = _forward(gpu, 10, x16, sel, w, w_half=w_half)
+    want = oracle.moe_forward(ex, x16.astype(np.float32), sel, w.astype(np.float32), mode=1)
+    mx, rms, nbad = _report(f"duplicate picks w_half={w_half}", got, want)
+    assert nbad == 0
