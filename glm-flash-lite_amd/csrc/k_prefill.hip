@@ -293,16 +293,20 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_act_kernel(const uint64_t* __re
 }
 
 // out_block (ft_core.h:1016) of every expert output block and the weighted sum in job order (ft_core.h:1020-1033),
-// one wave per token; lane k < npk holds the token's k-th pick (slot, weight, output scales), read back per pick with
-// readlane. Rows of tokens without a valid pick become 0.
+// one wave per (token, group of 4 blocks): each 16-lane row takes one block; lane k < npk holds the token's k-th pick
+// (slot, weight, output scales), read back per pick with readlane; four picks' loads are issued before their four
+// terms are added in order. Rows of tokens without a valid pick become 0.
+constexpr int GP_CK = 4;   // picks whose loads a combine wave keeps in flight
+
 __global__ __launch_bounds__(GP_TW * 64) void gp_comb_kernel(const uint64_t* __restrict__ ptrs, int H, int M, int topk,
                                                              GPlan g, const float* __restrict__ yraw,
                                                              float* __restrict__ out)
 {
     const int lane = threadIdx.x & 63, rl = lane >> 4, li = lane & 15;
-    const int tok = blockIdx.x * GP_TW + (threadIdx.x >> 6);
+    const int nbh = H / 128, ngr = (nbh + 3) / 4;
+    const int item = blockIdx.x * GP_TW + (threadIdx.x >> 6);
+    const int tok = item / ngr, b = (item % ngr) * 4 + rl;
     if (tok >= M) return;
-    const int nbh = H / 128;
     const int npk = g.tok_npk[tok];
     int my_s = 0;
     float my_w = 0.f;
@@ -313,32 +317,43 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_comb_kernel(const uint64_t* __r
         my_w = g.tok_w[tok * topk + lane];
         my_p = ptrs[(size_t)g.slot_e[my_s] * 9 + 8];
     }
-    float* orow = out + (size_t)tok * H;
-    for (int b0 = 0; b0 < nbh; b0 += 4)
-    {
-        const int b = b0 + rl, o = min(b, nbh - 1) * 128 + li * 8;
-        float acc[8];
+    const int o = min(b, nbh - 1) * 128 + li * 8;
+    float acc[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) acc[k] = 0.f;
-        for (int k = 0; k < npk; ++k)
+    for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+    for (int k0 = 0; k0 < npk; k0 += GP_CK)
+    {
+        float4 ya[GP_CK], yb[GP_CK];
+        uint4 sv[GP_CK];
+        float wk[GP_CK];
+#pragma unroll
+        for (int i = 0; i < GP_CK; ++i)
         {
+            const int k = min(k0 + i, npk - 1);
             const int s = __builtin_amdgcn_readlane(my_s, k);
-            const float wk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), k));
+            wk[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), k));
             const uint64_t pa = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(my_p >> 32), k) << 32) |
                                 (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)my_p, k);
             const float* yr = yraw + (size_t)s * H + o;
-            const float4 ya = *reinterpret_cast<const float4*>(yr), yb = *reinterpret_cast<const float4*>(yr + 4);
-            const uint4 sv = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(pa) + o);
-            float v[8] = { ya.x, ya.y, ya.z, ya.w, yb.x, yb.y, yb.z, yb.w };
-            out_block_row(v, sv);
+            ya[i] = *reinterpret_cast<const float4*>(yr);
+            yb[i] = *reinterpret_cast<const float4*>(yr + 4);
+            sv[i] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(pa) + o);
+        }
 #pragma unroll
-            for (int j = 0; j < 8; ++j) acc[j] = acc[j] + wk * v[j];
-        }
-        if (b < nbh)
+        for (int i = 0; i < GP_CK; ++i)
         {
-            *reinterpret_cast<float4*>(orow + b * 128 + li * 8) = float4{ acc[0], acc[1], acc[2], acc[3] };
-            *reinterpret_cast<float4*>(orow + b * 128 + li * 8 + 4) = float4{ acc[4], acc[5], acc[6], acc[7] };
+            if (k0 + i >= npk) break;
+            float v[8] = { ya[i].x, ya[i].y, ya[i].z, ya[i].w, yb[i].x, yb[i].y, yb[i].z, yb[i].w };
+            out_block_row(v, sv[i]);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] = acc[j] + wk[i] * v[j];
         }
+    }
+    if (b < nbh)
+    {
+        float* orow = out + (size_t)tok * H + b * 128 + li * 8;
+        *reinterpret_cast<float4*>(orow) = float4{ acc[0], acc[1], acc[2], acc[3] };
+        *reinterpret_cast<float4*>(orow + 4) = float4{ acc[4], acc[5], acc[6], acc[7] };
     }
 }
 
@@ -587,8 +602,11 @@ int launch_grouped(const uint64_t* ptrs, const int64_t* sel, const void* w, int 
     GemmArgs c = a;
     c.mat_base = 2; c.kdim = I; c.ndim = H; c.xin = xd; c.yout = yraw;
     if (gp_gemm(Kd, c, 1, st)) return -1;
-    hipLaunchKernelGGL(gp_comb_kernel, dim3((unsigned)((M + GP_TW - 1) / GP_TW)), dim3(GP_TW * 64), 0, st, ptrs, H, M,
-                       topk, g, yraw, out);
+    {
+        const long items = (long)M * ((H / 128 + 3) / 4);
+        hipLaunchKernelGGL(gp_comb_kernel, dim3((unsigned)((items + GP_TW - 1) / GP_TW)), dim3(GP_TW * 64), 0, st, ptrs,
+                           H, M, topk, g, yraw, out);
+    }
     return 0;
 }
 
