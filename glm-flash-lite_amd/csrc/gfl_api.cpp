@@ -337,7 +337,8 @@ int gfl_grouped_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* se
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const int P = M * topk, E = L.E, H = L.H, I = L.I;
     // layout: plan ints, then xt [2][P][H] fp16, ygu [2][P][I] fp32, xd [P][I] fp16, yraw [P][H] fp32
-    const size_t n_int = 4 + (size_t)E + (E + 1) + 7 * (size_t)P + (size_t)M + (size_t)P;
+    const size_t nch = (P + gfl::GP_PLAN_CHUNK - 1) / gfl::GP_PLAN_CHUNK;
+    const size_t n_int = 4 + (size_t)E + (E + 1) + 7 * (size_t)P + (size_t)M + (size_t)P + (size_t)E + nch * (E + 1);
     const size_t b_int = align256(sizeof(int) * n_int);
     const size_t b_xt = align256(2 * 2 * (size_t)P * H), b_ygu = align256(4 * 2 * (size_t)P * I);
     const size_t b_xd = align256(2 * (size_t)P * I), b_yr = align256(4 * (size_t)P * H);
@@ -373,6 +374,8 @@ int gfl_grouped_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* se
     gp.tok_slot = gp.slot_job + P;
     gp.tok_w = reinterpret_cast<float*>(gp.tok_slot + P);
     gp.tok_npk = reinterpret_cast<int*>(gp.tok_w + P);
+    gp.eord = gp.tok_npk + M;
+    gp.ccnt = gp.eord + E;
     uint16_t* xt = reinterpret_cast<uint16_t*>(b + b_int);
     float* ygu = reinterpret_cast<float*>(b + b_int + b_xt);
     uint16_t* xd = reinterpret_cast<uint16_t*>(b + b_int + b_xt + b_ygu);

@@ -47,6 +47,29 @@ __host__ __device__ inline LaneDec lane_dec(int lane, int K)
 
 __device__ inline uint32_t ld_u32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
 
+// Pointers into global memory in the global address space. Addresses read from the layer table are otherwise generic
+// to the compiler, and a generic (flat) load counts on both the vector-memory and the LDS counters, so the compiler
+// can only wait for it with vmcnt(0), which also waits for every load issued before it (prefetches and LDS-direct
+// loads included). The table holds device-memory addresses only.
+template <typename T>
+using gptr = const __attribute__((address_space(1))) T*;
+
+template <typename T>
+__device__ __forceinline__ gptr<T> gaddr(uint64_t a)
+{
+    return (gptr<T>)a;
+}
+
+// the 16 bytes at element i of a global pointer (loaded as a native vector: HIP's uint4 has no copy from another
+// address space)
+template <typename T>
+__device__ __forceinline__ uint4 gld16(gptr<T> p, long i)
+{
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = *reinterpret_cast<gptr<u32x4>>(p + i);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // A pointer that is the same in every lane of the wave, moved to scalar registers. __builtin_amdgcn_readfirstlane
 // takes and returns a 32-bit int, so the two halves of the 64-bit address go through it separately.
 __device__ inline const uint8_t* uniform_ptr(const uint8_t* p)
@@ -105,8 +128,8 @@ __device__ inline float r16(float x)
     return r;
 }
 
-// Value of lane L ^ W (W = 1..32) without the LDS crossbar: DPP quad permutes and row mirrors inside 16-lane rows
-// (xor 4 = half-row mirror then xor 3, xor 8 = row mirror then half-row mirror), gfx950's permlane swaps across rows.
+// Value of lane L ^ W (W = 1..32) without the LDS crossbar: DPP quad permutes, mirrors and rotates inside 16-lane
+// rows (xor 4 = half-row mirror then xor 3, xor 8 = rotate the row by 8), gfx950's permlane swaps across rows.
 template <int W>
 __device__ __forceinline__ float lane_xor(float v)
 {
@@ -118,11 +141,7 @@ __device__ __forceinline__ float lane_xor(float v)
         const int t = __builtin_amdgcn_update_dpp(0, iv, 0x141, 0xF, 0xF, true);   // row_half_mirror: L ^ 7
         return __int_as_float(__builtin_amdgcn_update_dpp(0, t, 0x1B, 0xF, 0xF, true));   // quad_perm 3210: ^ 3
     }
-    if constexpr (W == 8)
-    {
-        const int t = __builtin_amdgcn_update_dpp(0, iv, 0x140, 0xF, 0xF, true);   // row_mirror: L ^ 15
-        return __int_as_float(__builtin_amdgcn_update_dpp(0, t, 0x141, 0xF, 0xF, true));  // row_half_mirror: ^ 7
-    }
+    if constexpr (W == 8) return __int_as_float(__builtin_amdgcn_update_dpp(0, iv, 0x128, 0xF, 0xF, true));   // row_ror:8
     if constexpr (W == 16)
     {
         // odd rows of the first operand <-> even rows of the second: {rows 0,0,2,2 ; rows 1,1,3,3}
@@ -166,18 +185,61 @@ __device__ inline float h2f_bits(uint16_t h) { __half x; __builtin_memcpy(&x, &h
 // Hadamard-128 on one 16-lane row of the wave, 8 elements per lane: lane i of the row holds elements 8i..8i+7.
 // Stages h = 1, 2, 4 pair elements inside the lane, h = 8..64 pair lane i with i ^ (h / 8); every element sees the
 // same add/sub sequence as had128 (ft_core.h:89-94): the lower element of a pair becomes a + b, the upper a - b.
+// Across lanes the upper lane keeps its own value minus its partner's, the negated a - b, so that every lane does the
+// same one instruction per element (an fma with its partner's value by DPP and a per-lane +-1); the negations add up
+// to a per-lane sign (-1)^popcount(i), which fwht128_row returns. Negation commutes with rounding, so sign * v is
+// exactly had128's result, and callers fold the sign into their next product.
+//
+// v[k] += sg * (v[k] of the partner lane) for the 8 elements, as v_fmac_f32 with a DPP source (the compiler keeps a
+// separate DPP move there). The leading s_nop covers the VALU-write -> DPP-read hazard on the values written just
+// before; inside a block each element's DPP read comes 8 instructions after that element's previous write.
+#define GFL_FMAC8(CTRL, S0, S1, S2, S3, S4, S5, S6, S7)                                                          \
+    "s_nop 1\n\t"                                                                                                      \
+    "v_fmac_f32_dpp %0, " S0 ", %8 " CTRL "\n\tv_fmac_f32_dpp %1, " S1 ", %8 " CTRL "\n\t"                           \
+    "v_fmac_f32_dpp %2, " S2 ", %8 " CTRL "\n\tv_fmac_f32_dpp %3, " S3 ", %8 " CTRL "\n\t"                           \
+    "v_fmac_f32_dpp %4, " S4 ", %8 " CTRL "\n\tv_fmac_f32_dpp %5, " S5 ", %8 " CTRL "\n\t"                           \
+    "v_fmac_f32_dpp %6, " S6 ", %8 " CTRL "\n\tv_fmac_f32_dpp %7, " S7 ", %8 " CTRL
+#define GFL_DPP_ALL " row_mask:0xf bank_mask:0xf bound_ctrl:1"
+
 template <int W>
 __device__ __forceinline__ void fwht_row_stage(float (&v)[8], int L)
 {
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
+    const float sg = (L & W) ? -1.0f : 1.0f;
+    if constexpr (W == 1)
+        asm(GFL_FMAC8("quad_perm:[1,0,3,2]" GFL_DPP_ALL, "%0", "%1", "%2", "%3", "%4", "%5", "%6", "%7")
+            : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7])
+            : "v"(sg));
+    else if constexpr (W == 2)
+        asm(GFL_FMAC8("quad_perm:[2,3,0,1]" GFL_DPP_ALL, "%0", "%1", "%2", "%3", "%4", "%5", "%6", "%7")
+            : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7])
+            : "v"(sg));
+    else if constexpr (W == 8)
+        asm(GFL_FMAC8("row_ror:8" GFL_DPP_ALL, "%0", "%1", "%2", "%3", "%4", "%5", "%6", "%7")
+            : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7])
+            : "v"(sg));
+    else
     {
-        const float p = lane_xor<W>(v[k]);
-        v[k] = (L & W) ? p - v[k] : v[k] + p;
+        static_assert(W == 4, "row stages are 1, 2, 4, 8");
+        // lane L ^ 4 = half-row mirror (L ^ 7) of quad_perm 3210 (L ^ 3): the mirrored copies first, 8 moves apart
+        // from their DPP reads
+        float t[8];
+        asm("s_nop 1\n\t"
+            "v_mov_b32_dpp %0, %8 row_half_mirror" GFL_DPP_ALL "\n\tv_mov_b32_dpp %1, %9 row_half_mirror" GFL_DPP_ALL "\n\t"
+            "v_mov_b32_dpp %2, %10 row_half_mirror" GFL_DPP_ALL "\n\tv_mov_b32_dpp %3, %11 row_half_mirror" GFL_DPP_ALL "\n\t"
+            "v_mov_b32_dpp %4, %12 row_half_mirror" GFL_DPP_ALL "\n\tv_mov_b32_dpp %5, %13 row_half_mirror" GFL_DPP_ALL "\n\t"
+            "v_mov_b32_dpp %6, %14 row_half_mirror" GFL_DPP_ALL "\n\tv_mov_b32_dpp %7, %15 row_half_mirror" GFL_DPP_ALL
+            : "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3]), "=&v"(t[4]), "=&v"(t[5]), "=&v"(t[6]), "=&v"(t[7])
+            : "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]), "v"(v[7]));
+        asm(GFL_FMAC8("quad_perm:[3,2,1,0]" GFL_DPP_ALL, "%9", "%10", "%11", "%12", "%13", "%14", "%15", "%16")
+            : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7])
+            : "v"(sg), "v"(t[0]), "v"(t[1]), "v"(t[2]), "v"(t[3]), "v"(t[4]), "v"(t[5]), "v"(t[6]), "v"(t[7]));
     }
 }
+#undef GFL_FMAC8
+#undef GFL_DPP_ALL
 
-__device__ inline void fwht128_row(float (&v)[8])
+// Returns the lane's sign: the transform is sign * v.
+__device__ inline float fwht128_row(float (&v)[8])
 {
 #pragma unroll
     for (int h = 1; h < 8; h <<= 1)
@@ -194,6 +256,7 @@ __device__ inline void fwht128_row(float (&v)[8])
     fwht_row_stage<2>(v, L);
     fwht_row_stage<4>(v, L);
     fwht_row_stage<8>(v, L);
+    return (__builtin_popcount(L) & 1) ? -1.0f : 1.0f;
 }
 
 __device__ __forceinline__ float h2f_lane(uint4 v, int k)
@@ -207,9 +270,9 @@ __device__ inline void out_block_row(float (&v)[8], uint4 sc)
 {
 #pragma unroll
     for (int k = 0; k < 8; ++k) v[k] = r16(v[k]);
-    fwht128_row(v);
+    const float sh = fwht128_row(v) * HADF;   // (sign * v) * HADF == v * (sign * HADF), bit for bit
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = r16(v[k] * HADF * h2f_lane(sc, k));
+    for (int k = 0; k < 8; ++k) v[k] = r16(v[k] * sh * h2f_lane(sc, k));
 }
 
 // prep_block (ft_core.h:97-102) on a 16-lane row: x and suh are the lane's 8 fp16 inputs and scales (16 bytes each)
@@ -217,9 +280,9 @@ __device__ inline void prep_block_row_f(float (&v)[8], uint4 sc)
 {
 #pragma unroll
     for (int k = 0; k < 8; ++k) v[k] = v[k] * h2f_lane(sc, k);
-    fwht128_row(v);
+    const float sh = fwht128_row(v) * HADF;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = r16(v[k] * HADF);
+    for (int k = 0; k < 8; ++k) v[k] = r16(v[k] * sh);
 }
 
 __device__ inline void prep_block_row(float (&v)[8], uint4 x, uint4 sc)
@@ -228,9 +291,9 @@ __device__ inline void prep_block_row(float (&v)[8], uint4 x, uint4 sc)
 #pragma unroll
     for (int k = 0; k < 8; ++k)
         v[k] = h2f_bits((uint16_t)(xw[k >> 1] >> (16 * (k & 1)))) * h2f_bits((uint16_t)(sw[k >> 1] >> (16 * (k & 1))));
-    fwht128_row(v);
+    const float sh = fwht128_row(v) * HADF;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = r16(v[k] * HADF);
+    for (int k = 0; k < 8; ++k) v[k] = r16(v[k] * sh);
 }
 
 // prep_block (ft_core.h:97-102) on lane-held elements L, L+64
@@ -253,11 +316,9 @@ __device__ inline void out_block_wave(float& v0, float& v1, float s0, float s1)
     v1 = r16(v1 * HADF * s1);
 }
 
-// silu(g) * u with exllamav3's clamp (act_mul, ft_core.h:123-132); e = expf(-g) comes from the context's table,
-// indexed by the fp16 bits of g (g is fp16-valued)
-__device__ inline float act_mul(float g, float u, float limit, const float* __restrict__ exp_tab)
+// silu(g) * u with exllamav3's clamp (act_mul, ft_core.h:123-132), given e = expf(-g)
+__device__ inline float act_mul_e(float g, float u, float e, float limit)
 {
-    const float e = exp_tab[f2h_bits(g) & 0xFFFFu];
     float x = g / (1.0f + e);
     if (limit != 0.0f)
     {
@@ -265,6 +326,12 @@ __device__ inline float act_mul(float g, float u, float limit, const float* __re
         x = fminf(x, limit);
     }
     return x * u;
+}
+
+// the same with e = expf(-g) from the context's table, indexed by the fp16 bits of g (g is fp16-valued)
+__device__ inline float act_mul(float g, float u, float limit, const float* __restrict__ exp_tab)
+{
+    return act_mul_e(g, u, exp_tab[f2h_bits(g) & 0xFFFFu], limit);
 }
 
 }  // namespace gfl

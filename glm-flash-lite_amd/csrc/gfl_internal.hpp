@@ -55,7 +55,11 @@ struct GPlan
     int* tok_slot;   // [M][topk] slots of each token in combine order
     float* tok_w;    // [M][topk] their routing weights (fp32)
     int* tok_npk;    // [M] valid picks of each token
+    int* eord;       // [E] experts in GEMM dispatch order: most passes first, then ascending id
+    int* ccnt;       // [chunks][E + 1] picks of each expert per chunk of GP_PLAN_CHUNK picks, other ids at [E]
 };
+
+constexpr int GP_PLAN_CHUNK = 1024;   // picks per workgroup of the grouped plan
 
 // Prefill-sized layer forward with MFMA grouped GEMMs (k_prefill.hip): xt [2][cap][H] fp16, ygu [2][cap][I] fp32,
 // xd [cap][I] fp16, yraw [cap][H] fp32 workspace, cap >= P.

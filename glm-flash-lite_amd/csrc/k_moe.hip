@@ -466,9 +466,9 @@ __device__ __forceinline__ void st_agent(float* p, float v)
 __device__ void act_block(const GuArgs& a, int e, int s_begin, int s_end, int b)
 {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
-    const uint16_t* svh_g = reinterpret_cast<const uint16_t*>(a.ptrs[(size_t)e * 9 + 4]);
-    const uint16_t* svh_u = reinterpret_cast<const uint16_t*>(a.ptrs[(size_t)e * 9 + 6]);
-    const uint16_t* suh_d = reinterpret_cast<const uint16_t*>(a.ptrs[(size_t)e * 9 + 7]);
+    const gptr<uint16_t> svh_g = gaddr<uint16_t>(a.ptrs[(size_t)e * 9 + 4]);
+    const gptr<uint16_t> svh_u = gaddr<uint16_t>(a.ptrs[(size_t)e * 9 + 6]);
+    const gptr<uint16_t> suh_d = gaddr<uint16_t>(a.ptrs[(size_t)e * 9 + 7]);
     const int cap = a.pv.cap_slots;
     for (int s = s_begin + wave; s < s_end; s += nw)
     {
@@ -517,7 +517,7 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(K ==
     const int wid = __builtin_amdgcn_readfirstlane(wave);
     const int e = L.uexp[u];
     const uint8_t* tr = reinterpret_cast<const uint8_t*>(a.ptrs[(size_t)e * 9 + mat]);
-    const uint16_t* suh = reinterpret_cast<const uint16_t*>(a.ptrs[(size_t)e * 9 + 3 + 2 * mat]);
+    const gptr<uint16_t> suh = gaddr<uint16_t>(a.ptrs[(size_t)e * 9 + 3 + 2 * mat]);
     const int s_begin = L.uoff[u], s_end = L.uoff[u + 1];
     const size_t gstride = (size_t)TN * TB;
     const int t = cb * NW + wave;                         // this wave's tile column
@@ -539,7 +539,7 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(K ==
             const int it = min((r * NW + wave) * 4 + rl, nit - 1);
             const int s = it / nblk, b = it % nblk;
             xv[k] = *reinterpret_cast<const uint4*>(a.x + (size_t)(L.spick[c0 + s] / a.topk) * a.H + b * 128 + li * 8);
-            sv[k] = *reinterpret_cast<const uint4*>(suh + b * 128 + li * 8);
+            sv[k] = gld16(suh, b * 128 + li * 8);
         };
         auto prep_round = [&](int r, int k) {
             const int it = (r * NW + wave) * 4 + rl;
@@ -638,7 +638,7 @@ __global__ __launch_bounds__(DN_NW * 64) __attribute__((amdgpu_waves_per_eu(K ==
     const int U = a.pv.hdr[0];
     const int s_begin = a.pv.uoff[u], s_end = a.pv.uoff[u + 1];
     const uint8_t* tr = reinterpret_cast<const uint8_t*>(a.pv.uptr[2 * u]);
-    const uint16_t* svh = reinterpret_cast<const uint16_t*>(a.pv.uptr[2 * u + 1]);
+    const gptr<uint16_t> svh = gaddr<uint16_t>(a.pv.uptr[2 * u + 1]);
     if (u >= U) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15;
     const int wid = __builtin_amdgcn_readfirstlane(wave);

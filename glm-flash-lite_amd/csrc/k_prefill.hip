@@ -32,176 +32,227 @@ __device__ inline int gp_perm_pos(int b, int r)
     return b * 128 + q * 32 + tr * 4 + jj;
 }
 
-constexpr int GP_PLAN_THREADS = 1024;
+constexpr int GP_MT = 64;          // slots per GEMM pass (4 MFMA row blocks)
+constexpr int GP_PLAN_THREADS = GP_PLAN_CHUNK;   // one thread per pick of a chunk
 constexpr int GP_PLAN_WAVES = GP_PLAN_THREADS / 64;
+constexpr int GP_ORDER_THREADS = 256;
 
-// One workgroup of 1024 threads. Slots are expert-major, experts ascending, picks (hence tokens) ascending within an
-// expert; picks with ids outside [0, E) are skipped (ids other than -1 are counted in hdr[1]). The combine order of a
-// token's picks is the reference's job order: moe_forward (ft_core.h:1343-1349) scans picks token-major and opens a
-// job for an expert at its first pick and after every 8 of its picks, so pick p (the c-th of its expert) lands in the
-// job opened by that expert's pick number c - c % 8, and jobs are numbered in the order their opening picks appear.
-// Picks are placed 1024 per round in pick order, so the job numbers of the opening picks are a running count over the
-// rounds; the other picks read theirs from the opening pick's slot, which sits c % 8 slots before their own.
-__global__ __launch_bounds__(GP_PLAN_THREADS) void gp_plan_kernel(const int64_t* __restrict__ sel, const void* w,
-                                                                  int w_half, int P, int topk, int E, GPlan g)
+// Slots are expert-major, experts ascending, picks (hence tokens) ascending within an expert; picks with ids outside
+// [0, E) are skipped (ids other than -1 are counted in hdr[1]). The combine order of a token's picks is the
+// reference's job order: moe_forward (ft_core.h:1343-1349) scans picks token-major and opens a job for an expert at
+// its first pick and after every 8 of its picks, so pick p (the c-th of its expert) lands in the job opened by that
+// expert's pick number c - c % 8, and jobs are numbered in the order their opening picks appear. The plan takes three
+// launches over chunks of GP_PLAN_CHUNK picks: ranks within each chunk, then placement (every chunk sums the counts
+// of the chunks before it), then each token's picks in job order.
+
+// Bit mask of the lanes below this one.
+__device__ __forceinline__ uint64_t gp_lanes_below(int lane)
 {
-    __shared__ int s_cnt[MAX_EXPERTS];      // per-expert count during the scan, then running rank
-    __shared__ int s_off[MAX_EXPERTS + 1];
-    __shared__ unsigned char s_wcnt[GP_PLAN_WAVES][MAX_EXPERTS];   // per-wave group sizes (<= 64)
-    __shared__ int s_scan[GP_PLAN_THREADS];
-    __shared__ int s_wop[GP_PLAN_WAVES];    // job-opening picks of each wave in the current round
-    __shared__ int s_bad, s_jobs;
+    return lane == 0 ? 0ull : (~0ull >> (64 - lane));
+}
+
+// Pass 1, one workgroup per chunk: each pick's rank among the same-expert picks of its chunk, in pick order (same
+// expert lanes of a wave from ten ballots on the id bits, E <= 1024, plus the group sizes of the waves before), into
+// pick_c; and the chunk's per-expert counts into ccnt[chunk][0, E), with its count of ids outside [-1, E) at [E].
+__global__ __launch_bounds__(GP_PLAN_THREADS) void gp_rank_kernel(const int64_t* __restrict__ sel, int P, int E,
+                                                                  GPlan g)
+{
+    __shared__ int s_cnt[MAX_EXPERTS];
+    __shared__ unsigned char s_wcnt[GP_PLAN_WAVES][MAX_EXPERTS];   // group sizes (<= 64) of each wave
+    __shared__ int s_bad;
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
-    for (int e = t; e < E; e += GP_PLAN_THREADS) s_cnt[e] = 0;
-    if (t == 0) { s_bad = 0; s_jobs = 0; }
-    __syncthreads();
-    // counts (four independent loads in flight per thread)
-    for (int p0 = 0; p0 < P; p0 += 4 * GP_PLAN_THREADS)
+    const int p = blockIdx.x * GP_PLAN_THREADS + t;
+    const int64_t e64 = p < P ? sel[p] : -1;
+    if (t < E) s_cnt[t] = 0;
+    if (t == 0) s_bad = 0;
+    for (int i = t; i < GP_PLAN_WAVES * MAX_EXPERTS / 4; i += GP_PLAN_THREADS)
+        reinterpret_cast<int*>(&s_wcnt[0][0])[i] = 0;
+    const bool ok = e64 >= 0 && e64 < E;
+    const int e = ok ? (int)e64 : 0;
+    uint64_t eq = __ballot(ok);
+#pragma unroll
+    for (int b = 0; b < 10; ++b)
     {
-        int64_t ev[4];
+        const bool bit = ok && ((e >> b) & 1);
+        const uint64_t m = __ballot(bit);
+        eq &= bit ? m : ~m;
+    }
+    const int cin = __popcll(eq & gp_lanes_below(lane));
+    const bool lead = ok && cin == 0;   // lowest lane of its expert's group
+    __syncthreads();
+    if (lead) s_wcnt[wv][e] = (unsigned char)__popcll(eq);
+    else if (!ok && e64 != -1) atomicAdd(&s_bad, 1);
+    __syncthreads();
+    if (ok)
+    {
+        int r = cin;
+        for (int v = 0; v < wv; ++v) r += s_wcnt[v][e];
+        g.pick_c[p] = r;
+    }
+    if (lead) atomicAdd(&s_cnt[e], __popcll(eq));
+    __syncthreads();
+    int* cc = g.ccnt + (size_t)blockIdx.x * (E + 1);
+    if (t < E) cc[t] = s_cnt[t];
+    if (t == 0) cc[E] = s_bad;
+}
+
+// Inclusive scan over the 64 lanes of a wave.
+__device__ __forceinline__ int gp_wave_scan(int v, int lane)
+{
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+    for (int d = 1; d < 64; d <<= 1)
+    {
+        const int o = __shfl_up(v, d);
+        if (lane >= d) v += o;
+    }
+    return v;
+}
+
+// Pass 2, one workgroup per chunk: expert e's picks in earlier chunks (base_e) and in all chunks (its slot count),
+// slot offsets by a scan of the counts, and the jobs opened before the chunk, sum over e of ceil(base_e / 8) (the
+// expert's ranks 0, 8, 16, ... below base_e); a pick's global rank is base_e plus its rank in the chunk, and a pick
+// of rank r opens a job when r % 8 == 0, numbered after the chunk's earlier openers. Workgroup 0 also writes the
+// counts, offsets, header and the GEMM's expert order.
+__global__ __launch_bounds__(GP_PLAN_THREADS) void gp_place_kernel(const int64_t* __restrict__ sel, int P, int E,
+                                                                   GPlan g)
+{
+    __shared__ int s_base[MAX_EXPERTS];
+    __shared__ int s_off[MAX_EXPERTS];
+    __shared__ __align__(16) int s_pass[MAX_EXPERTS];
+    __shared__ int s_wtot[GP_PLAN_WAVES], s_wjob[GP_PLAN_WAVES], s_wop[GP_PLAN_WAVES];
+    __shared__ int s_bad;
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const int c = blockIdx.x, nch = gridDim.x;
+    const int p = c * GP_PLAN_THREADS + t;
+    const int64_t e64 = p < P ? sel[p] : -1;
+    const bool ok = e64 >= 0 && e64 < E;
+    const int e = ok ? (int)e64 : 0;
+    const int rc = ok ? g.pick_c[p] : 0;
+    if (t == 0) s_bad = 0;
+    int base = 0, tot = 0;
+    if (t < E)
+    {
+#pragma unroll 8
+        for (int k = 0; k < nch; ++k)
         {
-            const int p = p0 + j * GP_PLAN_THREADS + t;
-            ev[j] = p < P ? sel[p] : -1;
+            const int v = g.ccnt[(size_t)k * (E + 1) + t];
+            tot += v;
+            base += k < c ? v : 0;
         }
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
+    }
+    const int inc = gp_wave_scan(tot, lane);
+    const int jinc = gp_wave_scan((base + 7) >> 3, lane);
+    if (lane == 63)
+    {
+        s_wtot[wv] = inc;
+        s_wjob[wv] = jinc;
+    }
+    __syncthreads();
+    if (c == 0 && t < nch) atomicAdd(&s_bad, g.ccnt[(size_t)t * (E + 1) + E]);
+    int pre = 0, jbase = 0;
+    for (int v = 0; v < GP_PLAN_WAVES; ++v)
+    {
+        pre += v < wv ? s_wtot[v] : 0;
+        jbase += s_wjob[v];
+    }
+    const int off_e = pre + inc - tot;
+    if (t < E)
+    {
+        s_base[t] = base;
+        s_off[t] = off_e;
+        if (c == 0)
         {
-            if (ev[j] >= 0 && ev[j] < E) atomicAdd(&s_cnt[(int)ev[j]], 1);
-            else if (ev[j] != -1) atomicAdd(&s_bad, 1);
+            g.cnt[t] = tot;
+            g.off[t] = off_e;
+            if (t == E - 1)
+            {
+                g.off[E] = off_e + tot;
+                g.hdr[0] = off_e + tot;
+            }
         }
     }
     __syncthreads();
-    // exclusive scan of the counts (E <= 1024 = blockDim)
+    if (c == 0)
     {
-        const int v = t < E ? s_cnt[t] : 0;
-        s_scan[t] = v;
+        // experts by descending GEMM passes of GP_MT slots, ties by ascending id: the GEMM dispatches the longest
+        // workgroups first, so the short ones fill the end of the launch
+        if (t == 0) g.hdr[1] = s_bad;
+        const int pe = (tot + GP_MT - 1) / GP_MT;
+        s_pass[t] = t < E ? pe : -1;
         __syncthreads();
-        for (int d = 1; d < GP_PLAN_THREADS; d <<= 1)
+        int rk = 0;
+        for (int k = 0; k < E; k += 4)   // 16-byte broadcast reads; entries past E are -1
         {
-            const int o = t >= d ? s_scan[t - d] : 0;
-            __syncthreads();
-            s_scan[t] += o;
-            __syncthreads();
+            const int4 pk = *reinterpret_cast<const int4*>(&s_pass[k]);
+            rk += (pk.x > pe || (pk.x == pe && k < t)) + (pk.y > pe || (pk.y == pe && k + 1 < t)) +
+                  (pk.z > pe || (pk.z == pe && k + 2 < t)) + (pk.w > pe || (pk.w == pe && k + 3 < t));
         }
-        if (t < E)
-        {
-            s_off[t] = s_scan[t] - v;
-            g.off[t] = s_scan[t] - v;
-            g.cnt[t] = v;
-            s_cnt[t] = 0;   // becomes the running rank
-        }
-        if (t == 0)
-        {
-            s_off[E] = s_scan[E - 1];
-            g.off[E] = s_scan[E - 1];
-            g.hdr[0] = s_scan[E - 1];
-            g.hdr[1] = s_bad;
-        }
+        if (t < E) g.eord[rk] = t;
     }
-    for (int i = t; i < GP_PLAN_WAVES * E; i += GP_PLAN_THREADS) (&s_wcnt[0][0])[(i / E) * MAX_EXPERTS + i % E] = 0;
+    const int r = ok ? s_base[e] + rc : 0;
+    const bool opener = ok && (r & 7) == 0;
+    const uint64_t om = __ballot(opener);
+    if (lane == 0) s_wop[wv] = __popcll(om);
     __syncthreads();
-    // stable placement, 1024 picks per round: rank = running count + same-expert picks of earlier waves in the round
-    // + same-expert lanes below in the wave (ten ballots on the id bits, E <= 1024)
-    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-    int64_t e_next = t < P ? sel[t] : -1;
-    for (int p0 = 0; p0 < P; p0 += GP_PLAN_THREADS)
+    int job = jbase + __popcll(om & gp_lanes_below(lane));
+    for (int v = 0; v < wv; ++v) job += s_wop[v];
+    if (p < P)
     {
-        const int p = p0 + t;
-        const int64_t e64 = e_next;
-        e_next = p + GP_PLAN_THREADS < P ? sel[p + GP_PLAN_THREADS] : -1;   // next round's id, loaded under this one
-        const bool ok = e64 >= 0 && e64 < E;
-        const int e = ok ? (int)e64 : 0;
-        uint64_t eq = __ballot(ok);
-#pragma unroll
-        for (int b = 0; b < 10; ++b)
-        {
-            const bool bit = ok && ((e >> b) & 1);
-            const uint64_t m = __ballot(bit);
-            eq &= bit ? m : ~m;
-        }
-        const int cin = __popcll(eq & below);
-        if (ok && cin == 0) s_wcnt[wv][e] = (unsigned char)__popcll(eq);   // lowest lane of the group
-        __syncthreads();
-        int r = -1;
         if (ok)
         {
-            r = s_cnt[e] + cin;
-            for (int v = 0; v < wv; ++v) r += s_wcnt[v][e];
+            const int s = s_off[e] + r;
+            g.slot_pick[s] = p;
+            g.slot_e[s] = e;
+            if (opener) g.slot_job[s] = job;
+            g.pick_slot[p] = s;
+            g.pick_c[p] = r;
         }
-        const bool opener = ok && (r & 7) == 0;
-        const uint64_t om = __ballot(opener);
-        if (lane == 0) s_wop[wv] = __popcll(om);
-        __syncthreads();
-        if (ok && cin == 0) atomicAdd(&s_cnt[e], __popcll(eq));
-        int job = s_jobs + __popcll(om & below);
-        for (int v = 0; v < wv; ++v) job += s_wop[v];
-        __syncthreads();
-        if (ok && cin == 0) s_wcnt[wv][e] = 0;
-        if (t == 0)
-        {
-            int n = 0;
-            for (int v = 0; v < GP_PLAN_WAVES; ++v) n += s_wop[v];
-            s_jobs += n;
-        }
-        if (p < P)
-        {
-            if (ok)
-            {
-                const int s = s_off[e] + r;
-                g.slot_pick[s] = p;
-                g.slot_e[s] = e;
-                if (opener) g.slot_job[s] = job;
-                g.pick_slot[p] = s;
-                g.pick_c[p] = r;
-            }
-            else g.pick_slot[p] = -1;
-        }
-        __syncthreads();
+        else g.pick_slot[p] = -1;
     }
-    __threadfence_block();
-    __syncthreads();
-    // each token's picks in (job, pick) order with their fp32 weights
-    const int M = P / topk;
-    for (int tk = t; tk < M; tk += GP_PLAN_THREADS)
+}
+
+// Pass 3, one thread per token: its picks in (job, pick) order with their fp32 weights. A pick of global rank c
+// reads its job number from the slot of its job's opening pick, c % 8 slots before its own.
+__global__ __launch_bounds__(GP_ORDER_THREADS) void gp_order_kernel(const void* w, int w_half, int M, int topk, GPlan g)
+{
+    const int tk = blockIdx.x * GP_ORDER_THREADS + threadIdx.x;
+    if (tk >= M) return;
+    // loops unrolled to MAX_TOPK with k < topk guards, so the per-pick arrays stay in registers
+    int ps[MAX_TOPK], jb[MAX_TOPK];
+    int n = 0;
+#pragma unroll
+    for (int k = 0; k < MAX_TOPK; ++k)
     {
-        // loops unrolled to MAX_TOPK with k < topk guards, so the per-pick arrays stay in registers
-        int ps[MAX_TOPK], jb[MAX_TOPK];
-        int n = 0;
+        const int p = tk * topk + k;
+        const int s = k < topk ? g.pick_slot[p] : -1;
+        ps[k] = s;
+        jb[k] = s >= 0 ? g.slot_job[s - (g.pick_c[p] & 7)] : 0;
+        n += s >= 0;
+    }
+    g.tok_npk[tk] = n;
 #pragma unroll
-        for (int k = 0; k < MAX_TOPK; ++k)
-        {
-            const int p = tk * topk + k;
-            const int s = k < topk ? g.pick_slot[p] : -1;
-            ps[k] = s;
-            jb[k] = s >= 0 ? g.slot_job[s - (g.pick_c[p] & 7)] : 0;
-            n += s >= 0;
-        }
-        g.tok_npk[tk] = n;
+    for (int k = 0; k < MAX_TOPK; ++k)
+    {
+        if (ps[k] < 0) continue;
+        int r = 0;
 #pragma unroll
-        for (int k = 0; k < MAX_TOPK; ++k)
-        {
-            if (ps[k] < 0) continue;
-            int r = 0;
-#pragma unroll
-            for (int k2 = 0; k2 < MAX_TOPK; ++k2)
-                r += ps[k2] >= 0 && (jb[k2] < jb[k] || (jb[k2] == jb[k] && k2 < k));
-            const int p = tk * topk + k;
-            g.tok_slot[tk * topk + r] = ps[k];
-            g.tok_w[tk * topk + r] = w_half ? h2f_bits(reinterpret_cast<const uint16_t*>(w)[p])
-                                            : reinterpret_cast<const float*>(w)[p];
-        }
+        for (int k2 = 0; k2 < MAX_TOPK; ++k2)
+            r += ps[k2] >= 0 && (jb[k2] < jb[k] || (jb[k2] == jb[k] && k2 < k));
+        const int p = tk * topk + k;
+        g.tok_slot[tk * topk + r] = ps[k];
+        g.tok_w[tk * topk + r] = w_half ? h2f_bits(reinterpret_cast<const uint16_t*>(w)[p])
+                                        : reinterpret_cast<const float*>(w)[p];
     }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// transforms: one wave per slot (or token); each 16-lane row of the wave takes one 128-block, 8 elements per lane
-// (16-byte loads), so a wave works through 4 blocks at a time; exact rounding points
+// transforms: one wave per slot, or per (token, group of blocks); each 16-lane row of the wave takes one 128-block,
+// 8 elements per lane (16-byte loads), 4 blocks per round; exact rounding points
 // ---------------------------------------------------------------------------------------------------------------
 
 constexpr int GP_TW = 4;   // waves per transform workgroup
-constexpr int GP_TU = 2;   // rounds of 4 blocks whose loads a transform wave keeps in flight
+constexpr int GP_TU = 2;   // rounds of 4 blocks per chunk of the input transform (two chunks' loads in flight)
+constexpr int GP_TA = 3;   // rounds of 4 blocks per chunk of the SwiGLU transform (one chunk covers I = 1536)
 
 // Elements 8li..8li+7 of block b in the GEMM input layout gp_perm_pos: pairs (2q, 2q + 1) are adjacent, at
 // b * 128 + q * 32 + (li >> 1) * 4 + 2 * (li & 1)
@@ -223,35 +274,46 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_prep_kernel(const uint64_t* __r
     if (s >= g.hdr[0]) return;
     const int nblk = H / 128;
     const int e = g.slot_e[s], tok = g.slot_pick[s] / topk;
-    const uint16_t* su0 = reinterpret_cast<const uint16_t*>(ptrs[(size_t)e * 9 + 3]);
-    const uint16_t* su1 = reinterpret_cast<const uint16_t*>(ptrs[(size_t)e * 9 + 5]);
+    const gptr<uint16_t> su0 = gaddr<uint16_t>(ptrs[(size_t)e * 9 + 3]);
+    const gptr<uint16_t> su1 = gaddr<uint16_t>(ptrs[(size_t)e * 9 + 5]);
     const uint16_t* xr = x + (size_t)tok * H;
     uint16_t* d0 = xt + (size_t)s * H;
     uint16_t* d1 = xt + ((size_t)cap + s) * H;
-    for (int b0 = 0; b0 < nblk; b0 += 4 * GP_TU)
-    {
-        uint4 xv[GP_TU], g0[GP_TU], g1[GP_TU];
+    constexpr int CH = 4 * GP_TU;   // blocks per chunk
+    uint4 xv[2][GP_TU], g0[2][GP_TU], g1[2][GP_TU];
+    auto load = [&](int buf, int c0) {
 #pragma unroll
         for (int k = 0; k < GP_TU; ++k)
         {
-            const int o = min(b0 + 4 * k + rl, nblk - 1) * 128 + li * 8;
-            xv[k] = *reinterpret_cast<const uint4*>(xr + o);
-            g0[k] = *reinterpret_cast<const uint4*>(su0 + o);
-            g1[k] = *reinterpret_cast<const uint4*>(su1 + o);
+            const int o = min(c0 + 4 * k + rl, nblk - 1) * 128 + li * 8;
+            xv[buf][k] = *reinterpret_cast<const uint4*>(xr + o);
+            g0[buf][k] = gld16(su0, o);
+            g1[buf][k] = gld16(su1, o);
         }
+    };
+    auto work = [&](int buf, int c0) {
 #pragma unroll
         for (int k = 0; k < GP_TU; ++k)
         {
-            const int b = b0 + 4 * k + rl;
+            const int b = c0 + 4 * k + rl;
             float u[8], v[8];
-            prep_block_row(u, xv[k], g0[k]);
-            prep_block_row(v, xv[k], g1[k]);
+            prep_block_row(u, xv[buf][k], g0[buf][k]);
+            prep_block_row(v, xv[buf][k], g1[buf][k]);
             if (b < nblk)
             {
                 gp_store_row(d0, b, li, u);
                 gp_store_row(d1, b, li, v);
             }
         }
+    };
+    // two chunk buffers: the next chunk's loads are in flight while the current one is transformed
+    load(0, 0);
+    for (int c0 = 0; c0 < nblk; c0 += 2 * CH)
+    {
+        if (c0 + CH < nblk) load(1, c0 + CH);
+        work(0, c0);
+        if (c0 + 2 * CH < nblk) load(0, c0 + 2 * CH);
+        if (c0 + CH < nblk) work(1, c0 + CH);
     }
 }
 
@@ -266,29 +328,55 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_act_kernel(const uint64_t* __re
     if (s >= g.hdr[0]) return;
     const int nbi = I / 128;
     const int e = g.slot_e[s];
-    const uint16_t* svh_g = reinterpret_cast<const uint16_t*>(ptrs[(size_t)e * 9 + 4]);
-    const uint16_t* svh_u = reinterpret_cast<const uint16_t*>(ptrs[(size_t)e * 9 + 6]);
-    const uint16_t* suh_d = reinterpret_cast<const uint16_t*>(ptrs[(size_t)e * 9 + 7]);
+    const gptr<uint16_t> svh_g = gaddr<uint16_t>(ptrs[(size_t)e * 9 + 4]);
+    const gptr<uint16_t> svh_u = gaddr<uint16_t>(ptrs[(size_t)e * 9 + 6]);
+    const gptr<uint16_t> suh_d = gaddr<uint16_t>(ptrs[(size_t)e * 9 + 7]);
     const float* yg = ygu + (size_t)s * I;
     const float* yu = ygu + ((size_t)cap + s) * I;
     uint16_t* dst = xd + (size_t)s * I;
-    for (int b0 = 0; b0 < nbi; b0 += 4)
+    // GP_TA rounds of 4 blocks per chunk in three phases kept apart by scheduling barriers (left to itself the
+    // compiler sinks each round's loads next to their use): all loads; the output transforms and every exponential
+    // lookup; the activation, input transform and stores
+    for (int c0 = 0; c0 < nbi; c0 += 4 * GP_TA)
     {
-        const int b = b0 + rl, o = min(b, nbi - 1) * 128 + li * 8;
-        const float4 ga = *reinterpret_cast<const float4*>(yg + o), gb = *reinterpret_cast<const float4*>(yg + o + 4);
-        const float4 ua = *reinterpret_cast<const float4*>(yu + o), ub = *reinterpret_cast<const float4*>(yu + o + 4);
-        const uint4 sg = *reinterpret_cast<const uint4*>(svh_g + o);
-        const uint4 su = *reinterpret_cast<const uint4*>(svh_u + o);
-        const uint4 sd = *reinterpret_cast<const uint4*>(suh_d + o);
-        float gv[8] = { ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w };
-        float uv[8] = { ua.x, ua.y, ua.z, ua.w, ub.x, ub.y, ub.z, ub.w };
-        out_block_row(gv, sg);
-        out_block_row(uv, su);
-        float av[8];
+        float gv[GP_TA][8], uv[GP_TA][8], ev[GP_TA][8];
+        uint4 sg[GP_TA], su[GP_TA], sd[GP_TA];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) av[k] = r16(act_mul(gv[k], uv[k], act_limit, exp_tab));
-        prep_block_row_f(av, sd);
-        if (b < nbi) gp_store_row(dst, b, li, av);
+        for (int k = 0; k < GP_TA; ++k)
+        {
+            const int o = min(c0 + 4 * k + rl, nbi - 1) * 128 + li * 8;
+            const float4 ga = *reinterpret_cast<const float4*>(yg + o), gb = *reinterpret_cast<const float4*>(yg + o + 4);
+            const float4 ua = *reinterpret_cast<const float4*>(yu + o), ub = *reinterpret_cast<const float4*>(yu + o + 4);
+            gv[k][0] = ga.x; gv[k][1] = ga.y; gv[k][2] = ga.z; gv[k][3] = ga.w;
+            gv[k][4] = gb.x; gv[k][5] = gb.y; gv[k][6] = gb.z; gv[k][7] = gb.w;
+            uv[k][0] = ua.x; uv[k][1] = ua.y; uv[k][2] = ua.z; uv[k][3] = ua.w;
+            uv[k][4] = ub.x; uv[k][5] = ub.y; uv[k][6] = ub.z; uv[k][7] = ub.w;
+            sg[k] = gld16(svh_g, o);
+            su[k] = gld16(svh_u, o);
+            sd[k] = gld16(suh_d, o);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < GP_TA; ++k)
+        {
+            out_block_row(gv[k], sg[k]);
+            out_block_row(uv[k], su[k]);
+        }
+#pragma unroll
+        for (int k = 0; k < GP_TA; ++k)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ev[k][j] = exp_tab[f2h_bits(gv[k][j]) & 0xFFFFu];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < GP_TA; ++k)
+        {
+            const int b = c0 + 4 * k + rl;
+            float av[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) av[j] = r16(act_mul_e(gv[k][j], uv[k][j], ev[k][j], act_limit));
+            prep_block_row_f(av, sd[k]);
+            if (b < nbi) gp_store_row(dst, b, li, av);
+        }
     }
 }
 
@@ -337,7 +425,7 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_comb_kernel(const uint64_t* __r
             const float* yr = yraw + (size_t)s * H + o;
             ya[i] = *reinterpret_cast<const float4*>(yr);
             yb[i] = *reinterpret_cast<const float4*>(yr + 4);
-            sv[i] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(pa) + o);
+            sv[i] = gld16(gaddr<uint16_t>(pa), o);
         }
 #pragma unroll
         for (int i = 0; i < GP_CK; ++i)
@@ -363,7 +451,6 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_comb_kernel(const uint64_t* __r
 
 constexpr int GP_NW = 8;           // waves per GEMM workgroup
 constexpr int GP_CPW = 2;          // tile columns per wave (each A fragment read from LDS feeds GP_CPW MFMAs)
-constexpr int GP_MT = 64;          // slots per pass (4 MFMA row blocks)
 constexpr int GP_WCOLS = 16 * GP_NW * GP_CPW;   // output columns per workgroup (256)
 constexpr int GP_XPW = GP_MT / GP_NW;           // slots whose input chunk each wave loads per group
 constexpr int GP_NG = 2;           // ring depth (groups of 8 tile rows): 2 keeps two workgroups per CU
@@ -411,11 +498,13 @@ __global__ __launch_bounds__(GP_NW * 64) void gp_gemm_kernel(GemmArgs a)
     // the wave index in a scalar register, so every LDS-DMA destination (M0) is scalar arithmetic
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     // XCD-aware order: workgroups are dispatched round-robin over the 8 XCDs (XCD = linear id % 8), so every
-    // workgroup of expert e gets a linear id = e % 8 (mod 8) and the expert's slot inputs are fetched into one L2
+    // workgroup of the ei-th expert of the dispatch order gets a linear id = ei (mod 8) and the expert's slot inputs
+    // are fetched into one L2
     const int nch = a.ndim / GP_WCOLS, per = nch * a.nmat;
     const int xcd = blockIdx.x % 8, j = blockIdx.x / 8;
-    const int e = (j / per) * 8 + xcd, rr0 = j % per;
-    if (e >= a.E) return;
+    const int ei = (j / per) * 8 + xcd, rr0 = j % per;
+    if (ei >= a.E) return;
+    const int e = a.g.eord[ei];   // experts with the most passes first
     const int nc = rr0 % nch;
     const int mat = a.mat_base + rr0 / nch;
     const int s_begin = a.g.off[e], s_end = a.g.off[e + 1];
@@ -514,11 +603,15 @@ __global__ __launch_bounds__(GP_NW * 64) void gp_gemm_kernel(GemmArgs a)
                     const half4 B1 = decode4<K>(wd[rp][c][1][0], wd[rp][c][1][1], d.sh);
                     B[c] = half8{ B0[0], B0[1], B0[2], B0[3], B1[0], B1[1], B1[2], B1[3] };
                 }
+                // raised wave priority while this wave issues its MFMAs: the matrix pipe is refilled as soon as it
+                // frees, and the other waves of the SIMD take the VALU slots in between
+                __builtin_amdgcn_s_setprio(1);
 #pragma unroll
                 for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
                     for (int c = 0; c < GP_CPW; ++c)
                         acc[c][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mb], B[c], acc[c][mb], 0, 0, 0);
+                __builtin_amdgcn_s_setprio(0);
             }
         }
         // D[i][n]: lane holds rows 4q + rr of each 16-slot block, column (t0 + c) * 16 + i16
@@ -577,7 +670,11 @@ int launch_grouped(const uint64_t* ptrs, const int64_t* sel, const void* w, int 
                    uint16_t* xd, float* yraw, const float* exp_tab, float act_limit, float* out, hipStream_t st)
 {
     const int M = P / topk;
-    hipLaunchKernelGGL(gp_plan_kernel, dim3(1), dim3(GP_PLAN_THREADS), 0, st, sel, w, w_half, P, topk, E, g);
+    const unsigned nch = (unsigned)((P + GP_PLAN_CHUNK - 1) / GP_PLAN_CHUNK);
+    hipLaunchKernelGGL(gp_rank_kernel, dim3(nch), dim3(GP_PLAN_THREADS), 0, st, sel, P, E, g);
+    hipLaunchKernelGGL(gp_place_kernel, dim3(nch), dim3(GP_PLAN_THREADS), 0, st, sel, P, E, g);
+    hipLaunchKernelGGL(gp_order_kernel, dim3((unsigned)((M + GP_ORDER_THREADS - 1) / GP_ORDER_THREADS)),
+                       dim3(GP_ORDER_THREADS), 0, st, w, w_half, M, topk, g);
     const unsigned slot_wgs = (unsigned)((P + GP_TW - 1) / GP_TW);
     hipLaunchKernelGGL(gp_prep_kernel, dim3(slot_wgs), dim3(GP_TW * 64), 0, st, ptrs, x, H, topk, cap, g, xt);
     GemmArgs a;
