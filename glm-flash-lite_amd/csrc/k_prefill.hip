@@ -13,6 +13,8 @@
 // for tile row 2q + {0, 1, 8, 9}[jj]; the inputs are stored with the same row permutation ([tk][q][jj] per tile row),
 // so each decoded tile feeds the MFMA directly, with no transpose. gfx950's v_mfma_f32_16x16x32_f16 takes two such
 // slices (tile rows r and r + 1) per lane as its 8 k-values.
+#include <type_traits>
+
 #include "gfl_device.hpp"
 #include "gfl_internal.hpp"
 
@@ -32,7 +34,7 @@ __device__ inline int gp_perm_pos(int b, int r)
     return b * 128 + q * 32 + tr * 4 + jj;
 }
 
-constexpr int GP_MT = 64;          // slots per GEMM pass (4 MFMA row blocks)
+constexpr int GP_MT = 80;          // slots per GEMM pass (up to 5 MFMA row blocks)
 constexpr int GP_PLAN_THREADS = GP_PLAN_CHUNK;   // one thread per pick of a chunk
 constexpr int GP_PLAN_WAVES = GP_PLAN_THREADS / 64;
 constexpr int GP_ORDER_THREADS = 256;
@@ -482,9 +484,9 @@ struct GemmArgs
 };
 
 // Grid: 8 * ceil(E / 8) * (ndim / 256) * matrices, XCD-major. Workgroup = 8 waves x 2 tile columns = 256 output columns of one matrix of one
-// expert; the expert's slots go through in passes of 64. Per group of 8 tile rows every wave decodes its 16 tiles and,
-// per pair of tile rows, reads 4 A fragments (16 slots x 32 k) and runs 8 MFMAs (16x16x32), each fragment feeding both
-// columns. The tiles stream through per-wave LDS rings and the slots' inputs through a shared ring, both filled by
+// expert; the expert's slots go through in passes of GP_MT. Per group of 8 tile rows every wave decodes its 16 tiles
+// and, per pair of tile rows, reads one A fragment (16 slots x 32 k) per row block of the pass and runs 2 MFMAs
+// (16x16x32) with it, one per column. The tiles stream through per-wave LDS rings and the slots' inputs through a shared ring, both filled by
 // LDS-direct loads GP_NG - 1 groups ahead; one workgroup barrier per group (group g landed for every wave; every wave
 // is past group g - 1, whose slots are refilled after it).
 template <int K>
@@ -538,14 +540,12 @@ __global__ __launch_bounds__(GP_NW * 64) void gp_gemm_kernel(GemmArgs a)
     for (int c0 = s_begin; c0 < s_end; c0 += GP_MT)
     {
         const int T = min(GP_MT, s_end - c0);
-        // the input chunk of group g for this wave's slots (slots past the pass read the pass's last slot)
-        int xoff[GP_XPW];
+        // byte offsets of the input rows this wave loads, the same in every lane (slots past the pass read the pass's
+        // last slot): the scalar offset of its LDS-direct loads, whose vector offset is the lane's 4 bytes
+        int xrow[GP_XPW];
 #pragma unroll
-        for (int j = 0; j < GP_XPW; ++j)
-        {
-            const int sl = min(wave * GP_XPW + j, T - 1);
-            xoff[j] = (c0 + sl) * a.kdim * 2 + lane * 4;
-        }
+        for (int j = 0; j < GP_XPW; ++j) xrow[j] = (c0 + min(wave * GP_XPW + j, T - 1)) * a.kdim * 2;
+        const int xl = lane * 4;
         auto issue = [&](int g) {
             uint8_t* dst = ring + (g % NG) * GB;
 #pragma unroll
@@ -555,76 +555,88 @@ __global__ __launch_bounds__(GP_NW * 64) void gp_gemm_kernel(GemmArgs a)
             uint16_t* xd = xring + (size_t)(g % NG) * GP_MT * GP_XS;
 #pragma unroll
             for (int j = 0; j < GP_XPW; ++j)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (gp_lds_void*)(xd + (wave * GP_XPW + j) * GP_XS), 4, xoff[j],
-                                                         g * 256, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (gp_lds_void*)(xd + (wave * GP_XPW + j) * GP_XS), 4, xl,
+                                                         xrow[j] + g * 256, 0, 0);
         };
-        float4v acc[GP_CPW][4];
+        // the pass with its NMB = ceil(T / 16) row blocks of 16 slots: MFMAs and input fragments of empty blocks
+        // are not issued
+        auto pass = [&](auto nmb_c) {
+            constexpr int NMB = decltype(nmb_c)::value;
+            float4v acc[GP_CPW][NMB];
 #pragma unroll
-        for (int c = 0; c < GP_CPW; ++c)
+            for (int c = 0; c < GP_CPW; ++c)
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb) acc[c][mb] = float4v{ 0.f, 0.f, 0.f, 0.f };
-        __syncthreads();   // previous pass done with the rings
+                for (int mb = 0; mb < NMB; ++mb) acc[c][mb] = float4v{ 0.f, 0.f, 0.f, 0.f };
+            __syncthreads();   // previous pass done with the rings
 #pragma unroll
-        for (int g = 0; g < NG - 1; ++g)
-            if (g < ngroups) issue(g);
-        for (int g = 0; g < ngroups; ++g)
-        {
-            if (g + NG - 2 < ngroups) gp_wait_vmcnt<(NG - 2) * NV>();   // this wave's loads of group g landed
-            else gp_wait_vmcnt<0>();
-            gp_barrier();   // every wave's loads of group g landed; every wave is done with group g - 1
-            if (g + NG - 1 < ngroups) issue(g + NG - 1);   // into the slots of group g - 1
-            const uint8_t* sl = ring + (g % NG) * GB;
-            const uint16_t* xs = xring + (size_t)(g % NG) * GP_MT * GP_XS;
-            // all trellis words of the group first (in-order LDS returns let each decode wait only for its own)
-            uint32_t wd[4][GP_CPW][2][2];
-#pragma unroll
-            for (int rp = 0; rp < 4; ++rp)
-#pragma unroll
-                for (int c = 0; c < GP_CPW; ++c)
-#pragma unroll
-                    for (int h = 0; h < 2; ++h)
-                    {
-                        const uint8_t* tp = sl + (2 * rp + h) * RB + c * TB;
-                        wd[rp][c][h][0] = *reinterpret_cast<const uint32_t*>(tp + d.o0);
-                        wd[rp][c][h][1] = *reinterpret_cast<const uint32_t*>(tp + d.o1);
-                    }
-#pragma unroll
-            for (int rp = 0; rp < 4; ++rp)
+            for (int g = 0; g < NG - 1; ++g)
+                if (g < ngroups) issue(g);
+            for (int g = 0; g < ngroups; ++g)
             {
-                half8 A[4];
+                if (g + NG - 2 < ngroups) gp_wait_vmcnt<(NG - 2) * NV>();   // this wave's loads of group g landed
+                else gp_wait_vmcnt<0>();
+                gp_barrier();   // every wave's loads of group g landed; every wave is done with group g - 1
+                if (g + NG - 1 < ngroups) issue(g + NG - 1);   // into the slots of group g - 1
+                const uint8_t* sl = ring + (g % NG) * GB;
+                const uint16_t* xs = xring + (size_t)(g % NG) * GP_MT * GP_XS;
 #pragma unroll
-                for (int mb = 0; mb < 4; ++mb)
-                    A[mb] = *reinterpret_cast<const half8*>(xs + (mb * 16 + i16) * GP_XS + q * 32 + rp * 8);
-                half8 B[GP_CPW];
-#pragma unroll
-                for (int c = 0; c < GP_CPW; ++c)
+                for (int rp = 0; rp < 4; ++rp)
                 {
-                    const half4 B0 = decode4<K>(wd[rp][c][0][0], wd[rp][c][0][1], d.sh);
-                    const half4 B1 = decode4<K>(wd[rp][c][1][0], wd[rp][c][1][1], d.sh);
-                    B[c] = half8{ B0[0], B0[1], B0[2], B0[3], B1[0], B1[1], B1[2], B1[3] };
-                }
-                // raised wave priority while this wave issues its MFMAs: the matrix pipe is refilled as soon as it
-                // frees, and the other waves of the SIMD take the VALU slots in between
-                __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-                for (int mb = 0; mb < 4; ++mb)
+                    // the trellis words of this pair of tile rows (the next pair's reads go out under this decode)
+                    uint32_t wd[GP_CPW][2][2];
 #pragma unroll
                     for (int c = 0; c < GP_CPW; ++c)
-                        acc[c][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mb], B[c], acc[c][mb], 0, 0, 0);
-                __builtin_amdgcn_s_setprio(0);
-            }
-        }
-        // D[i][n]: lane holds rows 4q + rr of each 16-slot block, column (t0 + c) * 16 + i16
 #pragma unroll
-        for (int c = 0; c < GP_CPW; ++c)
+                        for (int h = 0; h < 2; ++h)
+                        {
+                            const uint8_t* tp = sl + (2 * rp + h) * RB + c * TB;
+                            wd[c][h][0] = *reinterpret_cast<const uint32_t*>(tp + d.o0);
+                            wd[c][h][1] = *reinterpret_cast<const uint32_t*>(tp + d.o1);
+                        }
+                    half8 A[NMB];
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb)
+                    for (int mb = 0; mb < NMB; ++mb)
+                        A[mb] = *reinterpret_cast<const half8*>(xs + (mb * 16 + i16) * GP_XS + q * 32 + rp * 8);
+                    half8 B[GP_CPW];
 #pragma unroll
-                for (int rr = 0; rr < 4; ++rr)
-                {
-                    const int sl = mb * 16 + q * 4 + rr;
-                    if (sl < T) yout[(size_t)(c0 + sl) * a.ndim + (t0 + c) * 16 + i16] = acc[c][mb][rr];
+                    for (int c = 0; c < GP_CPW; ++c)
+                    {
+                        const half4 B0 = decode4<K>(wd[c][0][0], wd[c][0][1], d.sh);
+                        const half4 B1 = decode4<K>(wd[c][1][0], wd[c][1][1], d.sh);
+                        B[c] = half8{ B0[0], B0[1], B0[2], B0[3], B1[0], B1[1], B1[2], B1[3] };
+                    }
+                    // raised wave priority while this wave issues its MFMAs: the matrix pipe is refilled as soon as
+                    // it frees, and the other waves of the SIMD take the VALU slots in between
+                    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+                    for (int mb = 0; mb < NMB; ++mb)
+#pragma unroll
+                        for (int c = 0; c < GP_CPW; ++c)
+                            acc[c][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mb], B[c], acc[c][mb], 0, 0, 0);
+                    __builtin_amdgcn_s_setprio(0);
                 }
+            }
+            // D[i][n]: lane holds rows 4q + rr of each 16-slot block, column (t0 + c) * 16 + i16
+#pragma unroll
+            for (int c = 0; c < GP_CPW; ++c)
+#pragma unroll
+                for (int mb = 0; mb < NMB; ++mb)
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr)
+                    {
+                        const int sl = mb * 16 + q * 4 + rr;
+                        if (sl < T) yout[(size_t)(c0 + sl) * a.ndim + (t0 + c) * 16 + i16] = acc[c][mb][rr];
+                    }
+        };
+        static_assert(GP_MT == 80, "one case per row-block count");
+        switch ((T + 15) / 16)
+        {
+            case 1: pass(std::integral_constant<int, 1>{}); break;
+            case 2: pass(std::integral_constant<int, 2>{}); break;
+            case 3: pass(std::integral_constant<int, 3>{}); break;
+            case 4: pass(std::integral_constant<int, 4>{}); break;
+            default: pass(std::integral_constant<int, 5>{}); break;
+        }
     }
 }
 
