@@ -119,6 +119,17 @@ __device__ inline uint32_t f2h_bits(float x)
     return h & 0xFFFFu;
 }
 
+// two fp32 -> their fp16 bits packed lo | hi << 16, each rounded like f2h_bits (the high half through the SDWA form,
+// which keeps the low half)
+__device__ inline uint32_t f2h2_bits(float lo, float hi)
+{
+    uint32_t h;
+    asm("v_cvt_f16_f32 %0, %1\n\tv_cvt_f16_f32_sdwa %0, %2 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD"
+        : "=&v"(h)
+        : "v"(lo), "v"(hi));
+    return h;
+}
+
 __device__ inline float r16(float x)
 {
     uint32_t h;
@@ -275,17 +286,19 @@ __device__ inline void out_block_row(float (&v)[8], uint4 sc)
     for (int k = 0; k < 8; ++k) v[k] = r16(v[k] * sh * h2f_lane(sc, k));
 }
 
-// prep_block (ft_core.h:97-102) on a 16-lane row: x and suh are the lane's 8 fp16 inputs and scales (16 bytes each)
-__device__ inline void prep_block_row_f(float (&v)[8], uint4 sc)
+// prep_block (ft_core.h:97-102) on a 16-lane row up to its last rounding: v holds the lane's 8 fp32 inputs and sc its
+// 8 fp16 scales; on return v = the fp32 products (H v) * HADF, each still to be rounded to fp16
+__device__ inline void prep_block_row_fp(float (&v)[8], uint4 sc)
 {
 #pragma unroll
     for (int k = 0; k < 8; ++k) v[k] = v[k] * h2f_lane(sc, k);
     const float sh = fwht128_row(v) * HADF;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = r16(v[k] * sh);
+    for (int k = 0; k < 8; ++k) v[k] = v[k] * sh;
 }
 
-__device__ inline void prep_block_row(float (&v)[8], uint4 x, uint4 sc)
+// the same from 8 fp16 inputs x (16 bytes); x * suh of two fp16 values is exact in fp32
+__device__ inline void prep_block_row_p(float (&v)[8], uint4 x, uint4 sc)
 {
     const uint32_t xw[4] = { x.x, x.y, x.z, x.w }, sw[4] = { sc.x, sc.y, sc.z, sc.w };
 #pragma unroll
@@ -293,7 +306,23 @@ __device__ inline void prep_block_row(float (&v)[8], uint4 x, uint4 sc)
         v[k] = h2f_bits((uint16_t)(xw[k >> 1] >> (16 * (k & 1)))) * h2f_bits((uint16_t)(sw[k >> 1] >> (16 * (k & 1))));
     const float sh = fwht128_row(v) * HADF;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = r16(v[k] * sh);
+    for (int k = 0; k < 8; ++k) v[k] = v[k] * sh;
+}
+
+// prep_block with the 8 fp16 results packed in pairs: o[i] = elements 2i | 2i + 1 << 16
+__device__ inline void prep_block_row_fh(uint32_t (&o)[4], float (&v)[8], uint4 sc)
+{
+    prep_block_row_fp(v, sc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = f2h2_bits(v[2 * i], v[2 * i + 1]);
+}
+
+__device__ inline void prep_block_row_h(uint32_t (&o)[4], uint4 x, uint4 sc)
+{
+    float v[8];
+    prep_block_row_p(v, x, sc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = f2h2_bits(v[2 * i], v[2 * i + 1]);
 }
 
 // prep_block (ft_core.h:97-102) on lane-held elements L, L+64

@@ -544,17 +544,17 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(K ==
         auto prep_round = [&](int r, int k) {
             const int it = (r * NW + wave) * 4 + rl;
             float v[8];
-            prep_block_row(v, xv[k], sv[k]);
+            prep_block_row_p(v, xv[k], sv[k]);
             if (it < nit)
             {
                 // elements 8li..8li+7 of block b: tile row li/2, accumulators j0 = 2(li&1) and j0 + 1, q = k/2
                 const int s = it / nblk, b = it % nblk, tk = b * 8 + (li >> 1), j0 = 2 * (li & 1);
                 uint16_t* dst = lds_x + (size_t)s * a.H + (tk * 4 + j0) * 4;
                 uint2 e0, e1;
-                e0.x = f2h_bits(v[0]) | (f2h_bits(v[2]) << 16);
-                e0.y = f2h_bits(v[4]) | (f2h_bits(v[6]) << 16);
-                e1.x = f2h_bits(v[1]) | (f2h_bits(v[3]) << 16);
-                e1.y = f2h_bits(v[5]) | (f2h_bits(v[7]) << 16);
+                e0.x = f2h2_bits(v[0], v[2]);
+                e0.y = f2h2_bits(v[4], v[6]);
+                e1.x = f2h2_bits(v[1], v[3]);
+                e1.y = f2h2_bits(v[5], v[7]);
                 *reinterpret_cast<uint2*>(dst) = e0;
                 *reinterpret_cast<uint2*>(dst + 4) = e1;
             }

@@ -258,12 +258,11 @@ constexpr int GP_TA = 3;   // rounds of 4 blocks per chunk of the SwiGLU transfo
 
 // Elements 8li..8li+7 of block b in the GEMM input layout gp_perm_pos: pairs (2q, 2q + 1) are adjacent, at
 // b * 128 + q * 32 + (li >> 1) * 4 + 2 * (li & 1)
-__device__ __forceinline__ void gp_store_row(uint16_t* dst, int b, int li, const float (&v)[8])
+__device__ __forceinline__ void gp_store_row(uint16_t* dst, int b, int li, const uint32_t (&o)[4])
 {
     uint16_t* d0 = dst + b * 128 + (li >> 1) * 4 + 2 * (li & 1);
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<uint32_t*>(d0 + q * 32) = f2h_bits(v[2 * q]) | (f2h_bits(v[2 * q + 1]) << 16);
+    for (int q = 0; q < 4; ++q) *reinterpret_cast<uint32_t*>(d0 + q * 32) = o[q];
 }
 
 // prep_block (ft_core.h:97-102) of the gate and up inputs of slot s (one wave per slot)
@@ -298,9 +297,9 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_prep_kernel(const uint64_t* __r
         for (int k = 0; k < GP_TU; ++k)
         {
             const int b = c0 + 4 * k + rl;
-            float u[8], v[8];
-            prep_block_row(u, xv[buf][k], g0[buf][k]);
-            prep_block_row(v, xv[buf][k], g1[buf][k]);
+            uint32_t u[4], v[4];
+            prep_block_row_h(u, xv[buf][k], g0[buf][k]);
+            prep_block_row_h(v, xv[buf][k], g1[buf][k]);
             if (b < nblk)
             {
                 gp_store_row(d0, b, li, u);
@@ -376,8 +375,9 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_act_kernel(const uint64_t* __re
             float av[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) av[j] = r16(act_mul_e(gv[k][j], uv[k][j], ev[k][j], act_limit));
-            prep_block_row_f(av, sd[k]);
-            if (b < nbi) gp_store_row(dst, b, li, av);
+            uint32_t ah[4];
+            prep_block_row_fh(ah, av, sd[k]);
+            if (b < nbi) gp_store_row(dst, b, li, ah);
         }
     }
 }
