@@ -14,7 +14,7 @@ LIB_PATH = os.path.join(HERE, "libgfl_moe.so")
 SYMBOLS = ("gfl_last_error", "gfl_version", "gfl_ctx_create", "gfl_ctx_destroy", "gfl_register_layer",
            "gfl_moe_forward", "gfl_grouped_forward", "gfl_dequant", "gfl_split", "gfl_combine", "gfl_grouped_rows",
            "gfl_synth_trellis", "gfl_route",
-           "gfl_stats", "gfl_profile_enable", "gfl_profile_read", "gfl_exp_table")
+           "gfl_stats", "gfl_profile_enable", "gfl_profile_read", "gfl_exp_table", "gfl_silu_table")
 
 MODE_AUTO, MODE_AFFINE, MODE_EXACT, MODE_I16 = -1, 0, 1, 2
 
@@ -222,6 +222,15 @@ def exp_table():
     import numpy as np
     out = np.empty(65536, np.float32)
     check(load().gfl_exp_table(out.ctypes.data_as(C.c_void_p), out.size))
+    return out
+
+
+def silu_table():
+    """Host copy of the SwiGLU gate table the device reads: g / (1 + expf(-g)) in fp32 for every fp16 bit pattern of g
+    (float32 [65536])."""
+    import numpy as np
+    out = np.empty(65536, np.float32)
+    check(load().gfl_silu_table(out.ctypes.data_as(C.c_void_p), out.size))
     return out
 
 

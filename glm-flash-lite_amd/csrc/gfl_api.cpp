@@ -55,8 +55,8 @@ struct gfl_ctx
     std::vector<hipEvent_t> ev_pool;
     struct Rec { int stage; hipEvent_t a, b; };
     std::vector<Rec> recs;
-    // expf(-g) for every fp16 bit pattern g (the SwiGLU exponential, see build_exp_table)
-    float* exp_tab = nullptr;
+    // silu(g) for every fp16 bit pattern g (the SwiGLU gate, see build_silu_table)
+    float* silu_tab = nullptr;
     // slots per GEMV pass forced by GFL_SLOTS_PER_PASS (1, 2, 4 or 8; 0 = chosen from M)
     int ns_override = 0;
     // workspace of the prefill path (gfl_grouped_forward), grown on demand
@@ -177,7 +177,7 @@ int gfl_version(void) { return 100; }
 // library's expf. g is always fp16-valued (out_block rounds it, ft_core.h:109), so the exponential the device needs
 // is expf over the 65,536 fp16 bit patterns. glibc's expf is not correctly rounded on every one of them (it is
 // within 0.502 ulp), so no device formula reproduces it exactly; the table is evaluated here, by the same library
-// call the reference makes, and the activation kernel looks it up.
+// call the reference makes, and the device table of silu (build_silu_table) is formed from it.
 static void build_exp_table(float* tab)
 {
     for (uint32_t b = 0; b < 65536; ++b)
@@ -190,10 +190,34 @@ static void build_exp_table(float* tab)
     }
 }
 
+// silu(g) = g / (1 + expf(-g)) as the reference evaluates it in fp32 (ft_core.h:123): the library expf, then one
+// fp32 add and one fp32 division, each rounded. As g is fp16-valued, the whole gate is a function of g's 16 bits and
+// the activation kernels look it up instead of dividing.
+static void build_silu_table(float* tab)
+{
+    build_exp_table(tab);
+    for (uint32_t b = 0; b < 65536; ++b)
+    {
+        const uint16_t bits = (uint16_t)b;
+        _Float16 h;
+        std::memcpy(&h, &bits, 2);
+        const float g = (float)h;
+        const float d = 1.0f + tab[b];
+        tab[b] = g / d;
+    }
+}
+
 int gfl_exp_table(float* out, int n)
 {
     if (!out || n < 65536) return fail(GFL_EINVAL, "gfl_exp_table: needs a host array of 65536 floats");
     build_exp_table(out);
+    return GFL_OK;
+}
+
+int gfl_silu_table(float* out, int n)
+{
+    if (!out || n < 65536) return fail(GFL_EINVAL, "gfl_silu_table: needs a host array of 65536 floats");
+    build_silu_table(out);
     return GFL_OK;
 }
 
@@ -205,9 +229,9 @@ int gfl_ctx_create(int device, gfl_ctx** out)
     if (device < 0 || device >= n) return fail(GFL_EINVAL, "gfl_ctx_create: no such device");
     GFL_HIP(hipSetDevice(device));
     std::vector<float> tab(65536);
-    build_exp_table(tab.data());
+    build_silu_table(tab.data());
     float* dtab = nullptr;
-    if (hipMalloc(&dtab, tab.size() * sizeof(float)) != hipSuccess) return fail(GFL_ENOMEM, "gfl_ctx_create: exp table");
+    if (hipMalloc(&dtab, tab.size() * sizeof(float)) != hipSuccess) return fail(GFL_ENOMEM, "gfl_ctx_create: silu table");
     const hipError_t e = hipMemcpy(dtab, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice);
     if (e != hipSuccess)
     {
@@ -216,7 +240,7 @@ int gfl_ctx_create(int device, gfl_ctx** out)
     }
     gfl_ctx* c = new gfl_ctx();
     c->device = device;
-    c->exp_tab = dtab;
+    c->silu_tab = dtab;
     if (const char* e = std::getenv("GFL_SLOTS_PER_PASS"))
     {
         const int v = std::atoi(e);
@@ -236,7 +260,7 @@ int gfl_ctx_destroy(gfl_ctx* c)
         if (L.dptrs) hipFree(L.dptrs);
     if (c->ws) hipFree(c->ws);
     if (c->gws) hipFree(c->gws);
-    if (c->exp_tab) hipFree(c->exp_tab);
+    if (c->silu_tab) hipFree(c->silu_tab);
     delete c;
     return GFL_OK;
 }
@@ -299,12 +323,12 @@ int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, c
     int r = staged(c, 1, st, [&] {
         if (L.K[0] == L.K[1])
             return gfl::launch_gate_up(L.K[0], ns, L.dptrs, 0, 2, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                       ws.xtd, ws.act_cnt, c->exp_tab, act_limit, ws.pv, out, st);
+                                       ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, st);
         if (gfl::launch_gate_up(L.K[0], ns, L.dptrs, 0, 1, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                ws.xtd, ws.act_cnt, c->exp_tab, act_limit, ws.pv, out, st))
+                                ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, st))
             return -1;
         return gfl::launch_gate_up(L.K[1], ns, L.dptrs, 1, 1, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                   ws.xtd, ws.act_cnt, c->exp_tab, act_limit, ws.pv, out, st);
+                                   ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, st);
     });
     if (!r)
         r = staged(c, 3, st, [&] {
@@ -382,7 +406,7 @@ int gfl_grouped_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* se
     float* yraw = reinterpret_cast<float*>(b + b_int + b_xt + b_ygu + b_xd);
     const int r = staged(c, 2, st, [&] {
         return gfl::launch_grouped(L.dptrs, sel, w, w_is_half ? 1 : 0, P, topk, E, H, I, L.K[0], L.K[1], L.K[2], x, gp,
-                                   P, xt, ygu, xd, yraw, c->exp_tab, act_limit, out, st);
+                                   P, xt, ygu, xd, yraw, c->silu_tab, act_limit, out, st);
     });
     if (r) return fail(GFL_ERUNTIME, "gfl_grouped_forward: launch set-up failed");
     GFL_HIP(hipGetLastError());

@@ -345,10 +345,9 @@ __device__ inline void out_block_wave(float& v0, float& v1, float s0, float s1)
     v1 = r16(v1 * HADF * s1);
 }
 
-// silu(g) * u with exllamav3's clamp (act_mul, ft_core.h:123-132), given e = expf(-g)
-__device__ inline float act_mul_e(float g, float u, float e, float limit)
+// silu(g) * u with exllamav3's clamp (act_mul, ft_core.h:123-132), given x = silu(g) = g / (1 + expf(-g))
+__device__ inline float act_mul_s(float x, float u, float limit)
 {
-    float x = g / (1.0f + e);
     if (limit != 0.0f)
     {
         u = fminf(fmaxf(u, -limit), limit);
@@ -357,10 +356,10 @@ __device__ inline float act_mul_e(float g, float u, float e, float limit)
     return x * u;
 }
 
-// the same with e = expf(-g) from the context's table, indexed by the fp16 bits of g (g is fp16-valued)
-__device__ inline float act_mul(float g, float u, float limit, const float* __restrict__ exp_tab)
+// the same with silu(g) from the context's table, indexed by the fp16 bits of g (g is fp16-valued)
+__device__ inline float act_mul(float g, float u, float limit, const float* __restrict__ silu_tab)
 {
-    return act_mul_e(g, u, exp_tab[f2h_bits(g) & 0xFFFFu], limit);
+    return act_mul_s(silu_tab[f2h_bits(g) & 0xFFFFu], u, limit);
 }
 
 }  // namespace gfl

@@ -32,7 +32,7 @@ struct PlanView
 // last workgroup of the block. mat_base/nmat: matrices of this launch (0,2 = both, 0,1 = gate, 1,1 = up).
 int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, const int64_t* sel, const void* w,
                    int w_half, int P, int topk, int E, int H, int I, int umax, const uint16_t* x, float* ygu,
-                   uint16_t* xtd, int* act_cnt, const float* exp_tab, float act_limit, const PlanView& pv, float* out,
+                   uint16_t* xtd, int* act_cnt, const float* silu_tab, float act_limit, const PlanView& pv, float* out,
                    hipStream_t st);
 // down launch: down GEMV + out_block, weighted combine per (token, 128-block) by the token's last expert
 int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int umax, const PlanView& pv,
@@ -65,7 +65,7 @@ constexpr int GP_PLAN_CHUNK = 1024;   // picks per workgroup of the grouped plan
 // xd [cap][I] fp16, yraw [cap][H] fp32 workspace, cap >= P.
 int launch_grouped(const uint64_t* ptrs, const int64_t* sel, const void* w, int w_half, int P, int topk, int E, int H,
                    int I, int Kg, int Ku, int Kd, const uint16_t* x, const GPlan& g, int cap, uint16_t* xt, float* ygu,
-                   uint16_t* xd, float* yraw, const float* exp_tab, float act_limit, float* out, hipStream_t st);
+                   uint16_t* xd, float* yraw, const float* silu_tab, float act_limit, float* out, hipStream_t st);
 size_t grouped_gemm_lds_bytes(int K);
 
 int launch_split(const int64_t* sel, const uint16_t* w, const uint16_t* z, int n, int bsz, int topk, int H, int E,

@@ -444,7 +444,7 @@ struct GuArgs
     float* ygu;                // [2][cap][I]
     uint16_t* xtd;             // [cap][I] down input, permuted
     int* act_cnt;              // [cap][I/128] last-one counters (zero between calls)
-    const float* exp_tab;
+    const float* silu_tab;
     float act_limit;
     PlanView pv;               // written by workgroup (0, 0)
     float* out;                // [M][H] (rows of tokens without picks zeroed here)
@@ -478,7 +478,7 @@ __device__ void act_block(const GuArgs& a, int e, int s_begin, int s_end, int b)
         float u0 = ld_agent(&yu[lane]), u1 = ld_agent(&yu[lane + 64]);
         out_block_wave(g0, g1, h2f_bits(svh_g[b * 128 + lane]), h2f_bits(svh_g[b * 128 + lane + 64]));
         out_block_wave(u0, u1, h2f_bits(svh_u[b * 128 + lane]), h2f_bits(svh_u[b * 128 + lane + 64]));
-        float a0 = r16(act_mul(g0, u0, a.act_limit, a.exp_tab)), a1 = r16(act_mul(g1, u1, a.act_limit, a.exp_tab));
+        float a0 = r16(act_mul(g0, u0, a.act_limit, a.silu_tab)), a1 = r16(act_mul(g1, u1, a.act_limit, a.silu_tab));
         prep_block_wave(a0, a1, h2f_bits(suh_d[b * 128 + lane]), h2f_bits(suh_d[b * 128 + lane + 64]));
         uint16_t* dst = a.xtd + (size_t)s * a.I;
         dst[perm_pos(b, lane)] = (uint16_t)f2h_bits(a0);
@@ -858,12 +858,12 @@ size_t down_lds_bytes(int K, int ns, int I)
 
 int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, const int64_t* sel, const void* w,
                    int w_half, int P, int topk, int E, int H, int I, int umax, const uint16_t* x, float* ygu,
-                   uint16_t* xtd, int* act_cnt, const float* exp_tab, float act_limit, const PlanView& pv, float* out,
+                   uint16_t* xtd, int* act_cnt, const float* silu_tab, float act_limit, const PlanView& pv, float* out,
                    hipStream_t st)
 {
     GuArgs a;
     a.ptrs = ptrs; a.sel = sel; a.w = w; a.w_half = w_half; a.P = P; a.topk = topk; a.E = E; a.H = H; a.I = I;
-    a.mat_base = mat_base; a.x = x; a.ygu = ygu; a.xtd = xtd; a.act_cnt = act_cnt; a.exp_tab = exp_tab;
+    a.mat_base = mat_base; a.x = x; a.ygu = ygu; a.xtd = xtd; a.act_cnt = act_cnt; a.silu_tab = silu_tab;
     a.act_limit = act_limit; a.pv = pv; a.out = out;
     a.nmat_total = 2 * (128 / (16 * GU_NW));
     a.ns_cap = ns;

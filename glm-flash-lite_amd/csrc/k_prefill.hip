@@ -321,7 +321,7 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_prep_kernel(const uint64_t* __r
 // fwd_phase phase 1 (ft_core.h:974-991) of slot s (one wave per slot): per 128-block of I, out_block of gate and up,
 // r16(act_mul), down prep_block, stored in the GEMM input layout
 __global__ __launch_bounds__(GP_TW * 64) void gp_act_kernel(const uint64_t* __restrict__ ptrs, int I, int cap, GPlan g,
-                                                            const float* __restrict__ ygu, const float* exp_tab,
+                                                            const float* __restrict__ ygu, const float* silu_tab,
                                                             float act_limit, uint16_t* __restrict__ xd)
 {
     const int lane = threadIdx.x & 63, rl = lane >> 4, li = lane & 15;
@@ -336,7 +336,7 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_act_kernel(const uint64_t* __re
     const float* yu = ygu + ((size_t)cap + s) * I;
     uint16_t* dst = xd + (size_t)s * I;
     // GP_TA rounds of 4 blocks per chunk in three phases kept apart by scheduling barriers (left to itself the
-    // compiler sinks each round's loads next to their use): all loads; the output transforms and every exponential
+    // compiler sinks each round's loads next to their use): all loads; the output transforms and every silu
     // lookup; the activation, input transform and stores
     for (int c0 = 0; c0 < nbi; c0 += 4 * GP_TA)
     {
@@ -366,7 +366,7 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_act_kernel(const uint64_t* __re
 #pragma unroll
         for (int k = 0; k < GP_TA; ++k)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) ev[k][j] = exp_tab[f2h_bits(gv[k][j]) & 0xFFFFu];
+            for (int j = 0; j < 8; ++j) ev[k][j] = silu_tab[f2h_bits(gv[k][j]) & 0xFFFFu];
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int k = 0; k < GP_TA; ++k)
@@ -374,7 +374,7 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_act_kernel(const uint64_t* __re
             const int b = c0 + 4 * k + rl;
             float av[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) av[j] = r16(act_mul_e(gv[k][j], uv[k][j], ev[k][j], act_limit));
+            for (int j = 0; j < 8; ++j) av[j] = r16(act_mul_s(ev[k][j], uv[k][j], act_limit));
             uint32_t ah[4];
             prep_block_row_fh(ah, av, sd[k]);
             if (b < nbi) gp_store_row(dst, b, li, ah);
@@ -679,7 +679,7 @@ static int gp_gemm(int K, const GemmArgs& a, int nmat, hipStream_t st)
 
 int launch_grouped(const uint64_t* ptrs, const int64_t* sel, const void* w, int w_half, int P, int topk, int E, int H,
                    int I, int Kg, int Ku, int Kd, const uint16_t* x, const GPlan& g, int cap, uint16_t* xt, float* ygu,
-                   uint16_t* xd, float* yraw, const float* exp_tab, float act_limit, float* out, hipStream_t st)
+                   uint16_t* xd, float* yraw, const float* silu_tab, float act_limit, float* out, hipStream_t st)
 {
     const int M = P / topk;
     const unsigned nch = (unsigned)((P + GP_PLAN_CHUNK - 1) / GP_PLAN_CHUNK);
@@ -706,7 +706,7 @@ int launch_grouped(const uint64_t* ptrs, const int64_t* sel, const void* w, int 
         b.yout = ygu + (size_t)cap * I;
         if (gp_gemm(Ku, b, 1, st)) return -1;
     }
-    hipLaunchKernelGGL(gp_act_kernel, dim3(slot_wgs), dim3(GP_TW * 64), 0, st, ptrs, I, cap, g, ygu, exp_tab,
+    hipLaunchKernelGGL(gp_act_kernel, dim3(slot_wgs), dim3(GP_TW * 64), 0, st, ptrs, I, cap, g, ygu, silu_tab,
                        act_limit, xd);
     GemmArgs c = a;
     c.mat_base = 2; c.kdim = I; c.ndim = H; c.xin = xd; c.yout = yraw;

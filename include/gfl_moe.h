@@ -121,9 +121,14 @@ int gfl_route(const float* logits, int M, int E, int topk, int64_t* sel, uint16_
 int gfl_synth_trellis(void* dst, size_t nbytes, uint64_t seed, gfl_stream stream);
 
 /* The SwiGLU gate exponential, host copy: out[b] = expf(-g) for every fp16 bit pattern b of g (n >= 65536 floats).
- * silu (kernels/cpu_avx2/ft_core.h:123) calls the host C library's expf; g is always fp16-valued, so this table,
- * evaluated with that same library call, is what every context uploads and the activation kernel reads. */
+ * silu (kernels/cpu_avx2/ft_core.h:123) calls the host C library's expf; g is always fp16-valued, so the gate is
+ * tabulated from this table, evaluated with that same library call. */
 int gfl_exp_table(float* out, int n);
+
+/* The SwiGLU gate, host copy: out[b] = g / (1.0f + expf(-g)) in fp32 (one rounded add, one rounded division, as
+ * ft_core.h:123 evaluates it) for every fp16 bit pattern b of g (n >= 65536 floats). Every context uploads this table
+ * and the activation kernels read it. No counterpart in the reference: it exposes the table for checking. */
+int gfl_silu_table(float* out, int n);
 
 /* Host-side counters of the context (no device sync): [0] forward calls, [1] picks submitted, [2] registered layers,
  * [3] workspace bytes. Writes min(n, 4) entries into the host array `out`. */

@@ -88,6 +88,27 @@ def test_missing_library_fails_loudly(tmp_path):
             _native._LIB = saved
 
 
+def test_silu_table_is_the_fp32_gate():
+    """The device's gate table equals g / (1 + expf(-g)) with one fp32 rounding per operation (silu, ft_core.h:123) at
+    every fp16 input, including the signed zeros, infinities (-inf gives NaN) and the underflow to -0 for large
+    negative g."""
+    import _native
+    tab = _native.silu_table()
+    e = _native.exp_table()
+    g = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float32)
+    with np.errstate(all="ignore"):
+        want = g / (np.float32(1.0) + e)
+    assert want.dtype == np.float32
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(tab), nan)
+    assert np.array_equal(tab[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    f16 = lambda v: int(np.array([v], np.float16).view(np.uint16)[0])
+    assert tab[f16(0.0)] == 0.0 and tab[f16(np.inf)] == np.inf and np.isnan(tab[f16(-np.inf)])
+    big = tab[f16(-60000.0)]
+    assert big == 0.0 and np.signbit(big)
+    assert abs(tab[f16(1.0)] - 1.0 / (1.0 + np.exp(-1.0))) < 1e-7
+
+
 def test_exp_table_is_the_c_library_expf():
     """The activation's exponential table equals the C library's expf at every fp16 input (what silu calls,
     ft_core.h:123). It also documents why a table is used: correctly rounded exp disagrees with it on some inputs."""
