@@ -254,7 +254,7 @@ __global__ __launch_bounds__(GP_ORDER_THREADS) void gp_order_kernel(const void* 
 
 constexpr int GP_TW = 4;   // waves per transform workgroup
 constexpr int GP_TU = 2;   // rounds of 4 blocks per chunk of the input transform (two chunks' loads in flight)
-constexpr int GP_TA = 3;   // rounds of 4 blocks per chunk of the SwiGLU transform (one chunk covers I = 1536)
+constexpr int GP_TA = 3;   // rounds of 4 blocks per SwiGLU-transform wave (one wave covers I = 1536)
 
 // Elements 8li..8li+7 of block b in the GEMM input layout gp_perm_pos: pairs (2q, 2q + 1) are adjacent, at
 // b * 128 + q * 32 + (li >> 1) * 4 + 2 * (li & 1)
@@ -318,16 +318,17 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_prep_kernel(const uint64_t* __r
     }
 }
 
-// fwd_phase phase 1 (ft_core.h:974-991) of slot s (one wave per slot): per 128-block of I, out_block of gate and up,
-// r16(act_mul), down prep_block, stored in the GEMM input layout
+// fwd_phase phase 1 (ft_core.h:974-991), one wave per (slot, 4 * GP_TA blocks of I): per 128-block, out_block of
+// gate and up, r16(act_mul), down prep_block, stored in the GEMM input layout
 __global__ __launch_bounds__(GP_TW * 64) void gp_act_kernel(const uint64_t* __restrict__ ptrs, int I, int cap, GPlan g,
                                                             const float* __restrict__ ygu, const float* silu_tab,
                                                             float act_limit, uint16_t* __restrict__ xd)
 {
     const int lane = threadIdx.x & 63, rl = lane >> 4, li = lane & 15;
-    const int s = blockIdx.x * GP_TW + (threadIdx.x >> 6);
+    const int nbi = I / 128, nch = (nbi + 4 * GP_TA - 1) / (4 * GP_TA);
+    const int item = blockIdx.x * GP_TW + (threadIdx.x >> 6);
+    const int s = item / nch, c0 = (item % nch) * 4 * GP_TA;
     if (s >= g.hdr[0]) return;
-    const int nbi = I / 128;
     const int e = g.slot_e[s];
     const gptr<uint16_t> svh_g = gaddr<uint16_t>(ptrs[(size_t)e * 9 + 4]);
     const gptr<uint16_t> svh_u = gaddr<uint16_t>(ptrs[(size_t)e * 9 + 6]);
@@ -335,10 +336,9 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_act_kernel(const uint64_t* __re
     const float* yg = ygu + (size_t)s * I;
     const float* yu = ygu + ((size_t)cap + s) * I;
     uint16_t* dst = xd + (size_t)s * I;
-    // GP_TA rounds of 4 blocks per chunk in three phases kept apart by scheduling barriers (left to itself the
-    // compiler sinks each round's loads next to their use): all loads; the output transforms and every silu
-    // lookup; the activation, input transform and stores
-    for (int c0 = 0; c0 < nbi; c0 += 4 * GP_TA)
+    // GP_TA rounds of 4 blocks in three phases kept apart by scheduling barriers (left to itself the compiler sinks
+    // each round's loads next to their use): all loads; the output transforms and every silu lookup; the
+    // activation, input transform and stores
     {
         float gv[GP_TA][8], uv[GP_TA][8], ev[GP_TA][8];
         uint4 sg[GP_TA], su[GP_TA], sd[GP_TA];
@@ -706,8 +706,9 @@ int launch_grouped(const uint64_t* ptrs, const int64_t* sel, const void* w, int 
         b.yout = ygu + (size_t)cap * I;
         if (gp_gemm(Ku, b, 1, st)) return -1;
     }
-    hipLaunchKernelGGL(gp_act_kernel, dim3(slot_wgs), dim3(GP_TW * 64), 0, st, ptrs, I, cap, g, ygu, silu_tab,
-                       act_limit, xd);
+    const long act_items = (long)P * ((I / 128 + 4 * GP_TA - 1) / (4 * GP_TA));
+    hipLaunchKernelGGL(gp_act_kernel, dim3((unsigned)((act_items + GP_TW - 1) / GP_TW)), dim3(GP_TW * 64), 0, st, ptrs,
+                       I, cap, g, ygu, silu_tab, act_limit, xd);
     GemmArgs c = a;
     c.mat_base = 2; c.kdim = I; c.ndim = H; c.xin = xd; c.yout = yraw;
     if (gp_gemm(Kd, c, 1, st)) return -1;
