@@ -14,7 +14,8 @@ LIB_PATH = os.path.join(HERE, "libgfl_moe.so")
 SYMBOLS = ("gfl_last_error", "gfl_version", "gfl_ctx_create", "gfl_ctx_destroy", "gfl_register_layer",
            "gfl_moe_forward", "gfl_grouped_forward", "gfl_dequant", "gfl_split", "gfl_combine", "gfl_grouped_rows",
            "gfl_synth_trellis", "gfl_route",
-           "gfl_stats", "gfl_profile_enable", "gfl_profile_read", "gfl_exp_table", "gfl_silu_table")
+           "gfl_stats", "gfl_profile_enable", "gfl_profile_read", "gfl_exp_table", "gfl_silu_table",
+           "gfl_grouped_plan")
 
 MODE_AUTO, MODE_AFFINE, MODE_EXACT, MODE_I16 = -1, 0, 1, 2
 
@@ -49,6 +50,7 @@ def load(path=LIB_PATH):
     L.gfl_register_layer.argtypes = [_P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _P]
     L.gfl_moe_forward.argtypes = [_P, C.c_int, _P, _P, _P, C.c_int, C.c_int, C.c_int, _P, C.c_int, C.c_float, _P]
     L.gfl_grouped_forward.argtypes = [_P, C.c_int, _P, _P, _P, C.c_int, C.c_int, C.c_int, _P, C.c_float, _P]
+    L.gfl_grouped_plan.argtypes = [_P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, _P, _P]
     L.gfl_dequant.argtypes = [_P, C.c_int, C.c_int, C.c_int, _P, _P]
     L.gfl_split.argtypes = [_P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P,
                             C.c_int64, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P]
@@ -150,6 +152,31 @@ class Context:
         check(load().gfl_grouped_forward(self.h, li, ptr(x), ptr(sel), ptr(w), int(w.dtype == torch.float16), M, topk,
                                          ptr(out), float(act_limit), _stream()))
         return out
+
+    def grouped_plan(self, sel, w, E):
+        """The device routing plan of grouped_forward alone, for sel int64 [M, topk] and w fp16/fp32 [M, topk] on this
+        context's device: dict of tensors hdr [2], off [E+1], slot_pick / slot_e [M*topk], tok_slot / tok_w [M, topk],
+        tok_npk [M] (layout of gfl_grouped_plan)."""
+        import torch
+        if not (sel.dim() == 2 and sel.dtype == torch.int64 and sel.is_contiguous()):
+            raise ValueError("sel must be contiguous int64 [M, topk]")
+        M, topk = sel.shape
+        if not (w.dtype in (torch.float16, torch.float32) and w.is_contiguous() and tuple(w.shape) == (M, topk)):
+            raise ValueError("w must be contiguous fp16 or fp32 [M, topk]")
+        for t in (sel, w):
+            if not (t.is_cuda and t.device.index == self.device):
+                raise ValueError(f"all tensors must be on cuda:{self.device}")
+        dev, i32 = sel.device, torch.int32
+        r = dict(hdr=torch.zeros(2, dtype=i32, device=dev), off=torch.zeros(E + 1, dtype=i32, device=dev),
+                 slot_pick=torch.full((M * topk,), -1, dtype=i32, device=dev),
+                 slot_e=torch.full((M * topk,), -1, dtype=i32, device=dev),
+                 tok_slot=torch.full((M, topk), -1, dtype=i32, device=dev),
+                 tok_w=torch.zeros((M, topk), dtype=torch.float32, device=dev),
+                 tok_npk=torch.zeros(M, dtype=i32, device=dev))
+        check(load().gfl_grouped_plan(self.h, ptr(sel), ptr(w), int(w.dtype == torch.float16), M, topk, E,
+                                      ptr(r["hdr"]), ptr(r["off"]), ptr(r["slot_pick"]), ptr(r["slot_e"]),
+                                      ptr(r["tok_slot"]), ptr(r["tok_w"]), ptr(r["tok_npk"]), _stream()))
+        return r
 
     STAGES = ("plan", "gate_up", "grouped", "down", "combine")
 

@@ -342,6 +342,55 @@ int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, c
     return GFL_OK;
 }
 
+// The prefill workspace of a context, grown on demand (never inside a graph capture), and the grouped plan carved
+// from it. Layout: plan ints, then xt [2][P][H] fp16, ygu [2][P][I] fp32, xd [P][I] fp16, yraw [P][H] fp32 (H = I = 0
+// for the plan alone). Returns GFL_OK or the failure code (message set).
+static int grouped_workspace(gfl_ctx* c, hipStream_t st, int P, int M, int E, int H, int I, const char* who,
+                             gfl::GPlan& gp, char*& b, size_t& b_int, size_t& b_xt, size_t& b_ygu, size_t& b_xd)
+{
+    const size_t nch = (P + gfl::GP_PLAN_CHUNK - 1) / gfl::GP_PLAN_CHUNK;
+    const size_t n_int = 4 + (size_t)E + (E + 1) + 7 * (size_t)P + (size_t)M + (size_t)P + (size_t)E + nch * (E + 1);
+    b_int = align256(sizeof(int) * n_int);
+    b_xt = align256(2 * 2 * (size_t)P * H);
+    b_ygu = align256(4 * 2 * (size_t)P * I);
+    b_xd = align256(2 * (size_t)P * I);
+    const size_t b_yr = align256(4 * (size_t)P * H);
+    const size_t need = b_int + b_xt + b_ygu + b_xd + b_yr;
+    if (need > c->gws_bytes)
+    {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+            return fail(GFL_EINVAL, std::string(who) + ": the workspace must be sized before graph capture "
+                                                      "(run one call of this shape first)");
+        if (c->gws)
+        {
+            GFL_HIP(hipDeviceSynchronize());
+            GFL_HIP(hipFree(c->gws));
+        }
+        c->gws = nullptr;
+        c->gws_bytes = 0;
+        hipError_t e = hipMalloc(&c->gws, need);
+        if (e != hipSuccess) return fail(GFL_ENOMEM, std::string("grouped workspace hipMalloc: ") + hipGetErrorString(e));
+        c->gws_bytes = need;
+    }
+    b = static_cast<char*>(c->gws);
+    int* ip = reinterpret_cast<int*>(b);
+    gp.hdr = ip;
+    gp.cnt = gp.hdr + 4;
+    gp.off = gp.cnt + E;
+    gp.slot_pick = gp.off + E + 1;
+    gp.slot_e = gp.slot_pick + P;
+    gp.pick_slot = gp.slot_e + P;
+    gp.pick_c = gp.pick_slot + P;
+    gp.slot_job = gp.pick_c + P;
+    gp.tok_slot = gp.slot_job + P;
+    gp.tok_w = reinterpret_cast<float*>(gp.tok_slot + P);
+    gp.tok_npk = reinterpret_cast<int*>(gp.tok_w + P);
+    gp.eord = gp.tok_npk + M;
+    gp.ccnt = gp.eord + E;
+    return GFL_OK;
+}
+
 int gfl_grouped_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half,
                         int M, int topk, float* out, float act_limit, gfl_stream stream)
 {
@@ -360,46 +409,11 @@ int gfl_grouped_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* se
     GFL_HIP(hipSetDevice(c->device));
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const int P = M * topk, E = L.E, H = L.H, I = L.I;
-    // layout: plan ints, then xt [2][P][H] fp16, ygu [2][P][I] fp32, xd [P][I] fp16, yraw [P][H] fp32
-    const size_t nch = (P + gfl::GP_PLAN_CHUNK - 1) / gfl::GP_PLAN_CHUNK;
-    const size_t n_int = 4 + (size_t)E + (E + 1) + 7 * (size_t)P + (size_t)M + (size_t)P + (size_t)E + nch * (E + 1);
-    const size_t b_int = align256(sizeof(int) * n_int);
-    const size_t b_xt = align256(2 * 2 * (size_t)P * H), b_ygu = align256(4 * 2 * (size_t)P * I);
-    const size_t b_xd = align256(2 * (size_t)P * I), b_yr = align256(4 * (size_t)P * H);
-    const size_t need = b_int + b_xt + b_ygu + b_xd + b_yr;
-    if (need > c->gws_bytes)
-    {
-        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
-            return fail(GFL_EINVAL, "gfl_grouped_forward: the workspace must be sized before graph capture "
-                                    "(run one forward of this shape first)");
-        if (c->gws)
-        {
-            GFL_HIP(hipDeviceSynchronize());
-            GFL_HIP(hipFree(c->gws));
-        }
-        c->gws = nullptr;
-        c->gws_bytes = 0;
-        hipError_t e = hipMalloc(&c->gws, need);
-        if (e != hipSuccess) return fail(GFL_ENOMEM, std::string("grouped workspace hipMalloc: ") + hipGetErrorString(e));
-        c->gws_bytes = need;
-    }
-    char* b = static_cast<char*>(c->gws);
-    int* ip = reinterpret_cast<int*>(b);
     gfl::GPlan gp;
-    gp.hdr = ip;
-    gp.cnt = gp.hdr + 4;
-    gp.off = gp.cnt + E;
-    gp.slot_pick = gp.off + E + 1;
-    gp.slot_e = gp.slot_pick + P;
-    gp.pick_slot = gp.slot_e + P;
-    gp.pick_c = gp.pick_slot + P;
-    gp.slot_job = gp.pick_c + P;
-    gp.tok_slot = gp.slot_job + P;
-    gp.tok_w = reinterpret_cast<float*>(gp.tok_slot + P);
-    gp.tok_npk = reinterpret_cast<int*>(gp.tok_w + P);
-    gp.eord = gp.tok_npk + M;
-    gp.ccnt = gp.eord + E;
+    char* b = nullptr;
+    size_t b_int = 0, b_xt = 0, b_ygu = 0, b_xd = 0;
+    if (const int rc = grouped_workspace(c, st, P, M, E, H, I, "gfl_grouped_forward", gp, b, b_int, b_xt, b_ygu, b_xd))
+        return rc;
     uint16_t* xt = reinterpret_cast<uint16_t*>(b + b_int);
     float* ygu = reinterpret_cast<float*>(b + b_int + b_xt);
     uint16_t* xd = reinterpret_cast<uint16_t*>(b + b_int + b_xt + b_ygu);
@@ -412,6 +426,36 @@ int gfl_grouped_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* se
     GFL_HIP(hipGetLastError());
     c->calls += 1;
     c->picks += P;
+    return GFL_OK;
+}
+
+int gfl_grouped_plan(gfl_ctx* c, const int64_t* sel, const void* w, int w_is_half, int M, int topk, int E,
+                     int* hdr, int* off, int* slot_pick, int* slot_e, int* tok_slot, float* tok_w, int* tok_npk,
+                     gfl_stream stream)
+{
+    if (!c || !sel || !w || !hdr || !off || !slot_pick || !slot_e || !tok_slot || !tok_w || !tok_npk)
+        return fail(GFL_EINVAL, "gfl_grouped_plan: NULL argument");
+    if (M < 1 || topk < 1 || topk > gfl::MAX_TOPK || (int64_t)M * topk > gfl::MAX_GROUPED_PICKS)
+        return fail(GFL_EINVAL, "gfl_grouped_plan: need 1 <= topk <= 16 and M*topk <= 65536");
+    if (E < 1 || E > gfl::MAX_EXPERTS) return fail(GFL_EINVAL, "gfl_grouped_plan: need 1 <= E <= 1024");
+    std::lock_guard<std::mutex> g(c->mu);
+    GFL_HIP(hipSetDevice(c->device));
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const int P = M * topk;
+    gfl::GPlan gp;
+    char* b = nullptr;
+    size_t b_int = 0, b_xt = 0, b_ygu = 0, b_xd = 0;
+    if (const int rc = grouped_workspace(c, st, P, M, E, 0, 0, "gfl_grouped_plan", gp, b, b_int, b_xt, b_ygu, b_xd))
+        return rc;
+    gfl::launch_grouped_plan(sel, w, w_is_half ? 1 : 0, P, topk, E, gp, st);
+    GFL_HIP(hipGetLastError());
+    GFL_HIP(hipMemcpyAsync(hdr, gp.hdr, 2 * sizeof(int), hipMemcpyDeviceToDevice, st));
+    GFL_HIP(hipMemcpyAsync(off, gp.off, (E + 1) * sizeof(int), hipMemcpyDeviceToDevice, st));
+    GFL_HIP(hipMemcpyAsync(slot_pick, gp.slot_pick, P * sizeof(int), hipMemcpyDeviceToDevice, st));
+    GFL_HIP(hipMemcpyAsync(slot_e, gp.slot_e, P * sizeof(int), hipMemcpyDeviceToDevice, st));
+    GFL_HIP(hipMemcpyAsync(tok_slot, gp.tok_slot, P * sizeof(int), hipMemcpyDeviceToDevice, st));
+    GFL_HIP(hipMemcpyAsync(tok_w, gp.tok_w, P * sizeof(float), hipMemcpyDeviceToDevice, st));
+    GFL_HIP(hipMemcpyAsync(tok_npk, gp.tok_npk, M * sizeof(int), hipMemcpyDeviceToDevice, st));
     return GFL_OK;
 }
 

@@ -67,6 +67,9 @@ int launch_grouped(const uint64_t* ptrs, const int64_t* sel, const void* w, int 
                    int I, int Kg, int Ku, int Kd, const uint16_t* x, const GPlan& g, int cap, uint16_t* xt, float* ygu,
                    uint16_t* xd, float* yraw, const float* silu_tab, float act_limit, float* out, hipStream_t st);
 size_t grouped_gemm_lds_bytes(int K);
+// The grouped plan alone (first three launches of launch_grouped): slots, offsets, job order per token.
+void launch_grouped_plan(const int64_t* sel, const void* w, int w_half, int P, int topk, int E, const GPlan& g,
+                         hipStream_t st);
 
 int launch_split(const int64_t* sel, const uint16_t* w, const uint16_t* z, int n, int bsz, int topk, int H, int E,
                  int first, const int32_t* slotof, const float* score, const float* pol, int64_t* ctrl, uint16_t* hx,

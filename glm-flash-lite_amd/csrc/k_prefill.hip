@@ -677,9 +677,8 @@ static int gp_gemm(int K, const GemmArgs& a, int nmat, hipStream_t st)
     }
 }
 
-int launch_grouped(const uint64_t* ptrs, const int64_t* sel, const void* w, int w_half, int P, int topk, int E, int H,
-                   int I, int Kg, int Ku, int Kd, const uint16_t* x, const GPlan& g, int cap, uint16_t* xt, float* ygu,
-                   uint16_t* xd, float* yraw, const float* silu_tab, float act_limit, float* out, hipStream_t st)
+void launch_grouped_plan(const int64_t* sel, const void* w, int w_half, int P, int topk, int E, const GPlan& g,
+                         hipStream_t st)
 {
     const int M = P / topk;
     const unsigned nch = (unsigned)((P + GP_PLAN_CHUNK - 1) / GP_PLAN_CHUNK);
@@ -687,6 +686,14 @@ int launch_grouped(const uint64_t* ptrs, const int64_t* sel, const void* w, int 
     hipLaunchKernelGGL(gp_place_kernel, dim3(nch), dim3(GP_PLAN_THREADS), 0, st, sel, P, E, g);
     hipLaunchKernelGGL(gp_order_kernel, dim3((unsigned)((M + GP_ORDER_THREADS - 1) / GP_ORDER_THREADS)),
                        dim3(GP_ORDER_THREADS), 0, st, w, w_half, M, topk, g);
+}
+
+int launch_grouped(const uint64_t* ptrs, const int64_t* sel, const void* w, int w_half, int P, int topk, int E, int H,
+                   int I, int Kg, int Ku, int Kd, const uint16_t* x, const GPlan& g, int cap, uint16_t* xt, float* ygu,
+                   uint16_t* xd, float* yraw, const float* silu_tab, float act_limit, float* out, hipStream_t st)
+{
+    const int M = P / topk;
+    launch_grouped_plan(sel, w, w_half, P, topk, E, g, st);
     const unsigned slot_wgs = (unsigned)((P + GP_TW - 1) / GP_TW);
     hipLaunchKernelGGL(gp_prep_kernel, dim3(slot_wgs), dim3(GP_TW * 64), 0, st, ptrs, x, H, topk, cap, g, xt);
     GemmArgs a;

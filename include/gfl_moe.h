@@ -85,6 +85,18 @@ int gfl_moe_forward(gfl_ctx* ctx, int li, const uint16_t* x, const int64_t* sel,
 int gfl_grouped_forward(gfl_ctx* ctx, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half,
                         int M, int topk, float* out, float act_limit, gfl_stream stream);
 
+/* The routing plan of gfl_grouped_forward alone, copied out of the context's workspace (all device pointers; no
+ * counterpart in the reference: it exposes the device's grouped rows and combine order so that they can be checked
+ * against tier_lut_build_grouped_rows, ft_tier_ext.cpp:1047-1097, and moe_forward's job order,
+ * kernels/cpu_avx2/ft_core.h:1343-1349). sel int64 [M*topk], w fp16 (w_is_half) or fp32 [M*topk], E <= 1024.
+ * hdr int32 [2] = {slots S, ids outside [-1, E)}; off int32 [E+1] slot offsets (experts ascending); slot_pick and
+ * slot_e int32 [M*topk] (first S valid) = each slot's pick and expert, picks ascending within an expert; tok_slot
+ * int32 and tok_w fp32 [M][topk] = each token's slots and weights in (job, pick) order, first tok_npk[t] valid;
+ * tok_npk int32 [M]. */
+int gfl_grouped_plan(gfl_ctx* ctx, const int64_t* sel, const void* w, int w_is_half, int M, int topk, int E,
+                     int* hdr, int* off, int* slot_pick, int* slot_e, int* tok_slot, float* tok_w, int* tok_npk,
+                     gfl_stream stream);
+
 /* Dequantize one trellis matrix to fp16 W[k][n] (dense_weights, kernels/cpu_avx2/ft_core.h:1657-1672). */
 int gfl_dequant(const void* trellis, int k, int n, int K, uint16_t* out, gfl_stream stream);
 
@@ -137,7 +149,7 @@ int gfl_stats(gfl_ctx* ctx, int64_t* out, int n);
 /* Per-stage device timing of gfl_moe_forward, the counterpart of the per-phase wall times tier_stats reports
  * (ft_tier_ext.cpp:906-914): while enabled, every forward brackets its launches with device events. Stage 1 is the
  * gate|up launch (routing plan, gate|up GEMV, SwiGLU and down-input prep), stage 3 the down launch (down GEMV,
- * output transform, weighted combine); stage 2 is a whole gfl_grouped_forward call (its six launches); stages 0 and
+ * output transform, weighted combine); stage 2 is a whole gfl_grouped_forward call (its eight launches); stages 0 and
  * 4 (plan, combine) run inside the other launches and stay 0.
  * gfl_profile_read synchronises the recorded events, adds their elapsed milliseconds into stage_ms[5] and launch
  * counts into launches[5] (host arrays), and clears the record. */

@@ -161,3 +161,70 @@ def test_grouped_duplicate_picks(gpu, oracle):
     want = oracle.moe_forward(ex, x16.astype(np.float32), sel, w.astype(np.float32), mode=1)
     rel, mx = _stats("grouped duplicates", got, want)
     assert rel <= REL_RMS and mx <= MAX_ABS
+
+
+def _routing(mode, M, topk, E, rng):
+    """Routings for the plan test: distinct experts per token (uniform), Zipf-skewed picks with repeats within a token
+    (skew, dups), and skipped (-1) and out-of-range ids sprinkled in (bad)."""
+    if mode == "uniform":
+        return np.stack([rng.permutation(E)[:topk] for _ in range(M)]).astype(np.int64)
+    p = 1.0 / np.arange(1, E + 1) ** (1.3 if mode == "skew" else 0.6)
+    sel = rng.choice(E, size=(M, topk), p=p / p.sum()).astype(np.int64)
+    if mode == "bad":
+        m = rng.random(sel.shape)
+        sel[m < 0.1] = -1
+        sel[(m >= 0.1) & (m < 0.13)] = E + rng.integers(0, 5)
+        sel[(m >= 0.13) & (m < 0.15)] = -7
+    return sel
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,topk,E,mode", [(2048, 8, 288, "uniform"), (1500, 6, 64, "skew"), (3000, 8, 16, "dups"),
+                                           (333, 16, 1024, "bad"), (4096, 16, 40, "bad")])
+def test_grouped_plan_is_the_reference_order(gpu, oracle, M, topk, E, mode):
+    """The device plan of the grouped path over several chunks of 1024 picks, exactly: expert-major slots with picks
+    ascending (tier_lut_build_grouped_rows), and each token's picks in the order of the reference's jobs
+    (moe_forward's token-major scan, a new job every 8 picks of an expert; the oracle's build_jobs)."""
+    import torch
+    rng = np.random.default_rng(M * 7 + topk + E)
+    sel = _routing(mode, M, topk, E, rng)
+    w = rng.standard_normal(sel.shape).astype(np.float16)
+    r = gpu.grouped_plan(torch.from_numpy(sel).cuda(), torch.from_numpy(w.view(np.int16)).view(torch.float16).cuda(), E)
+    torch.cuda.synchronize()
+    r = {k: v.cpu().numpy() for k, v in r.items()}
+    P = M * topk
+    flat = sel.reshape(-1)
+    valid = (flat >= 0) & (flat < E)
+    S = int(valid.sum())
+    assert r["hdr"].tolist() == [S, int(((flat != -1) & ~valid).sum())]
+    cnt = np.bincount(flat[valid], minlength=E)
+    assert np.array_equal(r["off"], np.concatenate([[0], np.cumsum(cnt)]))
+    picks = np.nonzero(valid)[0]
+    order = np.lexsort((picks, flat[picks]))
+    assert np.array_equal(r["slot_pick"][:S], picks[order])
+    assert np.array_equal(r["slot_e"][:S], flat[picks][order])
+    slot_of = np.full(P, -1, np.int64)
+    slot_of[picks[order]] = np.arange(S)
+    # job of every valid pick from the oracle's job list: the c-th pick (scan order) of expert e sits at entry c % 8
+    # of e's (c // 8)-th job
+    sel_o = np.where((sel >= 0) & (sel < E), sel, -1)
+    jobs = oracle.build_jobs(E, sel_o, w.astype(np.float32))
+    of_e = {}
+    for j, (e, members) in enumerate(jobs):
+        of_e.setdefault(e, []).append(j)
+    job = np.full(P, -1, np.int64)
+    seen = np.zeros(E, np.int64)
+    for p in picks:
+        e, t = int(flat[p]), p // topk
+        c = seen[e]
+        seen[e] += 1
+        j = of_e[e][c // 8]
+        assert jobs[j][1][c % 8] == (t, float(w.reshape(-1)[p]))
+        job[p] = j
+    npk = valid.reshape(M, topk).sum(1)
+    assert np.array_equal(r["tok_npk"], npk)
+    for t in range(M):
+        ks = [k for k in range(topk) if valid[t * topk + k]]
+        ks.sort(key=lambda k: (job[t * topk + k], k))
+        assert r["tok_slot"][t, :len(ks)].tolist() == [int(slot_of[t * topk + k]) for k in ks], t
+        assert np.array_equal(r["tok_w"][t, :len(ks)], np.array([w[t, k] for k in ks], np.float32)), t
