@@ -310,10 +310,13 @@ int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, c
     Workspace ws;
     if (int r = ensure_ws(c, P, L.H, L.I, st, ws)) return r;
     const int umax = P < L.E ? P : L.E;
-    // slots per pass of the GEMV (its LDS holds NS transformed inputs); experts with more slots take extra passes,
-    // each re-streaming the expert's weights. Measured on MI355X for M = 3..64 (uniform top-8 of 288): two slots per
-    // pass beat four or eight, whose larger LDS footprint costs more occupancy than the extra passes cost bandwidth.
-    int ns = M == 1 ? 1 : 2;
+    // slots per pass of the GEMV (its LDS holds NS transformed inputs). With one slot per pass the launches run a
+    // workgroup per slot, so an expert picked by several tokens is streamed once per slot in parallel; with more,
+    // a workgroup per union entry takes the entry's slots in passes. Measured on MI355X (config 1 uniform, config 2
+    // Zipf, top-8 of 288): per slot is 7-16% faster at M = 2..4 and even at M = 16..32; at M = 64 two slots per pass
+    // are 10% faster (the extra streams cost more than the lower LDS footprint gains). Four or eight slots per pass
+    // lose to two at every M from 3 to 64 (their LDS footprint costs occupancy).
+    int ns = M <= 8 ? 1 : 2;
     if (c->ns_override > 0) ns = std::min(c->ns_override, M);
     if (gfl::gate_up_lds_bytes(L.K[0], ns, L.H, P, L.E) > gfl::LDS_LIMIT ||
         gfl::gate_up_lds_bytes(L.K[1], ns, L.H, P, L.E) > gfl::LDS_LIMIT
@@ -332,8 +335,8 @@ int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, c
     });
     if (!r)
         r = staged(c, 3, st, [&] {
-            return gfl::launch_down(L.K[2], ns, L.dptrs, topk, L.H, L.I, umax, ws.pv, ws.xtd, ws.yd, ws.out_cnt, out,
-                                    st);
+            return gfl::launch_down(L.K[2], ns, L.dptrs, topk, L.H, L.I, umax, P, ws.pv, ws.xtd, ws.yd, ws.out_cnt,
+                                    out, st);
         });
     if (r) return r > 0 ? r : fail(GFL_EINVAL, "gfl_moe_forward: unsupported K");
     GFL_HIP(hipGetLastError());

@@ -24,7 +24,8 @@ struct PlanView
     int* tok_slot;   // [tokens][topk] slots of each token in combine order, -1 padded
     float* tok_w;    // [tokens][topk] their routing weights (fp32)
     int* tok_npk;    // [tokens] number of valid picks of each token
-    uint64_t* uptr;  // [U][2] down trellis and svh_down addresses of union entry u (one load for the down launch)
+    uint64_t* uptr;  // [U][2] down trellis and svh_down addresses of union entry u (one load for the down launch);
+                     // [slots][2], by slot, when the launches run a workgroup per slot (one slot per pass)
     int cap_slots;
 };
 
@@ -35,7 +36,7 @@ int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, 
                    uint16_t* xtd, int* act_cnt, const float* silu_tab, float act_limit, const PlanView& pv, float* out,
                    hipStream_t st);
 // down launch: down GEMV + out_block, weighted combine per (token, 128-block) by the token's last expert
-int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int umax, const PlanView& pv,
+int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int umax, int P, const PlanView& pv,
                 const uint16_t* xtd, float* yd, int* out_cnt, float* out, hipStream_t st);
 size_t gate_up_lds_bytes(int K, int ns, int H, int P, int E);
 size_t down_lds_bytes(int K, int ns, int I);

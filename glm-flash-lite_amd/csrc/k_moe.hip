@@ -239,7 +239,7 @@ __device__ inline int plan_job(const LPlan& L, int p)
 // with their fp32 weights; rows of tokens without a valid pick are written as zeros here (no down workgroup touches
 // them; the reference's sum over an empty route is 0).
 __device__ void publish_plan(const LPlan& L, const int* hdr, int P, int topk, const void* w, int w_half,
-                             const PlanView& pv, float* out, int H, const uint64_t* ptrs)
+                             const PlanView& pv, float* out, int H, const uint64_t* ptrs, int per_slot)
 {
     const int t = threadIdx.x, nt = blockDim.x;
     const int U = hdr[0], S = hdr[1];
@@ -248,8 +248,18 @@ __device__ void publish_plan(const LPlan& L, const int* hdr, int P, int topk, co
     {
         const int e = L.uexp[u];
         pv.uexp[u] = e;
-        pv.uptr[2 * u] = ptrs[(size_t)e * 9 + 2];
-        pv.uptr[2 * u + 1] = ptrs[(size_t)e * 9 + 8];
+        if (!per_slot)
+        {
+            pv.uptr[2 * u] = ptrs[(size_t)e * 9 + 2];
+            pv.uptr[2 * u + 1] = ptrs[(size_t)e * 9 + 8];
+        }
+    }
+    // with per_slot the down launch takes a workgroup per slot: the address table is indexed by slot
+    for (int s = t; per_slot && s < S; s += nt)
+    {
+        const int e = L.e[L.spick[s]];
+        pv.uptr[2 * s] = ptrs[(size_t)e * 9 + 2];
+        pv.uptr[2 * s + 1] = ptrs[(size_t)e * 9 + 8];
     }
     for (int u = t; u <= U; u += nt) pv.uoff[u] = L.uoff[u];
     for (int s = t; s < S; s += nt) pv.slot_pick[s] = L.spick[s];
@@ -450,6 +460,7 @@ struct GuArgs
     float* out;                // [M][H] (rows of tokens without picks zeroed here)
     int nmat_total;            // gate|up workgroups covering one 128-block
     int ns_cap;                // slots per pass the LDS allocation holds (<= NS)
+    int per_slot;              // workgroups per slot (one pass each) instead of per union entry (NS == 1 only)
 };
 
 __device__ __forceinline__ float ld_agent(const float* p)
@@ -487,7 +498,9 @@ __device__ void act_block(const GuArgs& a, int e, int s_begin, int s_end, int b)
 }
 
 // Grid: (umax * I/64 + 1, nmat). Workgroup = 4 waves = 64 outputs of one matrix of one routed expert, all its
-// slots; the last workgroup of row 0 publishes the plan.
+// slots; the last workgroup of row 0 publishes the plan. With per_slot the grid is (P * I/64 + 1, nmat) and a
+// workgroup takes one slot: an expert picked by several tokens is streamed once per slot, in parallel, instead of in
+// passes one after another.
 template <int K, int NS>
 __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(K == 5 ? 3 : 4))) void gu_kernel(GuArgs a)
 {
@@ -506,19 +519,20 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(K ==
     if (blockIdx.x == gridDim.x - 1)
     {
         // the grid's extra workgroup publishes the plan for the down launch (no GEMV work of its own)
-        if (blockIdx.y == 0) publish_plan(L, hdr, a.P, a.topk, a.w, a.w_half, a.pv, a.out, a.H, a.ptrs);
+        if (blockIdx.y == 0) publish_plan(L, hdr, a.P, a.topk, a.w, a.w_half, a.pv, a.out, a.H, a.ptrs, a.per_slot);
         return;
     }
 
-    const int u = blockIdx.x / ncb, cb = blockIdx.x % ncb;
-    if (u >= hdr[0]) return;
+    const int ent = blockIdx.x / ncb, cb = blockIdx.x % ncb;   // union entry, or slot with per_slot
+    if (ent >= hdr[a.per_slot ? 1 : 0]) return;
+    const int u = a.per_slot ? plan_u(L, L.spick[ent]) : ent;
     const int mat = a.mat_base + blockIdx.y;              // 0 gate, 1 up
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15;
     const int wid = __builtin_amdgcn_readfirstlane(wave);
     const int e = L.uexp[u];
     const uint8_t* tr = reinterpret_cast<const uint8_t*>(a.ptrs[(size_t)e * 9 + mat]);
     const gptr<uint16_t> suh = gaddr<uint16_t>(a.ptrs[(size_t)e * 9 + 3 + 2 * mat]);
-    const int s_begin = L.uoff[u], s_end = L.uoff[u + 1];
+    const int s_begin = a.per_slot ? ent : L.uoff[u], s_end = a.per_slot ? ent + 1 : L.uoff[u + 1];
     const size_t gstride = (size_t)TN * TB;
     const int t = cb * NW + wave;                         // this wave's tile column
     const uint8_t* col = tr + (size_t)t * TB;
@@ -593,7 +607,7 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(K ==
     const int blk = (cb * NW * 16) / 128;
     if (threadIdx.x == 0)
     {
-        int* ctr = a.act_cnt + (size_t)u * (a.I / 128) + blk;
+        int* ctr = a.act_cnt + (size_t)ent * (a.I / 128) + blk;
         const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = old == a.nmat_total - 1;
         if (s_last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -616,9 +630,11 @@ struct DnArgs
     int* out_cnt;              // [tokens][H/128] last-one counters (zero between calls)
     float* out;                // [M][H]
     int ns_cap;                // slots per pass the LDS allocation holds (<= NS)
+    int per_slot;              // workgroups per slot (one pass each), as the gate|up launch
 };
 
-// Grid: umax * H/128. Workgroup = 8 waves = one 128-output block of one routed expert, all its slots.
+// Grid: umax * H/128. Workgroup = 8 waves = one 128-output block of one routed expert, all its slots (with per_slot:
+// P * H/128, one slot each).
 template <int K, int NS>
 __global__ __launch_bounds__(DN_NW * 64) __attribute__((amdgpu_waves_per_eu(K == 5 || NS == 8 ? 3 : 4))) void down_kernel(DnArgs a)
 {
@@ -632,11 +648,11 @@ __global__ __launch_bounds__(DN_NW * 64) __attribute__((amdgpu_waves_per_eu(K ==
     uint16_t* lds_x = reinterpret_cast<uint16_t*>(lds_raw + NW * RB);                 // [ns_cap][I]
     float* lds_y = reinterpret_cast<float*>(lds_raw + NW * RB + (size_t)a.ns_cap * a.I * 2);   // [ns_cap][128]
     const int TN = a.H / 16, TK = a.I / 16, ncb = TN / NW;
-    const int u = blockIdx.x / ncb, blk = blockIdx.x % ncb;
-    // one round of independent loads: the union size, this entry's slot range and its expert's addresses (entries
-    // at u >= U hold stale values and are not used)
-    const int U = a.pv.hdr[0];
-    const int s_begin = a.pv.uoff[u], s_end = a.pv.uoff[u + 1];
+    const int u = blockIdx.x / ncb, blk = blockIdx.x % ncb;   // union entry, or slot with per_slot
+    // one round of independent loads: the union size (slot count), this entry's slot range and its expert's
+    // addresses (entries past the count hold stale values and are not used)
+    const int U = a.pv.hdr[a.per_slot ? 1 : 0];
+    const int s_begin = a.per_slot ? u : a.pv.uoff[u], s_end = a.per_slot ? u + 1 : a.pv.uoff[u + 1];
     const uint8_t* tr = reinterpret_cast<const uint8_t*>(a.pv.uptr[2 * u]);
     const gptr<uint16_t> svh = gaddr<uint16_t>(a.pv.uptr[2 * u + 1]);
     if (u >= U) return;
@@ -804,17 +820,19 @@ static void gu_launch(const GuArgs& a, int umax, int nmat, hipStream_t st)
     auto kern = gu_kernel<K, NS>;
     static const bool opened = open_lds(kern);
     (void)opened;
-    hipLaunchKernelGGL(kern, dim3(umax * (a.I / (16 * GU_NW)) + 1, nmat), dim3(GU_NW * 64), lds, st, a);
+    const int ents = a.per_slot ? a.P : umax;
+    hipLaunchKernelGGL(kern, dim3(ents * (a.I / (16 * GU_NW)) + 1, nmat), dim3(GU_NW * 64), lds, st, a);
 }
 
 template <int K, int NS>
-static void dn_launch(const DnArgs& a, int umax, hipStream_t st)
+static void dn_launch(const DnArgs& a, int umax, int P, hipStream_t st)
 {
     const size_t lds = dn_lds<K>(a.ns_cap, a.I);
     auto kern = down_kernel<K, NS>;
     static const bool opened = open_lds(kern);
     (void)opened;
-    hipLaunchKernelGGL(kern, dim3(umax * (a.H / (16 * DN_NW))), dim3(DN_NW * 64), lds, st, a);
+    const int ents = a.per_slot ? P : umax;
+    hipLaunchKernelGGL(kern, dim3(ents * (a.H / (16 * DN_NW))), dim3(DN_NW * 64), lds, st, a);
 }
 
 // slots per pass: 1, 4 or 8 (a 2-slot instantiation does not fit the register budget without spilling; passes with
@@ -867,18 +885,20 @@ int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, 
     a.act_limit = act_limit; a.pv = pv; a.out = out;
     a.nmat_total = 2 * (128 / (16 * GU_NW));
     a.ns_cap = ns;
+    a.per_slot = ns == 1;
     GFL_K_SWITCH(K, GFL_NS_SWITCH(ns, (gu_launch<K_, NS_>(a, umax, nmat, st))))
     return 0;
 }
 
-int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int umax, const PlanView& pv,
+int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int umax, int P, const PlanView& pv,
                 const uint16_t* xtd, float* yd, int* out_cnt, float* out, hipStream_t st)
 {
     DnArgs a;
     a.ptrs = ptrs; a.topk = topk; a.H = H; a.I = I; a.pv = pv; a.xtd = xtd; a.yd = yd; a.out_cnt = out_cnt;
     a.out = out;
     a.ns_cap = ns;
-    GFL_K_SWITCH(K, GFL_NS_SWITCH(ns, (dn_launch<K_, NS_>(a, umax, st))))
+    a.per_slot = ns == 1;
+    GFL_K_SWITCH(K, GFL_NS_SWITCH(ns, (dn_launch<K_, NS_>(a, umax, P, st))))
     return 0;
 }
 #undef GFL_NS_SWITCH
