@@ -317,7 +317,10 @@ __device__ inline int perm_pos(int b, int r)
 // fence, so outstanding global loads stay in flight).
 __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-constexpr int NGRP = 8;     // groups of 8 tiles in each wave's LDS ring (7 in flight)
+// groups of 8 tiles in each wave's LDS ring (3 in flight). Measured against 2..8 groups on MI355X: 3 and 4 are
+// fastest at M = 1..4 (a deeper ring puts more loads ahead of the input transform, whose waits cover every load issued
+// before it, since the compiler does not count the LDS-direct loads and waits with vmcnt(0)).
+constexpr int NGRP = 4;
 
 // One tile column of one matrix over all TK tile rows for up to NS slots whose transformed inputs sit in lds_x
 // ([ns][kdim] fp16 in the permuted [tk][j][q] order). Lane (j = l/16, n = l%16) carries the reference's accumulator j
