@@ -313,9 +313,9 @@ int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, c
     // slots per pass of the GEMV (its LDS holds NS transformed inputs). With one slot per pass the launches run a
     // workgroup per slot, so an expert picked by several tokens is streamed once per slot in parallel; with more,
     // a workgroup per union entry takes the entry's slots in passes. Measured on MI355X (config 1 uniform, config 2
-    // Zipf, top-8 of 288): per slot is 7-16% faster at M = 2..4 and even at M = 16..32; at M = 64 two slots per pass
-    // are 10% faster (the extra streams cost more than the lower LDS footprint gains). Four or eight slots per pass
-    // lose to two at every M from 3 to 64 (their LDS footprint costs occupancy).
+    // Zipf, top-8 of 288): per slot is 5-15% faster at M = 2..4; two slots per pass are 4% faster at M = 16, 8% at
+    // M = 32 and 16% at M = 64 (there the extra weight streams of per slot cost more than its smaller LDS footprint
+    // gains). Four slots per pass match two at M = 64 and lose elsewhere; eight lose everywhere.
     int ns = M <= 8 ? 1 : 2;
     if (c->ns_override > 0) ns = std::min(c->ns_override, M);
     if (gfl::gate_up_lds_bytes(L.K[0], ns, L.H, P, L.E) > gfl::LDS_LIMIT ||
