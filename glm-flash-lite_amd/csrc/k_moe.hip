@@ -398,11 +398,11 @@ __device__ __forceinline__ void chain_dma(const uint8_t* __restrict__ col_base, 
             wait_vmcnt<0>();
         const uint8_t* sl = ring + (g % NG) * GB;
 #pragma unroll
-        for (int h = 0; h < 8; h += 4)
+        for (int h = 0; h < 8; h += 8)   // all 8 tiles of the group per block (more independent work for a lone wave)
         {
-            float4v cw[4];
+            float4v cw[8];
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr)
+            for (int rr = 0; rr < 8; ++rr)
             {
                 const uint8_t* tp = sl + (h + rr) * TB;
                 const uint32_t hi = *reinterpret_cast<const uint32_t*>(tp + d.o0);
@@ -416,7 +416,7 @@ __device__ __forceinline__ void chain_dma(const uint8_t* __restrict__ col_base, 
                 {
                     float a = acc[s];
 #pragma unroll
-                    for (int rr = 0; rr < 4; ++rr)
+                    for (int rr = 0; rr < 8; ++rr)
                     {
                         const int tk = g * 8 + h + rr;
                         const half4 xv = *reinterpret_cast<const half4*>(xl + ((size_t)s * TK + tk) * 16);
