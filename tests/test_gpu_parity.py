@@ -80,9 +80,10 @@ def test_synth_trellis_matches_checker(gpu, oracle):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("ntok", [1, 3, 4])
+@pytest.mark.parametrize("ntok", [1, 3, 4, 8, 9])
 def test_forward_small_bitexact(gpu, oracle, ntok):
-    """Small shape, the reference harness's routing (t + 2k) % E (duplicate picks of one expert per token)."""
+    """Small shape, the reference harness's routing (t + 2k) % E (duplicate picks of one expert per token). Up to 8
+    tokens the launches run a workgroup per slot, from 9 a workgroup per expert with passes of two slots."""
     H, I, E = 512, 256, 6
     L = _layer(gpu, 1, E, H, I)
     ex = _host_experts(oracle, L)
