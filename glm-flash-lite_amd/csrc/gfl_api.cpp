@@ -346,7 +346,7 @@ int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, c
 }
 
 // The prefill workspace of a context, grown on demand (never inside a graph capture), and the grouped plan carved
-// from it. Layout: plan ints, then xt [2][P][H] fp16, ygu [2][P][I] fp32, xd [P][I] fp16, yraw [P][H] fp32 (H = I = 0
+// from it. Layout: plan ints, then xt [2][P][H] fp16, ygu [2][P][I] fp16, xd [P][I] fp16, yraw [P][H] fp16 (H = I = 0
 // for the plan alone). Returns GFL_OK or the failure code (message set).
 static int grouped_workspace(gfl_ctx* c, hipStream_t st, int P, int M, int E, int H, int I, const char* who,
                              gfl::GPlan& gp, char*& b, size_t& b_int, size_t& b_xt, size_t& b_ygu, size_t& b_xd)
@@ -355,9 +355,9 @@ static int grouped_workspace(gfl_ctx* c, hipStream_t st, int P, int M, int E, in
     const size_t n_int = 4 + (size_t)E + (E + 1) + 7 * (size_t)P + (size_t)M + (size_t)P + (size_t)E + nch * (E + 1);
     b_int = align256(sizeof(int) * n_int);
     b_xt = align256(2 * 2 * (size_t)P * H);
-    b_ygu = align256(4 * 2 * (size_t)P * I);
+    b_ygu = align256(2 * 2 * (size_t)P * I);
     b_xd = align256(2 * (size_t)P * I);
-    const size_t b_yr = align256(4 * (size_t)P * H);
+    const size_t b_yr = align256(2 * (size_t)P * H);
     const size_t need = b_int + b_xt + b_ygu + b_xd + b_yr;
     if (need > c->gws_bytes)
     {
@@ -418,9 +418,9 @@ int gfl_grouped_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* se
     if (const int rc = grouped_workspace(c, st, P, M, E, H, I, "gfl_grouped_forward", gp, b, b_int, b_xt, b_ygu, b_xd))
         return rc;
     uint16_t* xt = reinterpret_cast<uint16_t*>(b + b_int);
-    float* ygu = reinterpret_cast<float*>(b + b_int + b_xt);
+    uint16_t* ygu = reinterpret_cast<uint16_t*>(b + b_int + b_xt);
     uint16_t* xd = reinterpret_cast<uint16_t*>(b + b_int + b_xt + b_ygu);
-    float* yraw = reinterpret_cast<float*>(b + b_int + b_xt + b_ygu + b_xd);
+    uint16_t* yraw = reinterpret_cast<uint16_t*>(b + b_int + b_xt + b_ygu + b_xd);
     const int r = staged(c, 2, st, [&] {
         return gfl::launch_grouped(L.dptrs, sel, w, w_is_half ? 1 : 0, P, topk, E, H, I, L.K[0], L.K[1], L.K[2], x, gp,
                                    P, xt, ygu, xd, yraw, c->silu_tab, act_limit, out, st);

@@ -276,14 +276,29 @@ __device__ __forceinline__ float h2f_lane(uint4 v, int k)
     return h2f_bits((uint16_t)(w >> (16 * (k & 1))));
 }
 
+// out_block (ft_core.h:105-110) after its leading r16: v = the lane's 8 fp16-valued inputs, sc its 8 fp16 scales
+__device__ inline void out_block_row_rounded(float (&v)[8], uint4 sc)
+{
+    const float sh = fwht128_row(v) * HADF;   // (sign * v) * HADF == v * (sign * HADF), bit for bit
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = r16(v[k] * sh * h2f_lane(sc, k));
+}
+
 // out_block (ft_core.h:105-110) on a 16-lane row: v = the lane's 8 fp32 outputs, sc its 8 fp16 scales
 __device__ inline void out_block_row(float (&v)[8], uint4 sc)
 {
 #pragma unroll
     for (int k = 0; k < 8; ++k) v[k] = r16(v[k]);
-    const float sh = fwht128_row(v) * HADF;   // (sign * v) * HADF == v * (sign * HADF), bit for bit
+    out_block_row_rounded(v, sc);
+}
+
+// out_block from outputs stored already rounded to fp16 (raw = the lane's 8 fp16 values): the same results as
+// out_block_row on the fp32 outputs, whose first step is that rounding
+__device__ inline void out_block_row_h(float (&v)[8], uint4 raw, uint4 sc)
+{
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = r16(v[k] * sh * h2f_lane(sc, k));
+    for (int k = 0; k < 8; ++k) v[k] = h2f_lane(raw, k);
+    out_block_row_rounded(v, sc);
 }
 
 // prep_block (ft_core.h:97-102) on a 16-lane row up to its last rounding: v holds the lane's 8 fp32 inputs and sc its

@@ -62,11 +62,13 @@ struct GPlan
 
 constexpr int GP_PLAN_CHUNK = 1024;   // picks per workgroup of the grouped plan
 
-// Prefill-sized layer forward with MFMA grouped GEMMs (k_prefill.hip): xt [2][cap][H] fp16, ygu [2][cap][I] fp32,
-// xd [cap][I] fp16, yraw [cap][H] fp32 workspace, cap >= P.
+// Prefill-sized layer forward with MFMA grouped GEMMs (k_prefill.hip): xt [2][cap][H] fp16, ygu [2][cap][I] fp16,
+// xd [cap][I] fp16, yraw [cap][H] fp16 workspace, cap >= P. The GEMM outputs ygu and yraw are stored rounded to fp16,
+// the first step of the out_block that reads them.
 int launch_grouped(const uint64_t* ptrs, const int64_t* sel, const void* w, int w_half, int P, int topk, int E, int H,
-                   int I, int Kg, int Ku, int Kd, const uint16_t* x, const GPlan& g, int cap, uint16_t* xt, float* ygu,
-                   uint16_t* xd, float* yraw, const float* silu_tab, float act_limit, float* out, hipStream_t st);
+                   int I, int Kg, int Ku, int Kd, const uint16_t* x, const GPlan& g, int cap, uint16_t* xt,
+                   uint16_t* ygu, uint16_t* xd, uint16_t* yraw, const float* silu_tab, float act_limit, float* out,
+                   hipStream_t st);
 size_t grouped_gemm_lds_bytes(int K);
 // The grouped plan alone (first three launches of launch_grouped): slots, offsets, job order per token.
 void launch_grouped_plan(const int64_t* sel, const void* w, int w_half, int P, int topk, int E, const GPlan& g,

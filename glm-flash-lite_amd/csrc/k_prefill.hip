@@ -321,7 +321,7 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_prep_kernel(const uint64_t* __r
 // fwd_phase phase 1 (ft_core.h:974-991), one wave per (slot, 4 * GP_TA blocks of I): per 128-block, out_block of
 // gate and up, r16(act_mul), down prep_block, stored in the GEMM input layout
 __global__ __launch_bounds__(GP_TW * 64) void gp_act_kernel(const uint64_t* __restrict__ ptrs, int I, int cap, GPlan g,
-                                                            const float* __restrict__ ygu, const float* silu_tab,
+                                                            const uint16_t* __restrict__ ygu, const float* silu_tab,
                                                             float act_limit, uint16_t* __restrict__ xd)
 {
     const int lane = threadIdx.x & 63, rl = lane >> 4, li = lane & 15;
@@ -333,25 +333,21 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_act_kernel(const uint64_t* __re
     const gptr<uint16_t> svh_g = gaddr<uint16_t>(ptrs[(size_t)e * 9 + 4]);
     const gptr<uint16_t> svh_u = gaddr<uint16_t>(ptrs[(size_t)e * 9 + 6]);
     const gptr<uint16_t> suh_d = gaddr<uint16_t>(ptrs[(size_t)e * 9 + 7]);
-    const float* yg = ygu + (size_t)s * I;
-    const float* yu = ygu + ((size_t)cap + s) * I;
+    const uint16_t* yg = ygu + (size_t)s * I;
+    const uint16_t* yu = ygu + ((size_t)cap + s) * I;
     uint16_t* dst = xd + (size_t)s * I;
     // GP_TA rounds of 4 blocks in three phases kept apart by scheduling barriers (left to itself the compiler sinks
     // each round's loads next to their use): all loads; the output transforms and every silu lookup; the
     // activation, input transform and stores
     {
         float gv[GP_TA][8], uv[GP_TA][8], ev[GP_TA][8];
-        uint4 sg[GP_TA], su[GP_TA], sd[GP_TA];
+        uint4 gh[GP_TA], uh[GP_TA], sg[GP_TA], su[GP_TA], sd[GP_TA];
 #pragma unroll
         for (int k = 0; k < GP_TA; ++k)
         {
             const int o = min(c0 + 4 * k + rl, nbi - 1) * 128 + li * 8;
-            const float4 ga = *reinterpret_cast<const float4*>(yg + o), gb = *reinterpret_cast<const float4*>(yg + o + 4);
-            const float4 ua = *reinterpret_cast<const float4*>(yu + o), ub = *reinterpret_cast<const float4*>(yu + o + 4);
-            gv[k][0] = ga.x; gv[k][1] = ga.y; gv[k][2] = ga.z; gv[k][3] = ga.w;
-            gv[k][4] = gb.x; gv[k][5] = gb.y; gv[k][6] = gb.z; gv[k][7] = gb.w;
-            uv[k][0] = ua.x; uv[k][1] = ua.y; uv[k][2] = ua.z; uv[k][3] = ua.w;
-            uv[k][4] = ub.x; uv[k][5] = ub.y; uv[k][6] = ub.z; uv[k][7] = ub.w;
+            gh[k] = *reinterpret_cast<const uint4*>(yg + o);
+            uh[k] = *reinterpret_cast<const uint4*>(yu + o);
             sg[k] = gld16(svh_g, o);
             su[k] = gld16(svh_u, o);
             sd[k] = gld16(suh_d, o);
@@ -360,8 +356,8 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_act_kernel(const uint64_t* __re
 #pragma unroll
         for (int k = 0; k < GP_TA; ++k)
         {
-            out_block_row(gv[k], sg[k]);
-            out_block_row(uv[k], su[k]);
+            out_block_row_h(gv[k], gh[k], sg[k]);
+            out_block_row_h(uv[k], uh[k], su[k]);
         }
 #pragma unroll
         for (int k = 0; k < GP_TA; ++k)
@@ -389,7 +385,7 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_act_kernel(const uint64_t* __re
 constexpr int GP_CK = 4;   // picks whose loads a combine wave keeps in flight
 
 __global__ __launch_bounds__(GP_TW * 64) void gp_comb_kernel(const uint64_t* __restrict__ ptrs, int H, int M, int topk,
-                                                             GPlan g, const float* __restrict__ yraw,
+                                                             GPlan g, const uint16_t* __restrict__ yraw,
                                                              float* __restrict__ out)
 {
     const int lane = threadIdx.x & 63, rl = lane >> 4, li = lane & 15;
@@ -413,7 +409,7 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_comb_kernel(const uint64_t* __r
     for (int j = 0; j < 8; ++j) acc[j] = 0.f;
     for (int k0 = 0; k0 < npk; k0 += GP_CK)
     {
-        float4 ya[GP_CK], yb[GP_CK];
+        uint4 yh[GP_CK];
         uint4 sv[GP_CK];
         float wk[GP_CK];
 #pragma unroll
@@ -424,17 +420,15 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_comb_kernel(const uint64_t* __r
             wk[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), k));
             const uint64_t pa = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(my_p >> 32), k) << 32) |
                                 (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)my_p, k);
-            const float* yr = yraw + (size_t)s * H + o;
-            ya[i] = *reinterpret_cast<const float4*>(yr);
-            yb[i] = *reinterpret_cast<const float4*>(yr + 4);
+            yh[i] = *reinterpret_cast<const uint4*>(yraw + (size_t)s * H + o);
             sv[i] = gld16(gaddr<uint16_t>(pa), o);
         }
 #pragma unroll
         for (int i = 0; i < GP_CK; ++i)
         {
             if (k0 + i >= npk) break;
-            float v[8] = { ya[i].x, ya[i].y, ya[i].z, ya[i].w, yb[i].x, yb[i].y, yb[i].z, yb[i].w };
-            out_block_row(v, sv[i]);
+            float v[8];
+            out_block_row_h(v, yh[i], sv[i]);
 #pragma unroll
             for (int j = 0; j < 8; ++j) acc[j] = acc[j] + wk[i] * v[j];
         }
@@ -480,7 +474,7 @@ struct GemmArgs
     int kdim, ndim, cap, E;
     GPlan g;
     const uint16_t* xin;       // [mats][cap][kdim] fp16, GEMM input layout
-    float* yout;               // [mats][cap][ndim] fp32
+    uint16_t* yout;            // [mats][cap][ndim] fp16: out_block's leading r16 (ft_core.h:109) applied here
 };
 
 // Grid: 8 * ceil(E / 8) * (ndim / 256) * matrices, XCD-major. Workgroup = 8 waves x 2 tile columns = 256 output columns of one matrix of one
@@ -534,7 +528,7 @@ __global__ __launch_bounds__(GP_NW * 64) void gp_gemm_kernel(GemmArgs a)
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(uniform_ptr(reinterpret_cast<const uint8_t*>(xin))), (short)0,
         (int)((size_t)a.cap * a.kdim * 2), 0x00020000);
-    float* yout = a.yout + (size_t)(mat - a.mat_base) * a.cap * a.ndim;
+    uint16_t* yout = a.yout + (size_t)(mat - a.mat_base) * a.cap * a.ndim;
     const int q = lane >> 4, i16 = lane & 15;
 
     for (int c0 = s_begin; c0 < s_end; c0 += GP_MT)
@@ -625,7 +619,8 @@ __global__ __launch_bounds__(GP_NW * 64) void gp_gemm_kernel(GemmArgs a)
                     for (int rr = 0; rr < 4; ++rr)
                     {
                         const int sl = mb * 16 + q * 4 + rr;
-                        if (sl < T) yout[(size_t)(c0 + sl) * a.ndim + (t0 + c) * 16 + i16] = acc[c][mb][rr];
+                        if (sl < T)
+                            yout[(size_t)(c0 + sl) * a.ndim + (t0 + c) * 16 + i16] = (uint16_t)f2h_bits(acc[c][mb][rr]);
                     }
         };
         static_assert(GP_MT == 80, "one case per row-block count");
@@ -689,8 +684,8 @@ void launch_grouped_plan(const int64_t* sel, const void* w, int w_half, int P, i
 }
 
 int launch_grouped(const uint64_t* ptrs, const int64_t* sel, const void* w, int w_half, int P, int topk, int E, int H,
-                   int I, int Kg, int Ku, int Kd, const uint16_t* x, const GPlan& g, int cap, uint16_t* xt, float* ygu,
-                   uint16_t* xd, float* yraw, const float* silu_tab, float act_limit, float* out, hipStream_t st)
+                   int I, int Kg, int Ku, int Kd, const uint16_t* x, const GPlan& g, int cap, uint16_t* xt, uint16_t* ygu,
+                   uint16_t* xd, uint16_t* yraw, const float* silu_tab, float act_limit, float* out, hipStream_t st)
 {
     const int M = P / topk;
     launch_grouped_plan(sel, w, w_half, P, topk, E, g, st);
