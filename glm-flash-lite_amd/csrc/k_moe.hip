@@ -443,7 +443,7 @@ __device__ __forceinline__ void chain_dma(const uint8_t* __restrict__ col_base, 
 // ---------------------------------------------------------------------------------------------------------------
 
 constexpr int GU_NW = 4;    // waves (tile columns) per gate|up workgroup: 64 outputs
-constexpr int GU_PR = 3;    // input-transform rounds (4 blocks per wave each) whose loads a gate|up wave keeps in flight
+constexpr int GU_PR = 3;    // input-transform rounds (4 blocks per wave each) a gate|up wave keeps loads in flight for
 constexpr int DN_NW = 8;    // waves per down workgroup: one 128-output block, out_block fused
 
 struct GuArgs
@@ -639,7 +639,8 @@ struct DnArgs
 // Grid: umax * H/128. Workgroup = 8 waves = one 128-output block of one routed expert, all its slots (with per_slot:
 // P * H/128, one slot each).
 template <int K, int NS>
-__global__ __launch_bounds__(DN_NW * 64) __attribute__((amdgpu_waves_per_eu(K == 5 || NS == 8 ? 3 : 4))) void down_kernel(DnArgs a)
+__global__ __launch_bounds__(DN_NW * 64) __attribute__((amdgpu_waves_per_eu(K == 5 || NS == 8 ? 3 : 4))) void
+down_kernel(DnArgs a)
 {
     constexpr int NW = DN_NW, TB = 32 * K;
     extern __shared__ __align__(16) uint8_t lds_raw[];

@@ -477,12 +477,12 @@ struct GemmArgs
     uint16_t* yout;            // [mats][cap][ndim] fp16: out_block's leading r16 (ft_core.h:109) applied here
 };
 
-// Grid: 8 * ceil(E / 8) * (ndim / 256) * matrices, XCD-major. Workgroup = 8 waves x 2 tile columns = 256 output columns of one matrix of one
-// expert; the expert's slots go through in passes of GP_MT. Per group of 8 tile rows every wave decodes its 16 tiles
-// and, per pair of tile rows, reads one A fragment (16 slots x 32 k) per row block of the pass and runs 2 MFMAs
-// (16x16x32) with it, one per column. The tiles stream through per-wave LDS rings and the slots' inputs through a shared ring, both filled by
-// LDS-direct loads GP_NG - 1 groups ahead; one workgroup barrier per group (group g landed for every wave; every wave
-// is past group g - 1, whose slots are refilled after it).
+// Grid: 8 * ceil(E / 8) * (ndim / 256) * matrices, XCD-major. Workgroup = 8 waves x 2 tile columns = 256 output
+// columns of one matrix of one expert; the expert's slots go through in passes of GP_MT. Per group of 8 tile rows every
+// wave decodes its 16 tiles and, per pair of tile rows, reads one A fragment (16 slots x 32 k) per row block of the
+// pass and runs 2 MFMAs (16x16x32) with it, one per column. The tiles stream through per-wave LDS rings and the slots'
+// inputs through a shared ring, both filled by LDS-direct loads GP_NG - 1 groups ahead; one workgroup barrier per group
+// (group g landed for every wave; every wave is past group g - 1, whose slots are refilled after it).
 template <int K>
 __global__ __launch_bounds__(GP_NW * 64) void gp_gemm_kernel(GemmArgs a)
 {
@@ -524,7 +524,8 @@ __global__ __launch_bounds__(GP_NW * 64) void gp_gemm_kernel(GemmArgs a)
     }
     const LaneDec d = lane_dec(lane, K);
     const uint16_t* xin = a.xin + (size_t)(mat - a.mat_base) * a.cap * a.kdim;
-    // the slots' inputs through a buffer resource too: per-lane offsets fixed for a pass, the group in the scalar offset
+    // the slots' inputs through a buffer resource too: the lane's 4 bytes as the vector offset, row and group in the
+    // scalar offset
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(uniform_ptr(reinterpret_cast<const uint8_t*>(xin))), (short)0,
         (int)((size_t)a.cap * a.kdim * 2), 0x00020000);
@@ -684,8 +685,9 @@ void launch_grouped_plan(const int64_t* sel, const void* w, int w_half, int P, i
 }
 
 int launch_grouped(const uint64_t* ptrs, const int64_t* sel, const void* w, int w_half, int P, int topk, int E, int H,
-                   int I, int Kg, int Ku, int Kd, const uint16_t* x, const GPlan& g, int cap, uint16_t* xt, uint16_t* ygu,
-                   uint16_t* xd, uint16_t* yraw, const float* silu_tab, float act_limit, float* out, hipStream_t st)
+                   int I, int Kg, int Ku, int Kd, const uint16_t* x, const GPlan& g, int cap, uint16_t* xt,
+                   uint16_t* ygu, uint16_t* xd, uint16_t* yraw, const float* silu_tab, float act_limit, float* out,
+                   hipStream_t st)
 {
     const int M = P / topk;
     launch_grouped_plan(sel, w, w_half, P, topk, E, g, st);

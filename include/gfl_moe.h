@@ -51,7 +51,8 @@ int gfl_ctx_create(int device, gfl_ctx** out);
 int gfl_ctx_destroy(gfl_ctx* ctx);
 
 /* Register layer `li`: E experts of a SwiGLU MLP, hidden H, intermediate I (multiples of 256); gate/up are [H->I],
- * down [I->H], each an EXL3 trellis of K bits per weight (k_gate/k_up/k_down in 2..5) in 16x16 tiles stored row-major [k/16][n/16].
+ * down [I->H], each an EXL3 trellis of K bits per weight (k_gate/k_up/k_down in 2..5) in 16x16 tiles stored
+ * row-major [k/16][n/16].
  * ptrs: HOST array [E][9] of DEVICE addresses per expert:
  *   trellis gate, up, down; suh_gate, svh_gate, suh_up, svh_up, suh_down, svh_down (fp16 sign/scale vectors).
  * Trellis addresses must be 4-byte aligned, suh/svh addresses 16-byte aligned (both hold for torch allocations).
@@ -71,13 +72,14 @@ int gfl_moe_forward(gfl_ctx* ctx, int li, const uint16_t* x, const int64_t* sel,
                     int topk, float* out, int mode, float act_limit, gfl_stream stream);
 
 /* Environment: GFL_SLOTS_PER_PASS = 1, 2, 4 or 8 forces the number of (token, expert) slots one GEMV pass of
- * gfl_moe_forward accumulates (default: 1 at M = 1, else 2; an expert with more slots takes more passes). Read once
- * by gfl_ctx_create. */
+ * gfl_moe_forward accumulates (default: 1 up to M = 8, with a workgroup per slot; else 2, with a workgroup per expert
+ * whose slots take passes). Read once by gfl_ctx_create. */
 
 /* Routed-expert forward of one layer for prefill-sized M (the north star's MFMA grouped GEMM), same arguments and
  * result layout as gfl_moe_forward: x fp16 [M, H], sel int64 [M, topk] (ids outside [0, E) skipped), w fp16 or fp32
- * [M, topk], out fp32 [M, H]; M*topk <= 65536; x and out 16-byte aligned. Rows are grouped expert-major (tier_lut_build_grouped_rows,
- * kernels/cpu_avx2/ft_tier_ext.cpp:1047-1097), gate|up and down run as v_mfma_f32_16x16x32_f16 grouped GEMMs on the
+ * [M, topk], out fp32 [M, H]; M*topk <= 65536; x and out 16-byte aligned. Rows are grouped expert-major
+ * (tier_lut_build_grouped_rows, kernels/cpu_avx2/ft_tier_ext.cpp:1047-1097), gate|up and down run as
+ * v_mfma_f32_16x16x32_f16 grouped GEMMs on the
  * bit-exact dequantized fp16 weights, the transforms keep the reference's fp16 rounding points and the combine its job
  * order (kernels/cpu_avx2/ft_core.h:933-1033). The hidden-dimension sums are formed in MFMA order, so results differ
  * from the EXACT mode of gfl_moe_forward by fp32 accumulation rounding (as the reference's own fp64 expert,
