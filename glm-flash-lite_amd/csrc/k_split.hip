@@ -265,6 +265,8 @@ __device__ __forceinline__ void route_argmax_step(float& bv, int& bi)
 constexpr int ROUTE_WAVES = 4;
 constexpr int ROUTE_MAXE = 1024;   // experts per token: up to 16 per lane
 
+// NI = ceil(E / 64) scores per lane, a compile-time count so that the per-lane loops hold only live experts
+template <int NI>
 __global__ __launch_bounds__(ROUTE_WAVES * 64) void route_kernel(const float* __restrict__ logits, int M, int E, int topk,
                                                                  int64_t* __restrict__ sel, uint16_t* __restrict__ w)
 {
@@ -273,19 +275,14 @@ __global__ __launch_bounds__(ROUTE_WAVES * 64) void route_kernel(const float* __
     if (m >= M) return;
     const float* lg = logits + (size_t)m * E;
     // every load first (uniform guards, clamped addresses), so the token's logits arrive in one round trip
-    float sc[ROUTE_MAXE / 64];
+    float sc[NI];
 #pragma unroll
-    for (int i = 0; i < ROUTE_MAXE / 64; ++i)
-        if (64 * i < E) sc[i] = lg[min(lane + 64 * i, E - 1)];
+    for (int i = 0; i < NI; ++i) sc[i] = lg[min(lane + 64 * i, E - 1)];
 #pragma unroll
-    for (int i = 0; i < ROUTE_MAXE / 64; ++i)
+    for (int i = 0; i < NI; ++i)
     {
-        if (64 * i < E)
-        {
-            const float ex = (float)exp(-(double)sc[i]);
-            sc[i] = lane + 64 * i < E ? 1.0f / (1.0f + ex) : -INFINITY;
-        }
-        else sc[i] = -INFINITY;
+        const float ex = (float)exp(-(double)sc[i]);
+        sc[i] = lane + 64 * i < E ? 1.0f / (1.0f + ex) : -INFINITY;
     }
     uint32_t used = 0;
     float tot = 0.0f, mine = 0.0f;
@@ -296,7 +293,7 @@ __global__ __launch_bounds__(ROUTE_WAVES * 64) void route_kernel(const float* __
         float bv = -INFINITY;
         int bi = 0x7fffffff;
 #pragma unroll
-        for (int i = 0; i < ROUTE_MAXE / 64; ++i)
+        for (int i = 0; i < NI; ++i)
         {
             const int e = lane + 64 * i;
             if (e < E && !((used >> i) & 1) && (sc[i] > bv || bi == 0x7fffffff))
@@ -330,9 +327,17 @@ __global__ __launch_bounds__(ROUTE_WAVES * 64) void route_kernel(const float* __
 int launch_route(const float* logits, int M, int E, int topk, int64_t* sel, uint16_t* w, hipStream_t st)
 {
     if (E < 1 || E > ROUTE_MAXE || topk < 1 || topk > E || topk > 64) return -1;
-    hipLaunchKernelGGL(route_kernel, dim3((M + ROUTE_WAVES - 1) / ROUTE_WAVES), dim3(ROUTE_WAVES * 64), 0, st, logits,
-                       M, E, topk, sel, w);
-    return 0;
+    const dim3 grid((M + ROUTE_WAVES - 1) / ROUTE_WAVES), block(ROUTE_WAVES * 64);
+    switch ((E + 63) / 64)
+    {
+#define GFL_ROUTE_CASE(N)                                                                                          \
+    case N: hipLaunchKernelGGL(route_kernel<N>, grid, block, 0, st, logits, M, E, topk, sel, w); return 0;
+        GFL_ROUTE_CASE(1) GFL_ROUTE_CASE(2) GFL_ROUTE_CASE(3) GFL_ROUTE_CASE(4) GFL_ROUTE_CASE(5) GFL_ROUTE_CASE(6)
+        GFL_ROUTE_CASE(7) GFL_ROUTE_CASE(8) GFL_ROUTE_CASE(9) GFL_ROUTE_CASE(10) GFL_ROUTE_CASE(11) GFL_ROUTE_CASE(12)
+        GFL_ROUTE_CASE(13) GFL_ROUTE_CASE(14) GFL_ROUTE_CASE(15) GFL_ROUTE_CASE(16)
+#undef GFL_ROUTE_CASE
+        default: return -1;
+    }
 }
 
 // splitmix64 in counter form: output i of the sequence seeded with `seed` is mix(seed + (i+1) * golden)
@@ -370,7 +375,7 @@ void launch_combine(void* out, int is_half, int n, const int64_t* dflag, const i
                     int64_t* stats, int64_t timeout_ns, hipStream_t st)
 {
     int dev = 0, khz = 100000;
-    hipGetDevice(&dev);
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
     if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || khz <= 0) khz = 100000;
     const int64_t ticks = (int64_t)((double)timeout_ns * (double)khz / 1e6);
     const int64_t ns_per_tick_q16 = (int64_t)(65536.0 * 1e6 / (double)khz);
