@@ -322,9 +322,13 @@ __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_b
 // before it, since the compiler does not count the LDS-direct loads and waits with vmcnt(0)).
 constexpr int NGRP = 4;
 
+// bytes per transformed input element in LDS: fp32 with one slot per pass, so that the chain FMAs take fp32 operands,
+// else fp16 (eight 5120-wide fp32 inputs would not fit beside the rings)
+constexpr int x_lds_elem(int ns) { return ns <= 1 ? 4 : 2; }
+
 // One tile column of one matrix over all TK tile rows for up to NS slots whose transformed inputs sit in lds_x
-// ([ns][kdim] fp16 in the permuted [tk][j][q] order). Lane (j = l/16, n = l%16) carries the reference's accumulator j
-// of output column n.
+// ([ns][kdim] in the permuted [tk][j][q] order; fp32 when XF, else fp16 - the values are fp16 either way). Lane
+// (j = l/16, n = l%16) carries the reference's accumulator j of output column n.
 //
 // Each wave streams its own column through a private LDS ring of NG groups of 8 tiles with LDS-direct buffer loads
 // (global -> LDS without registers): a group of 8 tiles is 256*K bytes = K dword loads of the 64 lanes, lane l of load
@@ -346,9 +350,9 @@ __device__ __forceinline__ void wait_vmcnt()
 // pre_load() runs before the first NG - 1 groups are requested, pre() after them and before the first is read: the
 // caller issues its input loads in pre_load (so waiting for them does not wait for the trellis groups queued behind)
 // and fills lds_x in pre (ending with a workgroup barrier), so the input transform overlaps the trellis fetch.
-template <int K, int NS, int NG, class PreLoad, class Pre>
+template <int K, int NS, int NG, bool XF, class PreLoad, class Pre>
 __device__ __forceinline__ void chain_dma(const uint8_t* __restrict__ col_base, size_t gstride, int TK, int ns,
-                                          const uint16_t* lds_x, uint8_t* ring, float (&res)[NS], PreLoad&& pre_load,
+                                          const void* lds_x, uint8_t* ring, float (&res)[NS], PreLoad&& pre_load,
                                           Pre&& pre)
 {
     constexpr int TB = 32 * K, GB = 8 * TB;
@@ -385,7 +389,8 @@ __device__ __forceinline__ void chain_dma(const uint8_t* __restrict__ col_base, 
     float acc[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) acc[s] = 0.f;
-    const uint16_t* xl = lds_x + j * 4;
+    const uint16_t* xl = static_cast<const uint16_t*>(lds_x) + j * 4;
+    const float* xlf = static_cast<const float*>(lds_x) + j * 4;
     for (int g = 0; g < ngroups; ++g)
     {
         if (g + NG - 1 < ngroups)
@@ -415,15 +420,34 @@ __device__ __forceinline__ void chain_dma(const uint8_t* __restrict__ col_base, 
                 if (s == 0 || s < ns)
                 {
                     float a = acc[s];
+                    float4v xf[8];
+                    if constexpr (XF)
+                    {
+                        // fp32 operands: the FMAs are v_fmac_f32, which issue at twice the rate of the
+                        // mixed-precision v_fma_mix_f32 an fp16 operand needs; the 8 reads go out together
+#pragma unroll
+                        for (int rr = 0; rr < 8; ++rr)
+                            xf[rr] = *reinterpret_cast<const float4v*>(xlf + ((size_t)s * TK + g * 8 + h + rr) * 16);
+                    }
 #pragma unroll
                     for (int rr = 0; rr < 8; ++rr)
                     {
                         const int tk = g * 8 + h + rr;
-                        const half4 xv = *reinterpret_cast<const half4*>(xl + ((size_t)s * TK + tk) * 16);
-                        a = __builtin_fmaf(cw[rr][0], (float)xv[0], a);
-                        a = __builtin_fmaf(cw[rr][1], (float)xv[1], a);
-                        a = __builtin_fmaf(cw[rr][2], (float)xv[2], a);
-                        a = __builtin_fmaf(cw[rr][3], (float)xv[3], a);
+                        if constexpr (XF)
+                        {
+                            a = __builtin_fmaf(cw[rr][0], xf[rr][0], a);
+                            a = __builtin_fmaf(cw[rr][1], xf[rr][1], a);
+                            a = __builtin_fmaf(cw[rr][2], xf[rr][2], a);
+                            a = __builtin_fmaf(cw[rr][3], xf[rr][3], a);
+                        }
+                        else
+                        {
+                            const half4 xv = *reinterpret_cast<const half4*>(xl + ((size_t)s * TK + tk) * 16);
+                            a = __builtin_fmaf(cw[rr][0], (float)xv[0], a);
+                            a = __builtin_fmaf(cw[rr][1], (float)xv[1], a);
+                            a = __builtin_fmaf(cw[rr][2], (float)xv[2], a);
+                            a = __builtin_fmaf(cw[rr][3], (float)xv[3], a);
+                        }
                     }
                     acc[s] = a;
                 }
@@ -504,8 +528,11 @@ __device__ void act_block(const GuArgs& a, int e, int s_begin, int s_end, int b)
 // slots; the last workgroup of row 0 publishes the plan. With per_slot the grid is (P * I/64 + 1, nmat) and a
 // workgroup takes one slot: an expert picked by several tokens is streamed once per slot, in parallel, instead of in
 // passes one after another.
+// Occupancy hint: 3 waves per SIMD with one slot per pass (its batched fp32 input reads need up to 168 VGPRs; at 128
+// the compiler spills), else 4.
 template <int K, int NS>
-__global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(K == 5 ? 3 : 4))) void gu_kernel(GuArgs a)
+__global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(K == 5 || NS == 1 ? 3 : 4))) void
+gu_kernel(GuArgs a)
 {
     constexpr int NW = GU_NW, TB = 32 * K;
     extern __shared__ __align__(16) uint8_t lds_raw[];
@@ -513,8 +540,9 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(K ==
     __shared__ int s_last;
     constexpr int RB = NGRP * 8 * TB;                                                 // ring bytes per wave
     uint8_t* rings = lds_raw;                                                         // [NW][RB]
-    uint16_t* lds_x = reinterpret_cast<uint16_t*>(lds_raw + NW * RB);                // [ns_cap][H] fp16 permuted
-    int* plan_mem = reinterpret_cast<int*>(lds_raw + NW * RB + (size_t)a.ns_cap * a.H * 2);
+    constexpr bool XF = x_lds_elem(NS) == 4;
+    void* lds_x = lds_raw + NW * RB;                                                  // [ns_cap][H] permuted
+    int* plan_mem = reinterpret_cast<int*>(lds_raw + NW * RB + (size_t)a.ns_cap * a.H * x_lds_elem(NS));
     const LPlan L = lplan_carve(plan_mem, a.P, a.E);
     if (a.P <= 64) build_plan_wave(a.sel, a.P, a.E, L, hdr);
     else build_plan(a.sel, a.P, a.E, L, hdr);
@@ -566,18 +594,35 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(K ==
             {
                 // elements 8li..8li+7 of block b: tile row li/2, accumulators j0 = 2(li&1) and j0 + 1, q = k/2
                 const int s = it / nblk, b = it % nblk, tk = b * 8 + (li >> 1), j0 = 2 * (li & 1);
-                uint16_t* dst = lds_x + (size_t)s * a.H + (tk * 4 + j0) * 4;
-                uint2 e0, e1;
-                e0.x = f2h2_bits(v[0], v[2]);
-                e0.y = f2h2_bits(v[4], v[6]);
-                e1.x = f2h2_bits(v[1], v[3]);
-                e1.y = f2h2_bits(v[5], v[7]);
-                *reinterpret_cast<uint2*>(dst) = e0;
-                *reinterpret_cast<uint2*>(dst + 4) = e1;
+                const size_t pos = (size_t)s * a.H + (tk * 4 + j0) * 4;
+                if constexpr (XF)
+                {
+                    float* dst = static_cast<float*>(lds_x) + pos;
+                    float4v e0, e1;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                    {
+                        e0[q] = h2f_bits((uint16_t)f2h_bits(v[2 * q]));
+                        e1[q] = h2f_bits((uint16_t)f2h_bits(v[2 * q + 1]));
+                    }
+                    *reinterpret_cast<float4v*>(dst) = e0;
+                    *reinterpret_cast<float4v*>(dst + 4) = e1;
+                }
+                else
+                {
+                    uint16_t* dst = static_cast<uint16_t*>(lds_x) + pos;
+                    uint2 e0, e1;
+                    e0.x = f2h2_bits(v[0], v[2]);
+                    e0.y = f2h2_bits(v[4], v[6]);
+                    e1.x = f2h2_bits(v[1], v[3]);
+                    e1.y = f2h2_bits(v[5], v[7]);
+                    *reinterpret_cast<uint2*>(dst) = e0;
+                    *reinterpret_cast<uint2*>(dst + 4) = e1;
+                }
             }
         };
         const int nr = (nit + 4 * NW - 1) / (4 * NW);   // rounds of 4 * NW items
-        chain_dma<K, NS, NGRP>(col, gstride, TK, ns, lds_x, rings + wid * RB, res, [&] {
+        chain_dma<K, NS, NGRP, XF>(col, gstride, TK, ns, lds_x, rings + wid * RB, res, [&] {
 #pragma unroll
             for (int k = 0; k < GU_PR; ++k)
                 if (k < nr) load_round(k, k);
@@ -649,8 +694,9 @@ down_kernel(DnArgs a)
     __shared__ float c_w[NS][MAX_TOPK];
     constexpr int RB = NGRP * 8 * TB;                                                  // ring bytes per wave
     uint8_t* rings = lds_raw;                                                          // [NW][RB]
-    uint16_t* lds_x = reinterpret_cast<uint16_t*>(lds_raw + NW * RB);                 // [ns_cap][I]
-    float* lds_y = reinterpret_cast<float*>(lds_raw + NW * RB + (size_t)a.ns_cap * a.I * 2);   // [ns_cap][128]
+    constexpr bool XF = x_lds_elem(NS) == 4;
+    void* lds_x = lds_raw + NW * RB;                                                   // [ns_cap][I]
+    float* lds_y = reinterpret_cast<float*>(lds_raw + NW * RB + (size_t)a.ns_cap * a.I * x_lds_elem(NS));   // [ns][128]
     const int TN = a.H / 16, TK = a.I / 16, ncb = TN / NW;
     const int u = blockIdx.x / ncb, blk = blockIdx.x % ncb;   // union entry, or slot with per_slot
     // one round of independent loads: the union size (slot count), this entry's slot range and its expert's
@@ -688,16 +734,36 @@ down_kernel(DnArgs a)
         // trellis groups are requested
         const int nvec = ns * a.I / 8;
         const uint4* xsrc = reinterpret_cast<const uint4*>(a.xtd + (size_t)c0 * a.I);
-        uint4* xdst = reinterpret_cast<uint4*>(lds_x);
+        // 8 fp16 values -> LDS element 8i.. (widened to fp32 when XF)
+        auto put = [&](int i, const uint4& v) {
+            if constexpr (XF)
+            {
+                const uint32_t w[4] = { v.x, v.y, v.z, v.w };
+                float4v f0, f1;
+#pragma unroll
+                for (int q = 0; q < 2; ++q)
+                {
+                    f0[2 * q] = h2f_bits((uint16_t)w[q]);
+                    f0[2 * q + 1] = h2f_bits((uint16_t)(w[q] >> 16));
+                    f1[2 * q] = h2f_bits((uint16_t)w[q + 2]);
+                    f1[2 * q + 1] = h2f_bits((uint16_t)(w[q + 2] >> 16));
+                }
+                float4v* d = reinterpret_cast<float4v*>(lds_x) + 2 * i;
+                d[0] = f0;
+                d[1] = f1;
+            }
+            else
+                reinterpret_cast<uint4*>(lds_x)[i] = v;
+        };
         const int i0 = threadIdx.x, i1 = threadIdx.x + DN_NW * 64;
         uint4 xc0 = {}, xc1 = {};
-        chain_dma<K, NS, NGRP>(col, gstride, TK, ns, lds_x, rings + wid * RB, res, [&] {
+        chain_dma<K, NS, NGRP, XF>(col, gstride, TK, ns, lds_x, rings + wid * RB, res, [&] {
             if (i0 < nvec) xc0 = xsrc[i0];
             if (i1 < nvec) xc1 = xsrc[i1];
         }, [&] {
-            if (i0 < nvec) xdst[i0] = xc0;
-            if (i1 < nvec) xdst[i1] = xc1;
-            for (int i = threadIdx.x + 2 * DN_NW * 64; i < nvec; i += DN_NW * 64) xdst[i] = xsrc[i];
+            if (i0 < nvec) put(i0, xc0);
+            if (i1 < nvec) put(i1, xc1);
+            for (int i = threadIdx.x + 2 * DN_NW * 64; i < nvec; i += DN_NW * 64) put(i, xsrc[i]);
             lds_barrier();   // lds_x complete
         });
 #pragma unroll
@@ -808,13 +874,13 @@ static bool open_lds(F kern)
 template <int K>
 static size_t gu_lds(int ns, int H, int P, int E)
 {
-    return (size_t)GU_NW * NGRP * 8 * 32 * K + (size_t)ns * H * 2 + lplan_ints(P, E) * 4;
+    return (size_t)GU_NW * NGRP * 8 * 32 * K + (size_t)ns * H * x_lds_elem(ns) + lplan_ints(P, E) * 4;
 }
 
 template <int K>
 static size_t dn_lds(int ns, int I)
 {
-    return (size_t)DN_NW * NGRP * 8 * 32 * K + (size_t)ns * I * 2 + (size_t)ns * 128 * 4;
+    return (size_t)DN_NW * NGRP * 8 * 32 * K + (size_t)ns * I * x_lds_elem(ns) + (size_t)ns * 128 * 4;
 }
 
 template <int K, int NS>
