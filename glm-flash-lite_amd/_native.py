@@ -17,7 +17,7 @@ SYMBOLS = ("gfl_last_error", "gfl_version", "gfl_ctx_create", "gfl_ctx_destroy",
            "gfl_stats", "gfl_profile_enable", "gfl_profile_read", "gfl_exp_table", "gfl_silu_table",
            "gfl_grouped_plan")
 
-MODE_AUTO, MODE_AFFINE, MODE_EXACT, MODE_I16 = -1, 0, 1, 2
+MODE_AUTO, MODE_AFFINE, MODE_EXACT, MODE_I16, MODE_MFMA = -1, 0, 1, 2, 3
 
 
 class NativeUnavailable(RuntimeError):

@@ -296,8 +296,8 @@ int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, c
     if (!c || !x || !sel || !w || !out) return fail(GFL_EINVAL, "gfl_moe_forward: NULL argument");
     if (li < 0 || li >= (int)c->layers.size() || !c->layers[li].dptrs)
         return fail(GFL_EINVAL, "gfl_moe_forward: layer not registered");
-    if (mode != GFL_MODE_AUTO && mode != GFL_MODE_EXACT)
-        return fail(GFL_EINVAL, "gfl_moe_forward: the device path computes EXACT (mode 1 or -1)");
+    if (mode != GFL_MODE_AUTO && mode != GFL_MODE_EXACT && mode != GFL_MODE_MFMA)
+        return fail(GFL_EINVAL, "gfl_moe_forward: the device path computes EXACT (mode 1 or -1) or MFMA (mode 3)");
     if (M < 1 || topk < 1 || topk > gfl::MAX_TOPK || (int64_t)M * topk > gfl::MAX_PICKS)
         return fail(GFL_EINVAL, "gfl_moe_forward: need 1 <= topk <= 16 and M*topk <= 1024");
     if (!std::isfinite(act_limit) || act_limit < 0) return fail(GFL_EINVAL, "gfl_moe_forward: act_limit must be >= 0");
@@ -316,27 +316,32 @@ int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, c
     // Zipf, top-8 of 288): per slot is 5-15% faster at M = 2..4; two slots per pass are 4% faster at M = 16, 8% at
     // M = 32 and 16% at M = 64 (there the extra weight streams of per slot cost more than its smaller LDS footprint
     // gains). Four slots per pass match two at M = 64 and lose elsewhere; eight lose everywhere.
-    int ns = M <= 8 ? 1 : 2;
-    if (c->ns_override > 0) ns = std::min(c->ns_override, M);
-    if (gfl::gate_up_lds_bytes(L.K[0], ns, L.H, P, L.E) > gfl::LDS_LIMIT ||
-        gfl::gate_up_lds_bytes(L.K[1], ns, L.H, P, L.E) > gfl::LDS_LIMIT
-        || gfl::down_lds_bytes(L.K[2], ns, L.I) > gfl::LDS_LIMIT)
+    //
+    // Mode MFMA accumulates the GEMVs with MFMAs (same weights, transforms and rounding points; sums over the hidden
+    // dimension in MFMA order) with a workgroup per union entry taking up to 4 of its slots per pass: an expert's
+    // tiles are decoded once for all its tokens of the pass.
+    const int mf = mode == GFL_MODE_MFMA ? 1 : 0;
+    int ns = mf ? std::min(M, 4) : M <= 8 ? 1 : 2;
+    if (c->ns_override > 0) ns = std::min(c->ns_override, mf ? std::min(M, 16) : M);
+    if (gfl::gate_up_lds_bytes(L.K[0], ns, L.H, P, L.E, mf) > gfl::LDS_LIMIT ||
+        gfl::gate_up_lds_bytes(L.K[1], ns, L.H, P, L.E, mf) > gfl::LDS_LIMIT
+        || gfl::down_lds_bytes(L.K[2], ns, L.I, mf) > gfl::LDS_LIMIT)
         return fail(GFL_EINVAL, "gfl_moe_forward: shape needs more than 160 KB of LDS per workgroup");
     const int wh = w_is_half ? 1 : 0;
     int r = staged(c, 1, st, [&] {
         if (L.K[0] == L.K[1])
             return gfl::launch_gate_up(L.K[0], ns, L.dptrs, 0, 2, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                       ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, st);
+                                       ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, st);
         if (gfl::launch_gate_up(L.K[0], ns, L.dptrs, 0, 1, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, st))
+                                ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, st))
             return -1;
         return gfl::launch_gate_up(L.K[1], ns, L.dptrs, 1, 1, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                   ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, st);
+                                   ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, st);
     });
     if (!r)
         r = staged(c, 3, st, [&] {
             return gfl::launch_down(L.K[2], ns, L.dptrs, topk, L.H, L.I, umax, P, ws.pv, ws.xtd, ws.yd, ws.out_cnt,
-                                    out, st);
+                                    out, mf, st);
         });
     if (r) return r > 0 ? r : fail(GFL_EINVAL, "gfl_moe_forward: unsupported K");
     GFL_HIP(hipGetLastError());

@@ -191,6 +191,25 @@ __device__ inline void fwht128(float& v0, float& v1)
     v1 = a - c;
 }
 
+// Element r (0..127) of a 128-block (= one group of 8 tile rows) -> its position in the GEMM input layout
+// [block][q][tile row][jj]: row rho = r % 16 of tile row r / 16 is MFMA k-slot jj = (rho&1) + 2*(rho>>3) of lane group
+// q = (rho&7)>>1, so the 4 k-slots of two consecutive tile rows of one q are 8 contiguous fp16.
+__device__ inline int gp_perm_pos(int b, int r)
+{
+    const int tr = r >> 4, rho = r & 15;
+    const int jj = (rho & 1) + 2 * (rho >> 3), q = (rho & 7) >> 1;
+    return b * 128 + q * 32 + tr * 4 + jj;
+}
+
+// Elements 8li..8li+7 of block b in the GEMM input layout gp_perm_pos: pairs (2q, 2q + 1) are adjacent, at
+// b * 128 + q * 32 + (li >> 1) * 4 + 2 * (li & 1)
+__device__ __forceinline__ void gp_store_row(uint16_t* dst, int b, int li, const uint32_t (&o)[4])
+{
+    uint16_t* d0 = dst + b * 128 + (li >> 1) * 4 + 2 * (li & 1);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) *reinterpret_cast<uint32_t*>(d0 + q * 32) = o[q];
+}
+
 __device__ inline float h2f_bits(uint16_t h) { __half x; __builtin_memcpy(&x, &h, 2); return __half2float(x); }
 
 // Hadamard-128 on one 16-lane row of the wave, 8 elements per lane: lane i of the row holds elements 8i..8i+7.

@@ -30,16 +30,18 @@ struct PlanView
 };
 
 // gate|up launch: routing plan (published to pv by workgroup 0), gate and/or up GEMV, SwiGLU per 128-block by the
-// last workgroup of the block. mat_base/nmat: matrices of this launch (0,2 = both, 0,1 = gate, 1,1 = up).
+// last workgroup of the block. mat_base/nmat: matrices of this launch (0,2 = both, 0,1 = gate, 1,1 = up). mf = 1:
+// MFMA-accumulate GEMV (mode GFL_MODE_MFMA), ns = slots per pass (<= 16); mf = 0: EXACT chain order.
 int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, const int64_t* sel, const void* w,
                    int w_half, int P, int topk, int E, int H, int I, int umax, const uint16_t* x, float* ygu,
                    uint16_t* xtd, int* act_cnt, const float* silu_tab, float act_limit, const PlanView& pv, float* out,
-                   hipStream_t st);
-// down launch: down GEMV + out_block, weighted combine per (token, 128-block) by the token's last expert
+                   int mf, hipStream_t st);
+// down launch: down GEMV + out_block, weighted combine per (token, 128-block) by the token's last expert; mf and ns
+// as for launch_gate_up (the same values for both launches of a call)
 int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int umax, int P, const PlanView& pv,
-                const uint16_t* xtd, float* yd, int* out_cnt, float* out, hipStream_t st);
-size_t gate_up_lds_bytes(int K, int ns, int H, int P, int E);
-size_t down_lds_bytes(int K, int ns, int I);
+                const uint16_t* xtd, float* yd, int* out_cnt, float* out, int mf, hipStream_t st);
+size_t gate_up_lds_bytes(int K, int ns, int H, int P, int E, int mf);
+size_t down_lds_bytes(int K, int ns, int I, int mf);
 int launch_dequant(const uint8_t* tr, int k, int n, int K, uint16_t* W, hipStream_t st);
 
 // Grouped-rows plan of the prefill path (device arrays; P picks, E experts, M tokens).

@@ -462,6 +462,80 @@ __device__ __forceinline__ void chain_dma(const uint8_t* __restrict__ col_base, 
     }
 }
 
+// MFMA-accumulate form of the column GEMV (mode GFL_MODE_MFMA): tile groups [g0, g1) of one tile column for up to 16
+// slots whose transformed inputs sit in lds_x as fp16 in the MFMA input layout (gp_perm_pos, xs elements per slot).
+// Each pair of tile rows is one v_mfma_f32_16x16x32_f16 whose B slice is the decoded weights as decode4 leaves them
+// (lane 16q + n: column n, rows 2q + {0, 1, 8, 9} of both tiles) and whose A row m is slot m (rows >= ns read slot 0;
+// their sums are not used). Returns D: lane l holds slot 4(l/16) + i, column l % 16, in element i. The weights and
+// every transform are the reference's; only the sums over the hidden dimension are formed in MFMA order instead of
+// the EXACT chain order. Streaming is chain_dma's: a private LDS ring of NG groups per wave, NG - 1 in flight.
+template <int K, int NG, class PreLoad, class Pre>
+__device__ __forceinline__ float4v chain_mf(const uint8_t* __restrict__ col_base, size_t gstride, int TK, int g0,
+                                            int g1, const uint16_t* lds_x, int xs, int ns, uint8_t* ring,
+                                            PreLoad&& pre_load, Pre&& pre)
+{
+    constexpr int TB = 32 * K, GB = 8 * TB;
+    const int lane = threadIdx.x & 63;
+    const LaneDec d = lane_dec(lane, K);
+    const int q = lane >> 4, i16 = lane & 15;
+    uint8_t* cb = const_cast<uint8_t*>(uniform_ptr(col_base));
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(cb, (short)0, (int)((size_t)TK * gstride),
+                                                                        0x00020000);
+    const int gs = (int)gstride;
+    int voff[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i)
+    {
+        const int byte = i * 256 + lane * 4;
+        voff[i] = (byte / TB) * gs + (byte % TB);
+    }
+    const int ng = g1 - g0;
+    auto issue = [&](int gi) {
+        uint8_t* dst = ring + (gi % NG) * GB;
+#pragma unroll
+        for (int i = 0; i < K; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(dst + i * 256), 4, voff[i], (g0 + gi) * 8 * gs, 0,
+                                                     0);
+    };
+    pre_load();
+#pragma unroll
+    for (int gi = 0; gi < NG - 1; ++gi)
+        if (gi < ng) issue(gi);
+    pre();
+    float4v acc = { 0.f, 0.f, 0.f, 0.f };
+    const uint16_t* xa = lds_x + (size_t)(i16 < ns ? i16 : 0) * xs + q * 32;
+    for (int gi = 0; gi < ng; ++gi)
+    {
+        if (gi + NG - 1 < ng)
+        {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // reads of the slot being refilled are done
+            issue(gi + NG - 1);
+            wait_vmcnt<(NG - 1) * K>();                           // group gi has landed
+        }
+        else
+            wait_vmcnt<0>();
+        const uint8_t* sl = ring + (gi % NG) * GB;
+        const uint16_t* xg = xa + (size_t)(g0 + gi) * 128;   // the group's 8 tile rows are 128-block g0 + gi
+        uint32_t wd[8][2];
+#pragma unroll
+        for (int rr = 0; rr < 8; ++rr)
+        {
+            wd[rr][0] = *reinterpret_cast<const uint32_t*>(sl + rr * TB + d.o0);
+            wd[rr][1] = *reinterpret_cast<const uint32_t*>(sl + rr * TB + d.o1);
+        }
+#pragma unroll
+        for (int rp = 0; rp < 4; ++rp)
+        {
+            const half8 A = *reinterpret_cast<const half8*>(xg + rp * 8);
+            const half4 B0 = decode4<K>(wd[2 * rp][0], wd[2 * rp][1], d.sh);
+            const half4 B1 = decode4<K>(wd[2 * rp + 1][0], wd[2 * rp + 1][1], d.sh);
+            const half8 B = { B0[0], B0[1], B0[2], B0[3], B1[0], B1[1], B1[2], B1[3] };
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, acc, 0, 0, 0);
+        }
+    }
+    return acc;
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // gate|up launch
 // ---------------------------------------------------------------------------------------------------------------
@@ -488,6 +562,7 @@ struct GuArgs
     int nmat_total;            // gate|up workgroups covering one 128-block
     int ns_cap;                // slots per pass the LDS allocation holds (<= NS)
     int per_slot;              // workgroups per slot (one pass each) instead of per union entry (NS == 1 only)
+    int mf;                    // MFMA-accumulate mode: down inputs written in the MFMA input layout
 };
 
 __device__ __forceinline__ float ld_agent(const float* p)
@@ -519,8 +594,8 @@ __device__ void act_block(const GuArgs& a, int e, int s_begin, int s_end, int b)
         float a0 = r16(act_mul(g0, u0, a.act_limit, a.silu_tab)), a1 = r16(act_mul(g1, u1, a.act_limit, a.silu_tab));
         prep_block_wave(a0, a1, h2f_bits(suh_d[b * 128 + lane]), h2f_bits(suh_d[b * 128 + lane + 64]));
         uint16_t* dst = a.xtd + (size_t)s * a.I;
-        dst[perm_pos(b, lane)] = (uint16_t)f2h_bits(a0);
-        dst[perm_pos(b, lane + 64)] = (uint16_t)f2h_bits(a1);
+        dst[a.mf ? gp_perm_pos(b, lane) : perm_pos(b, lane)] = (uint16_t)f2h_bits(a0);
+        dst[a.mf ? gp_perm_pos(b, lane + 64) : perm_pos(b, lane + 64)] = (uint16_t)f2h_bits(a1);
     }
 }
 
@@ -528,25 +603,29 @@ __device__ void act_block(const GuArgs& a, int e, int s_begin, int s_end, int b)
 // slots; the last workgroup of row 0 publishes the plan. With per_slot the grid is (P * I/64 + 1, nmat) and a
 // workgroup takes one slot: an expert picked by several tokens is streamed once per slot, in parallel, instead of in
 // passes one after another.
-// Occupancy hint: 3 waves per SIMD with one slot per pass (its batched fp32 input reads need up to 168 VGPRs; at 128
-// the compiler spills), else 4.
-template <int K, int NS>
-__global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(K == 5 || NS == 1 ? 3 : 4))) void
+// MF (MFMA-accumulate mode): a workgroup covers 2 tile columns (32 outputs), each split over two waves by tile rows
+// (the halves' sums are added through LDS), for all slots of its union entry in passes of up to 16.
+// Occupancy hint: 3 waves per SIMD for the EXACT kernel with one slot per pass (its batched fp32 input reads need up
+// to 168 VGPRs; at 128 the compiler spills), else 4.
+template <int K, int NS, bool MF>
+__global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(K == 5 || (NS == 1 && !MF) ? 3 : 4))) void
 gu_kernel(GuArgs a)
 {
-    constexpr int NW = GU_NW, TB = 32 * K;
+    constexpr int NW = GU_NW, TB = 32 * K, CPW = MF ? NW / 2 : NW;   // tile columns per workgroup
     extern __shared__ __align__(16) uint8_t lds_raw[];
     __shared__ int hdr[4];
     __shared__ int s_last;
+    __shared__ float4v red[MF ? CPW : 1][64];                                         // MF: upper halves' sums
     constexpr int RB = NGRP * 8 * TB;                                                 // ring bytes per wave
     uint8_t* rings = lds_raw;                                                         // [NW][RB]
-    constexpr bool XF = x_lds_elem(NS) == 4;
+    constexpr bool XF = !MF && x_lds_elem(NS) == 4;
+    constexpr int XE = MF ? 2 : x_lds_elem(NS);
     void* lds_x = lds_raw + NW * RB;                                                  // [ns_cap][H] permuted
-    int* plan_mem = reinterpret_cast<int*>(lds_raw + NW * RB + (size_t)a.ns_cap * a.H * x_lds_elem(NS));
+    int* plan_mem = reinterpret_cast<int*>(lds_raw + NW * RB + (size_t)a.ns_cap * a.H * XE);
     const LPlan L = lplan_carve(plan_mem, a.P, a.E);
     if (a.P <= 64) build_plan_wave(a.sel, a.P, a.E, L, hdr);
     else build_plan(a.sel, a.P, a.E, L, hdr);
-    const int TN = a.I / 16, TK = a.H / 16, ncb = TN / NW;
+    const int TN = a.I / 16, TK = a.H / 16, ncb = TN / CPW;
     if (blockIdx.x == gridDim.x - 1)
     {
         // the grid's extra workgroup publishes the plan for the down launch (no GEMV work of its own)
@@ -565,15 +644,15 @@ gu_kernel(GuArgs a)
     const gptr<uint16_t> suh = gaddr<uint16_t>(a.ptrs[(size_t)e * 9 + 3 + 2 * mat]);
     const int s_begin = a.per_slot ? ent : L.uoff[u], s_end = a.per_slot ? ent + 1 : L.uoff[u + 1];
     const size_t gstride = (size_t)TN * TB;
-    const int t = cb * NW + wave;                         // this wave's tile column
+    const int t = MF ? cb * CPW + (wave >> 1) : cb * NW + wave;   // this wave's tile column
     const uint8_t* col = tr + (size_t)t * TB;
     float* ybase = a.ygu + (size_t)mat * a.pv.cap_slots * a.I;
 
-    const int nsp = NS == 1 ? 1 : max(1, min(NS, a.ns_cap));
+    const int nsp = MF ? max(1, min(16, a.ns_cap)) : NS == 1 ? 1 : max(1, min(NS, a.ns_cap));
     for (int c0 = s_begin; c0 < s_end; c0 += nsp)
     {
-        const int ns = NS == 1 ? 1 : min(nsp, s_end - c0);   // >= 1 (c0 < s_end)
-        lds_barrier();   // previous pass done with lds_x
+        const int ns = NS == 1 && !MF ? 1 : min(nsp, s_end - c0);   // >= 1 (c0 < s_end)
+        lds_barrier();   // previous pass done with lds_x (and red)
         float res[NS];
         // input transform of the pass's tokens into LDS (prep_block, ft_core.h:97-102): each 16-lane row of a wave
         // takes one (slot, 128-block) item, 8 elements per lane; the first GU_PR rounds of items are loaded before the
@@ -595,7 +674,14 @@ gu_kernel(GuArgs a)
                 // elements 8li..8li+7 of block b: tile row li/2, accumulators j0 = 2(li&1) and j0 + 1, q = k/2
                 const int s = it / nblk, b = it % nblk, tk = b * 8 + (li >> 1), j0 = 2 * (li & 1);
                 const size_t pos = (size_t)s * a.H + (tk * 4 + j0) * 4;
-                if constexpr (XF)
+                if constexpr (MF)
+                {
+                    uint32_t o[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) o[q] = f2h2_bits(v[2 * q], v[2 * q + 1]);
+                    gp_store_row(static_cast<uint16_t*>(lds_x) + (size_t)s * a.H, b, li, o);
+                }
+                else if constexpr (XF)
                 {
                     float* dst = static_cast<float*>(lds_x) + pos;
                     float4v e0, e1;
@@ -622,11 +708,12 @@ gu_kernel(GuArgs a)
             }
         };
         const int nr = (nit + 4 * NW - 1) / (4 * NW);   // rounds of 4 * NW items
-        chain_dma<K, NS, NGRP, XF>(col, gstride, TK, ns, lds_x, rings + wid * RB, res, [&] {
+        auto pre_load = [&] {
 #pragma unroll
             for (int k = 0; k < GU_PR; ++k)
                 if (k < nr) load_round(k, k);
-        }, [&] {
+        };
+        auto pre = [&] {
             for (int r0 = 0; r0 < nr; r0 += GU_PR)
             {
                 if (r0 > 0)
@@ -640,19 +727,44 @@ gu_kernel(GuArgs a)
                     if (r0 + k < nr) prep_round(r0 + k, k);
             }
             lds_barrier();   // lds_x complete
-        });
+        };
+        if constexpr (MF)
+        {
+            const int cw = wid >> 1, hf = wid & 1, ngr = TK / 8;   // wave-uniform
+            const float4v acc = chain_mf<K, NGRP>(col, gstride, TK, hf ? ngr / 2 : 0, hf ? ngr : ngr / 2,
+                                                  static_cast<const uint16_t*>(lds_x), a.H, ns, rings + wid * RB,
+                                                  pre_load, pre);
+            if (hf) red[cw][lane] = acc;
+            __syncthreads();
+            if (!hf)
+            {
+                const float4v tot = acc + red[cw][lane];
 #pragma unroll
-        for (int s = 0; s < NS; ++s)
-            if (s < ns && lane < 16)
-                __hip_atomic_store(&ybase[(size_t)(c0 + s) * a.I + t * 16 + n], res[s], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+                for (int rr = 0; rr < 4; ++rr)
+                {
+                    const int m = 4 * (lane >> 4) + rr;
+                    if (m < ns)
+                        __hip_atomic_store(&ybase[(size_t)(c0 + m) * a.I + t * 16 + n], tot[rr], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+        }
+        else
+        {
+            chain_dma<K, NS, NGRP, XF>(col, gstride, TK, ns, lds_x, rings + wid * RB, res, pre_load, pre);
+#pragma unroll
+            for (int s = 0; s < NS; ++s)
+                if (s < ns && lane < 16)
+                    __hip_atomic_store(&ybase[(size_t)(c0 + s) * a.I + t * 16 + n], res[s], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
     // the last of the workgroups covering this 128-block (its gate and up halves) runs the SwiGLU stage for it.
     // Outputs went out as agent-scope stores (written through to the device-coherent level, not held in this XCD's
     // L2); the barrier's wait for outstanding stores orders them before the counter update, and the finisher reads
     // them back with agent-scope loads. No L2 write-back or invalidate is needed.
     __syncthreads();
-    const int blk = (cb * NW * 16) / 128;
+    const int blk = (cb * CPW * 16) / 128;
     if (threadIdx.x == 0)
     {
         int* ctr = a.act_cnt + (size_t)ent * (a.I / 128) + blk;
@@ -683,7 +795,8 @@ struct DnArgs
 
 // Grid: umax * H/128. Workgroup = 8 waves = one 128-output block of one routed expert, all its slots (with per_slot:
 // P * H/128, one slot each).
-template <int K, int NS>
+// MF: the GEMV accumulates with MFMAs (chain_mf), for up to 16 slots per pass.
+template <int K, int NS, bool MF>
 __global__ __launch_bounds__(DN_NW * 64) __attribute__((amdgpu_waves_per_eu(K == 5 || NS == 8 ? 3 : 4))) void
 down_kernel(DnArgs a)
 {
@@ -694,9 +807,10 @@ down_kernel(DnArgs a)
     __shared__ float c_w[NS][MAX_TOPK];
     constexpr int RB = NGRP * 8 * TB;                                                  // ring bytes per wave
     uint8_t* rings = lds_raw;                                                          // [NW][RB]
-    constexpr bool XF = x_lds_elem(NS) == 4;
+    constexpr bool XF = !MF && x_lds_elem(NS) == 4;
+    constexpr int XE = MF ? 2 : x_lds_elem(NS);
     void* lds_x = lds_raw + NW * RB;                                                   // [ns_cap][I]
-    float* lds_y = reinterpret_cast<float*>(lds_raw + NW * RB + (size_t)a.ns_cap * a.I * x_lds_elem(NS));   // [ns][128]
+    float* lds_y = reinterpret_cast<float*>(lds_raw + NW * RB + (size_t)a.ns_cap * a.I * XE);   // [ns_cap][128]
     const int TN = a.H / 16, TK = a.I / 16, ncb = TN / NW;
     const int u = blockIdx.x / ncb, blk = blockIdx.x % ncb;   // union entry, or slot with per_slot
     // one round of independent loads: the union size (slot count), this entry's slot range and its expert's
@@ -757,18 +871,34 @@ down_kernel(DnArgs a)
         };
         const int i0 = threadIdx.x, i1 = threadIdx.x + DN_NW * 64;
         uint4 xc0 = {}, xc1 = {};
-        chain_dma<K, NS, NGRP, XF>(col, gstride, TK, ns, lds_x, rings + wid * RB, res, [&] {
+        auto pre_load = [&] {
             if (i0 < nvec) xc0 = xsrc[i0];
             if (i1 < nvec) xc1 = xsrc[i1];
-        }, [&] {
+        };
+        auto pre = [&] {
             if (i0 < nvec) put(i0, xc0);
             if (i1 < nvec) put(i1, xc1);
             for (int i = threadIdx.x + 2 * DN_NW * 64; i < nvec; i += DN_NW * 64) put(i, xsrc[i]);
             lds_barrier();   // lds_x complete
-        });
+        };
+        if constexpr (MF)
+        {
+            const float4v acc = chain_mf<K, NGRP>(col, gstride, TK, 0, TK / 8, static_cast<const uint16_t*>(lds_x),
+                                                  a.I, ns, rings + wid * RB, pre_load, pre);
 #pragma unroll
-        for (int s = 0; s < NS; ++s)
-            if (s < ns && lane < 16) lds_y[s * 128 + wave * 16 + n] = res[s];
+            for (int rr = 0; rr < 4; ++rr)
+            {
+                const int m = 4 * (lane >> 4) + rr;
+                if (m < ns) lds_y[m * 128 + wave * 16 + n] = acc[rr];
+            }
+        }
+        else
+        {
+            chain_dma<K, NS, NGRP, XF>(col, gstride, TK, ns, lds_x, rings + wid * RB, res, pre_load, pre);
+#pragma unroll
+            for (int s = 0; s < NS; ++s)
+                if (s < ns && lane < 16) lds_y[s * 128 + wave * 16 + n] = res[s];
+        }
         if (ci < ns * a.topk)
         {
             c_slot[cs][ck] = q_slot;
@@ -872,33 +1002,34 @@ static bool open_lds(F kern)
 }
 
 template <int K>
-static size_t gu_lds(int ns, int H, int P, int E)
+static size_t gu_lds(int ns, int H, int P, int E, int mf)
 {
-    return (size_t)GU_NW * NGRP * 8 * 32 * K + (size_t)ns * H * x_lds_elem(ns) + lplan_ints(P, E) * 4;
+    return (size_t)GU_NW * NGRP * 8 * 32 * K + (size_t)ns * H * (mf ? 2 : x_lds_elem(ns)) + lplan_ints(P, E) * 4;
 }
 
 template <int K>
-static size_t dn_lds(int ns, int I)
+static size_t dn_lds(int ns, int I, int mf)
 {
-    return (size_t)DN_NW * NGRP * 8 * 32 * K + (size_t)ns * I * x_lds_elem(ns) + (size_t)ns * 128 * 4;
+    return (size_t)DN_NW * NGRP * 8 * 32 * K + (size_t)ns * I * (mf ? 2 : x_lds_elem(ns)) + (size_t)ns * 128 * 4;
 }
 
-template <int K, int NS>
+template <int K, int NS, bool MF>
 static void gu_launch(const GuArgs& a, int umax, int nmat, hipStream_t st)
 {
-    const size_t lds = gu_lds<K>(a.ns_cap, a.H, a.P, a.E);
-    auto kern = gu_kernel<K, NS>;
+    const size_t lds = gu_lds<K>(a.ns_cap, a.H, a.P, a.E, MF);
+    auto kern = gu_kernel<K, NS, MF>;
     static const bool opened = open_lds(kern);
     (void)opened;
     const int ents = a.per_slot ? a.P : umax;
-    hipLaunchKernelGGL(kern, dim3(ents * (a.I / (16 * GU_NW)) + 1, nmat), dim3(GU_NW * 64), lds, st, a);
+    const int cpw = MF ? GU_NW / 2 : GU_NW;   // tile columns per workgroup
+    hipLaunchKernelGGL(kern, dim3(ents * (a.I / (16 * cpw)) + 1, nmat), dim3(GU_NW * 64), lds, st, a);
 }
 
-template <int K, int NS>
+template <int K, int NS, bool MF>
 static void dn_launch(const DnArgs& a, int umax, int P, hipStream_t st)
 {
-    const size_t lds = dn_lds<K>(a.ns_cap, a.I);
-    auto kern = down_kernel<K, NS>;
+    const size_t lds = dn_lds<K>(a.ns_cap, a.I, MF);
+    auto kern = down_kernel<K, NS, MF>;
     static const bool opened = open_lds(kern);
     (void)opened;
     const int ents = a.per_slot ? P : umax;
@@ -922,22 +1053,22 @@ static void dn_launch(const DnArgs& a, int umax, int P, hipStream_t st)
         default: return -1;                                                                                     \
     }
 
-size_t gate_up_lds_bytes(int K, int ns, int H, int P, int E)
+size_t gate_up_lds_bytes(int K, int ns, int H, int P, int E, int mf)
 {
     size_t r = 0;
     auto f = [&]() -> int {
-        GFL_K_SWITCH(K, (r = gu_lds<K_>(ns, H, P, E)))
+        GFL_K_SWITCH(K, (r = gu_lds<K_>(ns, H, P, E, mf)))
         return 0;
     };
     f();
     return r;
 }
 
-size_t down_lds_bytes(int K, int ns, int I)
+size_t down_lds_bytes(int K, int ns, int I, int mf)
 {
     size_t r = 0;
     auto f = [&]() -> int {
-        GFL_K_SWITCH(K, (r = dn_lds<K_>(ns, I)))
+        GFL_K_SWITCH(K, (r = dn_lds<K_>(ns, I, mf)))
         return 0;
     };
     f();
@@ -947,28 +1078,43 @@ size_t down_lds_bytes(int K, int ns, int I)
 int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, const int64_t* sel, const void* w,
                    int w_half, int P, int topk, int E, int H, int I, int umax, const uint16_t* x, float* ygu,
                    uint16_t* xtd, int* act_cnt, const float* silu_tab, float act_limit, const PlanView& pv, float* out,
-                   hipStream_t st)
+                   int mf, hipStream_t st)
 {
     GuArgs a;
     a.ptrs = ptrs; a.sel = sel; a.w = w; a.w_half = w_half; a.P = P; a.topk = topk; a.E = E; a.H = H; a.I = I;
     a.mat_base = mat_base; a.x = x; a.ygu = ygu; a.xtd = xtd; a.act_cnt = act_cnt; a.silu_tab = silu_tab;
     a.act_limit = act_limit; a.pv = pv; a.out = out;
-    a.nmat_total = 2 * (128 / (16 * GU_NW));
     a.ns_cap = ns;
+    a.mf = mf;
+    if (mf)
+    {
+        // MFMA-accumulate mode: workgroups per union entry, all its slots in passes of up to ns
+        a.nmat_total = 2 * (128 / (16 * (GU_NW / 2)));
+        a.per_slot = 0;
+        GFL_K_SWITCH(K, (gu_launch<K_, 4, true>(a, umax, nmat, st)))
+        return 0;
+    }
+    a.nmat_total = 2 * (128 / (16 * GU_NW));
     a.per_slot = ns == 1;
-    GFL_K_SWITCH(K, GFL_NS_SWITCH(ns, (gu_launch<K_, NS_>(a, umax, nmat, st))))
+    GFL_K_SWITCH(K, GFL_NS_SWITCH(ns, (gu_launch<K_, NS_, false>(a, umax, nmat, st))))
     return 0;
 }
 
 int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int umax, int P, const PlanView& pv,
-                const uint16_t* xtd, float* yd, int* out_cnt, float* out, hipStream_t st)
+                const uint16_t* xtd, float* yd, int* out_cnt, float* out, int mf, hipStream_t st)
 {
     DnArgs a;
     a.ptrs = ptrs; a.topk = topk; a.H = H; a.I = I; a.pv = pv; a.xtd = xtd; a.yd = yd; a.out_cnt = out_cnt;
     a.out = out;
     a.ns_cap = ns;
+    if (mf)
+    {
+        a.per_slot = 0;
+        GFL_K_SWITCH(K, (dn_launch<K_, 4, true>(a, umax, P, st)))
+        return 0;
+    }
     a.per_slot = ns == 1;
-    GFL_K_SWITCH(K, GFL_NS_SWITCH(ns, (dn_launch<K_, NS_>(a, umax, P, st))))
+    GFL_K_SWITCH(K, GFL_NS_SWITCH(ns, (dn_launch<K_, NS_, false>(a, umax, P, st))))
     return 0;
 }
 #undef GFL_NS_SWITCH

@@ -24,16 +24,6 @@ namespace gfl {
 // grouped rows (tier_lut_build_grouped_rows semantics, ft_tier_ext.cpp:1047-1097) and the combine order
 // ---------------------------------------------------------------------------------------------------------------
 
-// Element r (0..127) of a 128-block (= one group of 8 tile rows) -> its position in the GEMM input layout
-// [block][q][tile row][jj]: row rho = r % 16 of tile row r / 16 is MFMA k-slot jj = (rho&1) + 2*(rho>>3) of lane group
-// q = (rho&7)>>1, so the 4 k-slots of two consecutive tile rows of one q are 8 contiguous fp16.
-__device__ inline int gp_perm_pos(int b, int r)
-{
-    const int tr = r >> 4, rho = r & 15;
-    const int jj = (rho & 1) + 2 * (rho >> 3), q = (rho & 7) >> 1;
-    return b * 128 + q * 32 + tr * 4 + jj;
-}
-
 constexpr int GP_MT = 80;          // slots per GEMM pass (up to 5 MFMA row blocks)
 constexpr int GP_PLAN_THREADS = GP_PLAN_CHUNK;   // one thread per pick of a chunk
 constexpr int GP_PLAN_WAVES = GP_PLAN_THREADS / 64;
@@ -255,15 +245,6 @@ __global__ __launch_bounds__(GP_ORDER_THREADS) void gp_order_kernel(const void* 
 constexpr int GP_TW = 4;   // waves per transform workgroup
 constexpr int GP_TU = 2;   // rounds of 4 blocks per chunk of the input transform (two chunks' loads in flight)
 constexpr int GP_TA = 3;   // rounds of 4 blocks per SwiGLU-transform wave (one wave covers I = 1536)
-
-// Elements 8li..8li+7 of block b in the GEMM input layout gp_perm_pos: pairs (2q, 2q + 1) are adjacent, at
-// b * 128 + q * 32 + (li >> 1) * 4 + 2 * (li & 1)
-__device__ __forceinline__ void gp_store_row(uint16_t* dst, int b, int li, const uint32_t (&o)[4])
-{
-    uint16_t* d0 = dst + b * 128 + (li >> 1) * 4 + 2 * (li & 1);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) *reinterpret_cast<uint32_t*>(d0 + q * 32) = o[q];
-}
 
 // prep_block (ft_core.h:97-102) of the gate and up inputs of slot s (one wave per slot)
 __global__ __launch_bounds__(GP_TW * 64) void gp_prep_kernel(const uint64_t* __restrict__ ptrs,

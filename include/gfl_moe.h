@@ -31,13 +31,19 @@ enum
 };
 
 /* Expert arithmetic modes, numbered as tier_forward's `mode` (kernels/cpu_avx2/ft_tier_ext.cpp:865-904).
- * The device path computes EXACT (bit-identical to the reference's EXACT mode); AUTO selects it. */
+ * The device path computes EXACT (bit-identical to the reference's EXACT mode); AUTO selects it.
+ * GFL_MODE_MFMA has no counterpart in the reference: the same bit-exact weights, transforms, rounding points and
+ * combine order, with the GEMV sums over the hidden dimension formed by MFMAs (fp32 accumulate) instead of EXACT's
+ * chains, for callers that trade bit-exactness for speed. Its outputs differ from EXACT by accumulation rounding
+ * carried through the fp16 rounding points (max-abs about 1e-3..3e-3 of the output RMS, as far as the reference's own
+ * fp64 expert lies from EXACT), so it is outside the 2e-3 bar that EXACT meets by construction. */
 enum
 {
     GFL_MODE_AUTO = -1,
     GFL_MODE_AFFINE = 0,
     GFL_MODE_EXACT = 1,
     GFL_MODE_I16 = 2,
+    GFL_MODE_MFMA = 3,
 };
 
 /* Last error message of the calling thread ("" if none). */
@@ -71,9 +77,11 @@ int gfl_register_layer(gfl_ctx* ctx, int li, int E, int H, int I, int k_gate, in
 int gfl_moe_forward(gfl_ctx* ctx, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half, int M,
                     int topk, float* out, int mode, float act_limit, gfl_stream stream);
 
-/* Environment: GFL_SLOTS_PER_PASS = 1, 2, 4 or 8 forces the number of (token, expert) slots one GEMV pass of
+/* mode: AUTO or EXACT (bit-exact), or MFMA. With MFMA a workgroup per routed expert takes up to 4 of its slots per
+ * pass, so the expert's tiles are decoded once for all of them.
+ * Environment: GFL_SLOTS_PER_PASS = 1, 2, 4 or 8 forces the number of (token, expert) slots one GEMV pass of
  * gfl_moe_forward accumulates (default: 1 up to M = 8, with a workgroup per slot; else 2, with a workgroup per expert
- * whose slots take passes). Read once by gfl_ctx_create. */
+ * whose slots take passes; MFMA: min(M, 4)). Read once by gfl_ctx_create. */
 
 /* Routed-expert forward of one layer for prefill-sized M (the north star's MFMA grouped GEMM), same arguments and
  * result layout as gfl_moe_forward: x fp16 [M, H], sel int64 [M, topk] (ids outside [0, E) skipped), w fp16 or fp32
