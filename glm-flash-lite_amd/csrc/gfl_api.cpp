@@ -69,7 +69,7 @@ namespace {
 struct Workspace
 {
     gfl::PlanView pv;
-    float* ygu;      // [2][cap][I]
+    float* ygu;      // [2][2][cap][I]: [0] the gate|up outputs (EXACT), [1] the upper halves' partial sums (MFMA)
     uint16_t* xtd;   // [cap][I]
     float* yd;       // [cap][H]
     int* act_cnt;    // [cap][I/128] last-one counters of the SwiGLU stage (zero between calls)
@@ -84,7 +84,7 @@ int ensure_ws(gfl_ctx* c, int cap, int H, int I, hipStream_t st, Workspace& w)
 {
     // plan ints, then the 8-byte aligned [cap][2] address table
     const size_t ints = align256(sizeof(int) * (size_t)(4 + 9 * cap + 4) + sizeof(uint64_t) * 2 * (size_t)cap);
-    const size_t b_ygu = align256(sizeof(float) * 2 * (size_t)cap * I);
+    const size_t b_ygu = align256(sizeof(float) * 4 * (size_t)cap * I);
     const size_t b_xtd = align256(sizeof(uint16_t) * (size_t)cap * I);
     const size_t b_yd = align256(sizeof(float) * (size_t)cap * H);
     const size_t b_cnt = align256(sizeof(int) * (size_t)cap * (I / 128 + H / 128));

@@ -463,7 +463,8 @@ __device__ __forceinline__ void chain_dma(const uint8_t* __restrict__ col_base, 
 }
 
 // MFMA-accumulate form of the column GEMV (mode GFL_MODE_MFMA): tile groups [g0, g1) of one tile column for up to 16
-// slots whose transformed inputs sit in lds_x as fp16 in the MFMA input layout (gp_perm_pos, xs elements per slot).
+// slots whose transformed inputs of 128-blocks g0..g1-1 sit in lds_x as fp16 in the MFMA input layout (gp_perm_pos,
+// relative to block g0; xs elements per slot).
 // Each pair of tile rows is one v_mfma_f32_16x16x32_f16 whose B slice is the decoded weights as decode4 leaves them
 // (lane 16q + n: column n, rows 2q + {0, 1, 8, 9} of both tiles) and whose A row m is slot m (rows >= ns read slot 0;
 // their sums are not used). Returns D: lane l holds slot 4(l/16) + i, column l % 16, in element i. The weights and
@@ -515,7 +516,7 @@ __device__ __forceinline__ float4v chain_mf(const uint8_t* __restrict__ col_base
         else
             wait_vmcnt<0>();
         const uint8_t* sl = ring + (gi % NG) * GB;
-        const uint16_t* xg = xa + (size_t)(g0 + gi) * 128;   // the group's 8 tile rows are 128-block g0 + gi
+        const uint16_t* xg = xa + (size_t)gi * 128;   // the group's 8 tile rows are 128-block g0 + gi
         uint32_t wd[8][2];
 #pragma unroll
         for (int rr = 0; rr < 8; ++rr)
@@ -552,7 +553,7 @@ struct GuArgs
     int w_half, P, topk, E, H, I;
     int mat_base;              // matrix of blockIdx.y == 0 (0 gate, 1 up)
     const uint16_t* x;         // [M][H] fp16
-    float* ygu;                // [2][cap][I]
+    float* ygu;                // [2][cap][I] (MF: [2 halves][2][cap][I])
     uint16_t* xtd;             // [cap][I] down input, permuted
     int* act_cnt;              // [cap][I/128] last-one counters (zero between calls)
     const float* silu_tab;
@@ -589,6 +590,15 @@ __device__ void act_block(const GuArgs& a, int e, int s_begin, int s_end, int b)
         const float* yu = a.ygu + (size_t)cap * a.I + (size_t)s * a.I + b * 128;
         float g0 = ld_agent(&yg[lane]), g1 = ld_agent(&yg[lane + 64]);
         float u0 = ld_agent(&yu[lane]), u1 = ld_agent(&yu[lane + 64]);
+        if (a.mf)
+        {
+            // MF: the upper halves of the tile rows, added to the lower halves' sums
+            const size_t hoff = (size_t)2 * cap * a.I;
+            g0 = g0 + ld_agent(&yg[hoff + lane]);
+            g1 = g1 + ld_agent(&yg[hoff + lane + 64]);
+            u0 = u0 + ld_agent(&yu[hoff + lane]);
+            u1 = u1 + ld_agent(&yu[hoff + lane + 64]);
+        }
         out_block_wave(g0, g1, h2f_bits(svh_g[b * 128 + lane]), h2f_bits(svh_g[b * 128 + lane + 64]));
         out_block_wave(u0, u1, h2f_bits(svh_u[b * 128 + lane]), h2f_bits(svh_u[b * 128 + lane + 64]));
         float a0 = r16(act_mul(g0, u0, a.act_limit, a.silu_tab)), a1 = r16(act_mul(g1, u1, a.act_limit, a.silu_tab));
@@ -603,29 +613,30 @@ __device__ void act_block(const GuArgs& a, int e, int s_begin, int s_end, int b)
 // slots; the last workgroup of row 0 publishes the plan. With per_slot the grid is (P * I/64 + 1, nmat) and a
 // workgroup takes one slot: an expert picked by several tokens is streamed once per slot, in parallel, instead of in
 // passes one after another.
-// MF (MFMA-accumulate mode): a workgroup covers 2 tile columns (32 outputs), each split over two waves by tile rows
-// (the halves' sums are added through LDS), for all slots of its union entry in passes of up to 16.
+// MF (MFMA-accumulate mode): a workgroup covers 4 tile columns over one half of the tile rows (so it transforms only
+// that half of the inputs), for all slots of its union entry in passes of up to 16; the two halves' partial sums go
+// to ygu[half] and the SwiGLU stage adds them (half 0 + half 1).
 // Occupancy hint: 3 waves per SIMD for the EXACT kernel with one slot per pass (its batched fp32 input reads need up
 // to 168 VGPRs; at 128 the compiler spills), else 4.
 template <int K, int NS, bool MF>
 __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(K == 5 || (NS == 1 && !MF) ? 3 : 4))) void
 gu_kernel(GuArgs a)
 {
-    constexpr int NW = GU_NW, TB = 32 * K, CPW = MF ? NW / 2 : NW;   // tile columns per workgroup
+    constexpr int NW = GU_NW, TB = 32 * K;
     extern __shared__ __align__(16) uint8_t lds_raw[];
     __shared__ int hdr[4];
     __shared__ int s_last;
-    __shared__ float4v red[MF ? CPW : 1][64];                                         // MF: upper halves' sums
     constexpr int RB = NGRP * 8 * TB;                                                 // ring bytes per wave
     uint8_t* rings = lds_raw;                                                         // [NW][RB]
     constexpr bool XF = !MF && x_lds_elem(NS) == 4;
     constexpr int XE = MF ? 2 : x_lds_elem(NS);
     void* lds_x = lds_raw + NW * RB;                                                  // [ns_cap][H] permuted
-    int* plan_mem = reinterpret_cast<int*>(lds_raw + NW * RB + (size_t)a.ns_cap * a.H * XE);
+    // [ns_cap][H] elements, MF: [ns_cap][H / 2] (one half of the 128-blocks)
+    int* plan_mem = reinterpret_cast<int*>(lds_raw + NW * RB + (size_t)a.ns_cap * a.H * XE / (MF ? 2 : 1));
     const LPlan L = lplan_carve(plan_mem, a.P, a.E);
     if (a.P <= 64) build_plan_wave(a.sel, a.P, a.E, L, hdr);
     else build_plan(a.sel, a.P, a.E, L, hdr);
-    const int TN = a.I / 16, TK = a.H / 16, ncb = TN / CPW;
+    const int TN = a.I / 16, TK = a.H / 16, ncb = TN / NW;
     if (blockIdx.x == gridDim.x - 1)
     {
         // the grid's extra workgroup publishes the plan for the down launch (no GEMV work of its own)
@@ -633,7 +644,9 @@ gu_kernel(GuArgs a)
         return;
     }
 
-    const int ent = blockIdx.x / ncb, cb = blockIdx.x % ncb;   // union entry, or slot with per_slot
+    // union entry (or slot with per_slot), column block, and with MF the half of the tile rows (adjacent workgroups)
+    const int nper = MF ? 2 * ncb : ncb;
+    const int ent = blockIdx.x / nper, cb = (blockIdx.x % nper) / (MF ? 2 : 1), hf = MF ? blockIdx.x & 1 : 0;
     if (ent >= hdr[a.per_slot ? 1 : 0]) return;
     const int u = a.per_slot ? plan_u(L, L.spick[ent]) : ent;
     const int mat = a.mat_base + blockIdx.y;              // 0 gate, 1 up
@@ -644,9 +657,11 @@ gu_kernel(GuArgs a)
     const gptr<uint16_t> suh = gaddr<uint16_t>(a.ptrs[(size_t)e * 9 + 3 + 2 * mat]);
     const int s_begin = a.per_slot ? ent : L.uoff[u], s_end = a.per_slot ? ent + 1 : L.uoff[u + 1];
     const size_t gstride = (size_t)TN * TB;
-    const int t = MF ? cb * CPW + (wave >> 1) : cb * NW + wave;   // this wave's tile column
+    const int t = cb * NW + wave;                         // this wave's tile column
     const uint8_t* col = tr + (size_t)t * TB;
-    float* ybase = a.ygu + (size_t)mat * a.pv.cap_slots * a.I;
+    float* ybase = a.ygu + (size_t)(2 * hf + mat) * a.pv.cap_slots * a.I;
+    const int ngr = TK / 8, g0 = hf ? ngr / 2 : 0, g1 = MF && !hf ? ngr / 2 : ngr;   // this workgroup's 128-blocks
+    const int xs = (g1 - g0) * 128;                                                    // LDS input row (elements)
 
     const int nsp = MF ? max(1, min(16, a.ns_cap)) : NS == 1 ? 1 : max(1, min(NS, a.ns_cap));
     for (int c0 = s_begin; c0 < s_end; c0 += nsp)
@@ -657,11 +672,11 @@ gu_kernel(GuArgs a)
         // input transform of the pass's tokens into LDS (prep_block, ft_core.h:97-102): each 16-lane row of a wave
         // takes one (slot, 128-block) item, 8 elements per lane; the first GU_PR rounds of items are loaded before the
         // trellis groups are requested
-        const int nblk = a.H / 128, nit = ns * nblk, rl = lane >> 4, li = lane & 15;
+        const int nblk = g1 - g0, nit = ns * nblk, rl = lane >> 4, li = lane & 15;
         uint4 xv[GU_PR], sv[GU_PR];
         auto load_round = [&](int r, int k) {
             const int it = min((r * NW + wave) * 4 + rl, nit - 1);
-            const int s = it / nblk, b = it % nblk;
+            const int s = it / nblk, b = g0 + it % nblk;
             xv[k] = *reinterpret_cast<const uint4*>(a.x + (size_t)(L.spick[c0 + s] / a.topk) * a.H + b * 128 + li * 8);
             sv[k] = gld16(suh, b * 128 + li * 8);
         };
@@ -672,14 +687,14 @@ gu_kernel(GuArgs a)
             if (it < nit)
             {
                 // elements 8li..8li+7 of block b: tile row li/2, accumulators j0 = 2(li&1) and j0 + 1, q = k/2
-                const int s = it / nblk, b = it % nblk, tk = b * 8 + (li >> 1), j0 = 2 * (li & 1);
+                const int s = it / nblk, b = it % nblk, tk = b * 8 + (li >> 1), j0 = 2 * (li & 1);   // b from g0
                 const size_t pos = (size_t)s * a.H + (tk * 4 + j0) * 4;
                 if constexpr (MF)
                 {
                     uint32_t o[4];
 #pragma unroll
                     for (int q = 0; q < 4; ++q) o[q] = f2h2_bits(v[2 * q], v[2 * q + 1]);
-                    gp_store_row(static_cast<uint16_t*>(lds_x) + (size_t)s * a.H, b, li, o);
+                    gp_store_row(static_cast<uint16_t*>(lds_x) + (size_t)s * xs, b, li, o);
                 }
                 else if constexpr (XF)
                 {
@@ -730,23 +745,15 @@ gu_kernel(GuArgs a)
         };
         if constexpr (MF)
         {
-            const int cw = wid >> 1, hf = wid & 1, ngr = TK / 8;   // wave-uniform
-            const float4v acc = chain_mf<K, NGRP>(col, gstride, TK, hf ? ngr / 2 : 0, hf ? ngr : ngr / 2,
-                                                  static_cast<const uint16_t*>(lds_x), a.H, ns, rings + wid * RB,
-                                                  pre_load, pre);
-            if (hf) red[cw][lane] = acc;
-            __syncthreads();
-            if (!hf)
-            {
-                const float4v tot = acc + red[cw][lane];
+            const float4v acc = chain_mf<K, NGRP>(col, gstride, TK, g0, g1, static_cast<const uint16_t*>(lds_x), xs,
+                                                  ns, rings + wid * RB, pre_load, pre);
 #pragma unroll
-                for (int rr = 0; rr < 4; ++rr)
-                {
-                    const int m = 4 * (lane >> 4) + rr;
-                    if (m < ns)
-                        __hip_atomic_store(&ybase[(size_t)(c0 + m) * a.I + t * 16 + n], tot[rr], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-                }
+            for (int rr = 0; rr < 4; ++rr)
+            {
+                const int m = 4 * (lane >> 4) + rr;
+                if (m < ns)
+                    __hip_atomic_store(&ybase[(size_t)(c0 + m) * a.I + t * 16 + n], acc[rr], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
             }
         }
         else
@@ -764,7 +771,7 @@ gu_kernel(GuArgs a)
     // L2); the barrier's wait for outstanding stores orders them before the counter update, and the finisher reads
     // them back with agent-scope loads. No L2 write-back or invalidate is needed.
     __syncthreads();
-    const int blk = (cb * CPW * 16) / 128;
+    const int blk = (cb * NW * 16) / 128;
     if (threadIdx.x == 0)
     {
         int* ctr = a.act_cnt + (size_t)ent * (a.I / 128) + blk;
@@ -1004,7 +1011,7 @@ static bool open_lds(F kern)
 template <int K>
 static size_t gu_lds(int ns, int H, int P, int E, int mf)
 {
-    return (size_t)GU_NW * NGRP * 8 * 32 * K + (size_t)ns * H * (mf ? 2 : x_lds_elem(ns)) + lplan_ints(P, E) * 4;
+    return (size_t)GU_NW * NGRP * 8 * 32 * K + (size_t)ns * H * (mf ? 1 : x_lds_elem(ns)) + lplan_ints(P, E) * 4;
 }
 
 template <int K>
@@ -1021,8 +1028,8 @@ static void gu_launch(const GuArgs& a, int umax, int nmat, hipStream_t st)
     static const bool opened = open_lds(kern);
     (void)opened;
     const int ents = a.per_slot ? a.P : umax;
-    const int cpw = MF ? GU_NW / 2 : GU_NW;   // tile columns per workgroup
-    hipLaunchKernelGGL(kern, dim3(ents * (a.I / (16 * cpw)) + 1, nmat), dim3(GU_NW * 64), lds, st, a);
+    const int per_ent = (a.I / (16 * GU_NW)) * (MF ? 2 : 1);   // MF: both halves of the tile rows
+    hipLaunchKernelGGL(kern, dim3(ents * per_ent + 1, nmat), dim3(GU_NW * 64), lds, st, a);
 }
 
 template <int K, int NS, bool MF>
@@ -1089,7 +1096,7 @@ int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, 
     if (mf)
     {
         // MFMA-accumulate mode: workgroups per union entry, all its slots in passes of up to ns
-        a.nmat_total = 2 * (128 / (16 * (GU_NW / 2)));
+        a.nmat_total = 2 * 2 * (128 / (16 * GU_NW));   // gate, up x two halves
         a.per_slot = 0;
         GFL_K_SWITCH(K, (gu_launch<K_, 4, true>(a, umax, nmat, st)))
         return 0;

@@ -77,8 +77,8 @@ int gfl_register_layer(gfl_ctx* ctx, int li, int E, int H, int I, int k_gate, in
 int gfl_moe_forward(gfl_ctx* ctx, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half, int M,
                     int topk, float* out, int mode, float act_limit, gfl_stream stream);
 
-/* mode: AUTO or EXACT (bit-exact), or MFMA. With MFMA a workgroup per routed expert takes up to 4 of its slots per
- * pass, so the expert's tiles are decoded once for all of them.
+/* mode: AUTO or EXACT (bit-exact), or MFMA. With MFMA the workgroups of a routed expert take up to 4 of its slots
+ * per pass, so the expert's tiles are decoded once for all of them.
  * Environment: GFL_SLOTS_PER_PASS = 1, 2, 4 or 8 forces the number of (token, expert) slots one GEMV pass of
  * gfl_moe_forward accumulates (default: 1 up to M = 8, with a workgroup per slot; else 2, with a workgroup per expert
  * whose slots take passes; MFMA: min(M, 4)). Read once by gfl_ctx_create. */
