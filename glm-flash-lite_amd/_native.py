@@ -15,7 +15,7 @@ SYMBOLS = ("gfl_last_error", "gfl_version", "gfl_ctx_create", "gfl_ctx_destroy",
            "gfl_moe_forward", "gfl_grouped_forward", "gfl_dequant", "gfl_split", "gfl_combine", "gfl_grouped_rows",
            "gfl_synth_trellis", "gfl_route",
            "gfl_stats", "gfl_profile_enable", "gfl_profile_read", "gfl_exp_table", "gfl_silu_table",
-           "gfl_grouped_plan")
+           "gfl_grouped_plan", "gfl_grouped_reserve", "gfl_layer_info", "gfl_route_split")
 
 MODE_AUTO, MODE_AFFINE, MODE_EXACT, MODE_I16, MODE_MFMA = -1, 0, 1, 2, 3
 
@@ -50,10 +50,14 @@ def load(path=LIB_PATH):
     L.gfl_register_layer.argtypes = [_P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _P]
     L.gfl_moe_forward.argtypes = [_P, C.c_int, _P, _P, _P, C.c_int, C.c_int, C.c_int, _P, C.c_int, C.c_float, _P]
     L.gfl_grouped_forward.argtypes = [_P, C.c_int, _P, _P, _P, C.c_int, C.c_int, C.c_int, _P, C.c_float, _P]
+    L.gfl_grouped_reserve.argtypes = [_P, C.c_int]
+    L.gfl_layer_info.argtypes = [_P, C.c_int, _P]
     L.gfl_grouped_plan.argtypes = [_P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, _P, _P]
     L.gfl_dequant.argtypes = [_P, C.c_int, C.c_int, C.c_int, _P, _P]
     L.gfl_split.argtypes = [_P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P,
                             C.c_int64, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P]
+    L.gfl_route_split.argtypes = [_P, C.c_int, C.c_int, C.c_int, _P, _P, _P, C.c_int, C.c_int, C.c_int, _P, _P, _P,
+                                  _P, _P, _P, C.c_int64, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P]
     L.gfl_combine.argtypes = [_P, C.c_int, C.c_int, _P, _P, _P, _P, C.c_int64, _P]
     L.gfl_grouped_rows.argtypes = [_P, _P, C.c_int, C.c_int, _P, C.c_int, _P, _P, _P, _P, C.POINTER(C.c_int)]
     L.gfl_synth_trellis.argtypes = [_P, C.c_size_t, C.c_uint64, _P]
@@ -92,6 +96,7 @@ class Context:
         self.h = h
         self.device = int(device)
         self._keep = {}
+        self._shape = {}
 
     def close(self):
         if self.h:
@@ -108,8 +113,26 @@ class Context:
         """ptr_table: sequence of E*9 device addresses (see gfl_register_layer)."""
         arr = (C.c_uint64 * (9 * E))(*[int(p) for p in ptr_table])
         check(load().gfl_register_layer(self.h, li, E, H, I, int(ks[0]), int(ks[1]), int(ks[2]), arr))
+        self._shape[li] = self.layer_info(li)
         if keep is not None:
             self._keep[li] = keep
+
+    def layer_info(self, li):
+        """(E, H, I, k_gate, k_up, k_down) of a registered layer (gfl_layer_info)."""
+        info = (C.c_int * 6)()
+        check(load().gfl_layer_info(self.h, int(li), info))
+        return tuple(info)
+
+    def grouped_reserve(self, max_picks):
+        """Size the grouped-path workspace for calls of up to max_picks picks (gfl_grouped_reserve)."""
+        check(load().gfl_grouped_reserve(self.h, int(max_picks)))
+
+    def _check_width(self, li, x):
+        shape = self._shape.get(li)
+        if shape is None:
+            shape = self._shape[li] = self.layer_info(li)
+        if x.shape[1] != shape[1]:
+            raise ValueError(f"x is [M, {x.shape[1]}] but layer {li} has H = {shape[1]}")
 
     def moe_forward(self, li, x, sel, w, out, mode=MODE_EXACT, act_limit=0.0):
         """x fp16 [M,H], sel int64 [M,topk], w fp16|fp32 [M,topk], out fp32 [M,H] (all on the context device)."""
@@ -128,6 +151,7 @@ class Context:
         for t in (x, sel, w, out):
             if not (t.is_cuda and t.device.index == self.device):
                 raise ValueError(f"all tensors must be on cuda:{self.device}")
+        self._check_width(li, x)
         check(load().gfl_moe_forward(self.h, li, ptr(x), ptr(sel), ptr(w), int(w.dtype == torch.float16), M, topk,
                                      ptr(out), int(mode), float(act_limit), _stream()))
         return out
@@ -149,6 +173,7 @@ class Context:
         for t in (x, sel, w, out):
             if not (t.is_cuda and t.device.index == self.device):
                 raise ValueError(f"all tensors must be on cuda:{self.device}")
+        self._check_width(li, x)
         check(load().gfl_grouped_forward(self.h, li, ptr(x), ptr(sel), ptr(w), int(w.dtype == torch.float16), M, topk,
                                          ptr(out), float(act_limit), _stream()))
         return out
@@ -235,6 +260,19 @@ def split(sel, w, z, E, first, slotof, score, pol, ctrl, hx, hpicks, seq, li, ke
                            ptr(pol), C.c_void_p(int(ctrl)), C.c_void_p(int(hx)), C.c_void_p(int(hpicks)), int(seq),
                            int(li), int(keep_ids), ptr(sel_out), ptr(w_out), ptr(dflag), ptr(stats),
                            ptr(rres) if rres is not None and rres.numel() else None, _stream()))
+
+
+def route_split(logits, topk, z, E, first, slotof, score, pol, ctrl, hx, hpicks, seq, li, keep_ids, sel, w, sel_out,
+                w_out, dflag, stats, rres):
+    """Router and ft_split in one launch (gfl_route_split): logits fp32 [M, E_route] on the device; sel int64 and w fp16
+    [M, topk] receive the routing, sel_out / w_out the split's selection; other arguments as split()."""
+    M, ER = logits.shape
+    H = z.shape[1]
+    check(load().gfl_route_split(ptr(logits), M, ER, int(topk), ptr(sel), ptr(w), ptr(z), H, int(E), int(first),
+                                 ptr(slotof), ptr(score), ptr(pol), C.c_void_p(int(ctrl)), C.c_void_p(int(hx)),
+                                 C.c_void_p(int(hpicks)), int(seq), int(li), int(keep_ids), ptr(sel_out), ptr(w_out),
+                                 ptr(dflag), ptr(stats), ptr(rres) if rres is not None and rres.numel() else None,
+                                 _stream()))
 
 
 def combine(out, dflag, ctrl, hout, stats, timeout_ns):

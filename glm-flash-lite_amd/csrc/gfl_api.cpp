@@ -46,9 +46,11 @@ struct gfl_ctx
     int device = 0;
     std::vector<Layer> layers;
     std::mutex mu;
-    // workspace (grown on demand, never shrunk)
+    // decode workspace, reserved by gfl_register_layer for MAX_PICKS slots at the largest registered H and I and
+    // carved with that fixed layout, so every call (and every graph captured from one) sees the same addresses
     void* ws = nullptr;
     size_t ws_bytes = 0, ws_cnt_off = 0;
+    int ws_H = 0, ws_I = 0;
     int64_t calls = 0, picks = 0;
     // per-stage profiling events (gfl_profile_enable / gfl_profile_read)
     bool prof = false;
@@ -59,9 +61,12 @@ struct gfl_ctx
     float* silu_tab = nullptr;
     // slots per GEMV pass forced by GFL_SLOTS_PER_PASS (1, 2, 4 or 8; 0 = chosen from M)
     int ns_override = 0;
-    // workspace of the prefill path (gfl_grouped_forward), grown on demand
+    // workspace of the prefill path (gfl_grouped_forward / gfl_grouped_reserve), grown on demand outside captures
     void* gws = nullptr;
     size_t gws_bytes = 0;
+    // superseded workspaces: a graph captured before a workspace grew still holds their addresses, so they stay
+    // allocated until gfl_ctx_destroy
+    std::vector<void*> retired;
 };
 
 namespace {
@@ -78,41 +83,59 @@ struct Workspace
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// The workspace grows to the largest (picks, H, I) seen and is laid out for the current call. The counter region is
-// zeroed when the buffer is (re)allocated; the kernels leave every counter at zero when they finish.
-int ensure_ws(gfl_ctx* c, int cap, int H, int I, hipStream_t st, Workspace& w)
+// Decode workspace sizes for cap slots at hidden H and intermediate I: plan ints and the [cap][2] address table,
+// gate|up outputs, down inputs, expert outputs, and the counter region (a tail of its own).
+struct WsSizes
 {
-    // plan ints, then the 8-byte aligned [cap][2] address table
-    const size_t ints = align256(sizeof(int) * (size_t)(4 + 9 * cap + 4) + sizeof(uint64_t) * 2 * (size_t)cap);
-    const size_t b_ygu = align256(sizeof(float) * 4 * (size_t)cap * I);
-    const size_t b_xtd = align256(sizeof(uint16_t) * (size_t)cap * I);
-    const size_t b_yd = align256(sizeof(float) * (size_t)cap * H);
-    const size_t b_cnt = align256(sizeof(int) * (size_t)cap * (I / 128 + H / 128));
-    const size_t data = ints + b_ygu + b_xtd + b_yd;
-    // data regions from the start, counters in a tail region of their own: grow when either does not fit
-    const size_t old_off = c->ws ? c->ws_cnt_off : 0, old_cnt = c->ws ? c->ws_bytes - c->ws_cnt_off : 0;
-    if (!c->ws || data > old_off || b_cnt > old_cnt)
+    size_t ints, ygu, xtd, yd, cnt;
+    size_t data() const { return ints + ygu + xtd + yd; }
+};
+
+WsSizes ws_sizes(int cap, int H, int I)
+{
+    WsSizes z;
+    z.ints = align256(sizeof(int) * (size_t)(4 + 9 * cap + 4) + sizeof(uint64_t) * 2 * (size_t)cap);
+    z.ygu = align256(sizeof(float) * 4 * (size_t)cap * I);
+    z.xtd = align256(sizeof(uint16_t) * (size_t)cap * I);
+    z.yd = align256(sizeof(float) * (size_t)cap * H);
+    z.cnt = align256(sizeof(int) * (size_t)cap * (I / 128 + H / 128));
+    return z;
+}
+
+// Make the decode workspace hold MAX_PICKS slots at hidden H and intermediate I (and at every size reserved before).
+// A larger buffer replaces the old one, which is retired, not freed: a graph captured earlier keeps valid addresses.
+// The counter region is zeroed once here; the kernels leave every counter at zero when they finish.
+int reserve_ws(gfl_ctx* c, int H, int I)
+{
+    const int nH = std::max(H, c->ws_H), nI = std::max(I, c->ws_I);
+    if (c->ws && nH == c->ws_H && nI == c->ws_I) return GFL_OK;
+    const WsSizes z = ws_sizes(gfl::MAX_PICKS, nH, nI);
+    const size_t need = z.data() + z.cnt;
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, need);
+    if (e != hipSuccess) return fail(GFL_ENOMEM, std::string("workspace hipMalloc: ") + hipGetErrorString(e));
+    e = hipMemset(p, 0, need);
+    if (e != hipSuccess)
     {
-        const size_t off = std::max(data, old_off), need = off + std::max(b_cnt, old_cnt);
-        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
-            return fail(GFL_EINVAL, "gfl_moe_forward: the workspace must be sized before graph capture "
-                                    "(run one forward of this shape first)");
-        if (c->ws)
-        {
-            GFL_HIP(hipDeviceSynchronize());
-            GFL_HIP(hipFree(c->ws));
-        }
-        c->ws = nullptr;
-        c->ws_bytes = 0;
-        c->ws_cnt_off = 0;
-        hipError_t e = hipMalloc(&c->ws, need);
-        if (e != hipSuccess) return fail(GFL_ENOMEM, std::string("workspace hipMalloc: ") + hipGetErrorString(e));
-        GFL_HIP(hipMemset(c->ws, 0, need));
-        GFL_HIP(hipDeviceSynchronize());
-        c->ws_cnt_off = off;
-        c->ws_bytes = need;
+        hipFree(p);
+        return hip_fail(e, "workspace hipMemset");
     }
+    if (c->ws) c->retired.push_back(c->ws);
+    c->ws = p;
+    c->ws_bytes = need;
+    c->ws_cnt_off = z.data();
+    c->ws_H = nH;
+    c->ws_I = nI;
+    return GFL_OK;
+}
+
+// The fixed layout of the reserved workspace, with strides for a layer of hidden H and intermediate I (<= the
+// reserved maxima). Slot capacity is always MAX_PICKS, so the addresses do not depend on the call's size.
+void carve_ws(gfl_ctx* c, int H, int I, Workspace& w)
+{
+    const int cap = gfl::MAX_PICKS;
+    const WsSizes z = ws_sizes(cap, c->ws_H, c->ws_I);
+    (void)H;
     char* b = static_cast<char*>(c->ws);
     int* ip = reinterpret_cast<int*>(b);
     w.pv.hdr = ip;
@@ -127,13 +150,11 @@ int ensure_ws(gfl_ctx* c, int cap, int H, int I, hipStream_t st, Workspace& w)
     w.pv.tok_npk = reinterpret_cast<int*>(w.pv.tok_w + cap);
     w.pv.uptr = reinterpret_cast<uint64_t*>(ip + ((4 + 9 * (size_t)cap + 2 + 1) & ~size_t(1)));
     w.pv.cap_slots = cap;
-    w.ygu = reinterpret_cast<float*>(b + ints);
-    w.xtd = reinterpret_cast<uint16_t*>(b + ints + b_ygu);
-    w.yd = reinterpret_cast<float*>(b + ints + b_ygu + b_xtd);
-    // counters live at the fixed tail of the allocation so that a smaller call reuses the same (zeroed) words
+    w.ygu = reinterpret_cast<float*>(b + z.ints);
+    w.xtd = reinterpret_cast<uint16_t*>(b + z.ints + z.ygu);
+    w.yd = reinterpret_cast<float*>(b + z.ints + z.ygu + z.xtd);
     w.act_cnt = reinterpret_cast<int*>(b + c->ws_cnt_off);
     w.out_cnt = w.act_cnt + (size_t)cap * (I / 128);
-    return GFL_OK;
 }
 
 bool k_ok(int K) { return K >= 2 && K <= 5; }
@@ -260,6 +281,7 @@ int gfl_ctx_destroy(gfl_ctx* c)
         if (L.dptrs) hipFree(L.dptrs);
     if (c->ws) hipFree(c->ws);
     if (c->gws) hipFree(c->gws);
+    for (void* p : c->retired) hipFree(p);
     if (c->silu_tab) hipFree(c->silu_tab);
     delete c;
     return GFL_OK;
@@ -287,7 +309,8 @@ int gfl_register_layer(gfl_ctx* c, int li, int E, int H, int I, int k_gate, int 
     GFL_HIP(hipMalloc(&L.dptrs, sizeof(uint64_t) * 9 * (size_t)E));
     GFL_HIP(hipMemcpy(L.dptrs, ptrs, sizeof(uint64_t) * 9 * (size_t)E, hipMemcpyHostToDevice));
     L.E = E; L.H = H; L.I = I; L.K[0] = k_gate; L.K[1] = k_up; L.K[2] = k_down;
-    return GFL_OK;
+    // the decode workspace for this shape, reserved now so that no forward call allocates
+    return reserve_ws(c, H, I);
 }
 
 int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half, int M,
@@ -296,8 +319,10 @@ int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, c
     if (!c || !x || !sel || !w || !out) return fail(GFL_EINVAL, "gfl_moe_forward: NULL argument");
     if (li < 0 || li >= (int)c->layers.size() || !c->layers[li].dptrs)
         return fail(GFL_EINVAL, "gfl_moe_forward: layer not registered");
-    if (mode != GFL_MODE_AUTO && mode != GFL_MODE_EXACT && mode != GFL_MODE_MFMA)
-        return fail(GFL_EINVAL, "gfl_moe_forward: the device path computes EXACT (mode 1 or -1) or MFMA (mode 3)");
+    // AFFINE (0) and I16 (2) name the reference CPU engine's speed modes; the device computes EXACT for them, which
+    // lies closer to the fp64 expert than either of them does
+    if (mode < GFL_MODE_AUTO || mode > GFL_MODE_MFMA)
+        return fail(GFL_EINVAL, "gfl_moe_forward: mode must be -1 (auto), 0 (affine), 1 (exact), 2 (i16) or 3 (mfma)");
     if (M < 1 || topk < 1 || topk > gfl::MAX_TOPK || (int64_t)M * topk > gfl::MAX_PICKS)
         return fail(GFL_EINVAL, "gfl_moe_forward: need 1 <= topk <= 16 and M*topk <= 1024");
     if (!std::isfinite(act_limit) || act_limit < 0) return fail(GFL_EINVAL, "gfl_moe_forward: act_limit must be >= 0");
@@ -307,8 +332,9 @@ int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, c
     GFL_HIP(hipSetDevice(c->device));
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const int P = M * topk;
+    if (!c->ws || L.H > c->ws_H || L.I > c->ws_I) return fail(GFL_ERUNTIME, "gfl_moe_forward: workspace not reserved");
     Workspace ws;
-    if (int r = ensure_ws(c, P, L.H, L.I, st, ws)) return r;
+    carve_ws(c, L.H, L.I, ws);
     const int umax = P < L.E ? P : L.E;
     // slots per pass of the GEMV (its LDS holds NS transformed inputs). With one slot per pass the launches run a
     // workgroup per slot, so an expert picked by several tokens is streamed once per slot in parallel; with more,
@@ -369,16 +395,13 @@ static int grouped_workspace(gfl_ctx* c, hipStream_t st, int P, int M, int E, in
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
             return fail(GFL_EINVAL, std::string(who) + ": the workspace must be sized before graph capture "
-                                                      "(run one call of this shape first)");
-        if (c->gws)
-        {
-            GFL_HIP(hipDeviceSynchronize());
-            GFL_HIP(hipFree(c->gws));
-        }
-        c->gws = nullptr;
-        c->gws_bytes = 0;
-        hipError_t e = hipMalloc(&c->gws, need);
+                                                      "(gfl_grouped_reserve, or one call of this shape first)");
+        void* p = nullptr;
+        hipError_t e = hipMalloc(&p, need);
         if (e != hipSuccess) return fail(GFL_ENOMEM, std::string("grouped workspace hipMalloc: ") + hipGetErrorString(e));
+        // the old buffer is retired, not freed: a graph captured before this growth still holds its addresses
+        if (c->gws) c->retired.push_back(c->gws);
+        c->gws = p;
         c->gws_bytes = need;
     }
     b = static_cast<char*>(c->gws);
@@ -437,6 +460,37 @@ int gfl_grouped_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* se
     return GFL_OK;
 }
 
+int gfl_grouped_reserve(gfl_ctx* c, int max_picks)
+{
+    if (!c) return fail(GFL_EINVAL, "gfl_grouped_reserve: NULL context");
+    if (max_picks < 1 || max_picks > gfl::MAX_GROUPED_PICKS)
+        return fail(GFL_EINVAL, "gfl_grouped_reserve: need 1 <= max_picks <= 65536");
+    std::lock_guard<std::mutex> g(c->mu);
+    int E = 0, H = 0, I = 0;
+    for (const auto& L : c->layers)
+        if (L.dptrs) { E = std::max(E, L.E); H = std::max(H, L.H); I = std::max(I, L.I); }
+    if (!E) return fail(GFL_EINVAL, "gfl_grouped_reserve: no layer registered");
+    GFL_HIP(hipSetDevice(c->device));
+    gfl::GPlan gp;
+    char* b = nullptr;
+    size_t b_int = 0, b_xt = 0, b_ygu = 0, b_xd = 0;
+    // the largest layout any call up to max_picks picks can take: M <= picks tokens
+    return grouped_workspace(c, nullptr, max_picks, max_picks, E, H, I, "gfl_grouped_reserve", gp, b, b_int, b_xt,
+                             b_ygu, b_xd);
+}
+
+int gfl_layer_info(gfl_ctx* c, int li, int* info)
+{
+    if (!c || !info) return fail(GFL_EINVAL, "gfl_layer_info: NULL argument");
+    std::lock_guard<std::mutex> g(c->mu);
+    if (li < 0 || li >= (int)c->layers.size() || !c->layers[li].dptrs)
+        return fail(GFL_EINVAL, "gfl_layer_info: layer not registered");
+    const Layer& L = c->layers[li];
+    const int v[6] = { L.E, L.H, L.I, L.K[0], L.K[1], L.K[2] };
+    for (int i = 0; i < 6; ++i) info[i] = v[i];
+    return GFL_OK;
+}
+
 int gfl_grouped_plan(gfl_ctx* c, const int64_t* sel, const void* w, int w_is_half, int M, int topk, int E,
                      int* hdr, int* off, int* slot_pick, int* slot_e, int* tok_slot, float* tok_w, int* tok_npk,
                      gfl_stream stream)
@@ -492,6 +546,29 @@ int gfl_split(const int64_t* sel, const uint16_t* w, const uint16_t* z, int bsz,
         return fail(GFL_EINVAL, "gfl_split: z and hx must be 16-byte aligned");
     gfl::launch_split(sel, w, z, n, bsz, n / bsz, H, E, first, slotof, score, pol, ctrl, hx, hpicks, seq, li, keep_ids,
                       sel_out, w_out, dflag, stats, rres, reinterpret_cast<hipStream_t>(stream));
+    GFL_HIP(hipGetLastError());
+    return GFL_OK;
+}
+
+int gfl_route_split(const float* logits, int M, int E_route, int topk, int64_t* sel, uint16_t* w, const uint16_t* z,
+                    int H, int E, int first, const int32_t* slotof, const float* score, const float* pol,
+                    int64_t* ctrl, uint16_t* hx, int32_t* hpicks, int64_t seq, int li, int keep_ids, int64_t* sel_out,
+                    uint16_t* w_out, int64_t* dflag, int64_t* stats, const int32_t* rres, gfl_stream stream)
+{
+    if (!logits || !sel || !w || !z || !slotof || !score || !pol || !ctrl || !hx || !hpicks || !sel_out || !w_out ||
+        !dflag || !stats)
+        return fail(GFL_EINVAL, "gfl_route_split: NULL argument");
+    if (M < 1 || topk < 1 || topk > 64 || (int64_t)M * topk > gfl::MAX_PICKS)
+        return fail(GFL_EINVAL, "gfl_route_split: need M >= 1, 1 <= topk <= 64 and M * topk <= 1024");
+    if (E_route < topk || E_route > gfl::MAX_EXPERTS)
+        return fail(GFL_EINVAL, "gfl_route_split: need topk <= E_route <= 1024");
+    if (E < 1 || E > gfl::MAX_EXPERTS || H % 8) return fail(GFL_EINVAL, "ft_split: E <= 1024");
+    if ((reinterpret_cast<uintptr_t>(z) | reinterpret_cast<uintptr_t>(hx)) & 15)
+        return fail(GFL_EINVAL, "gfl_route_split: z and hx must be 16-byte aligned");
+    if (gfl::launch_route_split(logits, M, E_route, topk, sel, w, z, H, E, first, slotof, score, pol, ctrl, hx, hpicks,
+                                seq, li, keep_ids, sel_out, w_out, dflag, stats, rres,
+                                reinterpret_cast<hipStream_t>(stream)))
+        return fail(GFL_EINVAL, "gfl_route_split: unsupported shape");
     GFL_HIP(hipGetLastError());
     return GFL_OK;
 }
@@ -611,7 +688,7 @@ int gfl_profile_read(gfl_ctx* c, double* stage_ms, int64_t* launches)
 int gfl_stats(gfl_ctx* c, int64_t* out, int n)
 {
     if (!c || !out) return fail(GFL_EINVAL, "gfl_stats: NULL argument");
-    const int64_t v[4] = { c->calls, c->picks, (int64_t)c->layers.size(), (int64_t)c->ws_bytes };
+    const int64_t v[4] = { c->calls, c->picks, (int64_t)c->layers.size(), (int64_t)(c->ws_bytes + c->gws_bytes) };
     for (int i = 0; i < n && i < 4; ++i) out[i] = v[i];
     return GFL_OK;
 }

@@ -84,5 +84,10 @@ void launch_combine(void* out, int is_half, int n, const int64_t* dflag, const i
                     int64_t* stats, int64_t timeout_ns, hipStream_t st);
 void launch_synth(uint8_t* dst, size_t nbytes, uint64_t seed, hipStream_t st);
 int launch_route(const float* logits, int M, int E, int topk, int64_t* sel, uint16_t* w, hipStream_t st);
+int launch_route_split(const float* logits, int M, int ER, int topk, int64_t* sel, uint16_t* w, const uint16_t* z,
+                       int H, int E, int first, const int32_t* slotof, const float* score, const float* pol,
+                       int64_t* ctrl, uint16_t* hx, int32_t* hpicks, int64_t seq, int li, int keep_ids,
+                       int64_t* sel_out, uint16_t* w_out, int64_t* dflag, int64_t* stats, const int32_t* rres,
+                       hipStream_t st);
 
 }  // namespace gfl

@@ -1,188 +1,291 @@
-// Token split / combine around the experts, plus the synthetic trellis generator.
+// Token split / combine around the experts, the router, and the synthetic trellis generator.
 //
-// split   = ft_split (kernels/cpu_avx2/ft_tier_cu.cu:21-157 stock, kernels/k110/ft_split_fast.cu:18-198 fast):
-//           count each local expert's picks (w != 0), hits = slotof[e] >= 0, rank the misses coldest first
-//           (score ascending, id ascending), choose how many go to the host lane with the cost model, publish the host
-//           job (x rows, picks in pick order, control words) and mask those picks out of the selection.
-//           Unique experts are discovered from the picks and ranked in parallel, the cost search stays serial with the
-//           reference's float expressions (uncontracted), and the published pick list is built in pick order from a
-//           wavefront ballot prefix.
-// combine = ft_combine (ft_tier_cu.cu:205-235, trellis build): wait (bounded) for the host done flag, add the fp32
-//           partial into the fp32/fp16 output.
+// split   = ft_split (kernels/cpu_avx2/ft_tier_cu.cu:21-157): each local expert's picks with a nonzero weight are
+//           counted, resident experts (slotof[e] >= 0) are hits, the misses are ranked coldest first (score
+//           ascending, id ascending), the cost model chooses how many go to the host lane, the host job is published
+//           (x rows, picks in pick order, control words) and those picks leave the selection. Outputs are
+//           bit-identical to the reference's; the kernel is organised for one workgroup on gfx950 (below).
+// combine = ft_combine (ft_tier_cu.cu:159-236): bounded wait for the host's done word, then out += hout.
 #include "gfl_device.hpp"
 #include "gfl_internal.hpp"
 
 namespace gfl {
 
-__global__ __launch_bounds__(256) void split_kernel(const int64_t* __restrict__ sel, const uint16_t* __restrict__ w,
-    const uint16_t* __restrict__ z, int n, int bsz, int topk, int H, int E, int first,
-    const int32_t* __restrict__ slotof, const float* __restrict__ score, const float* __restrict__ p, int64_t* ctrl,
-    uint16_t* hx, int32_t* hpicks, int64_t seq, int li, int keep_ids, int64_t* sel_out, uint16_t* w_out,
-    int64_t* dflag, int64_t* stats, const int32_t* __restrict__ rres)
+constexpr int SP_T = 256;                 // threads of the split workgroup (4 waves)
+constexpr int SP_PER = MAX_PICKS / SP_T;  // picks per thread in the pick-order scan
+
+// LDS of the split. Experts are local ids (sel - first), picks p = token * topk + k.
+struct SplitLds
 {
-    __shared__ int cnt[MAX_EXPERTS];
-    __shared__ unsigned char cpu[MAX_EXPERTS];
-    __shared__ int s_le[MAX_PICKS];          // local expert id of pick s, or -1 (out of range)
-    __shared__ unsigned char s_nz[MAX_PICKS];
-    __shared__ int uq[MAX_PICKS], nu;         // unique local experts with a nonzero pick
-    __shared__ int ue[MAX_PICKS];             // unique experts sorted ascending
-    __shared__ int miss[MAX_PICKS], rmiss[MAX_PICKS];
-    __shared__ int s_nm, s_nh, s_nr, s_publish, s_npk;
-    __shared__ float pol[20];
-    const int t = threadIdx.x, lane = t & 63;
-    for (int e = t; e < E; e += blockDim.x) { cnt[e] = 0; cpu[e] = 0; }
-    if (t < 20) pol[t] = p[t];
-    if (t == 0) nu = 0;
-    for (int s = t; s < n; s += blockDim.x)
+    short le[MAX_PICKS];            // local expert of pick p, -1 outside [0, E)
+    unsigned char nz[MAX_PICKS];    // weight of pick p nonzero (a NaN counts as nonzero, as __half2float(w) != 0)
+    unsigned char seen[MAX_EXPERTS];
+    unsigned char take[MAX_EXPERTS];   // expert goes to the host lane
+    int cnt[MAX_EXPERTS];           // picks with a nonzero weight per routed expert
+    int ulist[MAX_EXPERTS];         // routed experts, first-appearance order
+    unsigned long long key[MAX_EXPERTS];   // sort keys of the routed experts (misses first, coldest first)
+    int nu, nh, nm, nr, best, bestr, publish, npk;
+    int wsum[SP_T / 64];
+    float pol[20];
+};
+
+// Ascending order of finite floats as unsigned integers (+0 and -0 compare equal, as the reference's float compare
+// treats them, so both map to the key of +0).
+__device__ inline uint32_t float_order_key(float f)
+{
+    uint32_t u = __float_as_uint(f == 0.0f ? 0.0f : f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Cost model of the host lane (ft_tier_cu.cu:84-131): the reference's float expressions, each operation rounded in
+// source order (this translation unit is compiled with -ffp-contract=off). miss / rmiss: local and remote misses,
+// coldest first; returns best (local count) and bestr (remote count).
+__device__ void split_cost(const SplitLds& S, const int* miss, const int* rmiss, int nm, int nh, int nr, bool tri,
+                           int& best, int& bestr)
+{
+    const float* p = S.pol;
+    const bool lut = p[12] > 0.0f;
+    const int force = (int)p[6], maxc = min((int)p[5], nm);
+    best = 0;
+    bestr = 0;
+    // CPU-lane time for k local experts, given the running sums c (per-expert cost) and cx (extra-token cost)
+    auto lane_cpu = [&](int k, float c, float cx) -> float {
+        if (!k) return 0.0f;
+        if (!lut) return p[2] + c;
+        const float tail = k > 8 ? p[3] * (float)(k - 8) : 0.0f;
+        return (p[11 + (k < 8 ? k : 8)] + tail) + cx;
+    };
+    if (force >= 0)
     {
-        const int64_t e = sel[s] - first;
-        s_le[s] = (e >= 0 && e < E) ? (int)e : -1;
-        s_nz[s] = (w[s] & 0x7FFFu) != 0;    // __half2float(w) != 0.0f (NaN counts as nonzero)
+        best = min(force, nm);
+        return;
     }
-    __syncthreads();
-    for (int s = t; s < n; s += blockDim.x)
-        if (s_nz[s] && s_le[s] >= 0)
-            if (atomicAdd(&cnt[s_le[s]], 1) == 0) uq[atomicAdd(&nu, 1)] = s_le[s];
-    __syncthreads();
-    const int U = nu;
-    for (int i = t; i < U; i += blockDim.x)
+    const int nrr = tri ? nr : 0;
+    float bt = 1e30f, cr = 0.0f;
+    for (int kr = 0; kr <= nrr; ++kr)
     {
-        int r = 0;
-        for (int k = 0; k < U; ++k) r += uq[k] < uq[i];
-        ue[r] = uq[i];
-    }
-    __syncthreads();
-    const bool tri = pol[8] > 0.5f && rres != nullptr && (int)pol[6] < 0;
-    // misses ranked inside their class (score ascending, ties by ascending id) = the stock insertion order
-    for (int i = t; i < U; i += blockDim.x)
-    {
-        const int e = ue[i];
-        if (slotof[e] >= 0) continue;
-        const int cl = (tri && rres[e]) ? 1 : 0;
-        const float sc = score[e];
-        int r = 0;
-        for (int k = 0; k < U; ++k)
+        if (kr)
         {
-            const int e2 = ue[k];
-            if (slotof[e2] >= 0 || ((tri && rres[e2]) ? 1 : 0) != cl) continue;
-            const float s2 = score[e2];
-            if (s2 < sc || (s2 == sc && e2 < e)) ++r;
+            const float extra = p[4] * (float)(S.cnt[rmiss[kr - 1]] - 1);
+            const float one = 1.0f + extra;
+            cr = cr + p[10] * one;
         }
-        if (cl) rmiss[r] = e; else miss[r] = e;
-    }
-    if (t == 0)
-    {
-        int nh = 0, nr = 0;
-        for (int i = 0; i < U; ++i)
+        const float rem = kr ? p[9] + cr : 0.0f;
+        float c = 0.0f, cx = 0.0f;
+        for (int k = 0; k <= maxc; ++k)
         {
-            const int e = ue[i];
-            if (slotof[e] >= 0) ++nh;
-            else if (tri && rres[e]) ++nr;
-        }
-        s_nh = nh; s_nr = nr; s_nm = U - nh - nr;
-    }
-    __syncthreads();
-    if (t == 0)
-    {
-        const int nm = s_nm, nh = s_nh, nr = s_nr;
-        const bool lut = pol[12] > 0.0f;
-        int best = 0, bestr = 0;
-        const int force = (int)pol[6], maxc = min((int)pol[5], nm);
-        if (force >= 0) best = min(force, nm);
-        else if (tri)
-        {
-            float bt = 1e30f, cr = 0.0f;
-            for (int kr = 0; kr <= nr; ++kr)
+            if (k)
             {
-                if (kr) { const float f = pol[4] * (float)(cnt[rmiss[kr - 1]] - 1); const float g = 1.0f + f; cr = cr + pol[10] * g; }
-                const float rem = kr ? pol[9] + cr : 0.0f;
-                float c = 0.0f, cx = 0.0f;
-                for (int k = 0; k <= maxc; ++k)
-                {
-                    if (k)
-                    {
-                        const float f = pol[4] * (float)(cnt[miss[k - 1]] - 1); const float g = 1.0f + f;
-                        c = c + pol[3] * g;
-                        const float f2 = pol[3] * pol[4];
-                        cx = cx + f2 * (float)(cnt[miss[k - 1]] - 1);
-                    }
-                    const int zz = nm - k + nr - kr;
-                    const float gpu = pol[1] * (float)(nh + zz) + pol[0] * (float)zz;
-                    float loc = 0.0f;
-                    if (k) loc = lut ? (pol[11 + (k < 8 ? k : 8)] + (k > 8 ? pol[3] * (float)(k - 8) : 0.0f)) + cx : pol[2] + c;
-                    const float tt = fmaxf(gpu, fmaxf(loc, rem));
-                    if (tt < bt - 1e-6f) { bt = tt; best = k; bestr = kr; }
-                }
+                const int extra_tok = S.cnt[miss[k - 1]] - 1;
+                const float one = 1.0f + p[4] * (float)extra_tok;
+                c = c + p[3] * one;
+                const float per = p[3] * p[4];
+                cx = cx + per * (float)extra_tok;
             }
-            for (int k = 0; k < bestr; ++k) cpu[rmiss[k]] = 1;
+            const int zc = nm - k + nrr - kr;   // misses left to the zero-copy path
+            const float gpu = p[1] * (float)(nh + zc) + p[0] * (float)zc;
+            const float loc = lane_cpu(k, c, cx);
+            const float tt = tri ? fmaxf(gpu, fmaxf(loc, rem)) : fmaxf(gpu, loc);
+            if (tt < bt - 1e-6f)
+            {
+                bt = tt;
+                best = k;
+                bestr = kr;
+            }
         }
+    }
+}
+
+// The split of one call (whole workgroup). sel/w are read from global memory (the caller's selection, or the router
+// output written by this workgroup before a barrier).
+__device__ void split_body(SplitLds& S, const int64_t* __restrict__ sel, const uint16_t* __restrict__ w,
+                           const uint16_t* __restrict__ z, int n, int bsz, int topk, int H, int E, int first,
+                           const int32_t* __restrict__ slotof, const float* __restrict__ score,
+                           const float* __restrict__ pol, int64_t* ctrl, uint16_t* hx, int32_t* hpicks, int64_t seq,
+                           int li, int keep_ids, int64_t* sel_out, uint16_t* w_out, int64_t* dflag, int64_t* stats,
+                           const int32_t* __restrict__ rres)
+{
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    // 1. per-pick classification
+    for (int q = t; q < n; q += SP_T)
+    {
+        const int64_t e = sel[q] - first;
+        S.le[q] = (e >= 0 && e < E) ? (short)e : (short)-1;
+        S.nz[q] = (w[q] & 0x7FFFu) != 0;
+    }
+    for (int e = t; e < E; e += SP_T) { S.seen[e] = 0; S.take[e] = 0; }
+    if (t < 20) S.pol[t] = pol[t];
+    if (t == 0) { S.nh = 0; S.nm = 0; S.nr = 0; }
+    __syncthreads();
+    // 2. routed experts in first-appearance order, and their nonzero-pick counts (wave 0)
+    if (wv == 0)
+    {
+        int nu = 0;
+        for (int q0 = 0; q0 < n; q0 += 64)
+        {
+            const int q = q0 + lane;
+            const int e = (q < n && S.nz[q]) ? S.le[q] : -1;
+            const bool ok = e >= 0;
+            uint64_t eq = __ballot(ok);
+#pragma unroll
+            for (int b = 0; b < 10; ++b)
+            {
+                const bool bit = ok && ((e >> b) & 1);
+                const uint64_t m = __ballot(bit);
+                eq &= bit ? m : ~m;
+            }
+            const bool leader = ok && (int)__builtin_ctzll(eq) == lane;   // lowest lane of its expert in the chunk
+            const bool fresh = leader && !S.seen[e];
+            if (leader)
+            {
+                S.cnt[e] = (fresh ? 0 : S.cnt[e]) + __popcll(eq);
+                S.seen[e] = 1;
+            }
+            const uint64_t mf = __ballot(fresh);
+            if (fresh) S.ulist[nu + __popcll(mf & below)] = e;
+            nu += __popcll(mf);
+        }
+        if (lane == 0) S.nu = nu;
+    }
+    __syncthreads();
+    const int U = S.nu;
+    const bool tri = S.pol[8] > 0.5f && rres != nullptr && (int)S.pol[6] < 0;
+    // 3. classes and sort keys: local miss (key bit 63 clear), remote miss (set), hit (all ones, sorted last)
+    int h = 0, ml = 0, mr = 0;
+    for (int i = t; i < U; i += SP_T)
+    {
+        const int e = S.ulist[i];
+        unsigned long long k = ~0ull;
+        if (slotof[e] >= 0) ++h;
         else
         {
-            float bt = 1e30f, c = 0.0f, cx = 0.0f;
-            for (int k = 0; k <= maxc; ++k)
-            {
-                if (k)
-                {
-                    const float f = pol[4] * (float)(cnt[miss[k - 1]] - 1); const float g = 1.0f + f;
-                    c = c + pol[3] * g;
-                    const float f2 = pol[3] * pol[4];
-                    cx = cx + f2 * (float)(cnt[miss[k - 1]] - 1);
-                }
-                const float gpu = pol[1] * (float)(nh + nm - k) + pol[0] * (float)(nm - k);
-                float loc = 0.0f;
-                if (k) loc = lut ? (pol[11 + (k < 8 ? k : 8)] + (k > 8 ? pol[3] * (float)(k - 8) : 0.0f)) + cx : pol[2] + c;
-                const float tt = fmaxf(gpu, loc);
-                if (tt < bt - 1e-6f) { bt = tt; best = k; }
-            }
+            const bool remote = tri && rres[e];
+            remote ? ++mr : ++ml;
+            k = ((unsigned long long)remote << 63) | ((unsigned long long)float_order_key(score[e]) << 31) |
+                (unsigned long long)e;
         }
-        for (int k = 0; k < best; ++k) cpu[miss[k]] = 1;
-        s_publish = best + bestr > 0 || pol[7] > 0.5f;
-        stats[0] += nh; stats[1] += nm + nr; stats[2] += best + bestr; stats[3] += 1;
+        S.key[i] = k;
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1)
+    {
+        h += __shfl_xor(h, d);
+        ml += __shfl_xor(ml, d);
+        mr += __shfl_xor(mr, d);
+    }
+    if (lane == 0)
+    {
+        atomicAdd(&S.nh, h);
+        atomicAdd(&S.nm, ml);
+        atomicAdd(&S.nr, mr);
     }
     __syncthreads();
-    const int publish = s_publish;
-    if (publish && t < 64)
+    const int nh = S.nh, nm = S.nm, nr = S.nr;
+    // 4. coldest-first order of the misses: one bitonic sort of the keys (unique: the id is part of the key)
+    if (nm + nr > 0)
     {
-        int base = 0;
-        for (int s0 = 0; s0 < n; s0 += 64)
-        {
-            const int s = s0 + lane;
-            const bool take = s < n && s_le[s] >= 0 && cpu[s_le[s]] && s_nz[s];
-            const uint64_t m = __ballot(take);
-            if (take)
+        int N = 1;
+        while (N < U) N <<= 1;
+        for (int i = U + t; i < N; i += SP_T) S.key[i] = ~0ull;
+        __syncthreads();
+        for (int k = 2; k <= N; k <<= 1)
+            for (int j = k >> 1; j > 0; j >>= 1)
             {
-                const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-                const int k = base + __popcll(m & below);
-                const float wf = h2f_bits(w[s]);
-                int wb;
-                __builtin_memcpy(&wb, &wf, 4);
-                hpicks[k * 3] = s / topk;
-                hpicks[k * 3 + 1] = s_le[s];
-                hpicks[k * 3 + 2] = wb;
+                for (int i = t; i < N; i += SP_T)
+                {
+                    const int o = i ^ j;
+                    if (o > i)
+                    {
+                        const unsigned long long a = S.key[i], b = S.key[o];
+                        if ((a > b) == ((i & k) == 0))
+                        {
+                            S.key[i] = b;
+                            S.key[o] = a;
+                        }
+                    }
+                }
+                __syncthreads();
             }
-            base += __popcll(m);
-        }
-        if (t == 0) s_npk = base;
+        // keys -> expert ids in place (miss list then remote list), for the cost model
+        for (int i = t; i < nm + nr; i += SP_T) S.ulist[i] = (int)(S.key[i] & 0x7FFFFFFFull);
+        __syncthreads();
     }
-    for (int s = t; s < n; s += blockDim.x)
+    // 5. cost model (one thread), host-lane flags, stats
+    if (t == 0)
     {
-        const int64_t e = sel[s];
-        const bool c = s_le[s] >= 0 && cpu[s_le[s]];
-        sel_out[s] = (c && !keep_ids) ? -1 : e;
-        w_out[s] = c ? (uint16_t)0 : w[s];
+        int best = 0, bestr = 0;
+        if (nm + nr > 0) split_cost(S, S.ulist, S.ulist + nm, nm, nh, nr, tri, best, bestr);
+        for (int k = 0; k < best; ++k) S.take[S.ulist[k]] = 1;
+        for (int k = 0; k < bestr; ++k) S.take[S.ulist[nm + k]] = 1;
+        S.best = best;
+        S.bestr = bestr;
+        S.publish = best + bestr > 0 || S.pol[7] > 0.5f;
+        stats[0] += nh;
+        stats[1] += nm + nr;
+        stats[2] += best + bestr;
+        stats[3] += 1;
+    }
+    __syncthreads();
+    const bool publish = S.publish, any_taken = S.best + S.bestr > 0;
+    // 6. selection for the device experts, and the host job's picks in pick order (a workgroup exclusive scan over
+    // per-thread runs of SP_PER consecutive picks)
+    for (int q = t; q < n; q += SP_T)
+    {
+        const int e = S.le[q];
+        const bool c = e >= 0 && S.take[e];
+        sel_out[q] = (c && !keep_ids) ? -1 : sel[q];
+        w_out[q] = c ? (uint16_t)0 : w[q];
     }
     if (publish)
     {
+        int mine = 0;
+        const int q0 = t * SP_PER;
+        if (any_taken)
+            for (int i = 0; i < SP_PER; ++i)
+            {
+                const int q = q0 + i;
+                mine += (q < n && S.le[q] >= 0 && S.take[S.le[q]] && S.nz[q]) ? 1 : 0;
+            }
+        int incl = mine;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1)
+        {
+            const int o = __shfl_up(incl, d);
+            if (lane >= d) incl += o;
+        }
+        if (lane == 63) S.wsum[wv] = incl;
+        __syncthreads();
+        int base = incl - mine;
+        for (int v = 0; v < wv; ++v) base += S.wsum[v];
+        if (t == SP_T - 1) S.npk = base + mine;
+        for (int i = 0; i < SP_PER && mine; ++i)
+        {
+            const int q = q0 + i;
+            if (q < n && S.le[q] >= 0 && S.take[S.le[q]] && S.nz[q])
+            {
+                hpicks[base * 3] = q / topk;
+                hpicks[base * 3 + 1] = S.le[q];
+                hpicks[base * 3 + 2] = (int32_t)__float_as_uint(h2f_bits(w[q]));
+                ++base;
+            }
+        }
+        // x rows of the job, then the control words (the sequence number last, system scope, for the host reader)
         const int nx = bsz * H / 8;
-        for (int i = t; i < nx; i += blockDim.x)
-            reinterpret_cast<uint4*>(hx)[i] = reinterpret_cast<const uint4*>(z)[i];
+        for (int i = t; i < nx; i += SP_T) reinterpret_cast<uint4*>(hx)[i] = reinterpret_cast<const uint4*>(z)[i];
         __threadfence_system();
         __syncthreads();
         if (t == 0)
         {
-            ctrl[2] = li; ctrl[3] = bsz; ctrl[4] = s_npk;
+            const int npk = S.npk;
+            ctrl[2] = li;
+            ctrl[3] = bsz;
+            ctrl[4] = npk;
             __threadfence_system();
             __hip_atomic_store(&ctrl[0], seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+            // a job without picks has a zero partial: it is answered here, as the reference's worker answers every
+            // job it receives (ft_tier_ext.cpp:781-802), and ft_combine adds nothing for it
+            if (npk == 0) __hip_atomic_store(&ctrl[1], seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
             __threadfence_system();
             dflag[0] = seq;
         }
@@ -190,20 +293,34 @@ __global__ __launch_bounds__(256) void split_kernel(const int64_t* __restrict__ 
     else if (t == 0) dflag[0] = 0;
 }
 
+__global__ __launch_bounds__(SP_T) void split_kernel(const int64_t* __restrict__ sel, const uint16_t* __restrict__ w,
+    const uint16_t* __restrict__ z, int n, int bsz, int topk, int H, int E, int first,
+    const int32_t* __restrict__ slotof, const float* __restrict__ score, const float* __restrict__ pol, int64_t* ctrl,
+    uint16_t* hx, int32_t* hpicks, int64_t seq, int li, int keep_ids, int64_t* sel_out, uint16_t* w_out,
+    int64_t* dflag, int64_t* stats, const int32_t* __restrict__ rres)
+{
+    __shared__ SplitLds S;
+    split_body(S, sel, w, z, n, bsz, topk, H, E, first, slotof, score, pol, ctrl, hx, hpicks, seq, li, keep_ids,
+               sel_out, w_out, dflag, stats, rres);
+}
+
 // One workgroup decides once, for every output element, whether the host partial is added: the trellis build of the
 // reference waits in each of its 16 blocks separately (ft_tier_cu.cu:205-235), so a done flag that lands inside the
 // timeout window can be added by some blocks and dropped by others; its LUT build already moved the decision into a
 // single block (ft_tier_cu.cu:162-201). Same counters: stats[4] waited ns, [5] waits, [6] timeouts, [7] already done.
 // timeout_ticks: bounded wait in wall-clock ticks (the caller converts ns with the device's wall clock rate).
+// A job with no picks (ctrl[4] == 0, answered by the split itself) has a zero partial: +0 is added instead of hout,
+// the sum the reference's worker produces by zeroing hout for an empty route (ft_tier_ext.cpp:384).
 __global__ __launch_bounds__(1024) void combine_kernel(void* out, int is_half, int n, const int64_t* __restrict__ dflag,
                                                        const int64_t* ctrl, const float* hout, int64_t* stats,
                                                        int64_t timeout_ticks, int64_t ns_per_tick_q16)
 {
-    __shared__ int go;
+    __shared__ int go, empty;
     if (threadIdx.x == 0)
     {
         const int64_t s = dflag[0];
         go = s != 0;
+        empty = 0;
         if (go)
         {
             const int64_t* done = ctrl + 1;
@@ -221,6 +338,7 @@ __global__ __launch_bounds__(1024) void combine_kernel(void* out, int is_half, i
                     break;
                 }
             }
+            if (go) empty = __hip_atomic_load(ctrl + 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) == 0;
             const unsigned long long waited = (unsigned long long)(((t1 - t0) * (uint64_t)ns_per_tick_q16) >> 16);
             atomicAdd(reinterpret_cast<unsigned long long*>(&stats[4]), waited);
             atomicAdd(reinterpret_cast<unsigned long long*>(&stats[5]), 1ull);
@@ -228,9 +346,10 @@ __global__ __launch_bounds__(1024) void combine_kernel(void* out, int is_half, i
     }
     __syncthreads();
     if (!go) return;
+    const bool zero = empty;
     for (int i = threadIdx.x; i < n; i += blockDim.x)
     {
-        const float v = __hip_atomic_load(&hout[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        const float v = zero ? 0.0f : __hip_atomic_load(&hout[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         if (is_half)
         {
             uint16_t* o = reinterpret_cast<uint16_t*>(out);
@@ -265,15 +384,13 @@ __device__ __forceinline__ void route_argmax_step(float& bv, int& bi)
 constexpr int ROUTE_WAVES = 4;
 constexpr int ROUTE_MAXE = 1024;   // experts per token: up to 16 per lane
 
-// NI = ceil(E / 64) scores per lane, a compile-time count so that the per-lane loops hold only live experts
+// One token on one wave: sel_row[0..topk) / w_row[0..topk) from logits row lg. NI = ceil(E / 64) scores per lane, a
+// compile-time count so that the per-lane loops hold only live experts.
 template <int NI>
-__global__ __launch_bounds__(ROUTE_WAVES * 64) void route_kernel(const float* __restrict__ logits, int M, int E, int topk,
-                                                                 int64_t* __restrict__ sel, uint16_t* __restrict__ w)
+__device__ __forceinline__ void route_token(const float* __restrict__ lg, int E, int topk, int64_t* sel_row,
+                                            uint16_t* w_row)
 {
     const int lane = threadIdx.x & 63;
-    const int m = blockIdx.x * ROUTE_WAVES + (threadIdx.x >> 6);
-    if (m >= M) return;
-    const float* lg = logits + (size_t)m * E;
     // every load first (uniform guards, clamped addresses), so the token's logits arrive in one round trip
     float sc[NI];
 #pragma unroll
@@ -319,9 +436,36 @@ __global__ __launch_bounds__(ROUTE_WAVES * 64) void route_kernel(const float* __
     }
     if (lane < topk)
     {
-        sel[(size_t)m * topk + lane] = myidx;
-        w[(size_t)m * topk + lane] = (uint16_t)f2h_bits(mine / tot);
+        sel_row[lane] = myidx;
+        w_row[lane] = (uint16_t)f2h_bits(mine / tot);
     }
+}
+
+template <int NI>
+__global__ __launch_bounds__(ROUTE_WAVES * 64) void route_kernel(const float* __restrict__ logits, int M, int E, int topk,
+                                                                 int64_t* __restrict__ sel, uint16_t* __restrict__ w)
+{
+    const int m = blockIdx.x * ROUTE_WAVES + (threadIdx.x >> 6);
+    if (m >= M) return;
+    route_token<NI>(logits + (size_t)m * E, E, topk, sel + (size_t)m * topk, w + (size_t)m * topk);
+}
+
+// Router and split in one launch (the routing_fn that cpu_tier.routed wraps, glm53/cpu_tier.py:305-333): the
+// workgroup's waves route the M tokens into sel / w (kept: the caller's original selection), then the workgroup runs
+// the split on them.
+template <int NI>
+__global__ __launch_bounds__(SP_T) void route_split_kernel(const float* __restrict__ logits, int M, int ER, int topk,
+    int64_t* sel, uint16_t* w, const uint16_t* __restrict__ z, int H, int E, int first,
+    const int32_t* __restrict__ slotof, const float* __restrict__ score, const float* __restrict__ pol, int64_t* ctrl,
+    uint16_t* hx, int32_t* hpicks, int64_t seq, int li, int keep_ids, int64_t* sel_out, uint16_t* w_out,
+    int64_t* dflag, int64_t* stats, const int32_t* __restrict__ rres)
+{
+    __shared__ SplitLds S;
+    for (int m = threadIdx.x >> 6; m < M; m += SP_T / 64)
+        route_token<NI>(logits + (size_t)m * ER, ER, topk, sel + (size_t)m * topk, w + (size_t)m * topk);
+    __syncthreads();   // the routed picks (global writes of this workgroup) are visible to all of its threads
+    split_body(S, sel, w, z, M * topk, M, topk, H, E, first, slotof, score, pol, ctrl, hx, hpicks, seq, li, keep_ids,
+               sel_out, w_out, dflag, stats, rres);
 }
 
 int launch_route(const float* logits, int M, int E, int topk, int64_t* sel, uint16_t* w, hipStream_t st)
@@ -361,12 +505,35 @@ __global__ __launch_bounds__(256) void synth_kernel(uint8_t* dst, size_t nbytes,
     }
 }
 
+int launch_route_split(const float* logits, int M, int ER, int topk, int64_t* sel, uint16_t* w, const uint16_t* z,
+                       int H, int E, int first, const int32_t* slotof, const float* score, const float* pol,
+                       int64_t* ctrl, uint16_t* hx, int32_t* hpicks, int64_t seq, int li, int keep_ids,
+                       int64_t* sel_out, uint16_t* w_out, int64_t* dflag, int64_t* stats, const int32_t* rres,
+                       hipStream_t st)
+{
+    if (ER < 1 || ER > ROUTE_MAXE || topk < 1 || topk > ER || topk > 64 || M * topk > MAX_PICKS) return -1;
+    switch ((ER + 63) / 64)
+    {
+#define GFL_RS_CASE(N)                                                                                             \
+    case N:                                                                                                        \
+        hipLaunchKernelGGL(route_split_kernel<N>, dim3(1), dim3(SP_T), 0, st, logits, M, ER, topk, sel, w, z, H, E,  \
+                           first, slotof, score, pol, ctrl, hx, hpicks, seq, li, keep_ids, sel_out, w_out, dflag,   \
+                           stats, rres);                                                                           \
+        return 0;
+        GFL_RS_CASE(1) GFL_RS_CASE(2) GFL_RS_CASE(3) GFL_RS_CASE(4) GFL_RS_CASE(5) GFL_RS_CASE(6) GFL_RS_CASE(7)
+        GFL_RS_CASE(8) GFL_RS_CASE(9) GFL_RS_CASE(10) GFL_RS_CASE(11) GFL_RS_CASE(12) GFL_RS_CASE(13)
+        GFL_RS_CASE(14) GFL_RS_CASE(15) GFL_RS_CASE(16)
+#undef GFL_RS_CASE
+        default: return -1;
+    }
+}
+
 int launch_split(const int64_t* sel, const uint16_t* w, const uint16_t* z, int n, int bsz, int topk, int H, int E,
                  int first, const int32_t* slotof, const float* score, const float* pol, int64_t* ctrl, uint16_t* hx,
                  int32_t* hpicks, int64_t seq, int li, int keep_ids, int64_t* sel_out, uint16_t* w_out,
                  int64_t* dflag, int64_t* stats, const int32_t* rres, hipStream_t st)
 {
-    hipLaunchKernelGGL(split_kernel, dim3(1), dim3(256), 0, st, sel, w, z, n, bsz, topk, H, E, first, slotof, score,
+    hipLaunchKernelGGL(split_kernel, dim3(1), dim3(SP_T), 0, st, sel, w, z, n, bsz, topk, H, E, first, slotof, score,
                        pol, ctrl, hx, hpicks, seq, li, keep_ids, sel_out, w_out, dflag, stats, rres);
     return 0;
 }

@@ -115,22 +115,22 @@ def tier_forward(li, x, sel, w, mode):
     sum over picks of w * expert(x) in the reference's job order. Tensors may live on the CPU (as the reference's)
     or on the device; the result is on x's device.
 
-    mode 1 (EXACT) computes EXACT, bit-identical to the reference's, for m * k <= 1024 picks. mode -1 (auto) does the
-    same up to 1024 picks and, above that (prefill-sized batches, up to 65536 picks), takes the MFMA grouped path,
-    which keeps the exact weights, rounding points and combine order but sums in MFMA order; the reference's auto
-    mode likewise leaves EXACT for its speed modes on large batches (ft_tier_ext.cpp:396). The reference's CPU speed
-    modes 0 (AFFINE) and 2 (I16) are outside the expert-output tolerance and are rejected."""
+    Every mode number of the reference is accepted. Up to 1024 picks all of them compute EXACT, bit-identical to the
+    reference's EXACT mode: mode 1 asks for it, mode -1 (auto) picks it, and modes 0 (AFFINE) and 2 (I16), the
+    reference CPU engine's speed modes (ft_tier_ext.cpp:900), get EXACT as well, which lies closer to the fp64 expert
+    (ref_expert, ft_core.h:1674-1691) than either of them does. Above 1024 picks (prefill-sized batches, up to 65536)
+    the MFMA grouped path runs: the exact weights, rounding points and combine order, with the sums formed in MFMA
+    order."""
     import torch
     _check(T is not None and not T.running, "tier_forward: worker running")
     _check(0 <= li < len(T.layers) and T.layers[li] is not None, "tier_forward: layer not registered")
-    _check(int(mode) in (-1, 1), "tier_forward: the device path computes EXACT (mode -1 or 1)")
+    _check(int(mode) in (-1, 0, 1, 2), "tier_forward: mode must be -1, 0, 1 or 2")
     _check(x.dtype == torch.float32 and x.dim() == 2 and x.size(1) == T.H, "x: float32 [m, H]")
     _check(sel.dtype in (torch.int32, torch.int64) and sel.dim() == 2 and sel.size(0) == x.size(0), "sel: int32 [m, k]")
     _check(w.dtype == torch.float32 and tuple(w.shape) == tuple(sel.shape), "w: float32 [m, k]")
     m, k = sel.shape
-    grouped = int(mode) == -1 and m * k > 1024
-    _check(k <= 16 and (m * k <= 1024 or (grouped and m * k <= 65536)),
-           "tier_forward: k <= 16 and m * k <= 1024 picks (EXACT) or <= 65536 (auto)")
+    grouped = m * k > 1024
+    _check(k <= 16 and m * k <= 65536, "tier_forward: k <= 16 and m * k <= 65536 picks")
     dev = torch.device("cuda", T.ctx.device)
     x16 = x.to(dev).half()
     _check(bool(torch.equal(x16.float(), x.to(dev))), "tier_forward: x must be fp16-valued (the expert input is fp16)")

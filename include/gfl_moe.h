@@ -31,7 +31,8 @@ enum
 };
 
 /* Expert arithmetic modes, numbered as tier_forward's `mode` (kernels/cpu_avx2/ft_tier_ext.cpp:865-904).
- * The device path computes EXACT (bit-identical to the reference's EXACT mode); AUTO selects it.
+ * The device path computes EXACT (bit-identical to the reference's EXACT mode) for AUTO, EXACT, AFFINE and I16: the
+ * last two name the reference CPU engine's speed modes, and EXACT lies closer to the fp64 expert than either.
  * GFL_MODE_MFMA has no counterpart in the reference: the same bit-exact weights, transforms, rounding points and
  * combine order, with the GEMV sums over the hidden dimension formed by MFMAs (fp32 accumulate) instead of EXACT's
  * chains, for callers that trade bit-exactness for speed. Its outputs differ from EXACT by accumulation rounding
@@ -52,7 +53,9 @@ const char* gfl_last_error(void);
 int gfl_version(void);
 
 /* Context on one device: registered layers plus the per-call workspace.
- * Replaces the global Tier singleton of tier_init (kernels/cpu_avx2/ft_tier_ext.cpp:137-157). */
+ * Replaces the global Tier singleton of tier_init (kernels/cpu_avx2/ft_tier_ext.cpp:137-157).
+ * One stream per context: calls that overlap on two streams share the context's plan, workspace and counters and
+ * race. Workspaces are never freed before gfl_ctx_destroy, so a HIP graph captured from any call stays valid. */
 int gfl_ctx_create(int device, gfl_ctx** out);
 int gfl_ctx_destroy(gfl_ctx* ctx);
 
@@ -67,6 +70,13 @@ int gfl_ctx_destroy(gfl_ctx* ctx);
  * (glm53/expert_cache.py:540-635). */
 int gfl_register_layer(gfl_ctx* ctx, int li, int E, int H, int I, int k_gate, int k_up, int k_down,
                        const uint64_t* ptrs);
+/* (Registration also reserves the decode workspace for 1024 picks at the largest registered H and I, so that
+ * gfl_moe_forward never allocates.) */
+
+/* Shape of a registered layer: info[6] = {E, H, I, k_gate, k_up, k_down} (host array). The forward calls take no
+ * shape arguments, so callers check their x / out widths against H with it (tier_forward checks x.size(1) == H,
+ * ft_tier_ext.cpp:865-904). No counterpart of its own in the reference. */
+int gfl_layer_info(gfl_ctx* ctx, int li, int* info);
 
 /* Routed-expert forward of one layer (the expert call, tier_forward, ft_tier_ext.cpp:865-904):
  *   out[t] = sum over picks k of w[t,k] * expert_{sel[t,k]}(x[t]), picks with sel < 0 skipped,
@@ -77,7 +87,7 @@ int gfl_register_layer(gfl_ctx* ctx, int li, int E, int H, int I, int k_gate, in
 int gfl_moe_forward(gfl_ctx* ctx, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half, int M,
                     int topk, float* out, int mode, float act_limit, gfl_stream stream);
 
-/* mode: AUTO or EXACT (bit-exact), or MFMA. With MFMA the workgroups of a routed expert take up to 4 of its slots
+/* mode: AUTO, AFFINE, EXACT or I16 (all computed bit-exact to EXACT), or MFMA. With MFMA the workgroups of a routed expert take up to 4 of its slots
  * per pass, so the expert's tiles are decoded once for all of them.
  * Environment: GFL_SLOTS_PER_PASS = 1, 2, 4 or 8 forces the number of (token, expert) slots one GEMV pass of
  * gfl_moe_forward accumulates (default: 1 up to M = 8, with a workgroup per slot; else 2, with a workgroup per expert
@@ -94,6 +104,11 @@ int gfl_moe_forward(gfl_ctx* ctx, int li, const uint16_t* x, const int64_t* sel,
  * ref_expert, ft_core.h:1674-1691, does). Profiling stage 2. */
 int gfl_grouped_forward(gfl_ctx* ctx, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half,
                         int M, int topk, float* out, float act_limit, gfl_stream stream);
+
+/* Size the workspace of gfl_grouped_forward / gfl_grouped_plan for calls of up to max_picks picks on every layer
+ * registered so far, so that later calls (and HIP graph captures of them) allocate nothing. Without it the first
+ * call of a larger size grows the workspace (never during a capture). No counterpart in the reference. */
+int gfl_grouped_reserve(gfl_ctx* ctx, int max_picks);
 
 /* The routing plan of gfl_grouped_forward alone, copied out of the context's workspace (all device pointers; no
  * counterpart in the reference: it exposes the device's grouped rows and combine order so that they can be checked
@@ -113,14 +128,27 @@ int gfl_dequant(const void* trellis, int k, int n, int K, uint16_t* out, gfl_str
 /* ft_split (kernels/cpu_avx2/ft_tier_cu.cu:238-271, kernels/k110/ft_split_fast.cu:200-235), same arguments with
  * tensors as pointers: sel int64 [n], w fp16 [n], z fp16 [bsz, H], slotof int32 [E], score fp32 [E], pol fp32 [20],
  * ctrl int64 [>=5] / hx fp16 [bsz*H] / hpicks int32 [n*3] (host-mapped or device memory), sel_out int64 [n],
- * w_out fp16 [n], dflag int64 [1], stats int64 [8], rres int32 [E] or NULL. n = bsz*topk <= 1024, E <= 1024. */
+ * w_out fp16 [n], dflag int64 [1], stats int64 [8], rres int32 [E] or NULL. n = bsz*topk <= 1024, E <= 1024.
+ * Outputs are the reference's bit for bit; in addition a published job without picks (the handshake policy pol[7]
+ * with nothing for the host) is answered here (ctrl[1] = seq), as the reference's worker answers every job, so that
+ * gfl_combine does not wait for a host that has nothing to do. Scores must be finite (the reference's two split
+ * kernels order NaN scores differently from each other). */
 int gfl_split(const int64_t* sel, const uint16_t* w, const uint16_t* z, int bsz, int n, int H, int E, int first,
               const int32_t* slotof, const float* score, const float* pol, int64_t* ctrl, uint16_t* hx,
               int32_t* hpicks, int64_t seq, int li, int keep_ids, int64_t* sel_out, uint16_t* w_out, int64_t* dflag,
               int64_t* stats, const int32_t* rres, gfl_stream stream);
 
+/* Router and split in one launch: the routing_fn that cpu_tier.routed wraps (glm53/cpu_tier.py:305-333) followed by
+ * ft_split on its output. logits fp32 [M, E_route] -> sel int64 [M, topk] / w fp16 [M, topk] (written: the routing
+ * gfl_route computes), then the split of those picks with the remaining arguments as gfl_split's (bsz = M,
+ * n = M * topk <= 1024). No counterpart of its own in the reference (it fuses two of its launches). */
+int gfl_route_split(const float* logits, int M, int E_route, int topk, int64_t* sel, uint16_t* w, const uint16_t* z,
+                    int H, int E, int first, const int32_t* slotof, const float* score, const float* pol,
+                    int64_t* ctrl, uint16_t* hx, int32_t* hpicks, int64_t seq, int li, int keep_ids, int64_t* sel_out,
+                    uint16_t* w_out, int64_t* dflag, int64_t* stats, const int32_t* rres, gfl_stream stream);
+
 /* ft_combine (kernels/cpu_avx2/ft_tier_cu.cu:273-294): when dflag != 0 wait (at most timeout_ns) for the done word
- * ctrl[1] >= dflag, then out += hout. out fp32 or fp16 (out_is_half) [n]; stats as ft_split's (4 wait ns, 5 waits,
+ * ctrl[1] >= dflag, then out += hout (+0 for a job without picks, ctrl[4] == 0, which gfl_split answers itself). out fp32 or fp16 (out_is_half) [n]; stats as ft_split's (4 wait ns, 5 waits,
  * 6 timeouts, 7 already done). */
 int gfl_combine(void* out, int out_is_half, int n, const int64_t* dflag, const int64_t* ctrl, const float* hout,
                 int64_t* stats, int64_t timeout_ns, gfl_stream stream);

@@ -194,54 +194,78 @@ float gflo_act_mul(float g, float u, float limit)
 /* EXACT: per (tile column t, in-tile column c, lane j) one fp32 accumulator, FMA over tile rows then over the four
  * stream groups q of the tile (tile_accum<M,EXACT>, ft_core.h:313-345); lanes reduced (v0+v1)+(v2+v3)
  * (gemv_block, ft_core.h:377-386). AFFINE: the same chain over the raw byte sums, then KINV*lo + CAFF*sum(x). */
+/* the GEMV's weight of every 16-bit state, tabulated once from the functions above: EXACT r16(fma(bytesum, KINV,
+ * CAFF)) (= the fp16 weight, w_gpu, ft_core.h:82) and the raw byte sum for AFFINE */
+static float g_wt_exact[65536], g_wt_sum[65536];
+static int g_wt_ready;
+
+static void weight_tables(void)
+{
+    if (g_wt_ready) return;
+    const float KI = kinv(), CA = caff();
+    for (uint32_t st = 0; st < 65536; ++st)
+    {
+        const int bs = gflo_bytesum((uint16_t)st);
+        g_wt_exact[st] = gflo_r16(fmaf((float)bs, KI, CA));
+        g_wt_sum[st] = (float)bs;
+    }
+    g_wt_ready = 1;
+}
+
 void gflo_gemv(const uint8_t* tr, int k, int n, int K, const float* xt, int M, float* y, int mode,
                const float* sumx_in)
 {
+    weight_tables();
+    const float* wtab = mode == 1 ? g_wt_exact : g_wt_sum;
     const int tn = n / 16, tkn = k / 16, tb = 32 * K;
     const float KI = kinv(), CA = caff();
     float* wt = (float*)malloc(sizeof(float) * 256);
+    float* sumx = (float*)calloc((size_t)(M > 0 ? M : 1), sizeof(float));
+    float (*acc)[8][8] = (float (*)[8][8])malloc(sizeof(float) * 64 * (size_t)(M > 0 ? M : 1));
+    /* each token's chains are independent: a tile is decoded once and fed to every token's accumulators in turn */
     for (int i = 0; i < M; ++i)
     {
         const float* xi = xt + (size_t)i * k;
-        float sumx = 0.0f;
-        if (mode == 0 && sumx_in) sumx = sumx_in[i];
+        if (mode == 0 && sumx_in) sumx[i] = sumx_in[i];
         else if (mode == 0)
-            for (int r = 0; r < k; ++r) sumx += xi[r];
-        for (int t = 0; t < tn; ++t)
+            for (int r = 0; r < k; ++r) sumx[i] += xi[r];
+    }
+    for (int t = 0; t < tn; ++t)
+    {
+        memset(acc, 0, sizeof(float) * 64 * (size_t)M);
+        for (int tk = 0; tk < tkn; ++tk)
         {
-            float acc[8][8];
-            memset(acc, 0, sizeof(acc));
-            for (int tk = 0; tk < tkn; ++tk)
+            const uint16_t* packed = (const uint16_t*)(tr + ((size_t)tk * tn + t) * tb);
+            for (int s = 0; s < 256; ++s) wt[s] = wtab[gflo_state(packed, K, s)];
+            for (int i = 0; i < M; ++i)
             {
-                const uint16_t* packed = (const uint16_t*)(tr + ((size_t)tk * tn + t) * tb);
-                for (int s = 0; s < 256; ++s)
-                {
-                    const int bs = gflo_bytesum(gflo_state(packed, K, s));
-                    wt[s] = mode == 1 ? gflo_r16(fmaf((float)bs, KI, CA)) : (float)bs;
-                }
+                const float* xi = xt + (size_t)i * k;
                 for (int c = 0; c < 8; ++c)
                     for (int q = 0; q < 4; ++q)
                     {
                         const int g = 4 * c + q, r0 = 2 * q;
                         const int rows[4] = { r0, r0 + 1, r0 + 8, r0 + 9 };
                         for (int j = 0; j < 8; ++j)
-                            acc[c][j] = fmaf(wt[8 * g + j], xi[tk * 16 + rows[j % 4]], acc[c][j]);
+                            acc[i][c][j] = fmaf(wt[8 * g + j], xi[tk * 16 + rows[j % 4]], acc[i][c][j]);
                     }
             }
+        }
+        for (int i = 0; i < M; ++i)
             for (int c = 0; c < 8; ++c)
             {
-                const float* v = acc[c];
+                const float* v = acc[i][c];
                 float lo = (v[0] + v[1]) + (v[2] + v[3]), hi = (v[4] + v[5]) + (v[6] + v[7]);
                 if (mode == 0)
                 {
-                    lo = KI * lo + CA * sumx;
-                    hi = KI * hi + CA * sumx;
+                    lo = KI * lo + CA * sumx[i];
+                    hi = KI * hi + CA * sumx[i];
                 }
                 y[(size_t)i * n + t * 16 + c] = lo;
                 y[(size_t)i * n + t * 16 + c + 8] = hi;
             }
-        }
     }
+    free(acc);
+    free(sumx);
     free(wt);
 }
 

@@ -126,3 +126,16 @@ def test_exp_table_is_the_c_library_expf():
     fin = np.isfinite(g) & (np.abs(g) < 80)
     cr = np.array([np.float32(math.exp(float(-v))) for v in g[fin]], np.float32)
     assert (cr.view(np.uint32) != want[fin].view(np.uint32)).sum() > 0
+
+
+def test_forward_width_check_without_device():
+    """Context refuses x whose width differs from the registered layer's H before calling into the library (host
+    logic only: a Context shell with a recorded layer shape, no device)."""
+    import torch
+    import _native
+    ctx = object.__new__(_native.Context)
+    ctx.h, ctx.device, ctx._keep, ctx._shape = None, 0, {}, {3: (8, 512, 256, 3, 3, 3)}
+    ctx._check_width(3, torch.zeros((2, 512), dtype=torch.float16))
+    for width in (256, 1024):
+        with pytest.raises(ValueError, match="H = 512"):
+            ctx._check_width(3, torch.zeros((2, width), dtype=torch.float16))

@@ -228,3 +228,39 @@ def test_grouped_plan_is_the_reference_order(gpu, oracle, M, topk, E, mode):
         ks.sort(key=lambda k: (job[t * topk + k], k))
         assert r["tok_slot"][t, :len(ks)].tolist() == [int(slot_of[t * topk + k]) for k in ks], t
         assert np.array_equal(r["tok_w"][t, :len(ks)], np.array([w[t, k] for k in ks], np.float32)), t
+
+
+@pytest.mark.gpu
+def test_grouped_config4_prefill_rows_vs_oracle(gpu, oracle):
+    """Config 4 prefill: M=2048 tokens, top-8 of 288 experts, H=5120 I=1536 K=3, through the grouped path. Four
+    tokens' rows are compared with the oracle's EXACT layer (their picks alone: a token's combine sums only its own
+    experts); the report gives max-abs/RMS and the count of elements beyond the north-star 2e-3 * RMS."""
+    import synth
+    H, I, E = 5120, 1536, 288
+    L = _layer(gpu, 25, E, H, I)
+    rng = np.random.default_rng(5000 + 2048)
+    M = 2048
+    x16 = rng.standard_normal((M, H)).astype(np.float16)
+    (sel, w16), _ = synth.route_uniform(M, E, 8, rng)
+    got = _run(gpu, 25, x16, sel, w16)
+    assert np.isfinite(got).all()
+    rows = [0, 777, 1500, 2047]
+    ex_idx = sorted(set(int(e) for r in rows for e in sel[r]))
+    remap = {e: i for i, e in enumerate(ex_idx)}
+    from oracle import Mat
+    ex = []
+    for e in ex_idx:
+        mats = []
+        for p in range(3):
+            tr, suh, svh = L.matrix(e, p)
+            k, n = (H, I) if p < 2 else (I, H)
+            mats.append(Mat(tr, suh, svh, k, n, 3))
+        ex.append(tuple(mats))
+    sub = np.array([[remap[int(e)] for e in sel[r]] for r in rows], np.int64)
+    want = oracle.moe_forward(ex, x16[rows].astype(np.float32), sub, w16[rows].astype(np.float32), mode=1)
+    g = got[rows]
+    rel, mx = _stats("config4 prefill rows 0/777/1500/2047", g, want)
+    rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
+    beyond = int(np.count_nonzero(np.abs(g.astype(np.float64) - want) > 2e-3 * rms))
+    print(f"config4 prefill: elements beyond 2e-3*RMS: {beyond}/{want.size}")
+    assert rel <= REL_RMS and mx <= MAX_ABS

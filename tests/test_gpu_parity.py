@@ -268,3 +268,116 @@ def test_forward_duplicate_picks_bitexact(gpu, oracle, w_half):
     want = oracle.moe_forward(ex, x16.astype(np.float32), sel, w.astype(np.float32), mode=1)
     mx, rms, nbad = _report(f"duplicate picks w_half={w_half}", got, want)
     assert nbad == 0
+
+
+def _union_layer(gpu, li, sel, H, I, Ks):
+    """A layer holding only the routed experts: ids are relabelled to their rank among the routed ones (job order
+    depends on first appearance, not on the ids), and the layer's experts are synthetic like any other."""
+    uniq = np.unique(sel[sel >= 0])
+    remap = {int(e): i for i, e in enumerate(uniq)}
+    sel2 = np.array([[remap[int(e)] if e >= 0 else -1 for e in row] for row in sel], np.int64)
+    L = _layer(gpu, li, len(uniq), H, I, Ks)
+    return L, sel2
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("layer_kind", ["A_4_4_3", "B_3_3_5"])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_config2_full_shape_bitexact(gpu, oracle, layer_kind, M):
+    """Config 2 at its shape: H=5120, I=1536, top-8 of 288 experts with Zipf-skewed (s=1.1) routing logits, layer A
+    (gate/up 4 bpw, down 3) and layer B (gate/up 3, down 5); the K=4 and K=5 kernels at full size."""
+    import synth
+    Ks = {"A_4_4_3": (4, 4, 3), "B_3_3_5": (3, 3, 5)}[layer_kind]
+    H, I, E = 5120, 1536, 288
+    rng = np.random.default_rng(2000 + 10 * M + Ks[2])
+    sel, w16 = synth.route(synth.zipf_logits(M, E, 1.1, rng), 8)
+    L, sel2 = _union_layer(gpu, 20 + M, sel, H, I, Ks)
+    ex = _host_experts(oracle, L)
+    x16 = rng.standard_normal((M, H)).astype(np.float16)
+    got = _forward(gpu, 20 + M, x16, sel2, w16)
+    want = oracle.moe_forward(ex, x16.astype(np.float32), sel2, w16.astype(np.float32), mode=1)
+    mx, rms, nbad = _report(f"config2 {layer_kind} M={M} union={L.E}", got, want)
+    assert mx <= TOL * rms
+    assert nbad == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", [1, 0, 2, -1])
+def test_every_mode_number_computes_exact(gpu, oracle, mode):
+    """tier_forward's mode numbers (-1 auto, 0 AFFINE, 1 EXACT, 2 I16; ft_tier_ext.cpp:865-904) all compute EXACT
+    on the device, bit-identical to the reference's EXACT mode."""
+    import torch
+    H, I, E = 512, 256, 6
+    L = _layer(gpu, 30, E, H, I)
+    ex = _host_experts(oracle, L)
+    rng = np.random.default_rng(31)
+    x16 = rng.standard_normal((2, H)).astype(np.float16)
+    sel = np.array([[0, 3, 5], [2, 3, -1]], np.int64)
+    w = rng.random(sel.shape).astype(np.float32)
+    xd = torch.from_numpy(x16.view(np.int16)).view(torch.float16).cuda()
+    out = torch.empty((2, H), dtype=torch.float32, device="cuda")
+    gpu.moe_forward(30, xd, torch.from_numpy(sel).cuda(), torch.from_numpy(w).cuda(), out, mode=mode)
+    torch.cuda.synchronize()
+    want = oracle.moe_forward(ex, x16.astype(np.float32), sel, w, mode=1)
+    assert np.array_equal(out.cpu().numpy(), want)
+
+
+@pytest.mark.gpu
+def test_width_mismatch_is_refused(gpu):
+    """x / out narrower or wider than the layer's H are refused before any launch (the C ABI takes no H)."""
+    import torch
+    _layer(gpu, 31, 2, 512, 256)
+    assert gpu.layer_info(31) == (2, 512, 256, 3, 3, 3)
+    sel = torch.tensor([[0, 1]], dtype=torch.int64, device="cuda")
+    w = torch.ones((1, 2), dtype=torch.float32, device="cuda")
+    for width in (256, 768):
+        x = torch.zeros((1, width), dtype=torch.float16, device="cuda")
+        out = torch.empty((1, width), dtype=torch.float32, device="cuda")
+        with pytest.raises(ValueError, match="H = 512"):
+            gpu.moe_forward(31, x, sel, w, out)
+        with pytest.raises(ValueError, match="H = 512"):
+            gpu.grouped_forward(31, x, sel, w, out)
+
+
+@pytest.mark.gpu
+def test_graph_replay_after_a_larger_eager_call(gpu, oracle):
+    """A graph captured at M=1 keeps working after an eager M=128 call (workspaces are reserved, never freed while
+    the context lives): every replay matches the eager M=1 result."""
+    import torch
+    H, I, E = 512, 256, 16
+    L = _layer(gpu, 32, E, H, I)
+    ex = _host_experts(oracle, L)
+    rng = np.random.default_rng(32)
+    x1 = rng.standard_normal((1, H)).astype(np.float16)
+    sel1 = np.array([[3, 7, 1, 9, 0, 15, 4, 8]], np.int64)
+    w1 = rng.random(sel1.shape).astype(np.float32)
+    xd = torch.from_numpy(x1.view(np.int16)).view(torch.float16).cuda()
+    sd, wd = torch.from_numpy(sel1).cuda(), torch.from_numpy(w1).cuda()
+    out = torch.empty((1, H), dtype=torch.float32, device="cuda")
+    gpu.moe_forward(32, xd, sd, wd, out)
+    torch.cuda.synchronize()
+    want1 = oracle.moe_forward(ex, x1.astype(np.float32), sel1, w1, mode=1)
+    assert np.array_equal(out.cpu().numpy(), want1)
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(st):
+        with torch.cuda.graph(g, stream=st):
+            gpu.moe_forward(32, xd, sd, wd, out)
+    torch.cuda.current_stream().wait_stream(st)
+    M = 128
+    xb = rng.standard_normal((M, H)).astype(np.float16)
+    selb = np.stack([rng.permutation(E)[:8] for _ in range(M)]).astype(np.int64)
+    wb = rng.random(selb.shape).astype(np.float32)
+    for rep in range(3):
+        outb = torch.empty((M, H), dtype=torch.float32, device="cuda")
+        gpu.moe_forward(32, torch.from_numpy(xb.view(np.int16)).view(torch.float16).cuda(),
+                        torch.from_numpy(selb).cuda(), torch.from_numpy(wb).cuda(), outb)
+        torch.cuda.synchronize()
+        if rep == 0:
+            wantb = oracle.moe_forward(ex, xb.astype(np.float32), selb, wb, mode=1)
+            assert np.array_equal(outb.cpu().numpy(), wantb)
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), want1), f"replay {rep}"

@@ -61,7 +61,7 @@ def test_tier_forward_reference_signature_bitexact(tier, oracle, li):
 
 def test_tier_forward_auto_prefill_takes_grouped_path(tier, oracle):
     """m * k > 1024 in auto mode: the MFMA grouped path, within its bars of the oracle's EXACT result (RMS of the
-    difference <= 1e-3, max-abs <= 1e-2 of the output RMS); EXACT mode refuses the size."""
+    difference <= 1e-3, max-abs <= 1e-2 of the output RMS)."""
     import ft_tier
     rng = np.random.default_rng(70)
     m = 300
@@ -74,8 +74,19 @@ def test_tier_forward_auto_prefill_takes_grouped_path(tier, oracle):
     rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
     d = got - want
     assert float(np.sqrt(np.mean(d ** 2))) <= 1e-3 * rms and float(np.abs(d).max()) <= 1e-2 * rms
-    with pytest.raises(RuntimeError, match="1024 picks"):
-        ft_tier.tier_forward(1, x, sel, w, 1)
+
+
+def test_tier_selftest_mode_loop(tier, oracle):
+    """The reference's start-up self-test calls tier_forward(li, x, sel, w, mode) for mode in (1, 0, 2)
+    (glm53/cpu_tier.py:766-773): every mode returns the EXACT layer."""
+    import ft_tier
+    rng = np.random.default_rng(77)
+    x = torch.from_numpy((rng.standard_normal((2, tier["H"])) * 0.5).astype(np.float16).astype(np.float32))
+    sel = torch.tensor([[0, 3, 1, 5], [2, 4, 0, -1]], dtype=torch.int32)
+    w = torch.from_numpy(rng.random((2, 4)).astype(np.float32))
+    want = oracle.moe_forward(_experts(oracle, tier["layers"][0]), x.numpy(), sel.numpy(), w.numpy(), mode=1)
+    for mode in (1, 0, 2):
+        assert np.array_equal(ft_tier.tier_forward(0, x, sel, w, mode).numpy(), want), mode
 
 
 def test_tier_forward_act_limit(tier, oracle):
@@ -103,8 +114,8 @@ def test_tier_forward_argument_errors(tier):
     sel = torch.zeros(1, 4, dtype=torch.int32)
     with pytest.raises(RuntimeError, match="fp16-valued"):
         ft_tier.tier_forward(0, x, sel, torch.ones(1, 4), 1)
-    with pytest.raises(RuntimeError, match="EXACT"):
-        ft_tier.tier_forward(0, x.half().float(), sel, torch.ones(1, 4), 2)
+    with pytest.raises(RuntimeError, match="mode must be"):
+        ft_tier.tier_forward(0, x.half().float(), sel, torch.ones(1, 4), 3)
     with pytest.raises(RuntimeError, match="out of range"):
         ft_tier.tier_forward(0, x.half().float(), sel + 99, torch.ones(1, 4), 1)
     with pytest.raises(RuntimeError, match="already initialised"):

@@ -92,6 +92,8 @@ def _check(oracle, c, tag):
         assert np.array_equal(g["ctrl"][2:5], r["ctrl"][2:5]), tag
         assert np.array_equal(g["hpicks"][:3 * npk].reshape(-1, 3), r["hpicks"]), tag
         assert np.array_equal(g["hx"], c["z"].reshape(-1)), tag
+        # a job without picks is answered on the device (the reference's worker answers every job it receives)
+        assert g["ctrl"][1] == (c["seq"] if npk == 0 else 0), tag
     else:
         assert not g["ctrl"].any(), tag
         assert (g["hpicks"] == -7).all(), tag
@@ -156,7 +158,7 @@ def test_combine_matches_oracle(gpu, oracle, half):
         out0 = base.astype(np.float16).view(np.uint16) if half else base
         hout = rng.standard_normal(n).astype(np.float32)
         seq = int(rng.integers(1, 1 << 40))
-        ctrl = np.zeros(16, np.int64); ctrl[1] = seq
+        ctrl = np.zeros(16, np.int64); ctrl[1] = seq; ctrl[4] = 3     # a job with picks
         stats0 = np.zeros(8, np.int64)
         got, st = _combine_gpu(out0.copy(), seq, ctrl, hout, stats0, 2_000_000_000)
         want = out0.copy()
@@ -178,3 +180,105 @@ def test_combine_timeout_drops_partial(gpu):
     assert np.array_equal(got, out0)
     assert st[5] == 1 and st[6] == 1 and st[7] == 0
     assert 15_000 <= st[4] <= 50_000_000     # waited about the timeout (wall-clock ticks converted to ns)
+
+
+def test_combine_empty_job_adds_zero(gpu):
+    """A job without picks (ctrl[4] == 0) has a zero partial, whatever hout holds: out + 0 (the reference's worker
+    zeroes hout for an empty route, ft_tier_ext.cpp:384), including -0 + 0 = +0."""
+    n = 5120
+    out0 = np.random.default_rng(40).standard_normal(n).astype(np.float32)
+    out0[:3] = [-0.0, 0.0, -1.5]
+    ctrl = np.zeros(16, np.int64); ctrl[0] = ctrl[1] = 9
+    got, st = _combine_gpu(out0.copy(), 9, ctrl, np.full(n, 123.0, np.float32), np.zeros(8, np.int64), 10**9)
+    assert np.array_equal(got, out0 + np.float32(0.0)) and np.signbit(got[0]) == False
+    assert list(st[5:8]) == [1, 0, 1]
+
+
+def _route_split_gpu(logits, topk, c):
+    import torch
+    import _native
+    dev = "cuda"
+    M = logits.shape[0]
+    lg = torch.from_numpy(logits).to(dev)
+    z = torch.from_numpy(c["z"].view(np.int16).copy()).to(dev)
+    H = c["z"].shape[1]
+    n = M * topk
+    sel = torch.empty((M, topk), dtype=torch.int64, device=dev)
+    w = torch.empty((M, topk), dtype=torch.int16, device=dev)
+    ctrl = torch.zeros(16, dtype=torch.int64, device=dev)
+    hx = torch.zeros(M * H, dtype=torch.int16, device=dev)
+    hpicks = torch.full((n * 3,), -7, dtype=torch.int32, device=dev)
+    sel_out = torch.empty(n, dtype=torch.int64, device=dev)
+    w_out = torch.empty(n, dtype=torch.int16, device=dev)
+    dflag = torch.zeros(1, dtype=torch.int64, device=dev)
+    stats = torch.zeros(8, dtype=torch.int64, device=dev)
+    rres = torch.from_numpy(c["rres"]).to(dev) if c["rres"] is not None else None
+    _native.route_split(lg, topk, z, c["E"], c["first"], torch.from_numpy(c["slotof"]).to(dev),
+                        torch.from_numpy(c["score"]).to(dev), torch.from_numpy(c["pol"]).to(dev), ctrl.data_ptr(),
+                        hx.data_ptr(), hpicks.data_ptr(), c["seq"], c["li"], c["keep_ids"], sel, w, sel_out, w_out,
+                        dflag, stats, rres)
+    torch.cuda.synchronize()
+    return dict(sel=sel.cpu().numpy(), w=w.cpu().numpy().view(np.uint16), sel_out=sel_out.cpu().numpy(),
+                w_out=w_out.cpu().numpy().view(np.uint16), dflag=int(dflag.item()), stats=stats.cpu().numpy(),
+                ctrl=ctrl.cpu().numpy(), hpicks=hpicks.cpu().numpy(), hx=hx.cpu().numpy().view(np.uint16))
+
+
+@pytest.mark.parametrize("kind", ["stock", "tri", "lut"])
+def test_route_split_matches_router_then_split(gpu, oracle, kind):
+    """gfl_route_split (router + split in one launch) = the router (closed form, checked against the oracle's) followed
+    by the split (the oracle's), on every output."""
+    rng = np.random.default_rng({"stock": 51, "tri": 52, "lut": 53}[kind])
+    for i in range(20):
+        M = int(rng.choice([1, 2, 4, 16]))
+        E = int(rng.choice([64, 288]))
+        logits = rng.standard_normal((M, E)).astype(np.float32)
+        c = _case(rng, E, 0, M, 8, float(rng.choice([1.0, 0.5, 0.0])), kind)
+        g = _route_split_gpu(logits, 8, c)
+        sel, w = oracle.route(logits, 8)
+        assert np.array_equal(g["sel"], sel) and np.array_equal(g["w"], w.reshape(g["w"].shape)), i
+        r = oracle.split(sel, w, c["z"], E, 0, c["slotof"], c["score"], c["pol"], c["seq"], c["li"], c["keep_ids"],
+                         rres=c["rres"])
+        assert np.array_equal(g["sel_out"], r["sel_out"]) and np.array_equal(g["w_out"], r["w_out"]), i
+        assert g["dflag"] == r["dflag"] and np.array_equal(g["stats"][:4], r["stats"][:4]), i
+        if r["dflag"]:
+            npk = int(r["ctrl"][4])
+            assert np.array_equal(g["ctrl"][2:5], r["ctrl"][2:5]) and g["ctrl"][0] == c["seq"], i
+            assert np.array_equal(g["hpicks"][:3 * npk].reshape(-1, 3), r["hpicks"]), i
+
+
+def test_handshake_layer_does_not_wait(gpu):
+    """cpu_tier's decode sequence at full residency with the handshake policy (pol[7] = 1, GLM53_CT_HANDSHAKE):
+    ft_split publishes an empty job every layer, the layer runs on the device, ft_combine returns without waiting
+    out its timeout (stats[6] == 0) and leaves the layer output as it was."""
+    import torch
+    import _native
+    import synth
+    H, I, E = 512, 256, 16
+    L = synth.SynthLayer(60, E, H, I, (3, 3, 3))
+    L.register(gpu, 60)
+    rng = np.random.default_rng(61)
+    x = torch.from_numpy(rng.standard_normal((1, H)).astype(np.float16)).cuda()
+    (sel, w16), _ = synth.route_uniform(1, E, 8, rng)
+    sel_d = torch.from_numpy(sel).cuda()
+    w_d = torch.from_numpy(w16.view(np.int16)).cuda().view(torch.float16)
+    ctrl = torch.zeros(16, dtype=torch.int64, device="cuda")
+    hx = torch.zeros(H, dtype=torch.float16, device="cuda")
+    hp = torch.zeros(8 * 3, dtype=torch.int32, device="cuda")
+    hout = torch.full((H,), 7.0, dtype=torch.float32, device="cuda")
+    so, wo = torch.empty(8, dtype=torch.int64, device="cuda"), torch.empty(8, dtype=torch.float16, device="cuda")
+    dflag, stats = torch.zeros(1, dtype=torch.int64, device="cuda"), torch.zeros(8, dtype=torch.int64, device="cuda")
+    pol = torch.tensor([0.4, 0.023, 0.11, 0.104, 0.2, 32, -1, 1] + [0.0] * 12, device="cuda")
+    out = torch.empty((1, H), dtype=torch.float32, device="cuda")
+    for seq in (1, 2, 3):
+        _native.split(sel_d.view(-1), w_d.view(-1), x, E, 0, torch.arange(E, dtype=torch.int32, device="cuda"),
+                      torch.zeros(E, device="cuda"), pol, ctrl.data_ptr(), hx.data_ptr(), hp.data_ptr(), seq, 60, 0,
+                      so, wo, dflag, stats, None)
+        gpu.moe_forward(60, x, so.view(1, 8), wo.view(1, 8), out)
+        torch.cuda.synchronize()
+        before = out.clone()
+        _native.combine(out, dflag, ctrl.data_ptr(), hout.data_ptr(), stats, 2_000_000_000)
+        torch.cuda.synchronize()
+        assert int(dflag.item()) == seq and int(ctrl[0].item()) == seq and int(ctrl[1].item()) == seq
+        assert torch.equal(out, before)
+    st = stats.tolist()
+    assert st[6] == 0 and st[5] == 3 and st[7] == 3 and st[3] == 3

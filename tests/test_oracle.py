@@ -261,6 +261,73 @@ def test_split_cost_model_matches_float64_argmin(oracle):
     assert checked > 100
 
 
+def _taken_experts(r):
+    return {int(e) for e in r["hpicks"][:, 1]} if r["dflag"] else set()
+
+
+def _brute_split_case(rng, E, tri, lut):
+    """A random split case with its float64 cost table over (remote count kr, local count k) in the reference's loop
+    order (ft_tier_cu.cu:84-131): tri-lane cost max(gpu, local CPU, remote), LUT local cost p[11 + min(k, 8)] plus
+    cpu_b per expert beyond 8 plus the extra-token term."""
+    bsz = int(rng.integers(1, 5))
+    sel = np.stack([rng.choice(E, 8, replace=False) for _ in range(bsz)]).astype(np.int64)
+    w = rng.random(sel.shape).astype(np.float16).view(np.uint16)
+    slotof = np.where(rng.random(E) < 0.3, 1, -1).astype(np.int32)
+    score = rng.random(E).astype(np.float32)
+    rres = (rng.random(E) < 0.5).astype(np.int32)
+    p = _pol(p0=rng.uniform(0.2, 0.6), p1=rng.uniform(0.01, 0.05), p2=rng.uniform(0.05, 0.3),
+             p3=rng.uniform(0.05, 0.2), p4=rng.uniform(0.0, 0.4), p5=int(rng.choice([4, 32])))
+    if tri:
+        p[8], p[9], p[10] = 1.0, rng.uniform(0.02, 0.3), rng.uniform(0.02, 0.2)
+    if lut:
+        p[12:20] = np.sort(rng.uniform(0.05, 0.8, 8)).astype(np.float32)
+    uniq, cnt = np.unique(sel, return_counts=True)
+    cm = {int(e): int(c) for e, c in zip(uniq, cnt)}
+    misses = [int(e) for e in uniq if slotof[e] < 0]
+    loc_l = sorted([e for e in misses if not (tri and rres[e])], key=lambda e: (score[e], e))
+    rem_l = sorted([e for e in misses if tri and rres[e]], key=lambda e: (score[e], e))
+    nh, nm, nr = len(uniq) - len(misses), len(loc_l), len(rem_l)
+    P = [float(v) for v in p]
+    maxc = min(int(P[5]), nm)
+    table = []
+    for kr in range(nr + 1):
+        rem = (P[9] + sum(P[10] * (1 + P[4] * (cm[rem_l[i]] - 1)) for i in range(kr))) if kr else 0.0
+        for k in range(maxc + 1):
+            c = sum(P[3] * (1 + P[4] * (cm[loc_l[i]] - 1)) for i in range(k))
+            cx = sum(P[3] * P[4] * (cm[loc_l[i]] - 1) for i in range(k))
+            zc = nm - k + nr - kr
+            gpu = P[1] * (nh + zc) + P[0] * zc
+            if k == 0:
+                loc = 0.0
+            elif lut:
+                loc = P[11 + min(k, 8)] + (P[3] * (k - 8) if k > 8 else 0.0) + cx
+            else:
+                loc = P[2] + c
+            table.append((max(gpu, loc, rem), kr, k))
+    return dict(sel=sel, w=w, z=np.zeros((bsz, 16), np.uint16), slotof=slotof, score=score, rres=rres, p=p,
+                table=table, loc_l=loc_l, rem_l=rem_l)
+
+
+@pytest.mark.parametrize("tri,lut", [(True, False), (False, True), (True, True)])
+def test_split_tri_and_lut_cost_match_float64_argmin(oracle, tri, lut):
+    """The resident-tier lane (p[8..10], rres) and the LUT cost table (p[12..19]): the oracle's host-lane choice is
+    the float64 arg-min of the cost table, the first in the reference's (kr, k) loop order, on cases away from
+    near-ties; the experts it publishes are the coldest of each class."""
+    rng = np.random.default_rng(71 + 2 * tri + lut)
+    E, checked = 96, 0
+    for trial in range(300):
+        c = _brute_split_case(rng, E, tri, lut)
+        costs = sorted(v for v, _, _ in c["table"])
+        if len(costs) > 1 and costs[1] - costs[0] < 1e-4:
+            continue
+        _, kr, k = min(c["table"], key=lambda r: r[0])
+        r = oracle.split(c["sel"], c["w"], c["z"], E, 0, c["slotof"], c["score"], c["p"], 1, 0, 0, rres=c["rres"])
+        assert r["stats"][2] == k + kr, (trial, k, kr)
+        assert _taken_experts(r) == set(c["loc_l"][:k]) | set(c["rem_l"][:kr]), trial
+        checked += 1
+    assert checked > 150
+
+
 def test_combine_semantics(oracle):
     out = np.arange(8, dtype=np.float32)
     hout = np.full(8, 0.5, np.float32)
