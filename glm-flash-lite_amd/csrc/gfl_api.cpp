@@ -79,6 +79,7 @@ struct Workspace
     float* yd;       // [cap][H]
     int* act_cnt;    // [cap][I/128] last-one counters of the SwiGLU stage (zero between calls)
     int* out_cnt;    // [cap][H/128] last-one counters of the combine (zero between calls)
+    int* blk_cnt;    // [cap][H/128] half-block counters of the one-slot-per-pass down launch (zero between calls)
 };
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -98,7 +99,7 @@ WsSizes ws_sizes(int cap, int H, int I)
     z.ygu = align256(sizeof(float) * 4 * (size_t)cap * I);
     z.xtd = align256(sizeof(uint16_t) * (size_t)cap * I);
     z.yd = align256(sizeof(float) * (size_t)cap * H);
-    z.cnt = align256(sizeof(int) * (size_t)cap * (I / 128 + H / 128));
+    z.cnt = align256(sizeof(int) * (size_t)cap * (I / 128 + 2 * (H / 128)));
     return z;
 }
 
@@ -135,7 +136,6 @@ void carve_ws(gfl_ctx* c, int H, int I, Workspace& w)
 {
     const int cap = gfl::MAX_PICKS;
     const WsSizes z = ws_sizes(cap, c->ws_H, c->ws_I);
-    (void)H;
     char* b = static_cast<char*>(c->ws);
     int* ip = reinterpret_cast<int*>(b);
     w.pv.hdr = ip;
@@ -155,6 +155,7 @@ void carve_ws(gfl_ctx* c, int H, int I, Workspace& w)
     w.yd = reinterpret_cast<float*>(b + z.ints + z.ygu + z.xtd);
     w.act_cnt = reinterpret_cast<int*>(b + c->ws_cnt_off);
     w.out_cnt = w.act_cnt + (size_t)cap * (I / 128);
+    w.blk_cnt = w.out_cnt + (size_t)cap * (H / 128);
 }
 
 bool k_ok(int K) { return K >= 2 && K <= 5; }
@@ -350,8 +351,8 @@ int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, c
     int ns = mf ? std::min(M, 4) : M <= 8 ? 1 : 2;
     if (c->ns_override > 0) ns = std::min(c->ns_override, mf ? std::min(M, 16) : M);
     if (gfl::gate_up_lds_bytes(L.K[0], ns, L.H, P, L.E, mf) > gfl::LDS_LIMIT ||
-        gfl::gate_up_lds_bytes(L.K[1], ns, L.H, P, L.E, mf) > gfl::LDS_LIMIT
-        || gfl::down_lds_bytes(L.K[2], ns, L.I, mf) > gfl::LDS_LIMIT)
+        gfl::gate_up_lds_bytes(L.K[1], ns, L.H, P, L.E, mf) > gfl::LDS_LIMIT ||
+        gfl::down_lds_bytes(L.K[2], ns, L.I, mf) > gfl::LDS_LIMIT)
         return fail(GFL_EINVAL, "gfl_moe_forward: shape needs more than 160 KB of LDS per workgroup");
     const int wh = w_is_half ? 1 : 0;
     int r = staged(c, 1, st, [&] {
@@ -367,7 +368,7 @@ int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, c
     if (!r)
         r = staged(c, 3, st, [&] {
             return gfl::launch_down(L.K[2], ns, L.dptrs, topk, L.H, L.I, umax, P, ws.pv, ws.xtd, ws.yd, ws.out_cnt,
-                                    out, mf, st);
+                                    ws.blk_cnt, out, mf, st);
         });
     if (r) return r > 0 ? r : fail(GFL_EINVAL, "gfl_moe_forward: unsupported K");
     GFL_HIP(hipGetLastError());

@@ -37,9 +37,10 @@ int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, 
                    uint16_t* xtd, int* act_cnt, const float* silu_tab, float act_limit, const PlanView& pv, float* out,
                    int mf, hipStream_t st);
 // down launch: down GEMV + out_block, weighted combine per (token, 128-block) by the token's last expert; mf and ns
-// as for launch_gate_up (the same values for both launches of a call)
+// as for launch_gate_up (the same values for both launches of a call). blk_cnt: [cap][H/128] half-block counters of
+// the one-slot-per-pass EXACT launch (zero between calls).
 int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int umax, int P, const PlanView& pv,
-                const uint16_t* xtd, float* yd, int* out_cnt, float* out, int mf, hipStream_t st);
+                const uint16_t* xtd, float* yd, int* out_cnt, int* blk_cnt, float* out, int mf, hipStream_t st);
 size_t gate_up_lds_bytes(int K, int ns, int H, int P, int E, int mf);
 size_t down_lds_bytes(int K, int ns, int I, int mf);
 int launch_dequant(const uint8_t* tr, int k, int n, int K, uint16_t* W, hipStream_t st);

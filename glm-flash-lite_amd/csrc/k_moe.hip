@@ -574,6 +574,17 @@ __device__ __forceinline__ void st_agent(float* p, float v)
 {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Last-one counters hand data between workgroups. Everything handed over is written with st_agent and read with
+// ld_agent: device-scope (sc1) accesses, performed at the level where all XCDs see them, never served from a stale
+// line of one XCD's L2. What the hand-over needs is order: every wave that stored data for the finisher runs
+// release_agent() before the workgroup barrier that precedes the counter update, so its stores have completed (the
+// barrier alone does not wait for them); the finisher issues its loads only after the counter value came back.
+// The generic agent-scope release/acquire fences would add an L2 write-back and invalidate per hand-over, which
+// none of these accesses needs (and which costs more than the whole GEMV at decode sizes).
+__device__ __forceinline__ void release_agent()
+{
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // s_waitcnt vmcnt(0) (expcnt and lgkmcnt at their maxima: no wait)
+}
 
 // fwd_phase phase 1 for one 128-block b of union entry u (ft_core.h:974-991): out_block of gate and up,
 // r16(act_mul), down prep_block, stored permuted as the down GEMV input
@@ -766,10 +777,8 @@ gu_kernel(GuArgs a)
                                        __HIP_MEMORY_SCOPE_AGENT);
         }
     }
-    // the last of the workgroups covering this 128-block (its gate and up halves) runs the SwiGLU stage for it.
-    // Outputs went out as agent-scope stores (written through to the device-coherent level, not held in this XCD's
-    // L2); the barrier's wait for outstanding stores orders them before the counter update, and the finisher reads
-    // them back with agent-scope loads. No L2 write-back or invalidate is needed.
+    // the last of the workgroups covering this 128-block (its gate and up halves) runs the SwiGLU stage for it
+    release_agent();
     __syncthreads();
     const int blk = (cb * NW * 16) / 128;
     if (threadIdx.x == 0)
@@ -795,6 +804,8 @@ struct DnArgs
     const uint16_t* xtd;       // [cap][I]
     float* yd;                 // [cap][H] expert outputs after out_block
     int* out_cnt;              // [tokens][H/128] last-one counters (zero between calls)
+    int* blk_cnt;              // [cap][H/128] half-block counters of the one-slot-per-pass launch (zero between
+                               // calls)
     float* out;                // [M][H]
     int ns_cap;                // slots per pass the LDS allocation holds (<= NS)
     int per_slot;              // workgroups per slot (one pass each), as the gate|up launch
@@ -803,11 +814,15 @@ struct DnArgs
 // Grid: umax * H/128. Workgroup = 8 waves = one 128-output block of one routed expert, all its slots (with per_slot:
 // P * H/128, one slot each).
 // MF: the GEMV accumulates with MFMAs (chain_mf), for up to 16 slots per pass.
+// One slot per pass (EXACT): 4-wave workgroups on half a 128-block each (HB), so that at M=1 the 2,560 down columns
+// spread over the CUs in units of 4 (at most 3 columns per SIMD) instead of 8; the two halves' raw sums meet in yd and
+// the second to finish runs out_block on the block.
 template <int K, int NS, bool MF>
-__global__ __launch_bounds__(DN_NW * 64) __attribute__((amdgpu_waves_per_eu(K == 5 || NS == 8 ? 3 : 4))) void
-down_kernel(DnArgs a)
+__global__ __launch_bounds__((NS == 1 && !MF ? DN_NW / 2 : DN_NW) * 64)
+__attribute__((amdgpu_waves_per_eu(K == 5 || NS == 8 ? 3 : 4))) void down_kernel(DnArgs a)
 {
-    constexpr int NW = DN_NW, TB = 32 * K;
+    constexpr bool HB = NS == 1 && !MF;
+    constexpr int NW = HB ? DN_NW / 2 : DN_NW, TB = 32 * K;
     extern __shared__ __align__(16) uint8_t lds_raw[];
     __shared__ int s_last[NS];
     __shared__ int c_tok[NS], c_npk[NS], c_slot[NS][MAX_TOPK];
@@ -819,7 +834,8 @@ down_kernel(DnArgs a)
     void* lds_x = lds_raw + NW * RB;                                                   // [ns_cap][I]
     float* lds_y = reinterpret_cast<float*>(lds_raw + NW * RB + (size_t)a.ns_cap * a.I * XE);   // [ns_cap][128]
     const int TN = a.H / 16, TK = a.I / 16, ncb = TN / NW;
-    const int u = blockIdx.x / ncb, blk = blockIdx.x % ncb;   // union entry, or slot with per_slot
+    const int u = blockIdx.x / ncb, cb = blockIdx.x % ncb;    // union entry (or slot with per_slot), column block
+    const int blk = HB ? cb >> 1 : cb;                         // its 128-output block
     // one round of independent loads: the union size (slot count), this entry's slot range and its expert's
     // addresses (entries past the count hold stale values and are not used)
     const int U = a.pv.hdr[a.per_slot ? 1 : 0];
@@ -830,7 +846,7 @@ down_kernel(DnArgs a)
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15;
     const int wid = __builtin_amdgcn_readfirstlane(wave);
     const size_t gstride = (size_t)TN * TB;
-    const uint8_t* col = tr + (size_t)(blk * NW + wave) * TB;   // this wave's tile column
+    const uint8_t* col = tr + (size_t)(cb * NW + wave) * TB;    // this wave's tile column
     const int nbh = a.H / 128;
 
     const int nsp = NS == 1 ? 1 : max(1, min(NS, a.ns_cap));
@@ -876,7 +892,7 @@ down_kernel(DnArgs a)
             else
                 reinterpret_cast<uint4*>(lds_x)[i] = v;
         };
-        const int i0 = threadIdx.x, i1 = threadIdx.x + DN_NW * 64;
+        const int i0 = threadIdx.x, i1 = threadIdx.x + NW * 64;
         uint4 xc0 = {}, xc1 = {};
         auto pre_load = [&] {
             if (i0 < nvec) xc0 = xsrc[i0];
@@ -885,7 +901,7 @@ down_kernel(DnArgs a)
         auto pre = [&] {
             if (i0 < nvec) put(i0, xc0);
             if (i1 < nvec) put(i1, xc1);
-            for (int i = threadIdx.x + 2 * DN_NW * 64; i < nvec; i += DN_NW * 64) put(i, xsrc[i]);
+            for (int i = threadIdx.x + 2 * NW * 64; i < nvec; i += NW * 64) put(i, xsrc[i]);
             lds_barrier();   // lds_x complete
         };
         if constexpr (MF)
@@ -902,9 +918,17 @@ down_kernel(DnArgs a)
         else
         {
             chain_dma<K, NS, NGRP, XF>(col, gstride, TK, ns, lds_x, rings + wid * RB, res, pre_load, pre);
+            if constexpr (HB)
+            {
+                // the half block's raw column sums, for whichever half finishes second
+                if (lane < 16) st_agent(&a.yd[(size_t)c0 * a.H + cb * (NW * 16) + wave * 16 + n], res[0]);
+            }
+            else
+            {
 #pragma unroll
-            for (int s = 0; s < NS; ++s)
-                if (s < ns && lane < 16) lds_y[s * 128 + wave * 16 + n] = res[s];
+                for (int s = 0; s < NS; ++s)
+                    if (s < ns && lane < 16) lds_y[s * 128 + wave * 16 + n] = res[s];
+            }
         }
         if (ci < ns * a.topk)
         {
@@ -912,18 +936,43 @@ down_kernel(DnArgs a)
             c_w[cs][ck] = q_w;
             if (ck == 0) { c_tok[cs] = q_tok; c_npk[cs] = q_npk; }
         }
+        if constexpr (HB) release_agent();
         __syncthreads();
-        // out_block (ft_core.h:1016) of the pass's 128-blocks, published as the experts' outputs
-        for (int s = wave; s < ns; s += NW)
+        if constexpr (HB)
         {
-            float v0 = lds_y[s * 128 + lane], v1 = lds_y[s * 128 + lane + 64];
-            out_block_wave(v0, v1, h2f_bits(svh[blk * 128 + lane]), h2f_bits(svh[blk * 128 + lane + 64]));
-            st_agent(&a.yd[(size_t)(c0 + s) * a.H + blk * 128 + lane], v0);
-            st_agent(&a.yd[(size_t)(c0 + s) * a.H + blk * 128 + lane + 64], v1);
+            // the second half to finish runs out_block (ft_core.h:1016) on the whole 128-block, in place
+            if (threadIdx.x == 0)
+            {
+                int* ctr = a.blk_cnt + (size_t)c0 * nbh + blk;
+                const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                s_last[0] = old == 1;
+                if (old == 1) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            __syncthreads();
+            if (!s_last[0]) return;
+            if (wave == 0)
+            {
+                float* y = a.yd + (size_t)c0 * a.H + blk * 128;
+                float v0 = ld_agent(&y[lane]), v1 = ld_agent(&y[lane + 64]);
+                out_block_wave(v0, v1, h2f_bits(svh[blk * 128 + lane]), h2f_bits(svh[blk * 128 + lane + 64]));
+                st_agent(&y[lane], v0);
+                st_agent(&y[lane + 64], v1);
+            }
         }
+        else
+        {
+            // out_block (ft_core.h:1016) of the pass's 128-blocks, published as the experts' outputs
+            for (int s = wave; s < ns; s += NW)
+            {
+                float v0 = lds_y[s * 128 + lane], v1 = lds_y[s * 128 + lane + 64];
+                out_block_wave(v0, v1, h2f_bits(svh[blk * 128 + lane]), h2f_bits(svh[blk * 128 + lane + 64]));
+                st_agent(&a.yd[(size_t)(c0 + s) * a.H + blk * 128 + lane], v0);
+                st_agent(&a.yd[(size_t)(c0 + s) * a.H + blk * 128 + lane + 64], v1);
+            }
+        }
+        release_agent();
         __syncthreads();
-        // count this block of every pass token in (agent-scope stores above, ordered by the barrier's store wait);
-        // the token's last expert sums the block in job order
+        // count this block of every pass token in; the token's last expert sums the block in job order
         if (threadIdx.x < ns)
         {
             const int s = threadIdx.x;
@@ -1017,7 +1066,8 @@ static size_t gu_lds(int ns, int H, int P, int E, int mf)
 template <int K>
 static size_t dn_lds(int ns, int I, int mf)
 {
-    return (size_t)DN_NW * NGRP * 8 * 32 * K + (size_t)ns * I * (mf ? 2 : x_lds_elem(ns)) + (size_t)ns * 128 * 4;
+    const int nw = (ns == 1 && !mf) ? DN_NW / 2 : DN_NW;
+    return (size_t)nw * NGRP * 8 * 32 * K + (size_t)ns * I * (mf ? 2 : x_lds_elem(ns)) + (size_t)ns * 128 * 4;
 }
 
 template <int K, int NS, bool MF>
@@ -1040,7 +1090,8 @@ static void dn_launch(const DnArgs& a, int umax, int P, hipStream_t st)
     static const bool opened = open_lds(kern);
     (void)opened;
     const int ents = a.per_slot ? P : umax;
-    hipLaunchKernelGGL(kern, dim3(ents * (a.H / (16 * DN_NW))), dim3(DN_NW * 64), lds, st, a);
+    constexpr int nw = (NS == 1 && !MF) ? DN_NW / 2 : DN_NW;
+    hipLaunchKernelGGL(kern, dim3(ents * (a.H / (16 * nw))), dim3(nw * 64), lds, st, a);
 }
 
 // slots per pass: 1, 4 or 8 (a 2-slot instantiation does not fit the register budget without spilling; passes with
@@ -1108,10 +1159,11 @@ int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, 
 }
 
 int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int umax, int P, const PlanView& pv,
-                const uint16_t* xtd, float* yd, int* out_cnt, float* out, int mf, hipStream_t st)
+                const uint16_t* xtd, float* yd, int* out_cnt, int* blk_cnt, float* out, int mf, hipStream_t st)
 {
     DnArgs a;
     a.ptrs = ptrs; a.topk = topk; a.H = H; a.I = I; a.pv = pv; a.xtd = xtd; a.yd = yd; a.out_cnt = out_cnt;
+    a.blk_cnt = blk_cnt;
     a.out = out;
     a.ns_cap = ns;
     if (mf)
