@@ -15,7 +15,10 @@ SYMBOLS = ("gfl_last_error", "gfl_version", "gfl_ctx_create", "gfl_ctx_destroy",
            "gfl_moe_forward", "gfl_grouped_forward", "gfl_dequant", "gfl_split", "gfl_combine", "gfl_grouped_rows",
            "gfl_synth_trellis", "gfl_route",
            "gfl_stats", "gfl_profile_enable", "gfl_profile_read", "gfl_exp_table", "gfl_silu_table",
-           "gfl_grouped_plan", "gfl_grouped_reserve", "gfl_layer_info", "gfl_route_split")
+           "gfl_grouped_plan", "gfl_grouped_reserve", "gfl_layer_info", "gfl_route_split", "gfl_moe_forward_noalloc")
+
+# layout limits of gfl_moe_forward_noalloc's static scratch array (GFL_NOALLOC_MAX_* in include/gfl_moe.h)
+NOALLOC_MAX_PICKS, NOALLOC_MAX_H, NOALLOC_MAX_I = 64, 8192, 4096
 
 MODE_AUTO, MODE_AFFINE, MODE_EXACT, MODE_I16, MODE_MFMA = -1, 0, 1, 2, 3
 
@@ -49,6 +52,7 @@ def load(path=LIB_PATH):
     L.gfl_ctx_destroy.argtypes = [_P]
     L.gfl_register_layer.argtypes = [_P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _P]
     L.gfl_moe_forward.argtypes = [_P, C.c_int, _P, _P, _P, C.c_int, C.c_int, C.c_int, _P, C.c_int, C.c_float, _P]
+    L.gfl_moe_forward_noalloc.argtypes = L.gfl_moe_forward.argtypes
     L.gfl_grouped_forward.argtypes = [_P, C.c_int, _P, _P, _P, C.c_int, C.c_int, C.c_int, _P, C.c_float, _P]
     L.gfl_grouped_reserve.argtypes = [_P, C.c_int]
     L.gfl_layer_info.argtypes = [_P, C.c_int, _P]
@@ -65,6 +69,8 @@ def load(path=LIB_PATH):
     L.gfl_stats.argtypes = [_P, _P, C.c_int]
     L.gfl_profile_enable.argtypes = [_P, C.c_int]
     L.gfl_profile_read.argtypes = [_P, _P, _P]
+    L.gfl_exp_table.argtypes = [_P, C.c_int]
+    L.gfl_silu_table.argtypes = [_P, C.c_int]
     for name in SYMBOLS:
         if name != "gfl_last_error":
             getattr(L, name).restype = C.c_int
@@ -136,6 +142,13 @@ class Context:
 
     def moe_forward(self, li, x, sel, w, out, mode=MODE_EXACT, act_limit=0.0):
         """x fp16 [M,H], sel int64 [M,topk], w fp16|fp32 [M,topk], out fp32 [M,H] (all on the context device)."""
+        return self._decode_forward(load().gfl_moe_forward, li, x, sel, w, out, mode, act_limit)
+
+    def moe_forward_noalloc(self, li, x, sel, w, out, mode=MODE_EXACT, act_limit=0.0):
+        """moe_forward on the library's static scratch array: allocates nothing (M*topk <= NOALLOC_MAX_PICKS)."""
+        return self._decode_forward(load().gfl_moe_forward_noalloc, li, x, sel, w, out, mode, act_limit)
+
+    def _decode_forward(self, fn, li, x, sel, w, out, mode, act_limit):
         import torch
         if sel.dim() != 2:
             raise ValueError("sel must be int64 [M, topk]")
@@ -152,8 +165,8 @@ class Context:
             if not (t.is_cuda and t.device.index == self.device):
                 raise ValueError(f"all tensors must be on cuda:{self.device}")
         self._check_width(li, x)
-        check(load().gfl_moe_forward(self.h, li, ptr(x), ptr(sel), ptr(w), int(w.dtype == torch.float16), M, topk,
-                                     ptr(out), int(mode), float(act_limit), _stream()))
+        check(fn(self.h, li, ptr(x), ptr(sel), ptr(w), int(w.dtype == torch.float16), M, topk, ptr(out), int(mode),
+                 float(act_limit), _stream()))
         return out
 
     def grouped_forward(self, li, x, sel, w, out, act_limit=0.0):

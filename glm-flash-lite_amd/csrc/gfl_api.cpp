@@ -49,7 +49,7 @@ struct gfl_ctx
     // decode workspace, reserved by gfl_register_layer for MAX_PICKS slots at the largest registered H and I and
     // carved with that fixed layout, so every call (and every graph captured from one) sees the same addresses
     void* ws = nullptr;
-    size_t ws_bytes = 0, ws_cnt_off = 0;
+    size_t ws_bytes = 0;
     int ws_H = 0, ws_I = 0;
     int64_t calls = 0, picks = 0;
     // per-stage profiling events (gfl_profile_enable / gfl_profile_read)
@@ -82,17 +82,17 @@ struct Workspace
     int* blk_cnt;    // [cap][H/128] half-block counters of the one-slot-per-pass down launch (zero between calls)
 };
 
-size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+constexpr size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // Decode workspace sizes for cap slots at hidden H and intermediate I: plan ints and the [cap][2] address table,
 // gate|up outputs, down inputs, expert outputs, and the counter region (a tail of its own).
 struct WsSizes
 {
-    size_t ints, ygu, xtd, yd, cnt;
-    size_t data() const { return ints + ygu + xtd + yd; }
+    size_t ints = 0, ygu = 0, xtd = 0, yd = 0, cnt = 0;
+    constexpr size_t data() const { return ints + ygu + xtd + yd; }
 };
 
-WsSizes ws_sizes(int cap, int H, int I)
+constexpr WsSizes ws_sizes(int cap, int H, int I)
 {
     WsSizes z;
     z.ints = align256(sizeof(int) * (size_t)(4 + 9 * cap + 4) + sizeof(uint64_t) * 2 * (size_t)cap);
@@ -124,19 +124,17 @@ int reserve_ws(gfl_ctx* c, int H, int I)
     if (c->ws) c->retired.push_back(c->ws);
     c->ws = p;
     c->ws_bytes = need;
-    c->ws_cnt_off = z.data();
     c->ws_H = nH;
     c->ws_I = nI;
     return GFL_OK;
 }
 
-// The fixed layout of the reserved workspace, with strides for a layer of hidden H and intermediate I (<= the
-// reserved maxima). Slot capacity is always MAX_PICKS, so the addresses do not depend on the call's size.
-void carve_ws(gfl_ctx* c, int H, int I, Workspace& w)
+// The fixed layout of a decode workspace at b laid out for cap slots at hidden wH and intermediate wI, with strides
+// for a layer of hidden H and intermediate I (<= wH, wI): the addresses do not depend on the call's size.
+void carve_at(void* base, int cap, int wH, int wI, int H, int I, Workspace& w)
 {
-    const int cap = gfl::MAX_PICKS;
-    const WsSizes z = ws_sizes(cap, c->ws_H, c->ws_I);
-    char* b = static_cast<char*>(c->ws);
+    const WsSizes z = ws_sizes(cap, wH, wI);
+    char* b = static_cast<char*>(base);
     int* ip = reinterpret_cast<int*>(b);
     w.pv.hdr = ip;
     w.pv.uexp = ip + 4;
@@ -153,9 +151,15 @@ void carve_ws(gfl_ctx* c, int H, int I, Workspace& w)
     w.ygu = reinterpret_cast<float*>(b + z.ints);
     w.xtd = reinterpret_cast<uint16_t*>(b + z.ints + z.ygu);
     w.yd = reinterpret_cast<float*>(b + z.ints + z.ygu + z.xtd);
-    w.act_cnt = reinterpret_cast<int*>(b + c->ws_cnt_off);
+    w.act_cnt = reinterpret_cast<int*>(b + z.data());
     w.out_cnt = w.act_cnt + (size_t)cap * (I / 128);
     w.blk_cnt = w.out_cnt + (size_t)cap * (H / 128);
+}
+
+// the context's reserved workspace: MAX_PICKS slots at the largest registered H and I
+void carve_ws(gfl_ctx* c, int H, int I, Workspace& w)
+{
+    carve_at(c->ws, gfl::MAX_PICKS, c->ws_H, c->ws_I, H, I, w);
 }
 
 bool k_ok(int K) { return K >= 2 && K <= 5; }
@@ -185,6 +189,118 @@ int staged(gfl_ctx* c, int stage, hipStream_t st, F&& launch)
     GFL_HIP(hipEventRecord(b, st));
     c->recs.push_back({ stage, a, b });
     return r;
+}
+
+// Argument checks shared by the decode forward entry points (returns GFL_OK or the failure code, message set).
+int check_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, const void* w, int M, int topk,
+                  const float* out, int mode, float act_limit, const char* who)
+{
+    const std::string f(who);
+    if (!c || !x || !sel || !w || !out) return fail(GFL_EINVAL, f + ": NULL argument");
+    if (li < 0 || li >= (int)c->layers.size() || !c->layers[li].dptrs) return fail(GFL_EINVAL, f + ": layer not registered");
+    // AFFINE (0) and I16 (2) name the reference CPU engine's speed modes; the device computes EXACT for them, which
+    // lies closer to the fp64 expert than either of them does
+    if (mode < GFL_MODE_AUTO || mode > GFL_MODE_MFMA)
+        return fail(GFL_EINVAL, f + ": mode must be -1 (auto), 0 (affine), 1 (exact), 2 (i16) or 3 (mfma)");
+    if (M < 1 || topk < 1 || topk > gfl::MAX_TOPK || (int64_t)M * topk > gfl::MAX_PICKS)
+        return fail(GFL_EINVAL, f + ": need 1 <= topk <= 16 and M*topk <= 1024");
+    if (!std::isfinite(act_limit) || act_limit < 0) return fail(GFL_EINVAL, f + ": act_limit must be >= 0");
+    if (reinterpret_cast<uintptr_t>(x) & 15) return fail(GFL_EINVAL, f + ": x must be 16-byte aligned");
+    return GFL_OK;
+}
+
+// The decode forward on workspace ws (caller holds c->mu, device set). prof: bracket the stages with the context's
+// profiling events when profiling is on (the no-allocation entry point does not: event creation is left out of it).
+int run_forward(gfl_ctx* c, const Layer& L, const Workspace& ws, const uint16_t* x, const int64_t* sel,
+                const void* w, int w_is_half, int M, int topk, float* out, int mode, float act_limit, hipStream_t st,
+                bool prof)
+{
+    const int P = M * topk;
+    const int umax = P < L.E ? P : L.E;
+    // slots per pass of the GEMV (its LDS holds NS transformed inputs). With one slot per pass the launches run a
+    // workgroup per slot, so an expert picked by several tokens is streamed once per slot in parallel; with more,
+    // a workgroup per union entry takes the entry's slots in passes. Measured on MI355X (config 1 uniform, config 2
+    // Zipf, top-8 of 288): per slot is 5-15% faster at M = 2..4; two slots per pass are 4% faster at M = 16, 8% at
+    // M = 32 and 16% at M = 64 (there the extra weight streams of per slot cost more than its smaller LDS footprint
+    // gains). Four slots per pass match two at M = 64 and lose elsewhere; eight lose everywhere.
+    //
+    // Mode MFMA accumulates the GEMVs with MFMAs (same weights, transforms and rounding points; sums over the hidden
+    // dimension in MFMA order) with a workgroup per union entry taking up to 4 of its slots per pass: an expert's
+    // tiles are decoded once for all its tokens of the pass.
+    const int mf = mode == GFL_MODE_MFMA ? 1 : 0;
+    int ns = mf ? std::min(M, 4) : M <= 8 ? 1 : 2;
+    if (c->ns_override > 0) ns = std::min(c->ns_override, mf ? std::min(M, 16) : M);
+    if (gfl::gate_up_lds_bytes(L.K[0], ns, L.H, P, L.E, mf) > gfl::LDS_LIMIT ||
+        gfl::gate_up_lds_bytes(L.K[1], ns, L.H, P, L.E, mf) > gfl::LDS_LIMIT ||
+        gfl::down_lds_bytes(L.K[2], ns, L.I, mf) > gfl::LDS_LIMIT)
+        return fail(GFL_EINVAL, "gfl_moe_forward: shape needs more than 160 KB of LDS per workgroup");
+    const int wh = w_is_half ? 1 : 0;
+    auto gate_up = [&] {
+        if (L.K[0] == L.K[1])
+            return gfl::launch_gate_up(L.K[0], ns, L.dptrs, 0, 2, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
+                                       ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, st);
+        if (gfl::launch_gate_up(L.K[0], ns, L.dptrs, 0, 1, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
+                                ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, st))
+            return -1;
+        return gfl::launch_gate_up(L.K[1], ns, L.dptrs, 1, 1, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
+                                   ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, st);
+    };
+    auto down = [&] {
+        return gfl::launch_down(L.K[2], ns, L.dptrs, topk, L.H, L.I, umax, P, ws.pv, ws.xtd, ws.yd, ws.out_cnt,
+                                ws.blk_cnt, out, mf, st);
+    };
+    int r = prof ? staged(c, 1, st, gate_up) : gate_up();
+    if (!r) r = prof ? staged(c, 3, st, down) : down();
+    if (r) return r > 0 ? r : fail(GFL_EINVAL, "gfl_moe_forward: unsupported K");
+    GFL_HIP(hipGetLastError());
+    c->calls += 1;
+    c->picks += P;
+    return GFL_OK;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Static scratch of gfl_moe_forward_noalloc: one decode workspace per device in a file-scope device array, laid out
+// for GFL_NOALLOC_MAX_PICKS slots at GFL_NOALLOC_MAX_H x GFL_NOALLOC_MAX_I. Every device the library runs on holds
+// its own copy until the process ends. The host-side name `scratch` is not a device address: its address on each
+// device is taken once with hipGetSymbolAddress and only that pointer is handed to kernels.
+// ---------------------------------------------------------------------------------------------------------------
+
+constexpr WsSizes kScratch = ws_sizes(GFL_NOALLOC_MAX_PICKS, GFL_NOALLOC_MAX_H, GFL_NOALLOC_MAX_I);
+constexpr size_t kScratchBytes = kScratch.data() + kScratch.cnt;
+static_assert(kScratchBytes <= ((size_t)8 << 20), "the no-allocation scratch stays below 8 MiB");
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+// zeroes the counter region (a kernel rather than hipMemsetAsync, so a stream capture may record it)
+__global__ void zero_words(int* p, size_t n)
+{
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 0;
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// This device's scratch address (device current). On the first call for the device: look the address up and clear
+// the counter region on `st` (the kernels leave every counter at zero when they finish, so once is enough).
+int scratch_for_device(int device, hipStream_t st, void** out)
+{
+    if (device < 0 || device >= kMaxDevices) return fail(GFL_EINVAL, "gfl_moe_forward_noalloc: device index too large");
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (!g_scratch_ptr[device])
+    {
+        void* p = nullptr;
+        GFL_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return fail(GFL_ERUNTIME, "gfl_moe_forward_noalloc: hipGetSymbolAddress returned NULL");
+        const size_t nw = kScratch.cnt / sizeof(int);
+        hipLaunchKernelGGL(zero_words, dim3(64), dim3(256), 0, st, reinterpret_cast<int*>(static_cast<char*>(p) +
+                                                                                         kScratch.data()), nw);
+        GFL_HIP(hipGetLastError());
+        g_scratch_ptr[device] = p;
+    }
+    *out = g_scratch_ptr[device];
+    return GFL_OK;
 }
 
 }  // namespace
@@ -317,64 +433,35 @@ int gfl_register_layer(gfl_ctx* c, int li, int E, int H, int I, int k_gate, int 
 int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half, int M,
                     int topk, float* out, int mode, float act_limit, gfl_stream stream)
 {
-    if (!c || !x || !sel || !w || !out) return fail(GFL_EINVAL, "gfl_moe_forward: NULL argument");
-    if (li < 0 || li >= (int)c->layers.size() || !c->layers[li].dptrs)
-        return fail(GFL_EINVAL, "gfl_moe_forward: layer not registered");
-    // AFFINE (0) and I16 (2) name the reference CPU engine's speed modes; the device computes EXACT for them, which
-    // lies closer to the fp64 expert than either of them does
-    if (mode < GFL_MODE_AUTO || mode > GFL_MODE_MFMA)
-        return fail(GFL_EINVAL, "gfl_moe_forward: mode must be -1 (auto), 0 (affine), 1 (exact), 2 (i16) or 3 (mfma)");
-    if (M < 1 || topk < 1 || topk > gfl::MAX_TOPK || (int64_t)M * topk > gfl::MAX_PICKS)
-        return fail(GFL_EINVAL, "gfl_moe_forward: need 1 <= topk <= 16 and M*topk <= 1024");
-    if (!std::isfinite(act_limit) || act_limit < 0) return fail(GFL_EINVAL, "gfl_moe_forward: act_limit must be >= 0");
-    if (reinterpret_cast<uintptr_t>(x) & 15) return fail(GFL_EINVAL, "gfl_moe_forward: x must be 16-byte aligned");
+    if (const int r = check_forward(c, li, x, sel, w, M, topk, out, mode, act_limit, "gfl_moe_forward")) return r;
     std::lock_guard<std::mutex> g(c->mu);
     const Layer& L = c->layers[li];
     GFL_HIP(hipSetDevice(c->device));
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const int P = M * topk;
     if (!c->ws || L.H > c->ws_H || L.I > c->ws_I) return fail(GFL_ERUNTIME, "gfl_moe_forward: workspace not reserved");
     Workspace ws;
     carve_ws(c, L.H, L.I, ws);
-    const int umax = P < L.E ? P : L.E;
-    // slots per pass of the GEMV (its LDS holds NS transformed inputs). With one slot per pass the launches run a
-    // workgroup per slot, so an expert picked by several tokens is streamed once per slot in parallel; with more,
-    // a workgroup per union entry takes the entry's slots in passes. Measured on MI355X (config 1 uniform, config 2
-    // Zipf, top-8 of 288): per slot is 5-15% faster at M = 2..4; two slots per pass are 4% faster at M = 16, 8% at
-    // M = 32 and 16% at M = 64 (there the extra weight streams of per slot cost more than its smaller LDS footprint
-    // gains). Four slots per pass match two at M = 64 and lose elsewhere; eight lose everywhere.
-    //
-    // Mode MFMA accumulates the GEMVs with MFMAs (same weights, transforms and rounding points; sums over the hidden
-    // dimension in MFMA order) with a workgroup per union entry taking up to 4 of its slots per pass: an expert's
-    // tiles are decoded once for all its tokens of the pass.
-    const int mf = mode == GFL_MODE_MFMA ? 1 : 0;
-    int ns = mf ? std::min(M, 4) : M <= 8 ? 1 : 2;
-    if (c->ns_override > 0) ns = std::min(c->ns_override, mf ? std::min(M, 16) : M);
-    if (gfl::gate_up_lds_bytes(L.K[0], ns, L.H, P, L.E, mf) > gfl::LDS_LIMIT ||
-        gfl::gate_up_lds_bytes(L.K[1], ns, L.H, P, L.E, mf) > gfl::LDS_LIMIT ||
-        gfl::down_lds_bytes(L.K[2], ns, L.I, mf) > gfl::LDS_LIMIT)
-        return fail(GFL_EINVAL, "gfl_moe_forward: shape needs more than 160 KB of LDS per workgroup");
-    const int wh = w_is_half ? 1 : 0;
-    int r = staged(c, 1, st, [&] {
-        if (L.K[0] == L.K[1])
-            return gfl::launch_gate_up(L.K[0], ns, L.dptrs, 0, 2, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                       ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, st);
-        if (gfl::launch_gate_up(L.K[0], ns, L.dptrs, 0, 1, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, st))
-            return -1;
-        return gfl::launch_gate_up(L.K[1], ns, L.dptrs, 1, 1, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                   ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, st);
-    });
-    if (!r)
-        r = staged(c, 3, st, [&] {
-            return gfl::launch_down(L.K[2], ns, L.dptrs, topk, L.H, L.I, umax, P, ws.pv, ws.xtd, ws.yd, ws.out_cnt,
-                                    ws.blk_cnt, out, mf, st);
-        });
-    if (r) return r > 0 ? r : fail(GFL_EINVAL, "gfl_moe_forward: unsupported K");
-    GFL_HIP(hipGetLastError());
-    c->calls += 1;
-    c->picks += P;
-    return GFL_OK;
+    return run_forward(c, L, ws, x, sel, w, w_is_half, M, topk, out, mode, act_limit,
+                       reinterpret_cast<hipStream_t>(stream), true);
+}
+
+int gfl_moe_forward_noalloc(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half,
+                            int M, int topk, float* out, int mode, float act_limit, gfl_stream stream)
+{
+    const char* who = "gfl_moe_forward_noalloc";
+    if (const int r = check_forward(c, li, x, sel, w, M, topk, out, mode, act_limit, who)) return r;
+    std::lock_guard<std::mutex> g(c->mu);
+    const Layer& L = c->layers[li];
+    if ((int64_t)M * topk > GFL_NOALLOC_MAX_PICKS || L.H > GFL_NOALLOC_MAX_H || L.I > GFL_NOALLOC_MAX_I)
+        return fail(GFL_EINVAL, std::string(who) + ": needs M*topk <= " + std::to_string(GFL_NOALLOC_MAX_PICKS) +
+                                    ", H <= " + std::to_string(GFL_NOALLOC_MAX_H) + " and I <= " +
+                                    std::to_string(GFL_NOALLOC_MAX_I) + " (the static scratch array's layout)");
+    GFL_HIP(hipSetDevice(c->device));
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    void* base = nullptr;
+    if (const int r = scratch_for_device(c->device, st, &base)) return r;
+    Workspace ws;
+    carve_at(base, GFL_NOALLOC_MAX_PICKS, GFL_NOALLOC_MAX_H, GFL_NOALLOC_MAX_I, L.H, L.I, ws);
+    return run_forward(c, L, ws, x, sel, w, w_is_half, M, topk, out, mode, act_limit, st, false);
 }
 
 // The prefill workspace of a context, grown on demand (never inside a graph capture), and the grouped plan carved

@@ -87,6 +87,21 @@ int gfl_layer_info(gfl_ctx* ctx, int li, int* info);
 int gfl_moe_forward(gfl_ctx* ctx, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half, int M,
                     int topk, float* out, int mode, float act_limit, gfl_stream stream);
 
+/* No counterpart in the reference. gfl_moe_forward with the per-call workspace in a file-scope device array of the
+ * library (about 6.5 MiB per device, held until the process ends) instead of the context's reserved workspace: for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). It calls no hipMalloc, hipFree or other allocating routine (and records no profiling events);
+ * everything it needs was allocated by gfl_ctx_create and gfl_register_layer. Same arguments and results as
+ * gfl_moe_forward (bit-identical), within the array's layout: M*topk <= GFL_NOALLOC_MAX_PICKS, the layer's
+ * H <= GFL_NOALLOC_MAX_H and I <= GFL_NOALLOC_MAX_I, else GFL_EINVAL. All calls on one device share the array (its
+ * counters are cleared on the device's first call and left at zero by every call): calls that overlap on one device,
+ * from any context or stream, race. */
+#define GFL_NOALLOC_MAX_PICKS 64
+#define GFL_NOALLOC_MAX_H 8192
+#define GFL_NOALLOC_MAX_I 4096
+int gfl_moe_forward_noalloc(gfl_ctx* ctx, int li, const uint16_t* x, const int64_t* sel, const void* w,
+                            int w_is_half, int M, int topk, float* out, int mode, float act_limit, gfl_stream stream);
+
 /* mode: AUTO, AFFINE, EXACT or I16 (all computed bit-exact to EXACT), or MFMA. With MFMA the workgroups of a routed expert take up to 4 of its slots
  * per pass, so the expert's tiles are decoded once for all of them.
  * Environment: GFL_SLOTS_PER_PASS = 1, 2, 4 or 8 forces the number of (token, expert) slots one GEMV pass of

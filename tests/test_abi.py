@@ -36,6 +36,9 @@ def test_library_exports_every_declared_symbol(lib):
     assert set(syms) == set(_native.SYMBOLS)
     for s in syms:
         getattr(lib, s)
+    # every entry point with arguments is typed for ctypes (an untyped float or int64 argument would be mangled)
+    untyped = [s for s in syms if s not in ("gfl_last_error", "gfl_version") and getattr(lib, s).argtypes is None]
+    assert not untyped, untyped
 
 
 def test_version_and_error_string(lib):
