@@ -64,6 +64,9 @@ struct gfl_ctx
     // workspace of the prefill path (gfl_grouped_forward / gfl_grouped_reserve), grown on demand outside captures
     void* gws = nullptr;
     size_t gws_bytes = 0;
+    // last-one counters of the EXACT path above 1024 picks (zero between calls), grown with the prefill workspace
+    void* xcnt = nullptr;
+    size_t xcnt_bytes = 0;
     // superseded workspaces: a graph captured before a workspace grew still holds their addresses, so they stay
     // allocated until gfl_ctx_destroy
     std::vector<void*> retired;
@@ -193,7 +196,7 @@ int staged(gfl_ctx* c, int stage, hipStream_t st, F&& launch)
 
 // Argument checks shared by the decode forward entry points (returns GFL_OK or the failure code, message set).
 int check_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, const void* w, int M, int topk,
-                  const float* out, int mode, float act_limit, const char* who)
+                  const float* out, int mode, float act_limit, const char* who, int max_picks)
 {
     const std::string f(who);
     if (!c || !x || !sel || !w || !out) return fail(GFL_EINVAL, f + ": NULL argument");
@@ -202,8 +205,11 @@ int check_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, con
     // lies closer to the fp64 expert than either of them does
     if (mode < GFL_MODE_AUTO || mode > GFL_MODE_MFMA)
         return fail(GFL_EINVAL, f + ": mode must be -1 (auto), 0 (affine), 1 (exact), 2 (i16) or 3 (mfma)");
-    if (M < 1 || topk < 1 || topk > gfl::MAX_TOPK || (int64_t)M * topk > gfl::MAX_PICKS)
-        return fail(GFL_EINVAL, f + ": need 1 <= topk <= 16 and M*topk <= 1024");
+    if (M < 1 || topk < 1 || topk > gfl::MAX_TOPK || (int64_t)M * topk > max_picks)
+        return fail(GFL_EINVAL, f + ": need 1 <= topk <= 16 and M*topk <= " + std::to_string(max_picks));
+    if ((int64_t)M * topk > gfl::MAX_PICKS && mode == GFL_MODE_MFMA)
+        return fail(GFL_EINVAL, f + ": mode MFMA takes M*topk <= 1024 (gfl_grouped_forward is the MFMA path for "
+                                    "more)");
     if (!std::isfinite(act_limit) || act_limit < 0) return fail(GFL_EINVAL, f + ": act_limit must be >= 0");
     if (reinterpret_cast<uintptr_t>(x) & 15) return fail(GFL_EINVAL, f + ": x must be 16-byte aligned");
     return GFL_OK;
@@ -398,6 +404,7 @@ int gfl_ctx_destroy(gfl_ctx* c)
         if (L.dptrs) hipFree(L.dptrs);
     if (c->ws) hipFree(c->ws);
     if (c->gws) hipFree(c->gws);
+    if (c->xcnt) hipFree(c->xcnt);
     for (void* p : c->retired) hipFree(p);
     if (c->silu_tab) hipFree(c->silu_tab);
     delete c;
@@ -430,13 +437,21 @@ int gfl_register_layer(gfl_ctx* c, int li, int E, int H, int I, int k_gate, int 
     return reserve_ws(c, H, I);
 }
 
+static int run_forward_grouped_plan(gfl_ctx* c, const Layer& L, const uint16_t* x, const int64_t* sel, const void* w,
+                                    int w_is_half, int M, int topk, float* out, float act_limit, hipStream_t st);
+
 int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half, int M,
                     int topk, float* out, int mode, float act_limit, gfl_stream stream)
 {
-    if (const int r = check_forward(c, li, x, sel, w, M, topk, out, mode, act_limit, "gfl_moe_forward")) return r;
+    if (const int r = check_forward(c, li, x, sel, w, M, topk, out, mode, act_limit, "gfl_moe_forward",
+                                    gfl::MAX_GROUPED_PICKS))
+        return r;
     std::lock_guard<std::mutex> g(c->mu);
     const Layer& L = c->layers[li];
     GFL_HIP(hipSetDevice(c->device));
+    if (M * topk > gfl::MAX_PICKS)
+        return run_forward_grouped_plan(c, L, x, sel, w, w_is_half, M, topk, out, act_limit,
+                                        reinterpret_cast<hipStream_t>(stream));
     if (!c->ws || L.H > c->ws_H || L.I > c->ws_I) return fail(GFL_ERUNTIME, "gfl_moe_forward: workspace not reserved");
     Workspace ws;
     carve_ws(c, L.H, L.I, ws);
@@ -448,7 +463,8 @@ int gfl_moe_forward_noalloc(gfl_ctx* c, int li, const uint16_t* x, const int64_t
                             int M, int topk, float* out, int mode, float act_limit, gfl_stream stream)
 {
     const char* who = "gfl_moe_forward_noalloc";
-    if (const int r = check_forward(c, li, x, sel, w, M, topk, out, mode, act_limit, who)) return r;
+    if (const int r = check_forward(c, li, x, sel, w, M, topk, out, mode, act_limit, who, GFL_NOALLOC_MAX_PICKS))
+        return r;
     std::lock_guard<std::mutex> g(c->mu);
     const Layer& L = c->layers[li];
     if ((int64_t)M * topk > GFL_NOALLOC_MAX_PICKS || L.H > GFL_NOALLOC_MAX_H || L.I > GFL_NOALLOC_MAX_I)
@@ -464,36 +480,60 @@ int gfl_moe_forward_noalloc(gfl_ctx* c, int li, const uint16_t* x, const int64_t
     return run_forward(c, L, ws, x, sel, w, w_is_half, M, topk, out, mode, act_limit, st, false);
 }
 
-// The prefill workspace of a context, grown on demand (never inside a graph capture), and the grouped plan carved
-// from it. Layout: plan ints, then xt [2][P][H] fp16, ygu [2][P][I] fp16, xd [P][I] fp16, yraw [P][H] fp16 (H = I = 0
-// for the plan alone). Returns GFL_OK or the failure code (message set).
-static int grouped_workspace(gfl_ctx* c, hipStream_t st, int P, int M, int E, int H, int I, const char* who,
-                             gfl::GPlan& gp, char*& b, size_t& b_int, size_t& b_xt, size_t& b_ygu, size_t& b_xd)
+// The prefill workspace of a context, grown on demand (never inside a graph capture). Layout: the grouped plan's ints,
+// the EXACT path's PlanView arrays (hdr, uexp, uoff, uptr), then one data region for whichever path runs: the MFMA
+// grouped path's xt [2][P][H], ygu [2][P][I], xd [P][I], yraw [P][H] (fp16), or the EXACT path's ygu [2][P][I] fp32,
+// xtd [P][I] fp16, yd [P][H] fp32. The EXACT path's last-one counters ([E][I/128] + [M][H/128]) live in a buffer of
+// their own, zeroed when allocated (the kernels leave them at zero; the data region is overwritten by both paths).
+struct Gws
+{
+    gfl::GPlan gp;
+    gfl::PlanView pv;
+    uint16_t *xt, *ygu16, *xd, *yraw;
+    float *ygu, *yd;
+    uint16_t* xtd;
+    int *act_cnt, *out_cnt;
+};
+
+static int grow(gfl_ctx* c, hipStream_t st, void** buf, size_t* have, size_t need, bool zero, const char* who)
+{
+    if (need <= *have) return GFL_OK;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (st && hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+        return fail(GFL_EINVAL, std::string(who) + ": the workspace must be sized before graph capture "
+                                                  "(gfl_grouped_reserve, or one call of this shape first)");
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, need);
+    if (e != hipSuccess) return fail(GFL_ENOMEM, std::string(who) + ": workspace hipMalloc: " + hipGetErrorString(e));
+    if (zero && (e = hipMemset(p, 0, need)) != hipSuccess)
+    {
+        hipFree(p);
+        return hip_fail(e, "workspace hipMemset");
+    }
+    // the old buffer is retired, not freed: a graph captured before this growth still holds its addresses
+    if (*buf) c->retired.push_back(*buf);
+    *buf = p;
+    *have = need;
+    return GFL_OK;
+}
+
+static int grouped_workspace(gfl_ctx* c, hipStream_t st, int P, int M, int E, int H, int I, const char* who, Gws& w)
 {
     const size_t nch = (P + gfl::GP_PLAN_CHUNK - 1) / gfl::GP_PLAN_CHUNK;
     const size_t n_int = 4 + (size_t)E + (E + 1) + 7 * (size_t)P + (size_t)M + (size_t)P + (size_t)E + nch * (E + 1);
-    b_int = align256(sizeof(int) * n_int);
-    b_xt = align256(2 * 2 * (size_t)P * H);
-    b_ygu = align256(2 * 2 * (size_t)P * I);
-    b_xd = align256(2 * (size_t)P * I);
-    const size_t b_yr = align256(2 * (size_t)P * H);
-    const size_t need = b_int + b_xt + b_ygu + b_xd + b_yr;
-    if (need > c->gws_bytes)
-    {
-        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
-            return fail(GFL_EINVAL, std::string(who) + ": the workspace must be sized before graph capture "
-                                                      "(gfl_grouped_reserve, or one call of this shape first)");
-        void* p = nullptr;
-        hipError_t e = hipMalloc(&p, need);
-        if (e != hipSuccess) return fail(GFL_ENOMEM, std::string("grouped workspace hipMalloc: ") + hipGetErrorString(e));
-        // the old buffer is retired, not freed: a graph captured before this growth still holds its addresses
-        if (c->gws) c->retired.push_back(c->gws);
-        c->gws = p;
-        c->gws_bytes = need;
-    }
-    b = static_cast<char*>(c->gws);
+    const size_t b_int = align256(sizeof(int) * n_int);
+    const size_t b_xpi = align256(sizeof(int) * (4 + (size_t)E + E + 1)), b_xpu = align256(sizeof(uint64_t) * 2 * E);
+    const size_t g_xt = align256(2 * 2 * (size_t)P * H), g_ygu = align256(2 * 2 * (size_t)P * I);
+    const size_t g_xd = align256(2 * (size_t)P * I), g_yr = align256(2 * (size_t)P * H);
+    const size_t x_ygu = align256(4 * 2 * (size_t)P * I), x_xtd = align256(2 * (size_t)P * I);
+    const size_t x_yd = align256(4 * (size_t)P * H);
+    const size_t data = std::max(g_xt + g_ygu + g_xd + g_yr, x_ygu + x_xtd + x_yd);
+    if (const int r = grow(c, st, &c->gws, &c->gws_bytes, b_int + b_xpi + b_xpu + data, false, who)) return r;
+    const size_t ncnt = (size_t)E * (I / 128) + (size_t)M * (H / 128);
+    if (const int r = grow(c, st, &c->xcnt, &c->xcnt_bytes, sizeof(int) * ncnt, true, who)) return r;
+    char* b = static_cast<char*>(c->gws);
     int* ip = reinterpret_cast<int*>(b);
+    gfl::GPlan& gp = w.gp;
     gp.hdr = ip;
     gp.cnt = gp.hdr + 4;
     gp.off = gp.cnt + E;
@@ -507,6 +547,52 @@ static int grouped_workspace(gfl_ctx* c, hipStream_t st, int P, int M, int E, in
     gp.tok_npk = reinterpret_cast<int*>(gp.tok_w + P);
     gp.eord = gp.tok_npk + M;
     gp.ccnt = gp.eord + E;
+    gfl::PlanView& pv = w.pv;
+    int* xp = reinterpret_cast<int*>(b + b_int);
+    pv.hdr = xp;
+    pv.uexp = xp + 4;
+    pv.uoff = pv.uexp + E;
+    pv.uptr = reinterpret_cast<uint64_t*>(b + b_int + b_xpi);
+    pv.slot_pick = gp.slot_pick;
+    pv.tok_slot = gp.tok_slot;
+    pv.tok_w = gp.tok_w;
+    pv.tok_npk = gp.tok_npk;
+    pv.slot_u = pv.pick_slot = pv.pick_job = nullptr;   // not read by the launches that take this plan
+    pv.cap_slots = P;
+    char* d = b + b_int + b_xpi + b_xpu;
+    w.xt = reinterpret_cast<uint16_t*>(d);
+    w.ygu16 = reinterpret_cast<uint16_t*>(d + g_xt);
+    w.xd = reinterpret_cast<uint16_t*>(d + g_xt + g_ygu);
+    w.yraw = reinterpret_cast<uint16_t*>(d + g_xt + g_ygu + g_xd);
+    w.ygu = reinterpret_cast<float*>(d);
+    w.xtd = reinterpret_cast<uint16_t*>(d + x_ygu);
+    w.yd = reinterpret_cast<float*>(d + x_ygu + x_xtd);
+    w.act_cnt = static_cast<int*>(c->xcnt);
+    w.out_cnt = w.act_cnt + (size_t)E * (I / 128);
+    return GFL_OK;
+}
+
+// EXACT above MAX_PICKS picks (caller holds c->mu, device set): the grouped plan of the prefill path, then the decode
+// kernels with a workgroup per expert in passes of 4 slots, driven by that plan (bit-identical to the decode path).
+static int run_forward_grouped_plan(gfl_ctx* c, const Layer& L, const uint16_t* x, const int64_t* sel, const void* w,
+                                    int w_is_half, int M, int topk, float* out, float act_limit, hipStream_t st)
+{
+    const int P = M * topk;
+    if (gfl::gate_up_lds_bytes(L.K[0], 4, L.H, 0, 0, 0) > gfl::LDS_LIMIT ||
+        gfl::gate_up_lds_bytes(L.K[1], 4, L.H, 0, 0, 0) > gfl::LDS_LIMIT ||
+        gfl::down_lds_bytes(L.K[2], 4, L.I, 0) > gfl::LDS_LIMIT)
+        return fail(GFL_EINVAL, "gfl_moe_forward: shape needs more than 160 KB of LDS per workgroup");
+    Gws ws;
+    if (const int rc = grouped_workspace(c, st, P, M, L.E, L.H, L.I, "gfl_moe_forward", ws)) return rc;
+    const int r = staged(c, 1, st, [&] {
+        gfl::launch_grouped_plan(sel, w, w_is_half ? 1 : 0, P, topk, L.E, ws.gp, st);
+        return gfl::launch_exact_grouped(L.K, L.dptrs, P, topk, L.E, M, L.H, L.I, x, ws.gp, ws.pv, ws.ygu, ws.xtd,
+                                         ws.yd, ws.act_cnt, ws.out_cnt, c->silu_tab, act_limit, out, st);
+    });
+    if (r) return r > 0 ? r : fail(GFL_EINVAL, "gfl_moe_forward: unsupported K");
+    GFL_HIP(hipGetLastError());
+    c->calls += 1;
+    c->picks += P;
     return GFL_OK;
 }
 
@@ -528,18 +614,11 @@ int gfl_grouped_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* se
     GFL_HIP(hipSetDevice(c->device));
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const int P = M * topk, E = L.E, H = L.H, I = L.I;
-    gfl::GPlan gp;
-    char* b = nullptr;
-    size_t b_int = 0, b_xt = 0, b_ygu = 0, b_xd = 0;
-    if (const int rc = grouped_workspace(c, st, P, M, E, H, I, "gfl_grouped_forward", gp, b, b_int, b_xt, b_ygu, b_xd))
-        return rc;
-    uint16_t* xt = reinterpret_cast<uint16_t*>(b + b_int);
-    uint16_t* ygu = reinterpret_cast<uint16_t*>(b + b_int + b_xt);
-    uint16_t* xd = reinterpret_cast<uint16_t*>(b + b_int + b_xt + b_ygu);
-    uint16_t* yraw = reinterpret_cast<uint16_t*>(b + b_int + b_xt + b_ygu + b_xd);
+    Gws ws;
+    if (const int rc = grouped_workspace(c, st, P, M, E, H, I, "gfl_grouped_forward", ws)) return rc;
     const int r = staged(c, 2, st, [&] {
-        return gfl::launch_grouped(L.dptrs, sel, w, w_is_half ? 1 : 0, P, topk, E, H, I, L.K[0], L.K[1], L.K[2], x, gp,
-                                   P, xt, ygu, xd, yraw, c->silu_tab, act_limit, out, st);
+        return gfl::launch_grouped(L.dptrs, sel, w, w_is_half ? 1 : 0, P, topk, E, H, I, L.K[0], L.K[1], L.K[2], x,
+                                   ws.gp, P, ws.xt, ws.ygu16, ws.xd, ws.yraw, c->silu_tab, act_limit, out, st);
     });
     if (r) return fail(GFL_ERUNTIME, "gfl_grouped_forward: launch set-up failed");
     GFL_HIP(hipGetLastError());
@@ -559,12 +638,9 @@ int gfl_grouped_reserve(gfl_ctx* c, int max_picks)
         if (L.dptrs) { E = std::max(E, L.E); H = std::max(H, L.H); I = std::max(I, L.I); }
     if (!E) return fail(GFL_EINVAL, "gfl_grouped_reserve: no layer registered");
     GFL_HIP(hipSetDevice(c->device));
-    gfl::GPlan gp;
-    char* b = nullptr;
-    size_t b_int = 0, b_xt = 0, b_ygu = 0, b_xd = 0;
+    Gws ws;
     // the largest layout any call up to max_picks picks can take: M <= picks tokens
-    return grouped_workspace(c, nullptr, max_picks, max_picks, E, H, I, "gfl_grouped_reserve", gp, b, b_int, b_xt,
-                             b_ygu, b_xd);
+    return grouped_workspace(c, nullptr, max_picks, max_picks, E, H, I, "gfl_grouped_reserve", ws);
 }
 
 int gfl_layer_info(gfl_ctx* c, int li, int* info)
@@ -592,11 +668,9 @@ int gfl_grouped_plan(gfl_ctx* c, const int64_t* sel, const void* w, int w_is_hal
     GFL_HIP(hipSetDevice(c->device));
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const int P = M * topk;
-    gfl::GPlan gp;
-    char* b = nullptr;
-    size_t b_int = 0, b_xt = 0, b_ygu = 0, b_xd = 0;
-    if (const int rc = grouped_workspace(c, st, P, M, E, 0, 0, "gfl_grouped_plan", gp, b, b_int, b_xt, b_ygu, b_xd))
-        return rc;
+    Gws ws;
+    if (const int rc = grouped_workspace(c, st, P, M, E, 0, 0, "gfl_grouped_plan", ws)) return rc;
+    const gfl::GPlan& gp = ws.gp;
     gfl::launch_grouped_plan(sel, w, w_is_half ? 1 : 0, P, topk, E, gp, st);
     GFL_HIP(hipGetLastError());
     GFL_HIP(hipMemcpyAsync(hdr, gp.hdr, 2 * sizeof(int), hipMemcpyDeviceToDevice, st));

@@ -115,12 +115,12 @@ def tier_forward(li, x, sel, w, mode):
     sum over picks of w * expert(x) in the reference's job order. Tensors may live on the CPU (as the reference's)
     or on the device; the result is on x's device.
 
-    Every mode number of the reference is accepted. Up to 1024 picks all of them compute EXACT, bit-identical to the
-    reference's EXACT mode: mode 1 asks for it, mode -1 (auto) picks it, and modes 0 (AFFINE) and 2 (I16), the
-    reference CPU engine's speed modes (ft_tier_ext.cpp:900), get EXACT as well, which lies closer to the fp64 expert
-    (ref_expert, ft_core.h:1674-1691) than either of them does. Above 1024 picks (prefill-sized batches, up to 65536)
-    the MFMA grouped path runs: the exact weights, rounding points and combine order, with the sums formed in MFMA
-    order."""
+    Every mode number of the reference is accepted. Mode 1 (EXACT) is bit-identical to the reference's EXACT mode at
+    every size up to 65536 picks. Modes -1 (auto), 0 (AFFINE) and 2 (I16) name the reference CPU engine's speed
+    choices (ft_tier_ext.cpp:900): up to 1024 picks they compute EXACT too (it costs nothing more on the device and lies
+    closer to the fp64 expert, ref_expert, ft_core.h:1674-1691, than AFFINE or I16 do); above 1024 picks they take the
+    MFMA grouped path (the exact weights, rounding points and combine order, with the hidden-dimension sums formed in
+    MFMA order: at the config-4 shape, M=2048, 3.6e-4 RMS and 2.9e-3 max-abs of the output RMS from EXACT)."""
     import torch
     _check(T is not None and not T.running, "tier_forward: worker running")
     _check(0 <= li < len(T.layers) and T.layers[li] is not None, "tier_forward: layer not registered")
@@ -129,7 +129,7 @@ def tier_forward(li, x, sel, w, mode):
     _check(sel.dtype in (torch.int32, torch.int64) and sel.dim() == 2 and sel.size(0) == x.size(0), "sel: int32 [m, k]")
     _check(w.dtype == torch.float32 and tuple(w.shape) == tuple(sel.shape), "w: float32 [m, k]")
     m, k = sel.shape
-    grouped = m * k > 1024
+    grouped = m * k > 1024 and int(mode) != 1
     _check(k <= 16 and m * k <= 65536, "tier_forward: k <= 16 and m * k <= 65536 picks")
     dev = torch.device("cuda", T.ctx.device)
     x16 = x.to(dev).half()

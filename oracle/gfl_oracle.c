@@ -385,8 +385,8 @@ int gflo_build_jobs(int E, int ntok, const int32_t* sel, const float* w, int top
     return nj;
 }
 
-int gflo_moe_forward(const gflo_expert* experts, int E, const float* x, int ntok, const int32_t* sel,
-                     const float* w, int topk, float* out, int mode, float act_limit)
+int gflo_moe_forward_rows(const gflo_expert* experts, int E, const float* x, int ntok, const int32_t* sel,
+                          const float* w, int topk, const uint8_t* want, float* out, int mode, float act_limit)
 {
     const int H = experts[0].g.k;
     const int cap = ntok * topk;
@@ -397,14 +397,27 @@ int gflo_moe_forward(const gflo_expert* experts, int E, const float* x, int ntok
     const int nj = gflo_build_jobs(E, ntok, sel, w, topk, je, jm, jt, jw);
     float* yd = (float*)malloc(sizeof(float) * (size_t)(nj + 1) * 8 * H);
     float* xj = (float*)malloc(sizeof(float) * (size_t)8 * H);
+    float* yj = (float*)malloc(sizeof(float) * (size_t)8 * H);
+    int mem[8];
     for (int j = 0; j < nj; ++j)
     {
-        for (int i = 0; i < jm[j]; ++i) memcpy(xj + (size_t)i * H, x + (size_t)jt[j * 8 + i] * H, sizeof(float) * H);
-        gflo_expert_forward(&experts[je[j]], xj, jm[j], yd + (size_t)j * 8 * H, mode, act_limit);
+        /* the job's members (all, or those whose rows are wanted); each token's expert output depends on its own
+           input only, so a job may be evaluated for a subset of its members */
+        int m = 0;
+        for (int i = 0; i < jm[j]; ++i)
+            if (!want || want[jt[j * 8 + i]]) mem[m++] = i;
+        if (m == 0) continue;
+        for (int q = 0; q < m; ++q)
+            memcpy(xj + (size_t)q * H, x + (size_t)jt[j * 8 + mem[q]] * H, sizeof(float) * H);
+        gflo_expert_forward(&experts[je[j]], xj, m, yj, mode, act_limit);
+        for (int q = 0; q < m; ++q)
+            memcpy(yd + ((size_t)j * 8 + mem[q]) * H, yj + (size_t)q * H, sizeof(float) * H);
     }
     /* weighted accumulate in job order (fwd_phase phase 3, ft_core.h:1020-1033) */
     memset(out, 0, sizeof(float) * (size_t)ntok * H);
     for (int t = 0; t < ntok; ++t)
+    {
+        if (want && !want[t]) continue;
         for (int j = 0; j < nj; ++j)
             for (int i = 0; i < jm[j]; ++i)
                 if (jt[j * 8 + i] == t)
@@ -414,8 +427,15 @@ int gflo_moe_forward(const gflo_expert* experts, int E, const float* x, int ntok
                     float* o = out + (size_t)t * H;
                     for (int c = 0; c < H; ++c) o[c] += wt * y[c];
                 }
-    free(je); free(jm); free(jt); free(jw); free(yd); free(xj);
+    }
+    free(je); free(jm); free(jt); free(jw); free(yd); free(xj); free(yj);
     return nj;
+}
+
+int gflo_moe_forward(const gflo_expert* experts, int E, const float* x, int ntok, const int32_t* sel,
+                     const float* w, int topk, float* out, int mode, float act_limit)
+{
+    return gflo_moe_forward_rows(experts, E, x, ntok, sel, w, topk, NULL, out, mode, act_limit);
 }
 
 /* ------------------------------------------------------------------------------------------------------------ */

@@ -65,6 +65,10 @@ void gflo_expert_ref64(const gflo_expert* E, const float* x, float* y, float act
  * Jobs in first-appearance order, <= 8 tokens per job; out[t] = sum over jobs in order of w * expert(x_t). */
 int gflo_moe_forward(const gflo_expert* experts, int E, const float* x, int ntok, const int32_t* sel,
                      const float* w, int topk, float* out, int mode, float act_limit);
+/* The same with the jobs built over all ntok tokens (so every token's combine order is the full batch's) but only
+ * the rows with want[t] != 0 evaluated; the other rows of out are zero. want = NULL: all rows. */
+int gflo_moe_forward_rows(const gflo_expert* experts, int E, const float* x, int ntok, const int32_t* sel,
+                          const float* w, int topk, const uint8_t* want, float* out, int mode, float act_limit);
 /* job list as the reference builds it: returns job count; job_e[j], job_m[j], job_tok[j*8+i], job_w[j*8+i] */
 int gflo_build_jobs(int E, int ntok, const int32_t* sel, const float* w, int topk, int32_t* job_e, int32_t* job_m,
                     int32_t* job_tok, float* job_w);

@@ -14,6 +14,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB = os.path.join(HERE, "_build", "libgfl_oracle.so")
 REFLIB = os.path.join(HERE, "_ref", "libftref.so")
+REFLIB_SERVER = os.path.join(HERE, "_ref", "libftref_server.so")   # the server's flags, default contraction
 
 _P = C.c_void_p
 
@@ -79,6 +80,9 @@ class Oracle:
         L.gflo_moe_forward.restype = C.c_int
         L.gflo_moe_forward.argtypes = [C.POINTER(_CExpert), C.c_int, _P, C.c_int, _P, _P, C.c_int, _P, C.c_int,
                                        C.c_float]
+        L.gflo_moe_forward_rows.restype = C.c_int
+        L.gflo_moe_forward_rows.argtypes = [C.POINTER(_CExpert), C.c_int, _P, C.c_int, _P, _P, C.c_int, _P, _P,
+                                            C.c_int, C.c_float]
         L.gflo_build_jobs.restype = C.c_int
         L.gflo_build_jobs.argtypes = [C.c_int, C.c_int, _P, _P, C.c_int, _P, _P, _P, _P]
         L.gflo_split.argtypes = [_P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P,
@@ -173,6 +177,22 @@ class Oracle:
         self.L.gflo_moe_forward(arr, len(experts), _ptr(x), x.shape[0], _ptr(sel), _ptr(w), sel.shape[1], _ptr(out),
                                 mode, act_limit)
         return out
+
+    def moe_forward_rows(self, experts, x, sel, w, rows, mode=1, act_limit=0.0):
+        """moe_forward with the jobs of the whole batch (each token's combine order as in the full call) but only the
+        given rows evaluated: returns fp32 [len(rows)][H]. experts: a list over all expert ids; entries of experts no
+        wanted row picks are never read (any Mat tuple will do)."""
+        H = experts[0][0].k
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, H)
+        sel = np.ascontiguousarray(sel, dtype=np.int32).reshape(x.shape[0], -1)
+        w = np.ascontiguousarray(w, dtype=np.float32).reshape(sel.shape)
+        want = np.zeros(x.shape[0], np.uint8)
+        want[list(rows)] = 1
+        arr = (_CExpert * len(experts))(*[_CExpert(_cmat(g), _cmat(u), _cmat(d)) for g, u, d in experts])
+        out = np.empty_like(x)
+        self.L.gflo_moe_forward_rows(arr, len(experts), _ptr(x), x.shape[0], _ptr(sel), _ptr(w), sel.shape[1],
+                                     _ptr(want), _ptr(out), mode, act_limit)
+        return out[list(rows)]
 
     def build_jobs(self, E, sel, w):
         sel = np.ascontiguousarray(sel, dtype=np.int32)
@@ -286,7 +306,8 @@ class RefEngine:
                                       C.c_float]
         L.ref_expert64.argtypes = [C.c_int, C.c_int, _P, _P, _P, _P]
         L.ref_time_decode.restype = C.c_int
-        L.ref_time_decode.argtypes = [C.c_int, C.c_int, C.c_int, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, _P]
+        L.ref_time_decode.argtypes = [C.c_int, C.c_int, C.c_int, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int,
+                                      C.c_int, _P]
         cpus = list(cpus) if cpus else [0]
         arr = np.array(cpus, np.int32)
         self.threads = L.ref_init(int(threads), _ptr(arr), len(cpus))
@@ -331,11 +352,13 @@ class RefEngine:
         return y
 
     def time_decode(self, experts, x, topk, iters, warmup, mode):
+        """Per-call wall seconds of `iters` decode calls of x.shape[0] tokens (x fp32 [H] or [M][H]) x topk experts,
+        expert sets cycling through the pool (ref_time_decode)."""
         g0 = experts[0][0]
         trs, scs = self._tables(experts)
-        x = np.ascontiguousarray(x, dtype=np.float32).reshape(g0.k)
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, g0.k)
         secs = np.zeros(iters, np.float64)
-        rc = self.L.ref_time_decode(len(experts), g0.k, g0.n, trs, scs, _ptr(x), topk, iters, warmup, mode,
-                                    _ptr(secs))
+        rc = self.L.ref_time_decode(len(experts), g0.k, g0.n, trs, scs, _ptr(x), x.shape[0], topk, iters, warmup,
+                                    mode, _ptr(secs))
         assert rc == 0
         return secs

@@ -92,24 +92,28 @@ void ref_expert64(int H, int I, const uint8_t* const* tr, const uint16_t* const*
     ref_expert(L.ex[0], W, x, y);
 }
 
-// Decode-call timing in the style of tools/bench/kernel-ab-harness.cpp HARNESS_TIME (:51-105): `iters` calls of one
-// token x `topk` experts, expert sets cycling through the E-expert pool so weights come from DRAM, after `warmup`
-// untimed calls. Writes per-call wall seconds into `secs` (length iters).
-int ref_time_decode(int E, int H, int I, const uint8_t* const* tr, const uint16_t* const* sc, const float* x, int topk,
-                    int iters, int warmup, int mode, double* secs)
+// Decode-call timing in the style of tools/bench/kernel-ab-harness.cpp HARNESS_TIME (:51-105): `iters` calls of
+// `ntok` tokens x `topk` experts each, expert sets cycling through the E-expert pool so weights come from DRAM, after
+// `warmup` untimed calls. x fp32 [ntok][H]. Writes per-call wall seconds into `secs` (length iters). Token t of call
+// `it` picks experts (it*ntok*topk + t*topk + q) % E, q < topk: distinct experts within and across the call's tokens
+// while ntok*topk <= E (the union is ntok*topk experts, the uniform-routing worst case).
+int ref_time_decode(int E, int H, int I, const uint8_t* const* tr, const uint16_t* const* sc, const float* x,
+                    int ntok, int topk, int iters, int warmup, int mode, double* secs)
 {
     if (!g_pool) return -1;
     init_perm();
     init_tables();
     Layer L;
     build_layer(L, E, H, I, tr, sc);
-    std::vector<float> out(H);
+    std::vector<float> out((size_t)ntok * H);
     for (int it = 0; it < warmup + iters; ++it)
     {
-        std::vector<std::vector<std::pair<int, float>>> route(1);
-        for (int q = 0; q < topk; ++q) route[0].push_back({ (it * topk + q) % E, 1.0f / topk });
+        std::vector<std::vector<std::pair<int, float>>> route(ntok);
+        for (int t = 0; t < ntok; ++t)
+            for (int q = 0; q < topk; ++q)
+                route[t].push_back({ (int)(((long)it * ntok * topk + t * topk + q) % E), 1.0f / topk });
         const double t0 = now();
-        moe_forward(*g_pool, L, x, 1, route, out.data(), mode);
+        moe_forward(*g_pool, L, x, ntok, route, out.data(), mode);
         const double dt = now() - t0;
         if (it >= warmup) secs[it - warmup] = dt;
     }

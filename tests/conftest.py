@@ -31,6 +31,15 @@ def ref():
 
 
 @pytest.fixture(scope="session")
+def ref_server():
+    """The reference engine built with its server's flags (default fp contraction), oracle/_ref/libftref_server.so."""
+    from oracle import REFLIB_SERVER, RefEngine
+    if not os.path.exists(REFLIB_SERVER):
+        pytest.skip("reference engine oracle/_ref/libftref_server.so not built")
+    return RefEngine(threads=2, cpus=sorted(os.sched_getaffinity(0))[:2], path=REFLIB_SERVER)
+
+
+@pytest.fixture(scope="session")
 def gpu():
     import torch
     if not torch.cuda.is_available():

@@ -76,6 +76,21 @@ def test_tier_forward_auto_prefill_takes_grouped_path(tier, oracle):
     assert float(np.sqrt(np.mean(d ** 2))) <= 1e-3 * rms and float(np.abs(d).max()) <= 1e-2 * rms
 
 
+def test_tier_forward_exact_prefill_bitexact(tier, oracle):
+    """m * k > 1024 in EXACT mode (1): bit-identical to the oracle's EXACT layer, as the reference's EXACT mode is at
+    any batch size."""
+    import ft_tier
+    rng = np.random.default_rng(71)
+    m = 300
+    x = torch.from_numpy((rng.standard_normal((m, tier["H"])) * 0.5).astype(np.float16).astype(np.float32))
+    sel = torch.from_numpy(np.stack([rng.choice(tier["E"], 4, replace=False) for _ in range(m)]).astype(np.int32))
+    sel[9, 0] = -1
+    w = torch.from_numpy(rng.random((m, 4)).astype(np.float32))
+    got = ft_tier.tier_forward(1, x, sel, w, 1).numpy()
+    want = oracle.moe_forward(_experts(oracle, tier["layers"][1]), x.numpy(), sel.numpy(), w.numpy(), mode=1)
+    assert np.array_equal(got, want)
+
+
 def test_tier_selftest_mode_loop(tier, oracle):
     """The reference's start-up self-test calls tier_forward(li, x, sel, w, mode) for mode in (1, 0, 2)
     (glm53/cpu_tier.py:766-773): every mode returns the EXACT layer."""

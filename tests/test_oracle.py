@@ -140,6 +140,22 @@ def test_moe_forward_golden(oracle, nt, mode, key):
     assert np.array_equal(oracle.moe_forward(ex, x, sel, w, mode=mode), G[f"moe_{key}_{nt}"])
 
 
+def test_moe_forward_rows_is_the_full_call_restricted(oracle):
+    """The row-subset layer forward (jobs of the whole batch, some rows evaluated) returns exactly those rows of the
+    full call, golden-pinned through moe_forward: 16 tokens give every expert two jobs, so later rows' combine orders
+    depend on earlier tokens' picks. A layer built from the wanted rows' picks alone would get another job order;
+    the check shows the subset call does not fall back to that."""
+    ex = [oracle.synth_expert(7, e, 512, 256) for e in range(6)]
+    x, sel = G["moe_x_16"], G["moe_sel_16"]
+    rng = np.random.default_rng(31)
+    w = rng.random(sel.shape).astype(np.float32)
+    full = oracle.moe_forward(ex, x, sel, w, mode=1)
+    rows = [0, 5, 11, 15]
+    assert np.array_equal(oracle.moe_forward_rows(ex, x, sel, w, rows, mode=1), full[rows])
+    alone = oracle.moe_forward(ex, x[rows], sel[rows], w[rows], mode=1)
+    assert not np.array_equal(alone, full[rows])
+
+
 def test_config0_expert_golden(oracle):
     e0 = oracle.synth_expert(8, 0, 5120, 1536)
     x = G["c0_x"]
