@@ -82,8 +82,12 @@ int gfl_layer_info(gfl_ctx* ctx, int li, int* info);
  *   out[t] = sum over picks k of w[t,k] * expert_{sel[t,k]}(x[t]), picks with sel < 0 skipped,
  * summed in the reference's job order (moe_forward, kernels/cpu_avx2/ft_core.h:1338-1407).
  * x: fp16 [M, H]; sel: int64 [M, topk]; w: [M, topk] fp16 (w_is_half=1) or fp32; out: fp32 [M, H].
- * act_limit: SwiGLU clamp (tier_set_act_limit, ft_tier_ext.cpp:629-636), 0 = off. M*topk <= 1024, topk <= 16;
- * x 16-byte aligned. */
+ * act_limit: SwiGLU clamp (tier_set_act_limit, ft_tier_ext.cpp:629-636), 0 = off. topk <= 16; x 16-byte aligned.
+ * M*topk <= 1024: the decode launches (routing plan built in every workgroup). 1024 < M*topk <= 65536 (EXACT modes
+ * only; MFMA is refused there): the grouped plan of the prefill path drives the same EXACT kernels, a workgroup per
+ * expert taking its slots in passes of 4, bit-identical to the reference's EXACT mode at any batch size. That path
+ * uses the prefill workspace (gfl_grouped_reserve sizes it ahead of graph capture; otherwise the first call of a
+ * larger size grows it). */
 int gfl_moe_forward(gfl_ctx* ctx, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half, int M,
                     int topk, float* out, int mode, float act_limit, gfl_stream stream);
 
@@ -120,9 +124,10 @@ int gfl_moe_forward_noalloc(gfl_ctx* ctx, int li, const uint16_t* x, const int64
 int gfl_grouped_forward(gfl_ctx* ctx, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half,
                         int M, int topk, float* out, float act_limit, gfl_stream stream);
 
-/* Size the workspace of gfl_grouped_forward / gfl_grouped_plan for calls of up to max_picks picks on every layer
- * registered so far, so that later calls (and HIP graph captures of them) allocate nothing. Without it the first
- * call of a larger size grows the workspace (never during a capture). No counterpart in the reference. */
+/* Size the prefill workspace (gfl_grouped_forward, gfl_grouped_plan and gfl_moe_forward above 1024 picks) for calls
+ * of up to max_picks picks on every layer registered so far, so that later calls (and HIP graph captures of them)
+ * allocate nothing. Without it the first call of a larger size grows the workspace (never during a capture). No
+ * counterpart in the reference. */
 int gfl_grouped_reserve(gfl_ctx* ctx, int max_picks);
 
 /* The routing plan of gfl_grouped_forward alone, copied out of the context's workspace (all device pointers; no
