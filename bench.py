@@ -7,17 +7,24 @@ layer call (split -> 8*M expert GEMVs -> weighted combine) through the C ABI. St
 288-expert layers (2.56 GB each) and 32 routings, so expert bytes come from HBM, not the 256 MB Infinity Cache.
 Steps are captured in a HIP graph and replayed; the timed region is bracketed by synchronisation.
 
-value        = microseconds per token at M=1 (lower is better); per_M holds M=1..4. Both run the EXACT mode, whose
-               outputs are bit-identical to the reference's EXACT expert (--mode mfma times GFL_MODE_MFMA instead).
+value        = microseconds per token at M=1 (lower is better): the median over exactly --steps timed steps of the
+               per-step times (device events between replays of up to 8 captured graphs of up to --graph-steps steps,
+               replayed round-robin so a graph's layers come back only after GBs of others); p10/p90 and the mean
+               over the whole timed region beside it. per_M holds M=1..4. All run the EXACT mode, whose outputs are
+               bit-identical to the reference's EXACT expert (--mode mfma times GFL_MODE_MFMA instead).
 roofline     = the gate|up GEMV kernel (the dominant one) at M=1: algorithmic quantized bytes per launch (union of
                routed experts x (gate+up trellis + their suh/svh)) / its mean launch time, from device events
-               recorded around every launch during a timed eager pass; peak = 8 TB/s HBM.
-configs      = BASELINE configs 2 (mixed bitrates, Zipf routing), 3 (M=16/32/64) and 4 (42 resident layers decoded
-               at M=1; prefill of M=2048 tokens through the MFMA grouped path, as TFLOP/s against 2.5 PF dense fp16);
-               the router (gfl_route) per call; routed layer + shared expert, sequential vs overlapped on a side stream;
-               config 1 in mode MFMA (MFMA-accumulate GEMVs, outside the 2e-3 bar, so never the headline).
+               recorded around every launch during an eager pass on the launch stream; peak = 8 TB/s HBM; traffic =
+               HBM bytes per launch from the FETCH_SIZE/WRITE_SIZE counter file (--pmc-probe / --pmc-digest).
+configs      = BASELINE configs 0 (one expert per call), 2 (mixed bitrates, Zipf routing), 3 (M=16/32/64) and 4 (42
+               resident layers decoded at M=1; prefill of M=2048 tokens through the MFMA grouped path, as TFLOP/s
+               against 2.5 PF dense fp16, and through the EXACT path); the router (gfl_route) per call; routed layer +
+               shared expert, sequential vs overlapped on a side stream; config 1 in mode MFMA (MFMA-accumulate GEMVs,
+               outside the 2e-3 bar, so never the headline).
 cpu_baseline = the reference's own AVX2 expert engine (kernels/cpu_avx2/ft_core.h, built into oracle/_ref) timed on
-               this host: decode calls of 1 token x 8 experts cycling a DRAM-cold pool of 288 experts, I16 mode.
+               this host: decode calls of M tokens x 8 experts cycling a DRAM-cold pool of 288 experts; value = I16
+               at M=1; EXACT at M=1..4, AFFINE at M=2..4 and the single expert of config 0 beside it, with the CPU
+               model.
 """
 import argparse
 import json
@@ -33,6 +40,7 @@ HBM_PEAK_GBPS = 8000.0
 MODE = 1   # decode mode of every gfl_moe_forward call (1 EXACT, 3 MFMA-accumulate GEMVs); set by --mode
 MFMA_PEAK_TFLOPS = 2500.0   # dense fp16 MFMA
 H, I, E, TOPK, KBITS = 5120, 1536, 288, 8, 3
+XSTEPS = 128   # steps per line of the configs beside the headline
 
 
 def physical_cpus(skip=2, cap=16):
@@ -53,8 +61,22 @@ def physical_cpus(skip=2, cap=16):
     return cpus[:cap]
 
 
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(iters, warmup):
-    """Reference AVX2 engine timing; returns the cpu_baseline object or None when the engine is not built."""
+    """Reference AVX2 engine timing; returns the cpu_baseline object or None when the engine is not built.
+    Decode calls of M tokens x 8 experts (1 expert for config 0) cycling a DRAM-cold pool of 288 experts, as
+    tools/bench/kernel-ab-harness.cpp HARNESS_TIME does: I16 (the production decode mode) and EXACT at M=1, EXACT and
+    AFFINE at M=2..4 (the reference's I16 scale arrays are sized for H=4096 and overrun at H=5120 once an expert
+    carries two tokens), and the single-expert config 0 in I16 and EXACT. Median and p10/p90 per call."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     from oracle import REFLIB, Mat, Oracle, RefEngine
@@ -74,31 +96,42 @@ def cpu_baseline(iters, warmup):
             mats.append(Mat(tr, suh, svh, k, n, KBITS))
         pool.append(tuple(mats))
     gen_s = time.time() - t0
-    rng = np.random.default_rng(4242)
-    x = rng.standard_normal(H).astype(np.float16).astype(np.float32)
-    res = {}
-    for name, mode in (("i16", 2), ("exact", 1)):
-        secs = eng.time_decode(pool, x, TOPK, iters, warmup, mode)
-        res[name] = float(np.median(secs)) * 1e6
     per_expert = sum(m.tr.size + 2 * (m.k + m.n) for m in pool[0])
-    return {"value": round(res["i16"], 2), "unit": "us/token", "cores": len(cpus), "kind": "reference",
-            "sample": f"{iters} decode calls (after {warmup} warm-up) of 1 token x {TOPK} experts, I16 mode, "
-                      f"cycling a DRAM-cold pool of {E} experts (H={H} I={I} K={KBITS}, {E * per_expert / 1e9:.2f} GB); "
-                      f"median",
-            "exact_mode_us_per_token": round(res["exact"], 2),
-            "GBps_i16": round(TOPK * per_expert / (res["i16"] * 1e-6) / 1e9, 2),
-            "cpus": cpus, "pool_gen_s": round(gen_s, 1)}
+    rng = np.random.default_rng(4242)
+    xs = rng.standard_normal((4, H)).astype(np.float16).astype(np.float32)
+
+    def run(M, topk, mode, n):
+        secs = np.asarray(eng.time_decode(pool, xs[:M], topk, n, warmup, mode)) * 1e6 / M
+        return {"median": round(float(np.median(secs)), 2), "p10": round(float(np.percentile(secs, 10)), 2),
+                "p90": round(float(np.percentile(secs, 90)), 2), "calls": n,
+                "GBps": round(M * topk * per_expert / (float(np.median(secs)) * M * 1e-6) / 1e9, 2)}
+
+    t1 = time.time()
+    res = {"M1_i16": run(1, TOPK, 2, iters), "M1_exact": run(1, TOPK, 1, iters)}
+    for M in (2, 3, 4):
+        res[f"M{M}_exact"] = run(M, TOPK, 1, max(20, iters // 3))
+        res[f"M{M}_affine"] = run(M, TOPK, 0, max(20, iters // 3))
+    res["config0_i16"] = run(1, 1, 2, iters)
+    res["config0_exact"] = run(1, 1, 1, iters)
+    return {"value": res["M1_i16"]["median"], "unit": "us/token", "cores": len(cpus), "kind": "reference",
+            "cpu_model": cpu_model(),
+            "sample": f"decode calls (after {warmup} warm-up each) of M tokens x {TOPK} experts (config 0: 1 x 1), "
+                      f"expert sets cycling a DRAM-cold pool of {E} experts (H={H} I={I} K={KBITS}, "
+                      f"{E * per_expert / 1e9:.2f} GB); value = I16 at M=1, median of {iters} calls; "
+                      f"per-mode medians and p10/p90 in us/token below",
+            "modes_us_per_token": res, "cpus": cpus, "pool_gen_s": round(gen_s, 1),
+            "timed_s": round(time.time() - t1, 1)}
 
 
 COPY_BYTES = 1 << 30
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gate_up_config1_M1.json")
-GATE_UP_KERNEL = "gu_kernel<3, 1>"
+GATE_UP_KERNEL = "gu_kernel<3, 1, false, false>"
 
 
-def pmc_probe(ctx, layers, steps=64):
+def pmc_probe(ctx, layers, steps=64, M=1):
     """Dispatches whose HBM counters calibrate and measure the gate|up kernel: four launches of an elementwise
     negation over COPY_BYTES of fp32 (reads COPY_BYTES, writes COPY_BYTES; 4x the 256 MB Infinity Cache), then
-    `steps` eager M=1 layer calls cycling the layers and 32 routings, as the timed benchmark does."""
+    `steps` eager M-token layer calls cycling the layers and 32 routings, as the timed benchmark does."""
     import numpy as np
     import torch
     import synth
@@ -111,16 +144,40 @@ def pmc_probe(ctx, layers, steps=64):
     rng = np.random.default_rng(1001)
     xs, sels, ws = [], [], []
     for r in range(32):
-        x = rng.standard_normal((1, H)).astype(np.float16)
-        (sel, w16), _ = synth.route_uniform(1, E, TOPK, rng)
+        x = rng.standard_normal((M, H)).astype(np.float16)
+        (sel, w16), _ = synth.route_uniform(M, E, TOPK, rng)
         xs.append(torch.from_numpy(x.view(np.int16)).view(torch.float16).cuda())
         sels.append(torch.from_numpy(sel).cuda())
         ws.append(torch.from_numpy(w16.view(np.int16)).view(torch.float16).cuda())
-    out = torch.empty((1, H), dtype=torch.float32, device="cuda")
+    out = torch.empty((M, H), dtype=torch.float32, device="cuda")
     for i in range(steps):
         ctx.moe_forward(i % len(layers), xs[i % 32], sels[i % 32], ws[i % 32], out, mode=MODE)
     torch.cuda.synchronize()
-    print(f"pmc probe: {4} copies of {COPY_BYTES} B, {steps} M=1 layer calls", flush=True)
+    print(f"pmc probe: {4} copies of {COPY_BYTES} B, {steps} M={M} layer calls", flush=True)
+
+
+def pmc_table(folders):
+    """Markdown table of per-kernel means of every counter in rocprofv3 --pmc outputs (counter_collection.csv) and
+    of the kernel-trace statistics (kernel_stats.csv) under the given folders: the decode kernels and the copy."""
+    import csv
+    import glob
+    from collections import defaultdict
+    acc, stats = defaultdict(list), {}
+    for folder in folders:
+        for f in glob.glob(os.path.join(folder, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                acc[(r["Kernel_Name"].split("(")[0][:48], r["Counter_Name"])].append(float(r["Counter_Value"]))
+        for f in glob.glob(os.path.join(folder, "**", "*kernel_stats.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                stats[r["Name"].split("(")[0][:48]] = (int(r["Calls"]), float(r["AverageNs"]) / 1e3)
+    print("| kernel | counter | mean per dispatch | dispatches |")
+    print("|---|---|---|---|")
+    for (k, c), v in sorted(acc.items()):
+        if "gfl::" in k or "neg" in k:
+            print(f"| `{k}` | {c} | {sum(v) / len(v):,.1f} | {len(v)} |")
+    for k, (n, us) in sorted(stats.items()):
+        if "gfl::" in k:
+            print(f"| `{k}` | mean duration (us) | {us:.2f} | {n} |")
 
 
 def _pmc_rows(folder, counter):
@@ -177,10 +234,42 @@ def make_routes(M, rng, n, kind):
     return out
 
 
-def time_layer_steps(ctx, layer_ids, routes, M, G, reps, warmup, bytes_per_expert, per_step=1):
-    """Graph-timed decode steps. A step is `per_step` consecutive layer calls (layer i of the step = layer_ids[(s *
-    per_step + i) % len]) with routing (s * per_step + i) % len(routes); G steps are captured in one HIP graph and
-    replayed `reps` times between synchronisations. Returns per-token time and bandwidth on the union's bytes."""
+def graph_size(steps, gmax):
+    """Steps per captured graph: the largest divisor of `steps` that is <= gmax, so exactly `steps` steps are timed."""
+    for g in range(max(1, min(gmax, steps)), 0, -1):
+        if steps % g == 0:
+            return g
+    return 1
+
+
+def replay_samples(graphs, reps):
+    """Replays graphs[r % len(graphs)] for r < reps back to back on the current stream, with a device event between
+    consecutive replays. Returns (per-replay ms list, ms from the first event to the last)."""
+    import torch
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    torch.cuda.synchronize()
+    ev[0].record()
+    for r in range(reps):
+        graphs[r % len(graphs)].replay()
+        ev[r + 1].record()
+    torch.cuda.synchronize()
+    return [ev[r].elapsed_time(ev[r + 1]) for r in range(reps)], ev[0].elapsed_time(ev[reps])
+
+
+def _dist(ms_per_step, M):
+    import numpy as np
+    a = np.asarray(ms_per_step) * 1e3 / M
+    return {"median": round(float(np.median(a)), 3), "p10": round(float(np.percentile(a, 10)), 3),
+            "p90": round(float(np.percentile(a, 90)), 3)}
+
+
+def time_layer_steps(ctx, layer_ids, routes, M, steps, G, warmup, bytes_per_expert, per_step=1, ngraphs=8):
+    """Graph-timed decode steps. A step is `per_step` consecutive layer calls (call c = s * per_step + i of step s runs
+    layer layer_ids[c % len] with routing c % len(routes)). Up to `ngraphs` graphs of G consecutive steps each are
+    captured (graph j holds steps jG .. jG+G-1) and replayed round-robin, steps / G replays in all, so exactly
+    `steps` steps are timed and a graph comes back only after the others' layers have streamed through (far more bytes
+    than the 256 MB Infinity Cache). Per-step times come from device events between replays: the headline is their
+    median; p10/p90 and the mean over the whole timed region are reported beside it."""
     import numpy as np
     import torch
     out = torch.empty((M, H), dtype=torch.float32, device="cuda")
@@ -201,39 +290,49 @@ def time_layer_steps(ctx, layer_ids, routes, M, G, reps, warmup, bytes_per_exper
         for i in range(2):
             step(i)
     torch.cuda.current_stream().wait_stream(st)
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        for i in range(G):
-            step(i)
-    g.replay()
+    reps = steps // G
+    ng = max(1, min(ngraphs, reps))
+    graphs = []
+    for j in range(ng):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(G):
+                step(j * G + i)
+        graphs.append(g)
+    for g in graphs:
+        g.replay()
+    torch.cuda.synchronize()
+    samples, total_ms = replay_samples(graphs, reps)
+    # the last graph's final step, replayed and then run eagerly: same output
+    graphs[-1].replay()
     torch.cuda.synchronize()
     got = out.clone()
-    step(G - 1)
+    step(ng * G - 1)
     torch.cuda.synchronize()
     graph_ok = bool(torch.equal(got, out))
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record()
-    for _ in range(reps):
-        g.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / (reps * G)
-    calls = [(s_ * per_step + i) for s_ in range(G) for i in range(per_step)]
-    step_bytes = sum(routes[c % NR][3] * bytes_per_expert(layer_ids[c % NL]) for c in calls) / G + per_step * M * H * 6
+    del graphs
+    per_step_ms = [t / G for t in samples]
+    ms = float(np.median(per_step_ms))
+    calls = [(s_ * per_step + i) for s_ in range(ng * G) for i in range(per_step)]
+    step_bytes = (sum(routes[c % NR][3] * bytes_per_expert(layer_ids[c % NL]) for c in calls) / (ng * G)
+                  + per_step * M * H * 6)
     gbps = step_bytes / (ms * 1e-3) / 1e9
-    del g
     return {"us_per_token": round(ms * 1e3 / M, 3), "ms_per_step": round(ms, 5),
+            "us_per_token_dist": _dist(per_step_ms, M), "us_per_token_mean": round(total_ms / steps * 1e3 / M, 3),
+            "steps": steps, "graph_steps": G, "graphs": ng,
             "union_experts": round(float(np.mean([r[3] for r in routes])), 2), "GBps": round(gbps, 1),
             "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "graph_replay_matches_eager": graph_ok}
 
 
-def extra_configs(ctx, layers, args, G, reps):
-    """BASELINE configs 2, 3 and the 42-layer resident stack of config 4, timed like config 1."""
+def extra_configs(ctx, layers, args):
+    """BASELINE configs 0, 2, 3 and 4 (42-layer resident stack, prefill through both paths), timed like config 1:
+    XSTEPS steps per line (fewer for the long ones), graphs of 4 steps."""
     import numpy as np
     import synth
     res = {}
     t0 = time.time()
+    res["config0_single_expert"] = time_config0(ctx, list(range(args.layers)), layers[0].quant_bytes_per_expert)
+    print(f"bench: config 0 done ({time.time() - t0:.0f} s)", file=sys.stderr, flush=True)
     # config 2: mixed bitrates, Zipf-skewed routing; two layers of each kind cycled (3.1 GB per layer)
     base = 100
     mixed = {"A_gate_up4_down3": (4, 4, 3), "B_gate_up3_down5": (3, 3, 5)}
@@ -249,7 +348,7 @@ def extra_configs(ctx, layers, args, G, reps):
         per = {}
         for M in (1, 2, 3, 4):
             routes = make_routes(M, np.random.default_rng(2000 + 10 * j + M), 32, "zipf")
-            per[str(M)] = time_layer_steps(ctx, ids, routes, M, G, reps, 8, lambda li, b=bpe: b)
+            per[str(M)] = time_layer_steps(ctx, ids, routes, M, XSTEPS, 4, 8, lambda li, b=bpe: b)
         res["config2_" + name] = per
         print(f"bench: config 2 {name} done ({time.time() - t0:.0f} s)", file=sys.stderr, flush=True)
     # config 1 in mode MFMA (MFMA-accumulate GEMVs: outside the 2e-3 bar that the EXACT headline meets bit-for-bit;
@@ -260,7 +359,7 @@ def extra_configs(ctx, layers, args, G, reps):
     per = {}
     for M in (1, 2, 3, 4):
         routes = make_routes(M, np.random.default_rng(1000 + M), 32, "uniform")
-        per[str(M)] = time_layer_steps(ctx, list(range(args.layers)), routes, M, G, reps, 8,
+        per[str(M)] = time_layer_steps(ctx, list(range(args.layers)), routes, M, XSTEPS, 4, 8,
                                        lambda li: layers[0].quant_bytes_per_expert)
     MODE = saved
     res["config1_mode_mfma"] = per
@@ -269,7 +368,7 @@ def extra_configs(ctx, layers, args, G, reps):
     per = {}
     for M in (16, 32, 64):
         routes = make_routes(M, np.random.default_rng(3000 + M), 16, "uniform")
-        per[str(M)] = time_layer_steps(ctx, list(range(args.layers)), routes, M, 16, max(1, reps // 2), 4,
+        per[str(M)] = time_layer_steps(ctx, list(range(args.layers)), routes, M, XSTEPS // 2, 4, 4,
                                        lambda li: layers[0].quant_bytes_per_expert)
     res["config3_batched"] = per
     print(f"bench: config 3 done ({time.time() - t0:.0f} s)", file=sys.stderr, flush=True)
@@ -284,20 +383,39 @@ def extra_configs(ctx, layers, args, G, reps):
         ids.append(li)
     print(f"bench: {nst}-layer stack resident ({time.time() - t0:.0f} s)", file=sys.stderr, flush=True)
     routes = make_routes(1, np.random.default_rng(4000), nst, "uniform")
-    r = time_layer_steps(ctx, ids, routes, 1, 2, max(2, reps // 4), 1, lambda li: layers[0].quant_bytes_per_expert,
-                         per_step=nst)
+    r = time_layer_steps(ctx, ids, routes, 1, 16, 2, 1, lambda li: layers[0].quant_bytes_per_expert, per_step=nst,
+                         ngraphs=4)
     r["layers"] = nst
     r["resident_GB"] = round(nst * E * layers[0].quant_bytes_per_expert / 1e9, 1)
     res["config4_stack_decode"] = r
     print(f"bench: config 4 stack done ({time.time() - t0:.0f} s)", file=sys.stderr, flush=True)
-    res["config4_prefill"] = time_prefill(ctx, list(range(args.layers)), layers[0].quant_bytes_per_expert, 2048,
-                                          max(4, reps // 2))
+    res["config4_prefill"] = time_prefill(ctx, list(range(args.layers)), layers[0].quant_bytes_per_expert, 2048, 8)
+    print(f"bench: config 4 prefill (MFMA grouped) done ({time.time() - t0:.0f} s)", file=sys.stderr, flush=True)
+    res["config4_prefill_exact"] = time_prefill(ctx, list(range(args.layers)), layers[0].quant_bytes_per_expert,
+                                                2048, 2, G=2, exact=True)
     print(f"bench: config 4 prefill done ({time.time() - t0:.0f} s)", file=sys.stderr, flush=True)
     res["router"] = {f"M{M}": time_router(M) for M in (1, 4, 64, 2048)}
-    res["shared_overlap"] = time_shared(ctx, list(range(args.layers)), G, reps)
+    res["shared_overlap"] = time_shared(ctx, list(range(args.layers)), 32, 4)
     print(f"bench: shared-expert overlap done ({time.time() - t0:.0f} s)", file=sys.stderr, flush=True)
     res["setup_and_time_s"] = round(time.time() - t0, 1)
     return res
+
+
+def time_config0(ctx, layer_ids, bytes_per_expert, steps=XSTEPS):
+    """Config 0: one expert (H=5120, I=1536, K=3) on one token per call: top-1 routing with weight 1.0, the expert id
+    cycling over the 288 of each config-1 layer (and the layers cycled), so every call streams a cold expert."""
+    import numpy as np
+    import torch
+    rng = np.random.default_rng(8000)
+    routes = []
+    for r in range(32):
+        x = rng.standard_normal((1, H)).astype(np.float16)
+        sel = torch.tensor([[int(rng.integers(0, E))]], dtype=torch.int64, device="cuda")
+        w = torch.ones((1, 1), dtype=torch.float32, device="cuda")
+        routes.append((torch.from_numpy(x.view(np.int16)).view(torch.float16).cuda(), sel, w, 1))
+    r = time_layer_steps(ctx, layer_ids, routes, 1, steps, 4, 8, lambda li: bytes_per_expert)
+    r["expert_bytes"] = bytes_per_expert
+    return r
 
 
 def time_shared(ctx, layer_ids, G, reps):
@@ -381,10 +499,12 @@ def time_router(M, reps=8, G=32):
     return {"us_per_call": round(e0.elapsed_time(e1) * 1e3 / (reps * G), 2), "tokens": M, "experts": E, "topk": TOPK}
 
 
-def time_prefill(ctx, layer_ids, bytes_per_expert, M, reps, G=4):
-    """Config 4 prefill: M tokens, uniform top-8 routing, through gfl_grouped_forward (MFMA grouped GEMMs). G layer
-    calls (layers cycled) are captured in one HIP graph and replayed `reps` times. Algorithmic work per call:
-    2 * picks * 3 * H * I flops (gate, up, down GEMMs) and the union's quantized expert bytes."""
+def time_prefill(ctx, layer_ids, bytes_per_expert, M, reps, G=4, exact=False):
+    """Config 4 prefill: M tokens, uniform top-8 routing, through gfl_grouped_forward (MFMA grouped GEMMs), or with
+    exact=True through gfl_moe_forward in EXACT mode (the decode kernels driven by the grouped plan, bit-identical to
+    the reference's EXACT mode). G layer calls (layers cycled) are captured in one HIP graph and replayed `reps` times.
+    Algorithmic work per call: 2 * picks * 3 * H * I flops (gate, up, down GEMMs) and the union's quantized expert
+    bytes."""
     import numpy as np
     import torch
     routes = make_routes(M, np.random.default_rng(5000 + M), 2, "uniform")
@@ -393,7 +513,10 @@ def time_prefill(ctx, layer_ids, bytes_per_expert, M, reps, G=4):
 
     def call(i):
         x, sel, w, _ = routes[i % 2]
-        ctx.grouped_forward(layer_ids[i % NL], x, sel, w, out)
+        if exact:
+            ctx.moe_forward(layer_ids[i % NL], x, sel, w, out, mode=1)
+        else:
+            ctx.grouped_forward(layer_ids[i % NL], x, sel, w, out)
 
     for i in range(3):
         call(i)
@@ -413,20 +536,17 @@ def time_prefill(ctx, layer_ids, bytes_per_expert, M, reps, G=4):
     call(G - 1)
     torch.cuda.synchronize()
     graph_ok = bool(torch.equal(got, out))
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        g.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / (reps * G)
+    samples, total = replay_samples([g], reps)
+    ms = total / (reps * G)
     del g
     picks = M * TOPK
     flops = 2.0 * picks * 3 * H * I
     tflops = flops / (ms * 1e-3) / 1e12
     union = float(np.mean([r[3] for r in routes]))
     gbps = (union * bytes_per_expert + M * H * 6) / (ms * 1e-3) / 1e9
-    return {"tokens": M, "ms_per_layer": round(ms, 4), "us_per_token": round(ms * 1e3 / M, 4),
+    return {"path": "EXACT (gfl_moe_forward)" if exact else "MFMA grouped (gfl_grouped_forward)",
+            "tokens": M, "ms_per_layer": round(ms, 4), "us_per_token": round(ms * 1e3 / M, 4),
+            "ms_per_layer_replays": [round(t / G, 4) for t in samples],
             "TFLOPs": round(tflops, 1), "mfma_peak_TFLOPs": MFMA_PEAK_TFLOPS,
             "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "GBps": round(gbps, 1), "union_experts": union,
             "graph_replay_matches_eager": graph_ok}
@@ -440,7 +560,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--layers", type=int, default=4)
     ap.add_argument("--Ms", default="1,2,3,4")
-    ap.add_argument("--graph-steps", type=int, default=32)
+    ap.add_argument("--graph-steps", type=int, default=4,
+                    help="most steps per captured graph (the largest divisor of --steps up to this is used)")
     ap.add_argument("--profile-steps", type=int, default=64)
     ap.add_argument("--cpu-iters", type=int, default=300)
     ap.add_argument("--no-cpu", action="store_true")
@@ -451,11 +572,17 @@ def main():
                     help="only the config-4 prefill measurement (M=2048 through the grouped path), one JSON line")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="counter run: the calibration copy, then eager M=1 steps (run under rocprofv3 --pmc)")
+    ap.add_argument("--probe-M", type=int, default=1, help="tokens per layer call of --pmc-probe")
+    ap.add_argument("--pmc-table", nargs="+", metavar="DIR",
+                    help="print per-kernel counter means and kernel-trace durations of rocprofv3 output folders")
     ap.add_argument("--pmc-digest", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn two rocprofv3 --pmc output folders (FETCH_SIZE, WRITE_SIZE) into the traffic file")
     args = ap.parse_args()
     if args.pmc_digest:
         pmc_digest(*args.pmc_digest)
+        return
+    if args.pmc_table:
+        pmc_table(args.pmc_table)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the routed-expert path on one GPU; multi-GPU runs are not part of this build "
@@ -479,7 +606,7 @@ def main():
         layers.append(L)
     setup_s = time.time() - t0
     if args.pmc_probe:
-        pmc_probe(ctx, layers)
+        pmc_probe(ctx, layers, M=args.probe_M)
         return
     if args.prefill_only:
         r = time_prefill(ctx, list(range(args.layers)), layers[0].quant_bytes_per_expert, 2048,
@@ -488,15 +615,14 @@ def main():
         return
     per_expert = layers[0].quant_bytes_per_expert
     gu_per_expert = layers[0].tbytes[0] + layers[0].tbytes[1] + 2 * 2 * (H + I)
-    G = args.graph_steps
-    reps = max(1, args.steps // G)
-    steps = reps * G
+    steps = max(1, args.steps)
+    G = graph_size(steps, args.graph_steps)
     per_M = {}
     roof = None
     for M in [int(m) for m in args.Ms.split(",")]:
         rng = np.random.default_rng(1000 + M)
         routes = make_routes(M, rng, 32, "uniform")
-        r = time_layer_steps(ctx, list(range(args.layers)), routes, M, G, reps, args.warmup,
+        r = time_layer_steps(ctx, list(range(args.layers)), routes, M, steps, G, args.warmup,
                              lambda li: layers[li].quant_bytes_per_expert)
         per_M[str(M)] = r
         if M == 1:
@@ -515,12 +641,12 @@ def main():
             ach = gu_bytes / (gu_ms / gu_n * 1e-3) / 1e9
             stage_us = {k: round(v[0] / max(1, v[1]) * 1e3, 2) for k, v in prof.items()}
             roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                    "frac": round(ach / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": "gu_kernel<3, 1> (gate|up GEMV + SwiGLU)",
+                    "frac": round(ach / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": GATE_UP_KERNEL + " (gate|up GEMV + SwiGLU)",
                     "algorithmic_bytes_per_launch": round(gu_bytes), "mean_launch_us": round(gu_ms / gu_n * 1e3, 2),
                     "stage_mean_us": stage_us}
     configs = {}
     if not args.no_extra:
-        configs = extra_configs(ctx, layers, args, G, reps)
+        configs = extra_configs(ctx, layers, args)
     if roof is not None and os.path.exists(TRAFFIC_FILE):
         try:
             roof["traffic"] = json.load(open(TRAFFIC_FILE)).get("hbm_bytes_per_launch")
