@@ -35,11 +35,12 @@ def context_summary(ctx):
 def tier_summary():
     """The tier shim's tier_stats words, named (ft_tier_ext.cpp:906-914)."""
     import ft_tier
-    if ft_tier.T is None:
+    init, running, act_limit, nlayers = ft_tier.tier_state()
+    if not init:
         return None
     h = ft_tier.tier_stats()
-    return {"jobs": h[0], "experts": h[1], "tokens": h[2], "empty_jobs": h[3], "running": ft_tier.T.running,
-            "act_limit": ft_tier.T.act_limit, "layers": sum(1 for L in ft_tier.T.layers if L is not None)}
+    return {"jobs": h[0], "experts": h[1], "tokens": h[2], "empty_jobs": h[3], "running": running,
+            "act_limit": act_limit, "layers": nlayers}
 
 
 def summary(split_stats=None, contexts=(), overlap=None, extra=None, pools=None):

@@ -22,7 +22,10 @@ def tier(gpu):
     pool = expert_cache.Pool(torch.device("cuda", 0), mods)
     ft_tier.tier_shutdown()
     ctrl = torch.zeros(16, dtype=torch.int64, device="cuda")
-    ft_tier.tier_init(1, [0], ctrl, None, None, None, -1, H, I, len(mods), 0)
+    hx = torch.zeros(4 * H, dtype=torch.float16, device="cuda")
+    picks = torch.zeros(4 * 8 * 3, dtype=torch.int32, device="cuda")
+    hout = torch.zeros(4 * H, dtype=torch.float32, device="cuda")
+    ft_tier.tier_init(1, [0], ctrl, hx, picks, hout, -1, H, I, len(mods), 0)
     ft_tier.add_pool_layers(pool, bits=[L.Ks for L in layers])
     yield dict(pool=pool, layers=layers, mods=mods, H=H, I=I, E=E)
     ft_tier.tier_set_act_limit(0.0)
@@ -134,7 +137,8 @@ def test_tier_forward_argument_errors(tier):
     with pytest.raises(RuntimeError, match="out of range"):
         ft_tier.tier_forward(0, x.half().float(), sel + 99, torch.ones(1, 4), 1)
     with pytest.raises(RuntimeError, match="already initialised"):
-        ft_tier.tier_init(1, [0], None, None, None, None, -1, tier["H"], tier["I"], 1, 0)
+        e = torch.empty(0)
+        ft_tier.tier_init(1, [0], e, e, e, e, -1, tier["H"], tier["I"], 1, 0)
 
 
 def test_pool_on_device_verifies_clean(tier):
@@ -181,10 +185,44 @@ def test_serve_stats_after_forward(tier):
     x = torch.zeros((1, tier["H"]), dtype=torch.float32)
     sel = torch.tensor([[0, 1, 2, 3]], dtype=torch.int32)
     ft_tier.tier_forward(0, x, sel, torch.full((1, 4), 0.25), 1)
-    c = TestClient(serve_stats.mount(FastAPI(), contexts=[ft_tier.T.ctx], pools=[tier["pool"]]))
+    c = TestClient(serve_stats.mount(FastAPI(), pools=[tier["pool"]]))
     r = c.get("/stats").json()
     assert r["tier"]["jobs"] >= 1 and r["tier"]["layers"] == 2
-    assert r["contexts"][0]["forward_calls"] >= 1 and r["contexts"][0]["layers"] >= 2
     assert r["expert_cache"] and r["expert_cache"][0]["residency"] == "full"
     v = c.get("/ec_verify").json()["verify"]
     assert all(p["bad_slots"] == 0 and p["bad_tables"] == 0 for p in v)
+
+
+def test_handshake_layer_through_the_extension(tier, oracle):
+    """cpu_tier's decode sequence through the extension's own entry points (ft_split, tier_forward, ft_combine) with
+    the handshake policy (pol[7] = 1, GLM53_CT_HANDSHAKE): every layer publishes an empty job, which the split answers
+    itself, so ft_combine returns without waiting out its timeout (stats[6] == 0) and leaves the layer output (the
+    EXACT layer, bit for bit) as it was."""
+    import ft_tier
+    H, E = tier["H"], tier["E"]
+    rng = np.random.default_rng(88)
+    x = torch.from_numpy((rng.standard_normal((1, H)) * 0.5).astype(np.float16)).cuda()
+    sel = torch.from_numpy(rng.choice(E, 4, replace=False).astype(np.int64)).cuda()
+    w = torch.from_numpy(rng.random(4).astype(np.float16)).cuda()
+    ctrl = torch.zeros(16, dtype=torch.int64, device="cuda")
+    hx = torch.zeros(H, dtype=torch.float16, device="cuda")
+    hp = torch.zeros(4 * 3, dtype=torch.int32, device="cuda")
+    hout = torch.full((H,), 7.0, dtype=torch.float32, device="cuda")
+    so, wo = torch.empty(4, dtype=torch.int64, device="cuda"), torch.empty(4, dtype=torch.float16, device="cuda")
+    dflag, stats = torch.zeros(1, dtype=torch.int64, device="cuda"), torch.zeros(8, dtype=torch.int64, device="cuda")
+    pol = torch.tensor([0.4, 0.023, 0.11, 0.104, 0.2, 32, -1, 1] + [0.0] * 12, device="cuda")
+    pool = tier["pool"]
+    want = oracle.moe_forward(_experts(oracle, tier["layers"][0]), x.float().cpu().numpy(),
+                              sel.cpu().numpy().reshape(1, 4), w.float().cpu().numpy().reshape(1, 4), mode=1)
+    for seq in (1, 2, 3):
+        ft_tier.ft_split(sel, w, x, E, pool.first, pool.slotof[0], torch.zeros(E, device="cuda"), pol,
+                         ctrl.data_ptr(), hx.data_ptr(), hp.data_ptr(), seq, 0, 0, so, wo, dflag, stats,
+                         torch.empty(0, dtype=torch.int32, device="cuda"))
+        out = ft_tier.tier_forward(0, x.float(), so.view(1, 4), wo.float().view(1, 4), 1)
+        before = out.clone()
+        ft_tier.ft_combine(out, dflag, ctrl.data_ptr(), hout.data_ptr(), stats, 2_000_000_000)
+        torch.cuda.synchronize()
+        assert int(dflag.item()) == seq and int(ctrl[1].item()) == seq
+        assert torch.equal(out, before) and np.array_equal(out.cpu().numpy(), want)
+    st = stats.tolist()
+    assert st[6] == 0 and st[5] == 3 and st[7] == 3

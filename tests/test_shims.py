@@ -11,15 +11,21 @@ import fake_moe
 
 
 def test_tier_surface_names():
+    """The names come from the PyTorch-ROCm extension (a pybind11 module built from csrc/torch_ext.cpp), under the
+    reference's pybind names (ft_tier_ext.cpp:1288-1334, ft_tier_cu.cu:296-300)."""
     import ft_tier
+    import torch_ext
+    ext = torch_ext.load()
+    assert ext.__file__.endswith("gfl_torch_ext.so")
     for name in ("tier_init", "tier_add_layer", "tier_start", "tier_stop", "tier_forward", "tier_stats",
-                 "tier_set_act_limit", "ft_split", "ft_combine", "tier_lut_build_grouped_rows"):
-        assert callable(getattr(ft_tier, name))
+                 "tier_set_act_limit", "tier_set_e6", "tier_job_hist", "ft_split", "ft_combine",
+                 "tier_lut_build_grouped_rows"):
+        assert callable(getattr(ft_tier, name)) and getattr(ft_tier, name) is getattr(ext, name)
 
 
 def test_tier_calls_before_init_fail_like_the_reference():
     import ft_tier
-    assert ft_tier.T is None
+    assert ft_tier.tier_state()[0] is False
     with pytest.raises(RuntimeError, match="init first"):
         ft_tier.tier_add_layer(0, torch.zeros(1, 3, dtype=torch.int64), *[torch.zeros(1, 1).half()] * 6)
     with pytest.raises(RuntimeError, match="worker running"):
@@ -78,12 +84,14 @@ def test_k_ftsplit_install_swaps_the_handle():
     assert cpu_tier._CU.ft_combine is ft_tier.ft_combine
     n0 = k_ftsplit.STATS["fast"]
     with pytest.raises(RuntimeError, match="policy needs 20 entries"):
-        cpu_tier._CU.ft_split(torch.zeros(8, dtype=torch.int64), torch.zeros(8).half(), torch.zeros(1, 64).half(), 8, 0,
-                              None, None, torch.zeros(3), 0, 0, 0, 1, 0, 0, None, None, None, None,
-                              torch.empty(0, dtype=torch.int32))
+        z64 = torch.zeros(8, dtype=torch.int64)
+        cpu_tier._CU.ft_split(z64, torch.zeros(8).half(), torch.zeros(1, 64).half(), 8, 0,
+                              torch.zeros(8, dtype=torch.int32), torch.zeros(8), torch.zeros(3), 0, 0, 0, 1, 0, 0,
+                              z64, torch.zeros(8).half(), z64[:1], z64, torch.empty(0, dtype=torch.int32))
     assert k_ftsplit.STATS["fast"] == n0 + 1
     t = ft_tier.install(types.SimpleNamespace())
-    assert t._H is ft_tier and t._CU.ft_split is ft_tier.ft_split
+    import torch_ext
+    assert t._H is torch_ext.load() and t._CU.ft_split is ft_tier.ft_split
 
 
 def _cpu_mods(L=2, E=6, H=256, I=256, seed=0):
