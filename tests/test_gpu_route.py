@@ -58,3 +58,48 @@ def test_route_empty_and_errors(gpu):
     assert sel.shape == (0, 8)
     with pytest.raises(_native.NativeError, match="topk"):
         _native.route(torch.zeros((2, 4), dtype=torch.float32, device="cuda"), 8)
+
+
+@pytest.mark.parametrize("handshake", [False, True])
+def test_routing_hook_decode_layer(gpu, oracle, handshake):
+    """routing.RoutingHook: routing_fn(bsz, cfg, z, params) -> the split's selection from one fused router+split
+    launch, equal to the router's picks (every expert resident); the layer on that selection is the oracle's EXACT
+    layer on the router's closed-form picks; the combine hook leaves it unchanged (with the handshake policy the
+    split publishes an empty job and answers it itself, so the combine does not wait: stats[6] stays 0)."""
+    import torch
+    import _native
+    import routing
+    import synth
+    H, I, E, li, bsz = 512, 256, 16, 63, 2
+    L = synth.SynthLayer(li, E, H, I, (3, 3, 3))
+    L.register(gpu, li)
+    rng = np.random.default_rng(63 + handshake)
+    W = torch.from_numpy((rng.standard_normal((E, H)) * 0.05).astype(np.float32)).cuda()
+    z = torch.from_numpy(rng.standard_normal((bsz, H)).astype(np.float16)).cuda()
+    ing = routing.Ingress(H, max_bsz=4, topk=8)
+    pol = torch.tensor([0.4, 0.023, 0.11, 0.104, 0.2, 32, -1, float(handshake)] + [0.0] * 12, device="cuda")
+    hook = routing.RoutingHook(W, E, 8, li, torch.arange(E, dtype=torch.int32, device="cuda"), pol, ing)
+    sel, w = hook.routing_fn(bsz, None, z, {})
+    out = torch.empty((bsz, H), dtype=torch.float32, device="cuda")
+    gpu.moe_forward(li, z, sel, w, out)
+    torch.cuda.synchronize()
+    before = out.clone()
+    out = hook.combine(out)
+    torch.cuda.synchronize()
+    logits = (z.float() @ W.t()).cpu().numpy()
+    want_s, want_w = oracle.route(logits, 8)
+    assert np.array_equal(sel.cpu().numpy(), want_s)
+    assert np.array_equal(w.cpu().numpy().view(np.uint16), want_w)
+    from oracle import Mat
+    ex = []
+    for e in range(E):
+        ms = []
+        for p in range(3):
+            tr, suh, svh = L.matrix(e, p)
+            k, n = (H, I) if p < 2 else (I, H)
+            ms.append(Mat(tr, suh, svh, k, n, 3))
+        ex.append(tuple(ms))
+    want = oracle.moe_forward(ex, z.float().cpu().numpy(), want_s, want_w.view(np.float16).astype(np.float32), mode=1)
+    assert torch.equal(out, before) and np.array_equal(out.cpu().numpy(), want)
+    st = ing.stats.tolist()
+    assert int(ing.dflag.item()) == (ing.seq if handshake else 0) and st[6] == 0
