@@ -61,6 +61,9 @@ struct gfl_ctx
     float* silu_tab = nullptr;
     // slots per GEMV pass forced by GFL_SLOTS_PER_PASS (1, 2, 4 or 8; 0 = chosen from M)
     int ns_override = 0;
+    // relay widths of the one-slot-per-pass EXACT launches forced by GFL_RELAY="g,d" (gate|up, down; 1, 2 or 4), or
+    // "0" for the per-slot launches without relay; -1 = chosen from the call's size
+    int rw_override[2] = { -1, -1 };
     // workspace of the prefill path (gfl_grouped_forward / gfl_grouped_reserve), grown on demand outside captures
     void* gws = nullptr;
     size_t gws_bytes = 0;
@@ -236,24 +239,41 @@ int run_forward(gfl_ctx* c, const Layer& L, const Workspace& ws, const uint16_t*
     const int mf = mode == GFL_MODE_MFMA ? 1 : 0;
     int ns = mf ? std::min(M, 4) : M <= 8 ? 1 : 2;
     if (c->ns_override > 0) ns = std::min(c->ns_override, mf ? std::min(M, 16) : M);
-    if (gfl::gate_up_lds_bytes(L.K[0], ns, L.H, P, L.E, mf) > gfl::LDS_LIMIT ||
-        gfl::gate_up_lds_bytes(L.K[1], ns, L.H, P, L.E, mf) > gfl::LDS_LIMIT ||
-        gfl::down_lds_bytes(L.K[2], ns, L.I, mf) > gfl::LDS_LIMIT)
+    // Calls with few tile columns run the relay launches: a workgroup per (pick, tile columns), rw waves per column,
+    // each streaming and decoding every rw-th group of 8 tile rows while the column's accumulators pass from wave to
+    // wave in tile-row order (chain_relay). One wave per column leaves most SIMDs idle when a call has few columns;
+    // rw waves per column put rw times the waves on the chip. Measured on MI355X (config 1 layers, 4 cycled): one
+    // expert per call (192 gate|up columns) 39.2 -> 29.8 us with 4 waves per column; at 8 picks (1,536 columns)
+    // 2 waves per column match the per-slot launches; above that the relay's turns cost more than the waves gain.
+    int rw[2] = { 0, 0 };
+    if (!mf && ns == 1)
+    {
+        const int64_t cgu = (int64_t)P * 2 * (L.I / 16), cdn = (int64_t)P * (L.H / 16);   // tile columns
+        if (cgu <= 1536)
+        {
+            rw[0] = cgu <= 768 ? 4 : 2;
+            rw[1] = cdn <= 768 ? 4 : cdn <= 1536 ? 2 : 1;
+        }
+        if (c->rw_override[0] >= 0) { rw[0] = c->rw_override[0]; rw[1] = c->rw_override[1]; }
+    }
+    if (gfl::gate_up_lds_bytes(L.K[0], ns, L.H, P, L.E, mf, rw[0]) > gfl::LDS_LIMIT ||
+        gfl::gate_up_lds_bytes(L.K[1], ns, L.H, P, L.E, mf, rw[0]) > gfl::LDS_LIMIT ||
+        gfl::down_lds_bytes(L.K[2], ns, L.I, mf, rw[1]) > gfl::LDS_LIMIT)
         return fail(GFL_EINVAL, "gfl_moe_forward: shape needs more than 160 KB of LDS per workgroup");
     const int wh = w_is_half ? 1 : 0;
     auto gate_up = [&] {
         if (L.K[0] == L.K[1])
             return gfl::launch_gate_up(L.K[0], ns, L.dptrs, 0, 2, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                       ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, st);
+                                       ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], st);
         if (gfl::launch_gate_up(L.K[0], ns, L.dptrs, 0, 1, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, st))
+                                ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], st))
             return -1;
         return gfl::launch_gate_up(L.K[1], ns, L.dptrs, 1, 1, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                   ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, st);
+                                   ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], st);
     };
     auto down = [&] {
         return gfl::launch_down(L.K[2], ns, L.dptrs, topk, L.H, L.I, umax, P, ws.pv, ws.xtd, ws.yd, ws.out_cnt,
-                                ws.blk_cnt, out, mf, st);
+                                ws.blk_cnt, out, mf, rw[1], st);
     };
     int r = prof ? staged(c, 1, st, gate_up) : gate_up();
     if (!r) r = prof ? staged(c, 3, st, down) : down();
@@ -390,6 +410,15 @@ int gfl_ctx_create(int device, gfl_ctx** out)
         const int v = std::atoi(e);
         if (v == 1 || v == 2 || v == 4 || v == 8) c->ns_override = v;
     }
+    if (const char* e = std::getenv("GFL_RELAY"))
+    {
+        int g = -1, d = -1;
+        const int n = std::sscanf(e, "%d,%d", &g, &d);
+        auto ok = [](int v) { return v == 0 || v == 1 || v == 2 || v == 4; };
+        if (n == 1 && g == 0) c->rw_override[0] = c->rw_override[1] = 0;
+        else if (n == 2 && ok(g) && ok(d) && g > 0 && d > 0) { c->rw_override[0] = g; c->rw_override[1] = d; }
+    }
+
     *out = c;
     return GFL_OK;
 }
@@ -578,9 +607,9 @@ static int run_forward_grouped_plan(gfl_ctx* c, const Layer& L, const uint16_t* 
                                     int w_is_half, int M, int topk, float* out, float act_limit, hipStream_t st)
 {
     const int P = M * topk;
-    if (gfl::gate_up_lds_bytes(L.K[0], 4, L.H, 0, 0, 0) > gfl::LDS_LIMIT ||
-        gfl::gate_up_lds_bytes(L.K[1], 4, L.H, 0, 0, 0) > gfl::LDS_LIMIT ||
-        gfl::down_lds_bytes(L.K[2], 4, L.I, 0) > gfl::LDS_LIMIT)
+    if (gfl::gate_up_lds_bytes(L.K[0], 4, L.H, 0, 0, 0, 0) > gfl::LDS_LIMIT ||
+        gfl::gate_up_lds_bytes(L.K[1], 4, L.H, 0, 0, 0, 0) > gfl::LDS_LIMIT ||
+        gfl::down_lds_bytes(L.K[2], 4, L.I, 0, 0) > gfl::LDS_LIMIT)
         return fail(GFL_EINVAL, "gfl_moe_forward: shape needs more than 160 KB of LDS per workgroup");
     Gws ws;
     if (const int rc = grouped_workspace(c, st, P, M, L.E, L.H, L.I, "gfl_moe_forward", ws)) return rc;

@@ -300,6 +300,55 @@ __device__ void publish_plan(const LPlan& L, const int* hdr, int P, int topk, co
     }
 }
 
+// publish_plan for the relay launches, where the slot of pick p is p itself (its workgroups read sel directly and need
+// no plan): the down launch's address table is indexed by pick, with 0 for skipped picks (their workgroups return),
+// and each token's picks in (job, pick) order come from the same job rule.
+__device__ void publish_plan_picks(const LPlan& L, const int* hdr, int P, int topk, const void* w, int w_half,
+                                   const PlanView& pv, float* out, int H, const uint64_t* ptrs)
+{
+    const int t = threadIdx.x, nt = blockDim.x;
+    const int U = hdr[0];
+    if (t < 3) pv.hdr[t] = t == 1 ? P : hdr[t];
+    for (int u = t; u < U; u += nt) pv.uexp[u] = L.uexp[u];
+    for (int p = t; p < P; p += nt)
+    {
+        const int e = L.e[p];
+        pv.uptr[2 * p] = e < 0 ? 0 : ptrs[(size_t)e * 9 + 2];
+        pv.uptr[2 * p + 1] = e < 0 ? 0 : ptrs[(size_t)e * 9 + 8];
+        pv.slot_pick[p] = p;
+        pv.pick_slot[p] = e < 0 ? -1 : p;
+        pv.pick_job[p] = e < 0 ? 0x7fffffff : plan_job(L, p);
+        if (e >= 0) pv.slot_u[p] = plan_u(L, p);
+    }
+    const int M = P / topk;
+    for (int tk = t; tk < M; tk += nt)
+    {
+        int ord[MAX_TOPK], job[MAX_TOPK];
+        int n = 0;
+        for (int k = 0; k < topk; ++k)
+        {
+            const int p = tk * topk + k;
+            if (L.e[p] < 0) continue;
+            const int jb = plan_job(L, p);
+            int b = n++;
+            while (b > 0 && job[b - 1] > jb) { ord[b] = ord[b - 1]; job[b] = job[b - 1]; --b; }
+            ord[b] = p;
+            job[b] = jb;
+        }
+        for (int k = 0; k < topk; ++k)
+        {
+            const int p = k < n ? ord[k] : -1;
+            pv.tok_slot[tk * topk + k] = p;
+            pv.tok_w[tk * topk + k] = p < 0 ? 0.f
+                                    : (w_half ? h2f_bits(reinterpret_cast<const uint16_t*>(w)[p])
+                                              : reinterpret_cast<const float*>(w)[p]);
+        }
+        pv.tok_npk[tk] = n;
+        if (n == 0)
+            for (int i = 0; i < H; ++i) out[(size_t)tk * H + i] = 0.f;
+    }
+}
+
 // EXACT above MAX_PICKS picks: the decode launches' PlanView from the grouped plan of the prefill path (one
 // workgroup of 1024 threads, E <= 1024). Union entries are the experts with slots, ascending, so each entry's slots
 // are its expert's contiguous range of the expert-major slot order; slot_pick, tok_slot, tok_w and tok_npk are the
@@ -500,6 +549,126 @@ __device__ __forceinline__ void chain_dma(const uint8_t* __restrict__ col_base, 
         const float a1 = __shfl(acc[s], n + 16), a2 = __shfl(acc[s], n + 32), a3 = __shfl(acc[s], n + 48);
         res[s] = (acc[s] + a1) + (a2 + a3);
     }
+}
+
+// One tile column of one matrix for one slot, its groups of 8 tile rows shared out over RW waves of the workgroup: the
+// wave with relay index r streams and decodes groups r, r + RW, r + 2 RW, ..., and the column's accumulators pass from
+// wave to wave through relay (64 floats in LDS) in group order, so every accumulator is still one chain of fused
+// multiply-adds over the tile rows in the reference's order.
+// Phase ph: each wave decodes and transposes its group ph * RW + r, then RW turns follow, each closed by a workgroup
+// barrier; in turn r this wave reads the accumulators of group g - 1, runs the group's 32 FMAs and writes them back.
+// Every wave of the workgroup runs the same phases and turns (the same barriers), whether or not it has a group left.
+// The trellis streams through registers: each wave keeps its next PF groups in flight as 16-byte buffer loads (lane l
+// of load i holds byte 16 (64 i + l) of the group: tile (64 i + l) / 2K, bytes 16 ((64 i + l) % 2K) onward) and writes
+// a group into its single LDS slot (8 tiles, tile-major) right before decoding it. LDS operations of one wave complete
+// in issue order, so the slot is rewritten only after the previous group's reads; the waits for the loads are the
+// compiler's own (registers it tracks). lds_x: the slot's transformed inputs as fp32 in the permuted [tk][j][q] order,
+// filled by pre() (which ends with a workgroup barrier) after the first group's decode, which does not need them.
+// Returns the column results (valid in lanes 0..15 of every relay wave of the column).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <int K, int PF, int RW, class PreLoad, class Pre>
+__device__ __forceinline__ float chain_relay(const uint8_t* __restrict__ col_base, size_t gstride, int TK,
+                                             const float* lds_x, uint8_t* slot, float* relay, int r,
+                                             PreLoad&& pre_load, Pre&& pre)
+{
+    constexpr int TB = 32 * K, CH = 2 * K, NCH = 8 * CH, NLD = (NCH + 63) / 64;   // 16-byte chunks
+    const int lane = threadIdx.x & 63;
+    const LaneDec d = lane_dec(lane, K);
+    const int j = lane >> 4, n = lane & 15;
+    half4 Pm;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) Pm[i] = (_Float16)((j == (n & 3) && i == (n >> 2)) ? 1.0f : 0.0f);
+    const float4v zero = { 0.f, 0.f, 0.f, 0.f };
+    uint8_t* cb = const_cast<uint8_t*>(uniform_ptr(col_base));
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(cb, (short)0, (int)((size_t)TK * gstride),
+                                                                        0x00020000);
+    const int gs = (int)gstride;
+    int voff[NLD];
+#pragma unroll
+    for (int i = 0; i < NLD; ++i)
+    {
+        const int q = 64 * i + lane;
+        voff[i] = q < NCH ? (q / CH) * gs + (q % CH) * 16 : 0;
+    }
+    const int ngroups = TK / 8, nph = (ngroups + RW - 1) / RW;
+    // every phase issues the same loads (group index clamped to the last group, which stays in bounds), so the
+    // compiler's wait before writing a group to LDS counts exactly the PF - 1 younger groups
+    u32x4 buf[PF][NLD];
+    auto load = [&](u32x4 (&b)[NLD], int ph) {
+        const int g = min(ph * RW + r, ngroups - 1);
+#pragma unroll
+        for (int i = 0; i < NLD; ++i)
+            b[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff[i], g * 8 * gs, 0);   // lanes past the group: chunk 0
+    };
+    pre_load();
+#pragma unroll
+    for (int k = 0; k < PF; ++k) load(buf[k], k);
+    float acc = 0.f;
+    const int nphp = (nph + PF - 1) / PF * PF;   // phases padded to whole rounds of PF (the padding has no work)
+    for (int ph0 = 0; ph0 < nphp; ph0 += PF)
+    {
+#pragma unroll
+        for (int k = 0; k < PF; ++k)
+        {
+            const int ph = ph0 + k;
+            const int g = ph * RW + r;
+            const bool mine = ph < nph && g < ngroups;
+            float4v cw[8], xf[8];
+            if (mine)
+            {
+#pragma unroll
+                for (int i = 0; i < NLD; ++i)
+                    if (64 * i + lane < NCH) *reinterpret_cast<u32x4*>(slot + (64 * i + lane) * 16) = buf[k][i];
+            }
+            load(buf[k], ph + PF);
+            if (mine)
+            {
+#pragma unroll
+                for (int rr = 0; rr < 8; ++rr)
+                {
+                    const uint8_t* tp = slot + rr * TB;
+                    const uint32_t hi = *reinterpret_cast<const uint32_t*>(tp + d.o0);
+                    const uint32_t lo = *reinterpret_cast<const uint32_t*>(tp + d.o1);
+                    cw[rr] = __builtin_amdgcn_mfma_f32_16x16x16f16(Pm, decode4<K>(hi, lo, d.sh), zero, 0, 0, 0);
+                }
+            }
+            // the input transform (ending with a workgroup barrier) after the first group's decode, which does not
+            // need the inputs: that decode overlaps the transform's loads
+            if (ph == 0) pre();
+            if (mine)
+            {
+#pragma unroll
+                for (int rr = 0; rr < 8; ++rr)
+                    xf[rr] = *reinterpret_cast<const float4v*>(lds_x + ((size_t)g * 8 + rr) * 16 + j * 4);
+            }
+            if (ph < nph)   // the same for every wave of the workgroup
+            {
+#pragma unroll
+                for (int turn = 0; turn < RW; ++turn)
+                {
+                    if (turn == r && mine)
+                    {
+                        if (g > 0) acc = relay[lane];
+#pragma unroll
+                        for (int rr = 0; rr < 8; ++rr)
+                        {
+                            acc = __builtin_fmaf(cw[rr][0], xf[rr][0], acc);
+                            acc = __builtin_fmaf(cw[rr][1], xf[rr][1], acc);
+                            acc = __builtin_fmaf(cw[rr][2], xf[rr][2], acc);
+                            acc = __builtin_fmaf(cw[rr][3], xf[rr][3], acc);
+                        }
+                        relay[lane] = acc;
+                    }
+                    if (RW > 1) lds_barrier();
+                }
+            }
+        }
+    }
+    wait_vmcnt<0>();   // the padding's clamped prefetches
+    if (RW > 1) acc = relay[lane];   // the last group's accumulators (its turn ended with a barrier)
+    const float a1 = __shfl(acc, n + 16), a2 = __shfl(acc, n + 32), a3 = __shfl(acc, n + 48);
+    return (acc + a1) + (a2 + a3);
 }
 
 // MFMA-accumulate form of the column GEMV (mode GFL_MODE_MFMA): tile groups [g0, g1) of one tile column for up to 16
@@ -1066,6 +1235,258 @@ __attribute__((amdgpu_waves_per_eu(K == 5 || NS == 8 ? 3 : 4))) void down_kernel
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// relay launches: one slot per workgroup (slot = pick), RW waves per tile column
+// ---------------------------------------------------------------------------------------------------------------
+
+// LDS of the relay gate|up launch: the waves' rings plus the slot's fp32 inputs, or the plan of the publishing
+// workgroup where that is larger
+template <int K>
+__host__ __device__ constexpr size_t gu_relay_lds(int H, int P, int E)
+{
+    const size_t x = (size_t)H * 4, plan = lplan_ints(P, E) * 4;
+    return (size_t)GU_NW * 8 * 32 * K + (x > plan ? x : plan);
+}
+
+// Grid: (1 + P * I / (16 * CW), nmat), CW = GU_NW / RW tile columns per workgroup. Workgroup 1 + p * (I / (16 CW))
+// + cb: pick p's 16 CW gate or up outputs [cb * 16 CW, (cb + 1) * 16 CW), RW waves per column (chain_relay); a skipped
+// pick's workgroups return at once. Workgroup 0 (dispatched first, so that it never waits for a GEMV workgroup's
+// slot) builds the plan and publishes it for the down launch (slots = picks).
+// The last of the workgroups covering a 128-block of a pick (gate and up) runs its SwiGLU stage, as in gu_kernel.
+template <int K, int RW>
+__global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3))) void gu_relay_kernel(GuArgs a)
+{
+    constexpr int NW = GU_NW, CW = NW / RW, TB = 32 * K;
+    static_assert(NW % RW == 0, "relay width divides the workgroup");
+    extern __shared__ __align__(16) uint8_t lds_raw[];
+    __shared__ int hdr[4];
+    __shared__ int s_last;
+    __shared__ float relay[CW][64];
+    constexpr int RB = 8 * TB;                                           // one group slot per wave
+    uint8_t* rings = lds_raw;                                            // [NW][RB]
+    float* lds_x = reinterpret_cast<float*>(lds_raw + NW * RB);          // [H] permuted, fp32
+    const int TN = a.I / 16, TK = a.H / 16, ncb = TN / CW;
+    if (blockIdx.x == 0)
+    {
+        if (blockIdx.y == 0)
+        {
+            const LPlan L = lplan_carve(reinterpret_cast<int*>(lds_x), a.P, a.E);
+            if (a.P <= 64) build_plan_wave(a.sel, a.P, a.E, L, hdr);
+            else build_plan(a.sel, a.P, a.E, L, hdr);
+            publish_plan_picks(L, hdr, a.P, a.topk, a.w, a.w_half, a.pv, a.out, a.H, a.ptrs);
+        }
+        return;
+    }
+    const int p = (blockIdx.x - 1) / ncb, cb = (blockIdx.x - 1) % ncb;
+    const int64_t e64 = a.sel[p];
+    if (e64 < 0 || e64 >= a.E) return;
+    const int e = (int)e64;
+    const int mat = a.mat_base + blockIdx.y;   // 0 gate, 1 up
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15;
+    const int wid = __builtin_amdgcn_readfirstlane(wave);
+    const int c = wid / RW, r = wid % RW;
+    const uint8_t* tr = reinterpret_cast<const uint8_t*>(a.ptrs[(size_t)e * 9 + mat]);
+    const gptr<uint16_t> suh = gaddr<uint16_t>(a.ptrs[(size_t)e * 9 + 3 + 2 * mat]);
+    const size_t gstride = (size_t)TN * TB;
+    const int t = cb * CW + c;   // this wave's tile column
+    const uint8_t* col = tr + (size_t)t * TB;
+    const uint16_t* xrow = a.x + (size_t)(p / a.topk) * a.H;
+
+    // input transform (prep_block, ft_core.h:97-102) into LDS: each 16-lane row takes one 128-block, 8 elements per
+    // lane; the first GU_PR rounds of blocks are loaded before the trellis groups are requested
+    const int nblk = TK / 8, rl = lane >> 4, li = lane & 15;
+    uint4 xv[GU_PR], sv[GU_PR];
+    auto load_round = [&](int rd, int k) {
+        const int b = min((rd * NW + wave) * 4 + rl, nblk - 1);
+        xv[k] = *reinterpret_cast<const uint4*>(xrow + b * 128 + li * 8);
+        sv[k] = gld16(suh, b * 128 + li * 8);
+    };
+    auto prep_round = [&](int rd, int k) {
+        const int b = (rd * NW + wave) * 4 + rl;
+        float v[8];
+        prep_block_row_p(v, xv[k], sv[k]);
+        if (b < nblk)
+        {
+            // elements 8li..8li+7 of block b: tile row li/2, accumulators j0 = 2(li&1) and j0 + 1, q = k/2
+            const int tk = b * 8 + (li >> 1), j0 = 2 * (li & 1);
+            float* dst = lds_x + (tk * 4 + j0) * 4;
+            float4v e0, e1;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+            {
+                e0[q] = h2f_bits((uint16_t)f2h_bits(v[2 * q]));
+                e1[q] = h2f_bits((uint16_t)f2h_bits(v[2 * q + 1]));
+            }
+            *reinterpret_cast<float4v*>(dst) = e0;
+            *reinterpret_cast<float4v*>(dst + 4) = e1;
+        }
+    };
+    const int nr = (nblk + 4 * NW - 1) / (4 * NW);   // rounds of 4 * NW blocks
+    auto pre_load = [&] {
+#pragma unroll
+        for (int k = 0; k < GU_PR; ++k)
+            if (k < nr) load_round(k, k);
+    };
+    auto pre = [&] {
+        for (int r0 = 0; r0 < nr; r0 += GU_PR)
+        {
+            if (r0 > 0)
+            {
+#pragma unroll
+                for (int k = 0; k < GU_PR; ++k)
+                    if (r0 + k < nr) load_round(r0 + k, k);
+            }
+#pragma unroll
+            for (int k = 0; k < GU_PR; ++k)
+                if (r0 + k < nr) prep_round(r0 + k, k);
+        }
+        lds_barrier();   // lds_x complete
+    };
+    const float res = chain_relay<K, NGRP - 1, RW>(col, gstride, TK, lds_x, rings + wid * RB, relay[c], r, pre_load,
+                                                   pre);
+    float* ybase = a.ygu + (size_t)mat * a.pv.cap_slots * a.I;
+    if (r == 0 && lane < 16) st_agent(&ybase[(size_t)p * a.I + t * 16 + n], res);
+    release_agent();
+    __syncthreads();
+    const int blk = (cb * CW * 16) / 128;
+    if (threadIdx.x == 0)
+    {
+        int* ctr = a.act_cnt + (size_t)p * (a.I / 128) + blk;
+        const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = old == a.nmat_total - 1;
+        if (s_last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (s_last) act_block(a, e, p, p + 1, blk);
+}
+
+// LDS of the relay down launch: the waves' rings plus the slot's fp32 inputs, or the combining workgroup's blocks of
+// up to MAX_TOPK picks where that is larger
+template <int K>
+__host__ __device__ constexpr size_t dn_relay_lds(int I)
+{
+    const size_t x = (size_t)I * 4, comb = (size_t)MAX_TOPK * 128 * 4;
+    return (size_t)GU_NW * 8 * 32 * K + (x > comb ? x : comb);
+}
+
+// Grid: P * H / (16 * CW). Workgroup (p, cb): the raw down sums [cb * 16 CW, (cb + 1) * 16 CW) of pick p (slot p)
+// into yd, RW waves per column; the last of the NQ * npk workgroups that cover a token's 128-output block (NQ quarters
+// of each of its npk picks) runs out_block on every pick's block and the token's weighted sum of the block.
+template <int K, int RW>
+__global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3))) void dn_relay_kernel(DnArgs a)
+{
+    constexpr int NW = GU_NW, CW = NW / RW, TB = 32 * K, NQ = 128 / (16 * CW);
+    extern __shared__ __align__(16) uint8_t lds_raw[];
+    __shared__ int s_last;
+    __shared__ int c_tok, c_npk, c_slot[MAX_TOPK];
+    __shared__ float c_w[MAX_TOPK];
+    __shared__ float relay[CW][64];
+    constexpr int RB = 8 * TB;                                      // one group slot per wave
+    uint8_t* rings = lds_raw;                                       // [NW][RB]
+    float* lds_x = reinterpret_cast<float*>(lds_raw + NW * RB);     // [I] permuted, fp32
+    const int TN = a.H / 16, TK = a.I / 16, ncb = TN / CW;
+    const int p = blockIdx.x / ncb, cb = blockIdx.x % ncb;
+    const int blk = cb / NQ;
+    const uint8_t* tr = reinterpret_cast<const uint8_t*>(a.pv.uptr[2 * p]);
+    const gptr<uint16_t> svh = gaddr<uint16_t>(a.pv.uptr[2 * p + 1]);
+    if (tr == nullptr) return;   // skipped pick
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15;
+    const int wid = __builtin_amdgcn_readfirstlane(wave);
+    const int c = wid / RW, r = wid % RW;
+    const size_t gstride = (size_t)TN * TB;
+    const int t = cb * CW + c;
+    const uint8_t* col = tr + (size_t)t * TB;
+    const int nbh = a.H / 128;
+    // the token's combine list (slots in job order and weights): loads issued before the GEMV, written to LDS after
+    const int ck = threadIdx.x;
+    int q_tok = 0, q_slot = -1, q_npk = 0;
+    float q_w = 0.f;
+    if (ck < a.topk)
+    {
+        q_tok = p / a.topk;
+        q_slot = a.pv.tok_slot[q_tok * a.topk + ck];
+        q_w = a.pv.tok_w[q_tok * a.topk + ck];
+        q_npk = a.pv.tok_npk[q_tok];
+    }
+    // the slot's down input (I fp16) into LDS as fp32; each thread's first two 16-byte loads are issued before the
+    // trellis groups are requested
+    const int nvec = a.I / 8;
+    const uint4* xsrc = reinterpret_cast<const uint4*>(a.xtd + (size_t)p * a.I);
+    auto put = [&](int i, const uint4& v) {
+        const uint32_t w[4] = { v.x, v.y, v.z, v.w };
+        float4v f0, f1;
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+        {
+            f0[2 * q] = h2f_bits((uint16_t)w[q]);
+            f0[2 * q + 1] = h2f_bits((uint16_t)(w[q] >> 16));
+            f1[2 * q] = h2f_bits((uint16_t)w[q + 2]);
+            f1[2 * q + 1] = h2f_bits((uint16_t)(w[q + 2] >> 16));
+        }
+        float4v* d = reinterpret_cast<float4v*>(lds_x) + 2 * i;
+        d[0] = f0;
+        d[1] = f1;
+    };
+    const int i0 = threadIdx.x, i1 = threadIdx.x + NW * 64;
+    uint4 xc0 = {}, xc1 = {};
+    auto pre_load = [&] {
+        if (i0 < nvec) xc0 = xsrc[i0];
+        if (i1 < nvec) xc1 = xsrc[i1];
+    };
+    auto pre = [&] {
+        if (i0 < nvec) put(i0, xc0);
+        if (i1 < nvec) put(i1, xc1);
+        for (int i = threadIdx.x + 2 * NW * 64; i < nvec; i += NW * 64) put(i, xsrc[i]);
+        lds_barrier();   // lds_x complete
+    };
+    const float res = chain_relay<K, NGRP - 1, RW>(col, gstride, TK, lds_x, rings + wid * RB, relay[c], r, pre_load,
+                                                   pre);
+    if (r == 0 && lane < 16) st_agent(&a.yd[(size_t)p * a.H + t * 16 + n], res);
+    if (ck < a.topk)
+    {
+        c_slot[ck] = q_slot;
+        c_w[ck] = q_w;
+        if (ck == 0) { c_tok = q_tok; c_npk = q_npk; }
+    }
+    release_agent();
+    __syncthreads();
+    // one counter per (token, 128-block) counts the block's quarter arrivals of every pick of the token; the last
+    // arrival runs out_block (ft_core.h:1016) on each pick's block and the weighted sum in (job, pick) order
+    // (ft_core.h:1020-1033): o = 0, then o += w * y
+    if (threadIdx.x == 0)
+    {
+        int* ctr = a.out_cnt + (size_t)c_tok * nbh + blk;
+        const int need = NQ * c_npk;
+        const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = old == need - 1;
+        if (old == need - 1) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    const int npk = c_npk;
+    float* ylds = lds_x;   // [npk][128] the picks' blocks after out_block (the GEMV inputs are no longer needed)
+    for (int k = wave; k < npk; k += NW)
+    {
+        const int sl = c_slot[k];
+        const float* y = a.yd + (size_t)sl * a.H + blk * 128;
+        const gptr<uint16_t> sv = gaddr<uint16_t>(a.pv.uptr[2 * sl + 1]);
+        float v0 = ld_agent(&y[lane]), v1 = ld_agent(&y[lane + 64]);
+        out_block_wave(v0, v1, h2f_bits(sv[blk * 128 + lane]), h2f_bits(sv[blk * 128 + lane + 64]));
+        ylds[k * 128 + lane] = v0;
+        ylds[k * 128 + lane + 64] = v1;
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    float o0 = 0.f, o1 = 0.f;
+    for (int k = 0; k < npk; ++k)
+    {
+        o0 = o0 + c_w[k] * ylds[k * 128 + lane];
+        o1 = o1 + c_w[k] * ylds[k * 128 + lane + 64];
+    }
+    a.out[(size_t)c_tok * a.H + blk * 128 + lane] = o0;
+    a.out[(size_t)c_tok * a.H + blk * 128 + lane + 64] = o1;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
 // dequant (dense_weights, ft_core.h:1657-1672): trellis -> fp16 W[k][n]
 // ---------------------------------------------------------------------------------------------------------------
 
@@ -1143,6 +1564,34 @@ static void dn_launch(const DnArgs& a, int umax, int P, hipStream_t st)
     hipLaunchKernelGGL(kern, dim3(ents * (a.H / (16 * nw))), dim3(nw * 64), lds, st, a);
 }
 
+template <int K, int RW>
+static void gu_relay_launch(const GuArgs& a, int nmat, hipStream_t st)
+{
+    constexpr int CW = GU_NW / RW;
+    auto kern = gu_relay_kernel<K, RW>;
+    static const bool opened = open_lds(kern);
+    (void)opened;
+    const size_t lds = gu_relay_lds<K>(a.H, a.P, a.E);
+    hipLaunchKernelGGL(kern, dim3(1 + a.P * (a.I / (16 * CW)), nmat), dim3(GU_NW * 64), lds, st, a);
+}
+
+template <int K, int RW>
+static void dn_relay_launch(const DnArgs& a, int P, hipStream_t st)
+{
+    constexpr int CW = GU_NW / RW;
+    auto kern = dn_relay_kernel<K, RW>;
+    static const bool opened = open_lds(kern);
+    (void)opened;
+    const size_t lds = dn_relay_lds<K>(a.I);
+    hipLaunchKernelGGL(kern, dim3(P * (a.H / (16 * CW))), dim3(GU_NW * 64), lds, st, a);
+}
+
+// relay width: 1, 2 or 4 waves per tile column
+#define GFL_RW_SWITCH(RWV, CALL)                                                                                \
+    if ((RWV) == 1) { constexpr int RW_ = 1; CALL; }                                                           \
+    else if ((RWV) == 2) { constexpr int RW_ = 2; CALL; }                                                      \
+    else { constexpr int RW_ = 4; CALL; }
+
 // slots per pass: 1, 4 or 8 (a 2-slot instantiation does not fit the register budget without spilling; passes with
 // fewer slots than NS skip the unused ones)
 #define GFL_NS_SWITCH(NSV, CALL)                                                                                \
@@ -1160,22 +1609,22 @@ static void dn_launch(const DnArgs& a, int umax, int P, hipStream_t st)
         default: return -1;                                                                                     \
     }
 
-size_t gate_up_lds_bytes(int K, int ns, int H, int P, int E, int mf)
+size_t gate_up_lds_bytes(int K, int ns, int H, int P, int E, int mf, int rw)
 {
     size_t r = 0;
     auto f = [&]() -> int {
-        GFL_K_SWITCH(K, (r = gu_lds<K_>(ns, H, P, E, mf)))
+        GFL_K_SWITCH(K, (r = rw ? gu_relay_lds<K_>(H, P, E) : gu_lds<K_>(ns, H, P, E, mf)))
         return 0;
     };
     f();
     return r;
 }
 
-size_t down_lds_bytes(int K, int ns, int I, int mf)
+size_t down_lds_bytes(int K, int ns, int I, int mf, int rw)
 {
     size_t r = 0;
     auto f = [&]() -> int {
-        GFL_K_SWITCH(K, (r = dn_lds<K_>(ns, I, mf)))
+        GFL_K_SWITCH(K, (r = rw ? dn_relay_lds<K_>(I) : dn_lds<K_>(ns, I, mf)))
         return 0;
     };
     f();
@@ -1185,7 +1634,7 @@ size_t down_lds_bytes(int K, int ns, int I, int mf)
 int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, const int64_t* sel, const void* w,
                    int w_half, int P, int topk, int E, int H, int I, int umax, const uint16_t* x, float* ygu,
                    uint16_t* xtd, int* act_cnt, const float* silu_tab, float act_limit, const PlanView& pv, float* out,
-                   int mf, hipStream_t st)
+                   int mf, int rw, hipStream_t st)
 {
     GuArgs a;
     a.ptrs = ptrs; a.sel = sel; a.w = w; a.w_half = w_half; a.P = P; a.topk = topk; a.E = E; a.H = H; a.I = I;
@@ -1201,6 +1650,14 @@ int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, 
         GFL_K_SWITCH(K, (gu_launch<K_, 4, true>(a, umax, nmat, st)))
         return 0;
     }
+    if (rw)
+    {
+        // one slot per workgroup, slot = pick, rw waves per tile column
+        a.nmat_total = 2 * (128 / (16 * (GU_NW / rw)));
+        a.per_slot = 1;
+        GFL_K_SWITCH(K, GFL_RW_SWITCH(rw, (gu_relay_launch<K_, RW_>(a, nmat, st))))
+        return 0;
+    }
     a.nmat_total = 2 * (128 / (16 * GU_NW));
     a.per_slot = ns == 1;
     GFL_K_SWITCH(K, GFL_NS_SWITCH(ns, (gu_launch<K_, NS_, false>(a, umax, nmat, st))))
@@ -1208,7 +1665,7 @@ int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, 
 }
 
 int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int umax, int P, const PlanView& pv,
-                const uint16_t* xtd, float* yd, int* out_cnt, int* blk_cnt, float* out, int mf, hipStream_t st)
+                const uint16_t* xtd, float* yd, int* out_cnt, int* blk_cnt, float* out, int mf, int rw, hipStream_t st)
 {
     DnArgs a;
     a.ptrs = ptrs; a.topk = topk; a.H = H; a.I = I; a.pv = pv; a.xtd = xtd; a.yd = yd; a.out_cnt = out_cnt;
@@ -1219,6 +1676,12 @@ int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int
     {
         a.per_slot = 0;
         GFL_K_SWITCH(K, (dn_launch<K_, 4, true>(a, umax, P, st)))
+        return 0;
+    }
+    if (rw)
+    {
+        a.per_slot = 1;
+        GFL_K_SWITCH(K, GFL_RW_SWITCH(rw, (dn_relay_launch<K_, RW_>(a, P, st))))
         return 0;
     }
     a.per_slot = ns == 1;
@@ -1263,6 +1726,7 @@ int launch_exact_grouped(const int* Ks, const uint64_t* ptrs, int P, int topk, i
 }
 
 #undef GFL_NS_SWITCH
+#undef GFL_RW_SWITCH
 #undef GFL_K_SWITCH
 
 int launch_dequant(const uint8_t* tr, int k, int n, int K, uint16_t* W, hipStream_t st)

@@ -206,7 +206,7 @@ def test_alignment_errors(gpu):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("ns", [1, 2, 4, 8])
-def test_forward_slots_per_pass_bitexact(oracle, ns):
+def test_forward_slots_per_pass_bitexact(gpu, oracle, ns):
     """Every slots-per-pass instantiation (GFL_SLOTS_PER_PASS, read at context creation): 12 tokens over 6 experts, so
     experts hold up to 12 slots and take several passes over their weights."""
     import os
@@ -403,3 +403,72 @@ def test_against_both_reference_builds(gpu, oracle, ref, ref_server):
     mx, rms, _ = _report("vs server build", got, b)
     assert np.array_equal(got, a)
     assert mx <= TOL * rms
+
+
+def _ctx_with_env(**env):
+    """A context created under the given environment (read once at creation: GFL_RELAY, GFL_STREAM, ...)."""
+    import os
+    import _native
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        return _native.Context(0)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("relay", ["0", "1,1", "2,2", "4,4", "2,1", "4,2", "1,4"])
+def test_relay_launches_bitexact(gpu, oracle, relay):
+    """Every decode launch family of one slot per pass (GFL_RELAY, read at context creation): without relay ("0"), and
+    the relay launches with 1, 2 or 4 waves per tile column for gate|up and down; mixed K (2..5), skipped picks, a token
+    picking one expert twice, and 1, 2 and 5 tokens."""
+    ctx = _ctx_with_env(GFL_RELAY=relay)
+    H, I = 512, 256
+    for li, Ks in enumerate([(3, 3, 3), (2, 5, 4), (4, 4, 3), (5, 2, 5)]):
+        L = _layer(ctx, 40 + li, 6, H, I, Ks)
+        ex = _host_experts(oracle, L)
+        for M in (1, 2, 5):
+            rng = np.random.default_rng(4000 + 10 * li + M)
+            x16 = rng.standard_normal((M, H)).astype(np.float16)
+            sel = np.stack([rng.permutation(6)[:4] for _ in range(M)]).astype(np.int64)
+            if M >= 2:
+                sel[1, 2] = -1
+                sel[0, 3] = sel[0, 0]
+            w = rng.random(sel.shape).astype(np.float32)
+            got = _forward(ctx, 40 + li, x16, sel, w)
+            want = oracle.moe_forward(ex, x16.astype(np.float32), sel, w, mode=1)
+            _, _, nbad = _report(f"relay {relay} Ks {Ks} M={M}", got, want)
+            assert nbad == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("relay", ["4,4", "2,1", "2,2"])
+def test_relay_launches_full_shape_bitexact(gpu, oracle, relay):
+    """The relay launches at the config-1 shape (H=5120, I=1536, K=3): one expert (config 0) and top-8 of a
+    10-expert layer at M = 1 and 3."""
+    import synth
+    ctx = _ctx_with_env(GFL_RELAY=relay)
+    H, I, E = 5120, 1536, 10
+    L = _layer(ctx, 50, E, H, I)
+    ex = _host_experts(oracle, L)
+    rng = np.random.default_rng(5000)
+    x16 = rng.standard_normal((1, H)).astype(np.float16)
+    sel = np.array([[7]], np.int64)
+    got = _forward(ctx, 50, x16, sel, np.ones((1, 1), np.float32))
+    want = oracle.expert_forward(ex[7], x16.astype(np.float32), mode=1)
+    _, _, nbad = _report(f"relay {relay} one expert", got, want)
+    assert nbad == 0
+    for M in (1, 3):
+        rng = np.random.default_rng(5000 + M)
+        x16 = rng.standard_normal((M, H)).astype(np.float16)
+        (sel, w16), _ = synth.route_uniform(M, E, 8, rng)
+        got = _forward(ctx, 50, x16, sel, w16)
+        want = oracle.moe_forward(ex, x16.astype(np.float32), sel, w16.astype(np.float32), mode=1)
+        mx, rms, nbad = _report(f"relay {relay} full shape M={M}", got, want)
+        assert mx <= TOL * rms
+        assert nbad == 0
