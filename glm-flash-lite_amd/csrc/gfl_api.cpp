@@ -241,17 +241,17 @@ int run_forward(gfl_ctx* c, const Layer& L, const Workspace& ws, const uint16_t*
     if (c->ns_override > 0) ns = std::min(c->ns_override, mf ? std::min(M, 16) : M);
     // Calls with few tile columns run the relay launches: a workgroup per (pick, tile columns), rw waves per column,
     // each streaming and decoding every rw-th group of 8 tile rows while the column's accumulators pass from wave to
-    // wave in tile-row order (chain_relay). One wave per column leaves most SIMDs idle when a call has few columns;
-    // rw waves per column put rw times the waves on the chip. Measured on MI355X (config 1 layers, 4 cycled): one
-    // expert per call (192 gate|up columns) 39.2 -> 29.8 us with 4 waves per column; at 8 picks (1,536 columns)
-    // 2 waves per column match the per-slot launches; above that the relay's turns cost more than the waves gain.
+    // wave in tile-row order (chain_relay). With one wave per column such a call leaves most SIMDs idle; rw waves per
+    // column put rw times the waves on the chip. Measured on MI355X (config-1 layers, 4 cycled): one expert per call
+    // (192 gate|up columns) 39.2 -> 29.8 us with 4 waves per column. At 8 picks (1,536 columns) the relay launches
+    // were 1-2% slower than the per-slot ones, so they are not used there.
     int rw[2] = { 0, 0 };
     if (!mf && ns == 1)
     {
         const int64_t cgu = (int64_t)P * 2 * (L.I / 16), cdn = (int64_t)P * (L.H / 16);   // tile columns
-        if (cgu <= 1536)
+        if (cgu <= 768)
         {
-            rw[0] = cgu <= 768 ? 4 : 2;
+            rw[0] = 4;
             rw[1] = cdn <= 768 ? 4 : cdn <= 1536 ? 2 : 1;
         }
         if (c->rw_override[0] >= 0) { rw[0] = c->rw_override[0]; rw[1] = c->rw_override[1]; }

@@ -1247,10 +1247,10 @@ __host__ __device__ constexpr size_t gu_relay_lds(int H, int P, int E)
     return (size_t)GU_NW * 8 * 32 * K + (x > plan ? x : plan);
 }
 
-// Grid: (1 + P * I / (16 * CW), nmat), CW = GU_NW / RW tile columns per workgroup. Workgroup 1 + p * (I / (16 CW))
-// + cb: pick p's 16 CW gate or up outputs [cb * 16 CW, (cb + 1) * 16 CW), RW waves per column (chain_relay); a skipped
-// pick's workgroups return at once. Workgroup 0 (dispatched first, so that it never waits for a GEMV workgroup's
-// slot) builds the plan and publishes it for the down launch (slots = picks).
+// Grid: 1 + nmat * P * I / (16 * CW), CW = GU_NW / RW tile columns per workgroup. Workgroup 1 + (m * P + p) *
+// (I / (16 CW)) + cb: pick p's 16 CW outputs [cb * 16 CW, (cb + 1) * 16 CW) of matrix mat_base + m, RW waves per column
+// (chain_relay); a skipped pick's workgroups return at once. Workgroup 0 (dispatched first, so that it never waits
+// for a GEMV workgroup's slot) builds the plan and publishes it for the down launch (slots = picks).
 // The last of the workgroups covering a 128-block of a pick (gate and up) runs its SwiGLU stage, as in gu_kernel.
 template <int K, int RW>
 __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3))) void gu_relay_kernel(GuArgs a)
@@ -1267,20 +1267,18 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
     const int TN = a.I / 16, TK = a.H / 16, ncb = TN / CW;
     if (blockIdx.x == 0)
     {
-        if (blockIdx.y == 0)
-        {
-            const LPlan L = lplan_carve(reinterpret_cast<int*>(lds_x), a.P, a.E);
-            if (a.P <= 64) build_plan_wave(a.sel, a.P, a.E, L, hdr);
-            else build_plan(a.sel, a.P, a.E, L, hdr);
-            publish_plan_picks(L, hdr, a.P, a.topk, a.w, a.w_half, a.pv, a.out, a.H, a.ptrs);
-        }
+        const LPlan L = lplan_carve(reinterpret_cast<int*>(lds_x), a.P, a.E);
+        if (a.P <= 64) build_plan_wave(a.sel, a.P, a.E, L, hdr);
+        else build_plan(a.sel, a.P, a.E, L, hdr);
+        publish_plan_picks(L, hdr, a.P, a.topk, a.w, a.w_half, a.pv, a.out, a.H, a.ptrs);
         return;
     }
-    const int p = (blockIdx.x - 1) / ncb, cb = (blockIdx.x - 1) % ncb;
+    const int wg = blockIdx.x - 1, per_mat = a.P * ncb;
+    const int p = (wg % per_mat) / ncb, cb = wg % ncb;
     const int64_t e64 = a.sel[p];
     if (e64 < 0 || e64 >= a.E) return;
     const int e = (int)e64;
-    const int mat = a.mat_base + blockIdx.y;   // 0 gate, 1 up
+    const int mat = a.mat_base + wg / per_mat;   // 0 gate, 1 up
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15;
     const int wid = __builtin_amdgcn_readfirstlane(wave);
     const int c = wid / RW, r = wid % RW;
@@ -1564,6 +1562,31 @@ static void dn_launch(const DnArgs& a, int umax, int P, hipStream_t st)
     hipLaunchKernelGGL(kern, dim3(ents * (a.H / (16 * nw))), dim3(nw * 64), lds, st, a);
 }
 
+// Compute units of the current device (cached per device).
+static int device_cus()
+{
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev])
+    {
+        int n = 0;
+        cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n
+                                                                                                              : 256;
+    }
+    return cus[dev];
+}
+
+// LDS to request for a launch of nwg equal workgroups that each need `need` bytes: at least enough that a CU holds
+// no more than ceil(nwg / CUs) of them. The relay kernels use few registers, so the dispatcher could otherwise put one
+// workgroup more on some CUs than on the rest, and those CUs set the launch's time.
+static size_t balanced_lds(size_t need, long nwg)
+{
+    const long cus = device_cus(), per_cu = (nwg + cus - 1) / cus;
+    const size_t cap = (size_t)LDS_LIMIT / (size_t)(per_cu + 1) + 16;
+    return cap > need && cap <= (size_t)LDS_LIMIT ? cap : need;
+}
+
 template <int K, int RW>
 static void gu_relay_launch(const GuArgs& a, int nmat, hipStream_t st)
 {
@@ -1571,8 +1594,9 @@ static void gu_relay_launch(const GuArgs& a, int nmat, hipStream_t st)
     auto kern = gu_relay_kernel<K, RW>;
     static const bool opened = open_lds(kern);
     (void)opened;
-    const size_t lds = gu_relay_lds<K>(a.H, a.P, a.E);
-    hipLaunchKernelGGL(kern, dim3(1 + a.P * (a.I / (16 * CW)), nmat), dim3(GU_NW * 64), lds, st, a);
+    const long nwg = (long)a.P * (a.I / (16 * CW)) * nmat;   // GEMV workgroups (plus the publishing one)
+    const size_t lds = balanced_lds(gu_relay_lds<K>(a.H, a.P, a.E), nwg);
+    hipLaunchKernelGGL(kern, dim3(1 + nwg), dim3(GU_NW * 64), lds, st, a);
 }
 
 template <int K, int RW>
@@ -1582,8 +1606,9 @@ static void dn_relay_launch(const DnArgs& a, int P, hipStream_t st)
     auto kern = dn_relay_kernel<K, RW>;
     static const bool opened = open_lds(kern);
     (void)opened;
-    const size_t lds = dn_relay_lds<K>(a.I);
-    hipLaunchKernelGGL(kern, dim3(P * (a.H / (16 * CW))), dim3(GU_NW * 64), lds, st, a);
+    const long nwg = (long)P * (a.H / (16 * CW));
+    const size_t lds = balanced_lds(dn_relay_lds<K>(a.I), nwg);
+    hipLaunchKernelGGL(kern, dim3(nwg), dim3(GU_NW * 64), lds, st, a);
 }
 
 // relay width: 1, 2 or 4 waves per tile column
