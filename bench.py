@@ -13,9 +13,10 @@ value        = microseconds per token at M=1 (lower is better): the median over 
                over the whole timed region beside it. per_M holds M=1..4. All run the EXACT mode, whose outputs are
                bit-identical to the reference's EXACT expert (--mode mfma times GFL_MODE_MFMA instead).
 roofline     = the gate|up GEMV kernel (the dominant one) at M=1: algorithmic quantized bytes per launch (union of
-               routed experts x (gate+up trellis + their suh/svh)) / its mean launch time, from device events
-               recorded around every launch during an eager pass on the launch stream; peak = 8 TB/s HBM; traffic =
-               HBM bytes per launch from the FETCH_SIZE/WRITE_SIZE counter file (--pmc-probe / --pmc-digest).
+               routed experts x (gate+up trellis + their suh/svh)) / its mean execution time, from start/stop events
+               the runtime stamps on each launch's own dispatch (hipExtLaunchKernelGGL, through gfl_profile_*) during
+               an eager pass on the launch stream; peak = 8 TB/s HBM; traffic = HBM bytes per launch from the
+               FETCH_SIZE/WRITE_SIZE counter file (--pmc-probe / --pmc-digest).
 configs      = BASELINE configs 0 (one expert per call), 2 (mixed bitrates, Zipf routing), 3 (M=16/32/64) and 4 (42
                resident layers decoded at M=1; prefill of M=2048 tokens through the MFMA grouped path, as TFLOP/s
                against 2.5 PF dense fp16, and through the EXACT path); the router (gfl_route) per call; routed layer +
@@ -626,7 +627,7 @@ def main():
                              lambda li: layers[li].quant_bytes_per_expert)
         per_M[str(M)] = r
         if M == 1:
-            # live per-kernel timing of the dominant kernel (gate|up GEMV): device events around every launch
+            # live per-kernel timing of the dominant kernel (gate|up GEMV): start/stop events on every launch's dispatch
             out = torch.empty((1, H), dtype=torch.float32, device="cuda")
             NR = len(routes)
             ctx.profile(True)

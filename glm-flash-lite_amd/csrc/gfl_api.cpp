@@ -11,6 +11,10 @@
 #include <string>
 #include <vector>
 
+namespace gfl {
+thread_local KernelTimer* g_kernel_timer = nullptr;
+}
+
 namespace {
 
 thread_local std::string g_err;
@@ -183,17 +187,32 @@ hipEvent_t take_event(gfl_ctx* c)
     return e;
 }
 
-// runs `launch` bracketed by a pair of events when profiling is on
+hipEvent_t take_event_cb(void* owner) { return take_event(static_cast<gfl_ctx*>(owner)); }
+
+// runs `launch` with its kernels timed when profiling is on: launchers that take the kernel timer record each kernel's
+// execution (start/stop events on its own dispatch); a stage whose launchers do not is bracketed by a pair of events
 template <class F>
 int staged(gfl_ctx* c, int stage, hipStream_t st, F&& launch)
 {
     if (!c->prof) return launch();
     hipEvent_t a = take_event(c), b = take_event(c);
     if (!a || !b) return fail(GFL_ERUNTIME, "profiling: hipEventCreate failed");
+    gfl::KernelTimer kt{ take_event_cb, c, {} };
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const bool capturing = hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
     GFL_HIP(hipEventRecord(a, st));
+    if (!capturing) gfl::g_kernel_timer = &kt;
     const int r = launch();
+    gfl::g_kernel_timer = nullptr;
     GFL_HIP(hipEventRecord(b, st));
-    c->recs.push_back({ stage, a, b });
+    if (kt.pairs.empty())
+        c->recs.push_back({ stage, a, b });
+    else
+    {
+        for (auto& pr : kt.pairs) c->recs.push_back({ stage, pr.first, pr.second });
+        c->ev_pool.push_back(a);
+        c->ev_pool.push_back(b);
+    }
     return r;
 }
 

@@ -1,9 +1,40 @@
 // Internal declarations shared by the kernel translation units and the C-ABI host layer.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
+#include <utility>
+#include <vector>
 
 namespace gfl {
+
+// Kernel timing of profiled stages. While the host layer profiles a stage it points g_kernel_timer (thread-local) at a
+// timer; the decode launchers then launch through hipExtLaunchKernelGGL with a start and a stop event that the runtime
+// stamps on the kernel's own dispatch, so a stage's time is its kernels' execution without the gaps between packets.
+// Each such launch appends one (start, stop) pair. take() hands out a created event, or nullptr.
+struct KernelTimer
+{
+    hipEvent_t (*take)(void* owner);
+    void* owner;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> pairs;
+};
+extern thread_local KernelTimer* g_kernel_timer;
+
+template <typename K, typename... A>
+inline void timed_launch(K kern, dim3 grid, dim3 block, size_t lds, hipStream_t st, A... args)
+{
+    if (KernelTimer* t = g_kernel_timer)
+    {
+        hipEvent_t e0 = t->take(t->owner), e1 = t->take(t->owner);
+        if (e0 && e1)
+        {
+            hipExtLaunchKernelGGL(kern, grid, block, (std::uint32_t)lds, st, e0, e1, 0, args...);
+            t->pairs.emplace_back(e0, e1);
+            return;
+        }
+    }
+    hipLaunchKernelGGL(kern, grid, block, lds, st, args...);
+}
 
 constexpr int MAX_PICKS = 1024;    // tokens * topk per forward call
 constexpr int MAX_EXPERTS = 1024;  // experts per layer (ft_split's own limit, ft_tier_cu.cu:260)

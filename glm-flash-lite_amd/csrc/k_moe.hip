@@ -1547,7 +1547,7 @@ static void gu_launch(const GuArgs& a, int umax, int nmat, hipStream_t st)
     (void)opened;
     const int ents = a.per_slot ? a.P : umax;
     const int per_ent = (a.I / (16 * GU_NW)) * (MF ? 2 : 1);   // MF: both halves of the tile rows
-    hipLaunchKernelGGL(kern, dim3(ents * per_ent + (GP ? 0 : 1), nmat), dim3(GU_NW * 64), lds, st, a);
+    timed_launch(kern, dim3(ents * per_ent + (GP ? 0 : 1), nmat), dim3(GU_NW * 64), lds, st, a);
 }
 
 template <int K, int NS, bool MF>
@@ -1559,7 +1559,7 @@ static void dn_launch(const DnArgs& a, int umax, int P, hipStream_t st)
     (void)opened;
     const int ents = a.per_slot ? P : umax;
     constexpr int nw = (NS == 1 && !MF) ? DN_NW / 2 : DN_NW;
-    hipLaunchKernelGGL(kern, dim3(ents * (a.H / (16 * nw))), dim3(nw * 64), lds, st, a);
+    timed_launch(kern, dim3(ents * (a.H / (16 * nw))), dim3(nw * 64), lds, st, a);
 }
 
 // Compute units of the current device (cached per device).
@@ -1596,7 +1596,7 @@ static void gu_relay_launch(const GuArgs& a, int nmat, hipStream_t st)
     (void)opened;
     const long nwg = (long)a.P * (a.I / (16 * CW)) * nmat;   // GEMV workgroups (plus the publishing one)
     const size_t lds = balanced_lds(gu_relay_lds<K>(a.H, a.P, a.E), nwg);
-    hipLaunchKernelGGL(kern, dim3(1 + nwg), dim3(GU_NW * 64), lds, st, a);
+    timed_launch(kern, dim3(1 + nwg), dim3(GU_NW * 64), lds, st, a);
 }
 
 template <int K, int RW>
@@ -1608,7 +1608,7 @@ static void dn_relay_launch(const DnArgs& a, int P, hipStream_t st)
     (void)opened;
     const long nwg = (long)P * (a.H / (16 * CW));
     const size_t lds = balanced_lds(dn_relay_lds<K>(a.I), nwg);
-    hipLaunchKernelGGL(kern, dim3(nwg), dim3(GU_NW * 64), lds, st, a);
+    timed_launch(kern, dim3(nwg), dim3(GU_NW * 64), lds, st, a);
 }
 
 // relay width: 1, 2 or 4 waves per tile column
