@@ -541,6 +541,10 @@ struct Gws
     float *ygu, *yd;
     uint16_t* xtd;
     int *act_cnt, *out_cnt;
+    // the EXACT chains' region: inputs fp32 [2][P][H], gate|up outputs fp16 [2][P][I], down inputs fp32 [P][I], down
+    // outputs fp16 [P][H]
+    float *xte, *xde;
+    uint16_t *ygue, *yre;
 };
 
 static int grow(gfl_ctx* c, hipStream_t st, void** buf, size_t* have, size_t need, bool zero, const char* who)
@@ -575,7 +579,9 @@ static int grouped_workspace(gfl_ctx* c, hipStream_t st, int P, int M, int E, in
     const size_t g_xd = align256(2 * (size_t)P * I), g_yr = align256(2 * (size_t)P * H);
     const size_t x_ygu = align256(4 * 2 * (size_t)P * I), x_xtd = align256(2 * (size_t)P * I);
     const size_t x_yd = align256(4 * (size_t)P * H);
-    const size_t data = std::max(g_xt + g_ygu + g_xd + g_yr, x_ygu + x_xtd + x_yd);
+    const size_t c_xt = align256(4 * 2 * (size_t)P * H), c_ygu = align256(2 * 2 * (size_t)P * I);
+    const size_t c_xd = align256(4 * (size_t)P * I), c_yr = align256(2 * (size_t)P * H);
+    const size_t data = std::max({ g_xt + g_ygu + g_xd + g_yr, x_ygu + x_xtd + x_yd, c_xt + c_ygu + c_xd + c_yr });
     if (const int r = grow(c, st, &c->gws, &c->gws_bytes, b_int + b_xpi + b_xpu + data, false, who)) return r;
     const size_t ncnt = (size_t)E * (I / 128) + (size_t)M * (H / 128);
     if (const int r = grow(c, st, &c->xcnt, &c->xcnt_bytes, sizeof(int) * ncnt, true, who)) return r;
@@ -615,27 +621,32 @@ static int grouped_workspace(gfl_ctx* c, hipStream_t st, int P, int M, int E, in
     w.ygu = reinterpret_cast<float*>(d);
     w.xtd = reinterpret_cast<uint16_t*>(d + x_ygu);
     w.yd = reinterpret_cast<float*>(d + x_ygu + x_xtd);
+    w.xte = reinterpret_cast<float*>(d);
+    w.ygue = reinterpret_cast<uint16_t*>(d + c_xt);
+    w.xde = reinterpret_cast<float*>(d + c_xt + c_ygu);
+    w.yre = reinterpret_cast<uint16_t*>(d + c_xt + c_ygu + c_xd);
     w.act_cnt = static_cast<int*>(c->xcnt);
     w.out_cnt = w.act_cnt + (size_t)E * (I / 128);
     return GFL_OK;
 }
 
-// EXACT above MAX_PICKS picks (caller holds c->mu, device set): the grouped plan of the prefill path, then the decode
-// kernels with a workgroup per expert in passes of 4 slots, driven by that plan (bit-identical to the decode path).
+// EXACT above MAX_PICKS picks (caller holds c->mu, device set): the grouped plan of the prefill path, then the
+// reference's accumulator chains with each weight decoded once per pass of up to 64 of an expert's slots
+// (launch_exact_chains, bit-identical to the decode path).
 static int run_forward_grouped_plan(gfl_ctx* c, const Layer& L, const uint16_t* x, const int64_t* sel, const void* w,
                                     int w_is_half, int M, int topk, float* out, float act_limit, hipStream_t st)
 {
     const int P = M * topk;
-    if (gfl::gate_up_lds_bytes(L.K[0], 4, L.H, 0, 0, 0, 0) > gfl::LDS_LIMIT ||
-        gfl::gate_up_lds_bytes(L.K[1], 4, L.H, 0, 0, 0, 0) > gfl::LDS_LIMIT ||
-        gfl::down_lds_bytes(L.K[2], 4, L.I, 0, 0) > gfl::LDS_LIMIT)
-        return fail(GFL_EINVAL, "gfl_moe_forward: shape needs more than 160 KB of LDS per workgroup");
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out)) & 15)
+        return fail(GFL_EINVAL, "gfl_moe_forward: above 1024 picks x and out must be 16-byte aligned");
+    if ((size_t)P * (size_t)std::max(L.H, L.I) * 4 > (size_t)0x7fffffff)
+        return fail(GFL_EINVAL, "gfl_moe_forward: M*topk*max(H, I) must stay below 2^29 above 1024 picks");
     Gws ws;
     if (const int rc = grouped_workspace(c, st, P, M, L.E, L.H, L.I, "gfl_moe_forward", ws)) return rc;
     const int r = staged(c, 1, st, [&] {
-        gfl::launch_grouped_plan(sel, w, w_is_half ? 1 : 0, P, topk, L.E, ws.gp, st);
-        return gfl::launch_exact_grouped(L.K, L.dptrs, P, topk, L.E, M, L.H, L.I, x, ws.gp, ws.pv, ws.ygu, ws.xtd,
-                                         ws.yd, ws.act_cnt, ws.out_cnt, c->silu_tab, act_limit, out, st);
+        return gfl::launch_exact_chains(L.dptrs, sel, w, w_is_half ? 1 : 0, P, topk, L.E, L.H, L.I, L.K[0], L.K[1],
+                                        L.K[2], x, ws.gp, P, ws.xte, ws.ygue, ws.xde, ws.yre, c->silu_tab, act_limit,
+                                        out, st);
     });
     if (r) return r > 0 ? r : fail(GFL_EINVAL, "gfl_moe_forward: unsupported K");
     GFL_HIP(hipGetLastError());

@@ -80,15 +80,10 @@ __device__ inline const uint8_t* uniform_ptr(const uint8_t* p)
     return reinterpret_cast<const uint8_t*>(((uint64_t)hi << 32) | lo);
 }
 
-// four consecutive states -> four fp16 codebook weights, packed {w0,w1}, {w2,w3}
-template <int K>
-__device__ inline half4 decode4(uint32_t hi, uint32_t lo, uint32_t sh)
+// four 16-bit states -> their four fp16 codebook weights
+__device__ inline half4 codebook4(uint32_t st0, uint32_t st1, uint32_t st2, uint32_t st3)
 {
-    const uint32_t R = __builtin_amdgcn_alignbit(hi, lo, sh);
-    const uint32_t p0 = __builtin_amdgcn_ubfe(R, 3 * K, 16) * MUL1;
-    const uint32_t p1 = __builtin_amdgcn_ubfe(R, 2 * K, 16) * MUL1;
-    const uint32_t p2 = __builtin_amdgcn_ubfe(R, K, 16) * MUL1;
-    const uint32_t p3 = __builtin_amdgcn_ubfe(R, 0, 16) * MUL1;
+    const uint32_t p0 = st0 * MUL1, p1 = st1 * MUL1, p2 = st2 * MUL1, p3 = st3 * MUL1;
     // sum of the product bytes on top of 0x6400 = fp16 bits of (1024 + sum); the hi variant lands in bits 16..31
     uint32_t s01 = __builtin_amdgcn_sad_u8(p0, 0u, 0x64006400u);
     uint32_t s23 = __builtin_amdgcn_sad_u8(p2, 0u, 0x64006400u);
@@ -107,6 +102,15 @@ __device__ inline half4 decode4(uint32_t hi, uint32_t lo, uint32_t sh)
     const half2v w23 = __builtin_elementwise_fma(b, kinv2, kbias2);
     half4 r = { w01[0], w01[1], w23[0], w23[1] };
     return r;
+}
+
+// four consecutive states -> four fp16 codebook weights, packed {w0,w1}, {w2,w3}
+template <int K>
+__device__ inline half4 decode4(uint32_t hi, uint32_t lo, uint32_t sh)
+{
+    const uint32_t R = __builtin_amdgcn_alignbit(hi, lo, sh);
+    return codebook4(__builtin_amdgcn_ubfe(R, 3 * K, 16), __builtin_amdgcn_ubfe(R, 2 * K, 16),
+                     __builtin_amdgcn_ubfe(R, K, 16), __builtin_amdgcn_ubfe(R, 0, 16));
 }
 
 // fp32 -> fp16 (round to nearest even, subnormals kept) as an opaque conversion. The reference rounds every product

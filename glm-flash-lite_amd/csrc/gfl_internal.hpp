@@ -106,6 +106,15 @@ int launch_grouped(const uint64_t* ptrs, const int64_t* sel, const void* w, int 
                    uint16_t* ygu, uint16_t* xd, uint16_t* yraw, const float* silu_tab, float act_limit, float* out,
                    hipStream_t st);
 size_t grouped_gemm_lds_bytes(int K);
+// EXACT layer forward at prefill sizes (k_prefill.hip), bit-identical to the decode path: the grouped plan, the
+// input transforms as fp32 in the accumulator-chain layout, the reference's accumulator chains with each weight
+// decoded once per pass of up to 64 of an expert's slots, SwiGLU, the combine in job order. xt [2][cap][H] fp32,
+// ygu [2][cap][I] fp16, xd [cap][I] fp32, yraw [cap][H] fp16 workspace, cap >= P, cap * max(H, I) * 4 < 2^31
+// (else -1, nothing launched).
+int launch_exact_chains(const uint64_t* ptrs, const int64_t* sel, const void* w, int w_half, int P, int topk, int E,
+                        int H, int I, int Kg, int Ku, int Kd, const uint16_t* x, const GPlan& g, int cap, float* xt,
+                        uint16_t* ygu, float* xd, uint16_t* yraw, const float* silu_tab, float act_limit, float* out,
+                        hipStream_t st);
 // The grouped plan alone (first three launches of launch_grouped): slots, offsets, job order per token.
 void launch_grouped_plan(const int64_t* sel, const void* w, int w_half, int P, int topk, int E, const GPlan& g,
                          hipStream_t st);

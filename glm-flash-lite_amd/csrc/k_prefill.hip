@@ -246,11 +246,28 @@ constexpr int GP_TW = 4;   // waves per transform workgroup
 constexpr int GP_TU = 2;   // rounds of 4 blocks per chunk of the input transform (two chunks' loads in flight)
 constexpr int GP_TA = 3;   // rounds of 4 blocks per SwiGLU-transform wave (one wave covers I = 1536)
 
-// prep_block (ft_core.h:97-102) of the gate and up inputs of slot s (one wave per slot)
+// Elements 8li..8li+7 of 128-block b (one lane of a 16-lane row), rounded to fp16, into the accumulator-chain input
+// layout: fp32, position tk * 16 + 4j + q holds row 2q + {0, 1, 8, 9}[j] of tile row tk (the rows chain j of every
+// output column reads in tile row tk, in its order)
+__device__ __forceinline__ void xg_store_row(float* dst, int b, int li, const float (&v)[8])
+{
+    float r[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) r[k] = h2f_bits((uint16_t)f2h_bits(v[k]));
+    float* d = dst + (size_t)b * 128 + (li >> 1) * 16 + 8 * (li & 1);
+    *reinterpret_cast<float4*>(d) = float4{ r[0], r[2], r[4], r[6] };
+    *reinterpret_cast<float4*>(d + 4) = float4{ r[1], r[3], r[5], r[7] };
+}
+
+// prep_block (ft_core.h:97-102) of the gate and up inputs of slot s (one wave per slot). XL: fp32 in the
+// accumulator-chain layout (xg_store_row), else fp16 in the MFMA layout (gp_store_row).
+template <bool XL>
 __global__ __launch_bounds__(GP_TW * 64) void gp_prep_kernel(const uint64_t* __restrict__ ptrs,
                                                              const uint16_t* __restrict__ x, int H, int topk, int cap,
-                                                             GPlan g, uint16_t* __restrict__ xt)
+                                                             GPlan g, void* __restrict__ xt_out)
 {
+    uint16_t* xt = static_cast<uint16_t*>(xt_out);
+    float* xtf = static_cast<float*>(xt_out);
     const int lane = threadIdx.x & 63, rl = lane >> 4, li = lane & 15;
     const int s = blockIdx.x * GP_TW + (threadIdx.x >> 6);
     if (s >= g.hdr[0]) return;
@@ -261,6 +278,8 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_prep_kernel(const uint64_t* __r
     const uint16_t* xr = x + (size_t)tok * H;
     uint16_t* d0 = xt + (size_t)s * H;
     uint16_t* d1 = xt + ((size_t)cap + s) * H;
+    float* f0 = xtf + (size_t)s * H;
+    float* f1 = xtf + ((size_t)cap + s) * H;
     constexpr int CH = 4 * GP_TU;   // blocks per chunk
     uint4 xv[2][GP_TU], g0[2][GP_TU], g1[2][GP_TU];
     auto load = [&](int buf, int c0) {
@@ -278,13 +297,27 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_prep_kernel(const uint64_t* __r
         for (int k = 0; k < GP_TU; ++k)
         {
             const int b = c0 + 4 * k + rl;
-            uint32_t u[4], v[4];
-            prep_block_row_h(u, xv[buf][k], g0[buf][k]);
-            prep_block_row_h(v, xv[buf][k], g1[buf][k]);
-            if (b < nblk)
+            if constexpr (XL)
             {
-                gp_store_row(d0, b, li, u);
-                gp_store_row(d1, b, li, v);
+                float u[8], v[8];
+                prep_block_row_p(u, xv[buf][k], g0[buf][k]);
+                prep_block_row_p(v, xv[buf][k], g1[buf][k]);
+                if (b < nblk)
+                {
+                    xg_store_row(f0, b, li, u);
+                    xg_store_row(f1, b, li, v);
+                }
+            }
+            else
+            {
+                uint32_t u[4], v[4];
+                prep_block_row_h(u, xv[buf][k], g0[buf][k]);
+                prep_block_row_h(v, xv[buf][k], g1[buf][k]);
+                if (b < nblk)
+                {
+                    gp_store_row(d0, b, li, u);
+                    gp_store_row(d1, b, li, v);
+                }
             }
         }
     };
@@ -301,10 +334,12 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_prep_kernel(const uint64_t* __r
 
 // fwd_phase phase 1 (ft_core.h:974-991), one wave per (slot, 4 * GP_TA blocks of I): per 128-block, out_block of
 // gate and up, r16(act_mul), down prep_block, stored in the GEMM input layout
+template <bool XL>
 __global__ __launch_bounds__(GP_TW * 64) void gp_act_kernel(const uint64_t* __restrict__ ptrs, int I, int cap, GPlan g,
                                                             const uint16_t* __restrict__ ygu, const float* silu_tab,
-                                                            float act_limit, uint16_t* __restrict__ xd)
+                                                            float act_limit, void* __restrict__ xd_out)
 {
+    uint16_t* xd = static_cast<uint16_t*>(xd_out);
     const int lane = threadIdx.x & 63, rl = lane >> 4, li = lane & 15;
     const int nbi = I / 128, nch = (nbi + 4 * GP_TA - 1) / (4 * GP_TA);
     const int item = blockIdx.x * GP_TW + (threadIdx.x >> 6);
@@ -317,6 +352,7 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_act_kernel(const uint64_t* __re
     const uint16_t* yg = ygu + (size_t)s * I;
     const uint16_t* yu = ygu + ((size_t)cap + s) * I;
     uint16_t* dst = xd + (size_t)s * I;
+    float* dstf = static_cast<float*>(xd_out) + (size_t)s * I;
     // GP_TA rounds of 4 blocks in three phases kept apart by scheduling barriers (left to itself the compiler sinks
     // each round's loads next to their use): all loads; the output transforms and every silu lookup; the
     // activation, input transform and stores
@@ -352,9 +388,17 @@ __global__ __launch_bounds__(GP_TW * 64) void gp_act_kernel(const uint64_t* __re
             float av[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) av[j] = r16(act_mul_s(ev[k][j], uv[k][j], act_limit));
-            uint32_t ah[4];
-            prep_block_row_fh(ah, av, sd[k]);
-            if (b < nbi) gp_store_row(dst, b, li, ah);
+            if constexpr (XL)
+            {
+                prep_block_row_fp(av, sd[k]);
+                if (b < nbi) xg_store_row(dstf, b, li, av);
+            }
+            else
+            {
+                uint32_t ah[4];
+                prep_block_row_fh(ah, av, sd[k]);
+                if (b < nbi) gp_store_row(dst, b, li, ah);
+            }
         }
     }
 }
@@ -618,6 +662,213 @@ __global__ __launch_bounds__(GP_NW * 64) void gp_gemm_kernel(GemmArgs a)
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// EXACT at prefill sizes: the reference's accumulator chains, each weight decoded once per pass of up to 64 slots
+// ---------------------------------------------------------------------------------------------------------------
+//
+// The reference's EXACT sum (tile_accum<M,EXACT>, ft_core.h:313-345) gives every output column n four fp32
+// accumulators; accumulator j takes, in each tile row tk, the products of rows 2q + {0, 1, 8, 9}[j] for q = 0..3, in
+// that order, tile rows ascending, and the four are reduced (a0 + a1) + (a2 + a3) (gemv_block, ft_core.h:377-386).
+// Here wave j of a workgroup runs chain j for 64 output columns (lane = column) and for every slot of the pass (one
+// accumulator per slot), so:
+//   - a lane decodes exactly the four weights its chain needs from each tile (stream indices 32 (n % 8) + 4 (n / 8)
+//     + j + 8q of the tile's stream, a3/PERM), and each decoded weight serves all the pass's slots;
+//   - the inputs a chain multiplies them with are the same in every lane: x[slot][tk * 16 + 2q + off_j] for q = 0..3
+//     (the input layout of xg_store_row). Lane k of each 16-lane row reads slot k's four with one ds_read_b128, and
+//     v_fmac_f32_dpp broadcasts them across the row (xg_fma16): one LDS read per 64 FMAs of a wave.
+// Every accumulator is one chain of fused multiply-adds in the reference's order, so the results are bit-identical to
+// the decode path's, while the decode is amortised over the pass (it is about a tenth of the work; the fp32 FMAs are
+// the rest).
+
+constexpr int XG_COLS = 64;                 // output columns per workgroup (lane = column)
+constexpr int XG_TC = XG_COLS / 16;         // tile columns per workgroup
+constexpr int XG_MS = 64;                   // slots per pass
+constexpr int XG_NG = 2;                    // ring depth (groups of 8 tile rows)
+constexpr int XG_XROW = 8 * 16 * 4;         // input bytes of one slot per group: 8 tile rows x 16 rows x fp32
+constexpr int XG_XGB = XG_MS * XG_XROW;     // input bytes per group (32 KB)
+
+struct XgArgs
+{
+    const uint64_t* ptrs;
+    int mat_base, nmat;        // first matrix of the launch (0 gate, 1 up, 2 down) and how many
+    int kdim, ndim, cap, E;
+    GPlan g;
+    const float* xin;          // [mats][cap][kdim] fp32 (fp16-valued), accumulator-chain layout
+    uint16_t* yout;            // [mats][cap][ndim] fp16: out_block's leading r16 (ft_core.h:109) applied here
+};
+
+// The 16-bit state of stream index t of a tile: the window of bits ending at (t + 1) K of the circular 256K-bit
+// stream (state_scalar, ft_core.h:65-73), as a funnel shift of two words (byte offsets o0, o1 in the tile) by sh.
+struct StateDec
+{
+    uint32_t o0, o1, sh;
+};
+__device__ __forceinline__ StateDec state_dec(int t, int K)
+{
+    const int e = (t + 1) * K, words = 8 * K;
+    const int wa = e >= 33 ? (e - 33) / 32 : -1;   // e - 32 wa in [33, 64]
+    StateDec d;
+    d.sh = (uint32_t)(64 - (e - 32 * wa));
+    d.o0 = (uint32_t)(4 * ((wa + words) % words));
+    d.o1 = (uint32_t)(4 * ((wa + 1 + words) % words));
+    return d;
+}
+
+// acc[k] = fma(w_q, x_q of lane k of the row, acc[k]) for k = 0..15 and q = 0..3 (q outer, so 16 independent FMAs
+// lie between dependent ones): lane k of every 16-lane row holds slot k's four inputs, and v_fmac_f32_dpp with
+// row_newbcast:k hands them to the whole row. One asm block, so nothing the compiler schedules can write a DPP source
+// between the leading s_nop (the VALU-write -> DPP-read hazard) and the reads.
+#define XG_F(K, XQ, WQ) "v_fmac_f32_dpp %" #K ", %" XQ ", %" WQ " row_newbcast:" #K " row_mask:0xf bank_mask:0xf\n\t"
+#define XG_Q(XQ, WQ)                                                                                                   \
+    XG_F(0, XQ, WQ) XG_F(1, XQ, WQ) XG_F(2, XQ, WQ) XG_F(3, XQ, WQ) XG_F(4, XQ, WQ) XG_F(5, XQ, WQ) XG_F(6, XQ, WQ)    \
+    XG_F(7, XQ, WQ) XG_F(8, XQ, WQ) XG_F(9, XQ, WQ) XG_F(10, XQ, WQ) XG_F(11, XQ, WQ) XG_F(12, XQ, WQ)                \
+    XG_F(13, XQ, WQ) XG_F(14, XQ, WQ) XG_F(15, XQ, WQ)
+
+__device__ __forceinline__ void xg_fma16(float* acc, const float4& x, float w0, float w1, float w2, float w3)
+{
+    asm("s_nop 1\n\t" XG_Q("16", "20") XG_Q("17", "21") XG_Q("18", "22") XG_Q("19", "23")
+        : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]), "+v"(acc[4]), "+v"(acc[5]), "+v"(acc[6]),
+          "+v"(acc[7]), "+v"(acc[8]), "+v"(acc[9]), "+v"(acc[10]), "+v"(acc[11]), "+v"(acc[12]), "+v"(acc[13]),
+          "+v"(acc[14]), "+v"(acc[15])
+        : "v"(x.x), "v"(x.y), "v"(x.z), "v"(x.w), "v"(w0), "v"(w1), "v"(w2), "v"(w3));
+}
+#undef XG_Q
+#undef XG_F
+
+// Grid: 8 * ceil(E / 8) * (ndim / 64) * matrices, XCD-major as the MFMA GEMM. Workgroup = 4 waves (the 4 chains) x
+// 64 columns of one matrix of one expert; the expert's slots go through in passes of XG_MS. Per group of 8 tile rows
+// the trellis of the 4 tile columns and the pass's inputs arrive by LDS-direct loads one group ahead (one workgroup
+// barrier per group); at the end of a pass the 4 chains meet in LDS and are reduced per output.
+template <int K>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void xg_gemm_kernel(XgArgs a)
+{
+    constexpr int TB = 32 * K, RB = XG_TC * TB, GB = 8 * RB, NG = XG_NG;
+    constexpr int NLD = GB / 256 / 4;          // trellis dword loads per lane per group (the 4 waves share a group)
+    static_assert(GB % 1024 == 0, "a group of tiles splits into whole loads of the 4 waves");
+    extern __shared__ __align__(16) uint8_t xg_lds[];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int nch = a.ndim / XG_COLS, per = nch * a.nmat;
+    const int xcd = blockIdx.x % 8, jb = blockIdx.x / 8;
+    const int ei = (jb / per) * 8 + xcd, rr0 = jb % per;
+    if (ei >= a.E) return;
+    const int e = a.g.eord[ei];
+    const int nc = rr0 % nch;
+    const int mat = a.mat_base + rr0 / nch;
+    const int s_begin = a.g.off[e], s_end = a.g.off[e + 1];
+    if (s_begin >= s_end) return;
+    const int TN = a.ndim / 16, TK = a.kdim / 16, ngroups = TK / 8;
+    uint8_t* tring = xg_lds;                                   // [NG][8 tile rows][XG_TC tile columns][TB]
+    uint8_t* xring = xg_lds + NG * GB;                         // [NG][XG_MS slots][8 tile rows][4 chains][4] fp32
+    const uint8_t* tr = reinterpret_cast<const uint8_t*>(a.ptrs[(size_t)e * 9 + mat]);
+    const int gs = TN * TB;                                    // bytes per tile row of the matrix
+    uint8_t* cb = const_cast<uint8_t*>(uniform_ptr(tr + (size_t)nc * XG_TC * TB));
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(cb, (short)0, (int)((size_t)TK * gs),
+                                                                        0x00020000);
+    int voff[NLD];
+#pragma unroll
+    for (int i = 0; i < NLD; ++i)
+    {
+        const int byte = (wave * NLD + i) * 256 + lane * 4;   // within the group's [8][XG_TC][TB] block
+        voff[i] = (byte / RB) * gs + (byte % RB);
+    }
+    const float* xin = a.xin + (size_t)(mat - a.mat_base) * a.cap * a.kdim;
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(uniform_ptr(reinterpret_cast<const uint8_t*>(xin))), (short)0,
+        (int)((size_t)a.cap * a.kdim * 4), 0x00020000);
+    uint16_t* yout = a.yout + (size_t)(mat - a.mat_base) * a.cap * a.ndim;
+    // this lane's column and the stream windows of its chain's four weights in each tile
+    const int j = wave, tcl = lane >> 4, n = lane & 15;
+    StateDec sd[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) sd[q] = state_dec(32 * (n & 7) + 4 * (n >> 3) + j + 8 * q, K);
+    const int col0 = nc * XG_COLS;
+
+    for (int c0 = s_begin; c0 < s_end; c0 += XG_MS)
+    {
+        const int T = min(XG_MS, s_end - c0);
+        auto issue = [&](int g, int nsl) {
+            uint8_t* dst = tring + (g % NG) * GB;
+#pragma unroll
+            for (int i = 0; i < NLD; ++i)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (gp_lds_void*)(dst + (wave * NLD + i) * 256), 4, voff[i],
+                                                         g * 8 * gs, 0, 0);
+            // this wave's 16 slot rows of the group (rows of slots past the pass repeat its last slot)
+            uint8_t* xd = xring + (g % NG) * XG_XGB;
+            if (wave * 16 < nsl)
+            {
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                {
+                    const int sl = wave * 16 + r;
+                    const int srow = (c0 + min(sl, T - 1)) * a.kdim * 4 + g * XG_XROW;
+#pragma unroll
+                    for (int h = 0; h < XG_XROW / 256; ++h)
+                        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (gp_lds_void*)(xd + sl * XG_XROW + h * 256), 4,
+                                                                 h * 256 + lane * 4, srow, 0, 0);
+                }
+            }
+        };
+        auto pass = [&](auto nsl_c) {
+            constexpr int NSL = decltype(nsl_c)::value;
+            float acc[NSL];
+#pragma unroll
+            for (int s = 0; s < NSL; ++s) acc[s] = 0.f;
+            __syncthreads();   // the previous pass is done with the rings
+            issue(0, NSL);
+            for (int g = 0; g < ngroups; ++g)
+            {
+                gp_wait_vmcnt<0>();
+                gp_barrier();   // group g landed for every wave; every wave is done with group g - 1
+                if (g + 1 < ngroups) issue(g + 1, NSL);
+                const uint8_t* tl = tring + (g % NG) * GB + tcl * TB;
+                const uint8_t* xl = xring + (g % NG) * XG_XGB + j * 16;
+#pragma unroll
+                for (int t8 = 0; t8 < 8; ++t8)
+                {
+                    const uint8_t* tp = tl + t8 * RB;
+                    uint32_t st[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                    {
+                        const uint32_t hi = *reinterpret_cast<const uint32_t*>(tp + sd[q].o0);
+                        const uint32_t lo = *reinterpret_cast<const uint32_t*>(tp + sd[q].o1);
+                        st[q] = __builtin_amdgcn_alignbit(hi, lo, sd[q].sh) & 0xFFFFu;
+                    }
+                    const half4 wh = codebook4(st[0], st[1], st[2], st[3]);
+                    const float w0 = (float)wh[0], w1 = (float)wh[1], w2 = (float)wh[2], w3 = (float)wh[3];
+#pragma unroll
+                    for (int b16 = 0; b16 < NSL / 16; ++b16)
+                    {
+                        const float4 xv =
+                            *reinterpret_cast<const float4*>(xl + (b16 * 16 + n) * XG_XROW + t8 * 64);
+                        xg_fma16(acc + b16 * 16, xv, w0, w1, w2, w3);
+                    }
+                }
+            }
+            // the 4 chains of every output meet in LDS (the input ring, free once every wave is past the last group)
+            __syncthreads();
+            float* red = reinterpret_cast<float*>(xring);   // [4 chains][NSL slots][64 columns]
+#pragma unroll
+            for (int s = 0; s < NSL; ++s) red[(j * NSL + s) * XG_COLS + lane] = acc[s];
+            __syncthreads();
+            const int colw = threadIdx.x & 63;
+            for (int s = threadIdx.x >> 6; s < T; s += 4)
+            {
+                const float r0 = red[(0 * NSL + s) * XG_COLS + colw], r1 = red[(1 * NSL + s) * XG_COLS + colw];
+                const float r2 = red[(2 * NSL + s) * XG_COLS + colw], r3 = red[(3 * NSL + s) * XG_COLS + colw];
+                yout[(size_t)(c0 + s) * a.ndim + col0 + colw] = (uint16_t)f2h_bits((r0 + r1) + (r2 + r3));
+            }
+        };
+        switch ((T + 15) / 16)
+        {
+            case 1: pass(std::integral_constant<int, 16>{}); break;
+            case 2: pass(std::integral_constant<int, 32>{}); break;
+            case 3: pass(std::integral_constant<int, 48>{}); break;
+            default: pass(std::integral_constant<int, 64>{}); break;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------------------------------------------
 
@@ -654,6 +905,38 @@ static int gp_gemm(int K, const GemmArgs& a, int nmat, hipStream_t st)
     }
 }
 
+template <int K>
+static size_t xg_gemm_lds()
+{
+    return (size_t)XG_NG * 8 * XG_TC * 32 * K + (size_t)XG_NG * XG_XGB;
+}
+
+template <int K>
+static int xg_gemm_launch(const XgArgs& a, int nmat, hipStream_t st)
+{
+    const size_t lds = xg_gemm_lds<K>();
+    static const bool opened = hipFuncSetAttribute(reinterpret_cast<const void*>(xg_gemm_kernel<K>),
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess;
+    if (!opened) return -1;
+    XgArgs b = a;
+    b.nmat = nmat;
+    const unsigned grid = (unsigned)(((a.E + 7) / 8) * 8 * (a.ndim / XG_COLS) * nmat);
+    hipLaunchKernelGGL(xg_gemm_kernel<K>, dim3(grid), dim3(256), lds, st, b);
+    return 0;
+}
+
+static int xg_gemm(int K, const XgArgs& a, int nmat, hipStream_t st)
+{
+    switch (K)
+    {
+        case 2: return xg_gemm_launch<2>(a, nmat, st);
+        case 3: return xg_gemm_launch<3>(a, nmat, st);
+        case 4: return xg_gemm_launch<4>(a, nmat, st);
+        case 5: return xg_gemm_launch<5>(a, nmat, st);
+        default: return -1;
+    }
+}
+
 void launch_grouped_plan(const int64_t* sel, const void* w, int w_half, int P, int topk, int E, const GPlan& g,
                          hipStream_t st)
 {
@@ -673,7 +956,8 @@ int launch_grouped(const uint64_t* ptrs, const int64_t* sel, const void* w, int 
     const int M = P / topk;
     launch_grouped_plan(sel, w, w_half, P, topk, E, g, st);
     const unsigned slot_wgs = (unsigned)((P + GP_TW - 1) / GP_TW);
-    hipLaunchKernelGGL(gp_prep_kernel, dim3(slot_wgs), dim3(GP_TW * 64), 0, st, ptrs, x, H, topk, cap, g, xt);
+    hipLaunchKernelGGL(gp_prep_kernel<false>, dim3(slot_wgs), dim3(GP_TW * 64), 0, st, ptrs, x, H, topk, cap, g,
+                       static_cast<void*>(xt));
     GemmArgs a;
     a.ptrs = ptrs; a.kdim = H; a.ndim = I; a.cap = cap; a.E = E; a.g = g; a.xin = xt; a.yout = ygu;
     if (Kg == Ku)
@@ -692,11 +976,54 @@ int launch_grouped(const uint64_t* ptrs, const int64_t* sel, const void* w, int 
         if (gp_gemm(Ku, b, 1, st)) return -1;
     }
     const long act_items = (long)P * ((I / 128 + 4 * GP_TA - 1) / (4 * GP_TA));
-    hipLaunchKernelGGL(gp_act_kernel, dim3((unsigned)((act_items + GP_TW - 1) / GP_TW)), dim3(GP_TW * 64), 0, st, ptrs,
-                       I, cap, g, ygu, silu_tab, act_limit, xd);
+    hipLaunchKernelGGL(gp_act_kernel<false>, dim3((unsigned)((act_items + GP_TW - 1) / GP_TW)), dim3(GP_TW * 64), 0,
+                       st, ptrs, I, cap, g, ygu, silu_tab, act_limit, static_cast<void*>(xd));
     GemmArgs c = a;
     c.mat_base = 2; c.kdim = I; c.ndim = H; c.xin = xd; c.yout = yraw;
     if (gp_gemm(Kd, c, 1, st)) return -1;
+    {
+        const long items = (long)M * ((H / 128 + 3) / 4);
+        hipLaunchKernelGGL(gp_comb_kernel, dim3((unsigned)((items + GP_TW - 1) / GP_TW)), dim3(GP_TW * 64), 0, st, ptrs,
+                           H, M, topk, g, yraw, out);
+    }
+    return 0;
+}
+
+int launch_exact_chains(const uint64_t* ptrs, const int64_t* sel, const void* w, int w_half, int P, int topk, int E,
+                        int H, int I, int Kg, int Ku, int Kd, const uint16_t* x, const GPlan& g, int cap, float* xt,
+                        uint16_t* ygu, float* xd, uint16_t* yraw, const float* silu_tab, float act_limit, float* out,
+                        hipStream_t st)
+{
+    // the chain GEMM addresses its fp32 inputs with 32-bit byte offsets
+    if ((size_t)cap * (size_t)(H > I ? H : I) * 4 > (size_t)0x7fffffff) return -1;
+    const int M = P / topk;
+    launch_grouped_plan(sel, w, w_half, P, topk, E, g, st);
+    const unsigned slot_wgs = (unsigned)((P + GP_TW - 1) / GP_TW);
+    hipLaunchKernelGGL(gp_prep_kernel<true>, dim3(slot_wgs), dim3(GP_TW * 64), 0, st, ptrs, x, H, topk, cap, g,
+                       static_cast<void*>(xt));
+    XgArgs a;
+    a.ptrs = ptrs; a.kdim = H; a.ndim = I; a.cap = cap; a.E = E; a.g = g; a.xin = xt; a.yout = ygu;
+    if (Kg == Ku)
+    {
+        a.mat_base = 0;
+        if (xg_gemm(Kg, a, 2, st)) return -1;
+    }
+    else
+    {
+        a.mat_base = 0;
+        if (xg_gemm(Kg, a, 1, st)) return -1;
+        XgArgs b = a;
+        b.mat_base = 1;
+        b.xin = xt + (size_t)cap * H;
+        b.yout = ygu + (size_t)cap * I;
+        if (xg_gemm(Ku, b, 1, st)) return -1;
+    }
+    const long act_items = (long)P * ((I / 128 + 4 * GP_TA - 1) / (4 * GP_TA));
+    hipLaunchKernelGGL(gp_act_kernel<true>, dim3((unsigned)((act_items + GP_TW - 1) / GP_TW)), dim3(GP_TW * 64), 0,
+                       st, ptrs, I, cap, g, ygu, silu_tab, act_limit, static_cast<void*>(xd));
+    XgArgs c = a;
+    c.mat_base = 2; c.kdim = I; c.ndim = H; c.xin = xd; c.yout = yraw;
+    if (xg_gemm(Kd, c, 1, st)) return -1;
     {
         const long items = (long)M * ((H / 128 + 3) / 4);
         hipLaunchKernelGGL(gp_comb_kernel, dim3((unsigned)((items + GP_TW - 1) / GP_TW)), dim3(GP_TW * 64), 0, st, ptrs,
