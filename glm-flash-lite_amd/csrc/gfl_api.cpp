@@ -71,9 +71,6 @@ struct gfl_ctx
     // workspace of the prefill path (gfl_grouped_forward / gfl_grouped_reserve), grown on demand outside captures
     void* gws = nullptr;
     size_t gws_bytes = 0;
-    // last-one counters of the EXACT path above 1024 picks (zero between calls), grown with the prefill workspace
-    void* xcnt = nullptr;
-    size_t xcnt_bytes = 0;
     // superseded workspaces: a graph captured before a workspace grew still holds their addresses, so they stay
     // allocated until gfl_ctx_destroy
     std::vector<void*> retired;
@@ -452,7 +449,6 @@ int gfl_ctx_destroy(gfl_ctx* c)
         if (L.dptrs) hipFree(L.dptrs);
     if (c->ws) hipFree(c->ws);
     if (c->gws) hipFree(c->gws);
-    if (c->xcnt) hipFree(c->xcnt);
     for (void* p : c->retired) hipFree(p);
     if (c->silu_tab) hipFree(c->silu_tab);
     delete c;
@@ -529,20 +525,12 @@ int gfl_moe_forward_noalloc(gfl_ctx* c, int li, const uint16_t* x, const int64_t
 }
 
 // The prefill workspace of a context, grown on demand (never inside a graph capture). Layout: the grouped plan's ints,
-// the EXACT path's PlanView arrays (hdr, uexp, uoff, uptr), then one data region for whichever path runs: the MFMA
-// grouped path's xt [2][P][H], ygu [2][P][I], xd [P][I], yraw [P][H] (fp16), or the EXACT path's ygu [2][P][I] fp32,
-// xtd [P][I] fp16, yd [P][H] fp32. The EXACT path's last-one counters ([E][I/128] + [M][H/128]) live in a buffer of
-// their own, zeroed when allocated (the kernels leave them at zero; the data region is overwritten by both paths).
+// then one data region for whichever path runs: the MFMA grouped path's xt [2][P][H], ygu [2][P][I], xd [P][I],
+// yraw [P][H] (fp16), or the EXACT chains' xte [2][P][H] fp32, ygue [2][P][I] fp16, xde [P][I] fp32, yre [P][H] fp16.
 struct Gws
 {
     gfl::GPlan gp;
-    gfl::PlanView pv;
     uint16_t *xt, *ygu16, *xd, *yraw;
-    float *ygu, *yd;
-    uint16_t* xtd;
-    int *act_cnt, *out_cnt;
-    // the EXACT chains' region: inputs fp32 [2][P][H], gate|up outputs fp16 [2][P][I], down inputs fp32 [P][I], down
-    // outputs fp16 [P][H]
     float *xte, *xde;
     uint16_t *ygue, *yre;
 };
@@ -574,17 +562,12 @@ static int grouped_workspace(gfl_ctx* c, hipStream_t st, int P, int M, int E, in
     const size_t nch = (P + gfl::GP_PLAN_CHUNK - 1) / gfl::GP_PLAN_CHUNK;
     const size_t n_int = 4 + (size_t)E + (E + 1) + 7 * (size_t)P + (size_t)M + (size_t)P + (size_t)E + nch * (E + 1);
     const size_t b_int = align256(sizeof(int) * n_int);
-    const size_t b_xpi = align256(sizeof(int) * (4 + (size_t)E + E + 1)), b_xpu = align256(sizeof(uint64_t) * 2 * E);
     const size_t g_xt = align256(2 * 2 * (size_t)P * H), g_ygu = align256(2 * 2 * (size_t)P * I);
     const size_t g_xd = align256(2 * (size_t)P * I), g_yr = align256(2 * (size_t)P * H);
-    const size_t x_ygu = align256(4 * 2 * (size_t)P * I), x_xtd = align256(2 * (size_t)P * I);
-    const size_t x_yd = align256(4 * (size_t)P * H);
     const size_t c_xt = align256(4 * 2 * (size_t)P * H), c_ygu = align256(2 * 2 * (size_t)P * I);
     const size_t c_xd = align256(4 * (size_t)P * I), c_yr = align256(2 * (size_t)P * H);
-    const size_t data = std::max({ g_xt + g_ygu + g_xd + g_yr, x_ygu + x_xtd + x_yd, c_xt + c_ygu + c_xd + c_yr });
-    if (const int r = grow(c, st, &c->gws, &c->gws_bytes, b_int + b_xpi + b_xpu + data, false, who)) return r;
-    const size_t ncnt = (size_t)E * (I / 128) + (size_t)M * (H / 128);
-    if (const int r = grow(c, st, &c->xcnt, &c->xcnt_bytes, sizeof(int) * ncnt, true, who)) return r;
+    const size_t data = std::max(g_xt + g_ygu + g_xd + g_yr, c_xt + c_ygu + c_xd + c_yr);
+    if (const int r = grow(c, st, &c->gws, &c->gws_bytes, b_int + data, false, who)) return r;
     char* b = static_cast<char*>(c->gws);
     int* ip = reinterpret_cast<int*>(b);
     gfl::GPlan& gp = w.gp;
@@ -601,32 +584,15 @@ static int grouped_workspace(gfl_ctx* c, hipStream_t st, int P, int M, int E, in
     gp.tok_npk = reinterpret_cast<int*>(gp.tok_w + P);
     gp.eord = gp.tok_npk + M;
     gp.ccnt = gp.eord + E;
-    gfl::PlanView& pv = w.pv;
-    int* xp = reinterpret_cast<int*>(b + b_int);
-    pv.hdr = xp;
-    pv.uexp = xp + 4;
-    pv.uoff = pv.uexp + E;
-    pv.uptr = reinterpret_cast<uint64_t*>(b + b_int + b_xpi);
-    pv.slot_pick = gp.slot_pick;
-    pv.tok_slot = gp.tok_slot;
-    pv.tok_w = gp.tok_w;
-    pv.tok_npk = gp.tok_npk;
-    pv.slot_u = pv.pick_slot = pv.pick_job = nullptr;   // not read by the launches that take this plan
-    pv.cap_slots = P;
-    char* d = b + b_int + b_xpi + b_xpu;
+    char* d = b + b_int;
     w.xt = reinterpret_cast<uint16_t*>(d);
     w.ygu16 = reinterpret_cast<uint16_t*>(d + g_xt);
     w.xd = reinterpret_cast<uint16_t*>(d + g_xt + g_ygu);
     w.yraw = reinterpret_cast<uint16_t*>(d + g_xt + g_ygu + g_xd);
-    w.ygu = reinterpret_cast<float*>(d);
-    w.xtd = reinterpret_cast<uint16_t*>(d + x_ygu);
-    w.yd = reinterpret_cast<float*>(d + x_ygu + x_xtd);
     w.xte = reinterpret_cast<float*>(d);
     w.ygue = reinterpret_cast<uint16_t*>(d + c_xt);
     w.xde = reinterpret_cast<float*>(d + c_xt + c_ygu);
     w.yre = reinterpret_cast<uint16_t*>(d + c_xt + c_ygu + c_xd);
-    w.act_cnt = static_cast<int*>(c->xcnt);
-    w.out_cnt = w.act_cnt + (size_t)E * (I / 128);
     return GFL_OK;
 }
 

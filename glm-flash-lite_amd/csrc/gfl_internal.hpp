@@ -119,16 +119,6 @@ int launch_exact_chains(const uint64_t* ptrs, const int64_t* sel, const void* w,
 void launch_grouped_plan(const int64_t* sel, const void* w, int w_half, int P, int topk, int E, const GPlan& g,
                          hipStream_t st);
 
-// EXACT decode launches driven by the grouped plan g (launch_grouped_plan, already run on st) for any number of picks
-// up to MAX_GROUPED_PICKS: PlanView pv (hdr, uexp, uoff, uptr in workspace; slot_pick, tok_slot, tok_w, tok_npk
-// pointing at g's arrays; cap_slots >= P) is filled from g, then gate|up and down run with a workgroup per expert taking
-// its slots in passes of 4. ygu fp32 [2][cap][I], xtd fp16 [cap][I], yd fp32 [cap][H]; act_cnt [E][I/128] and out_cnt
-// [M][H/128] are zero between calls. Ks = {k_gate, k_up, k_down}.
-int launch_exact_grouped(const int* Ks, const uint64_t* ptrs, int P, int topk, int E, int M, int H, int I,
-                         const uint16_t* x, const GPlan& g, const PlanView& pv, float* ygu, uint16_t* xtd, float* yd,
-                         int* act_cnt, int* out_cnt, const float* silu_tab, float act_limit, float* out,
-                         hipStream_t st);
-
 int launch_split(const int64_t* sel, const uint16_t* w, const uint16_t* z, int n, int bsz, int topk, int H, int E,
                  int first, const int32_t* slotof, const float* score, const float* pol, int64_t* ctrl, uint16_t* hx,
                  int32_t* hpicks, int64_t seq, int li, int keep_ids, int64_t* sel_out, uint16_t* w_out,

@@ -349,46 +349,6 @@ __device__ void publish_plan_picks(const LPlan& L, const int* hdr, int P, int to
     }
 }
 
-// EXACT above MAX_PICKS picks: the decode launches' PlanView from the grouped plan of the prefill path (one
-// workgroup of 1024 threads, E <= 1024). Union entries are the experts with slots, ascending, so each entry's slots
-// are its expert's contiguous range of the expert-major slot order; slot_pick, tok_slot, tok_w and tok_npk are the
-// grouped plan's own arrays, which the PlanView points at (each token's slots in (job, pick) order). Rows of tokens
-// without a valid pick are zeroed here (the reference's sum over an empty route is 0).
-__global__ __launch_bounds__(1024) void exact_plan_kernel(GPlan g, PlanView pv, int E, int M, int H,
-                                                          const uint64_t* ptrs, float* out)
-{
-    __shared__ int wsum[16];
-    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
-    const bool has = t < E && g.cnt[t] > 0;
-    const uint64_t m = __ballot(has);
-    if (lane == 0) wsum[wv] = __popcll(m);
-    __syncthreads();
-    int base = 0, U = 0;
-    for (int i = 0; i < 16; ++i)
-    {
-        if (i < wv) base += wsum[i];
-        U += wsum[i];
-    }
-    if (has)
-    {
-        const int u = base + __popcll(m & ((uint64_t(1) << lane) - 1));
-        pv.uexp[u] = t;
-        pv.uoff[u] = g.off[t];
-        pv.uptr[2 * u] = ptrs[(size_t)t * 9 + 2];
-        pv.uptr[2 * u + 1] = ptrs[(size_t)t * 9 + 8];
-    }
-    if (t == 0)
-    {
-        pv.hdr[0] = U;
-        pv.hdr[1] = g.off[E];
-        pv.hdr[2] = g.hdr[1];
-        pv.uoff[U] = g.off[E];
-    }
-    for (int tk = t; tk < M; tk += blockDim.x)
-        if (g.tok_npk[tk] == 0)
-            for (int i = 0; i < H; ++i) out[(size_t)tk * H + i] = 0.f;
-}
-
 // ---------------------------------------------------------------------------------------------------------------
 // bit-exact trellis GEMV
 // ---------------------------------------------------------------------------------------------------------------
@@ -836,11 +796,9 @@ __device__ void act_block(const GuArgs& a, int e, int s_begin, int s_end, int b)
 // MF (MFMA-accumulate mode): a workgroup covers 4 tile columns over one half of the tile rows (so it transforms only
 // that half of the inputs), for all slots of its union entry in passes of up to 16; the two halves' partial sums go
 // to ygu[half] and the SwiGLU stage adds them (half 0 + half 1).
-// GP (EXACT above MAX_PICKS picks): the plan is read from a.pv in global memory, prepared by the launches before
-// (the grouped plan of the prefill path, expert-major, and exact_plan_kernel); the grid has no publishing workgroup.
 // Occupancy hint: 3 waves per SIMD for the EXACT kernel with one slot per pass (its batched fp32 input reads need up
 // to 168 VGPRs; at 128 the compiler spills), else 4.
-template <int K, int NS, bool MF, bool GP = false>
+template <int K, int NS, bool MF>
 __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(K == 5 || (NS == 1 && !MF) ? 3 : 4))) void
 gu_kernel(GuArgs a)
 {
@@ -855,35 +813,30 @@ gu_kernel(GuArgs a)
     void* lds_x = lds_raw + NW * RB;                                                  // [ns_cap][H] permuted
     // [ns_cap][H] elements, MF: [ns_cap][H / 2] (one half of the 128-blocks)
     int* plan_mem = reinterpret_cast<int*>(lds_raw + NW * RB + (size_t)a.ns_cap * a.H * XE / (MF ? 2 : 1));
-    LPlan L = {};
     const int TN = a.I / 16, TK = a.H / 16, ncb = TN / NW;
-    if constexpr (!GP)
+    const LPlan L = lplan_carve(plan_mem, a.P, a.E);
+    if (a.P <= 64) build_plan_wave(a.sel, a.P, a.E, L, hdr);
+    else build_plan(a.sel, a.P, a.E, L, hdr);
+    if (blockIdx.x == gridDim.x - 1)
     {
-        L = lplan_carve(plan_mem, a.P, a.E);
-        if (a.P <= 64) build_plan_wave(a.sel, a.P, a.E, L, hdr);
-        else build_plan(a.sel, a.P, a.E, L, hdr);
-        if (blockIdx.x == gridDim.x - 1)
-        {
-            // the grid's extra workgroup publishes the plan for the down launch (no GEMV work of its own)
-            if (blockIdx.y == 0)
-                publish_plan(L, hdr, a.P, a.topk, a.w, a.w_half, a.pv, a.out, a.H, a.ptrs, a.per_slot);
-            return;
-        }
+        // the grid's extra workgroup publishes the plan for the down launch (no GEMV work of its own)
+        if (blockIdx.y == 0) publish_plan(L, hdr, a.P, a.topk, a.w, a.w_half, a.pv, a.out, a.H, a.ptrs, a.per_slot);
+        return;
     }
 
     // union entry (or slot with per_slot), column block, and with MF the half of the tile rows (adjacent workgroups)
     const int nper = MF ? 2 * ncb : ncb;
     const int ent = blockIdx.x / nper, cb = (blockIdx.x % nper) / (MF ? 2 : 1), hf = MF ? blockIdx.x & 1 : 0;
-    if (ent >= (GP ? a.pv.hdr[0] : hdr[a.per_slot ? 1 : 0])) return;
-    const int u = !GP && a.per_slot ? plan_u(L, L.spick[ent]) : ent;
+    if (ent >= hdr[a.per_slot ? 1 : 0]) return;
+    const int u = a.per_slot ? plan_u(L, L.spick[ent]) : ent;
     const int mat = a.mat_base + blockIdx.y;              // 0 gate, 1 up
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15;
     const int wid = __builtin_amdgcn_readfirstlane(wave);
-    const int e = GP ? a.pv.uexp[u] : L.uexp[u];
+    const int e = L.uexp[u];
     const uint8_t* tr = reinterpret_cast<const uint8_t*>(a.ptrs[(size_t)e * 9 + mat]);
     const gptr<uint16_t> suh = gaddr<uint16_t>(a.ptrs[(size_t)e * 9 + 3 + 2 * mat]);
-    const int s_begin = GP ? a.pv.uoff[u] : a.per_slot ? ent : L.uoff[u];
-    const int s_end = GP ? a.pv.uoff[u + 1] : a.per_slot ? ent + 1 : L.uoff[u + 1];
+    const int s_begin = a.per_slot ? ent : L.uoff[u];
+    const int s_end = a.per_slot ? ent + 1 : L.uoff[u + 1];
     const size_t gstride = (size_t)TN * TB;
     const int t = cb * NW + wave;                         // this wave's tile column
     const uint8_t* col = tr + (size_t)t * TB;
@@ -905,7 +858,7 @@ gu_kernel(GuArgs a)
         auto load_round = [&](int r, int k) {
             const int it = min((r * NW + wave) * 4 + rl, nit - 1);
             const int s = it / nblk, b = g0 + it % nblk;
-            const int pk = GP ? a.pv.slot_pick[c0 + s] : L.spick[c0 + s];
+            const int pk = L.spick[c0 + s];
             xv[k] = *reinterpret_cast<const uint4*>(a.x + (size_t)(pk / a.topk) * a.H + b * 128 + li * 8);
             sv[k] = gld16(suh, b * 128 + li * 8);
         };
@@ -1538,16 +1491,16 @@ static size_t dn_lds(int ns, int I, int mf)
     return (size_t)nw * NGRP * 8 * 32 * K + (size_t)ns * I * (mf ? 2 : x_lds_elem(ns)) + (size_t)ns * 128 * 4;
 }
 
-template <int K, int NS, bool MF, bool GP = false>
+template <int K, int NS, bool MF>
 static void gu_launch(const GuArgs& a, int umax, int nmat, hipStream_t st)
 {
-    const size_t lds = GP ? gu_lds<K>(a.ns_cap, a.H, 0, 0, MF) : gu_lds<K>(a.ns_cap, a.H, a.P, a.E, MF);
-    auto kern = gu_kernel<K, NS, MF, GP>;
+    const size_t lds = gu_lds<K>(a.ns_cap, a.H, a.P, a.E, MF);
+    auto kern = gu_kernel<K, NS, MF>;
     static const bool opened = open_lds(kern);
     (void)opened;
     const int ents = a.per_slot ? a.P : umax;
     const int per_ent = (a.I / (16 * GU_NW)) * (MF ? 2 : 1);   // MF: both halves of the tile rows
-    timed_launch(kern, dim3(ents * per_ent + (GP ? 0 : 1), nmat), dim3(GU_NW * 64), lds, st, a);
+    timed_launch(kern, dim3(ents * per_ent + 1, nmat), dim3(GU_NW * 64), lds, st, a);
 }
 
 template <int K, int NS, bool MF>
@@ -1713,43 +1666,6 @@ int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int
     GFL_K_SWITCH(K, GFL_NS_SWITCH(ns, (dn_launch<K_, NS_, false>(a, umax, P, st))))
     return 0;
 }
-int launch_exact_grouped(const int* Ks, const uint64_t* ptrs, int P, int topk, int E, int M, int H, int I,
-                         const uint16_t* x, const GPlan& g, const PlanView& pv, float* ygu, uint16_t* xtd, float* yd,
-                         int* act_cnt, int* out_cnt, const float* silu_tab, float act_limit, float* out,
-                         hipStream_t st)
-{
-    constexpr int XNS = 4;   // slots per GEMV pass: an expert's tiles are decoded once for up to 4 of its slots
-    hipLaunchKernelGGL(exact_plan_kernel, dim3(1), dim3(1024), 0, st, g, pv, E, M, H, ptrs, out);
-    GuArgs a;
-    a.ptrs = ptrs; a.sel = nullptr; a.w = nullptr; a.w_half = 0; a.P = P; a.topk = topk; a.E = E; a.H = H; a.I = I;
-    a.x = x; a.ygu = ygu; a.xtd = xtd; a.act_cnt = act_cnt; a.silu_tab = silu_tab; a.act_limit = act_limit;
-    a.pv = pv; a.out = out;
-    a.ns_cap = XNS;
-    a.mf = 0;
-    a.per_slot = 0;
-    a.nmat_total = 2 * (128 / (16 * GU_NW));
-    if (Ks[0] == Ks[1])
-    {
-        a.mat_base = 0;
-        GFL_K_SWITCH(Ks[0], (gu_launch<K_, XNS, false, true>(a, E, 2, st)))
-    }
-    else
-    {
-        a.mat_base = 0;
-        GFL_K_SWITCH(Ks[0], (gu_launch<K_, XNS, false, true>(a, E, 1, st)))
-        a.mat_base = 1;
-        GFL_K_SWITCH(Ks[1], (gu_launch<K_, XNS, false, true>(a, E, 1, st)))
-    }
-    DnArgs d;
-    d.ptrs = ptrs; d.topk = topk; d.H = H; d.I = I; d.pv = pv; d.xtd = xtd; d.yd = yd; d.out_cnt = out_cnt;
-    d.blk_cnt = nullptr;
-    d.out = out;
-    d.ns_cap = XNS;
-    d.per_slot = 0;
-    GFL_K_SWITCH(Ks[2], (dn_launch<K_, XNS, false>(d, E, P, st)))
-    return 0;
-}
-
 #undef GFL_NS_SWITCH
 #undef GFL_RW_SWITCH
 #undef GFL_K_SWITCH
