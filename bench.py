@@ -571,6 +571,8 @@ def main():
     ap.add_argument("--stack-layers", type=int, default=42)
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the config-4 prefill measurement (M=2048 through the grouped path), one JSON line")
+    ap.add_argument("--prefill-exact", action="store_true",
+                    help="with --prefill-only: the EXACT path (gfl_moe_forward, accumulator chains) instead")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="counter run: the calibration copy, then eager M=1 steps (run under rocprofv3 --pmc)")
     ap.add_argument("--probe-M", type=int, default=1, help="tokens per layer call of --pmc-probe")
@@ -610,6 +612,11 @@ def main():
         pmc_probe(ctx, layers, M=args.probe_M)
         return
     if args.prefill_only:
+        if args.prefill_exact:
+            r = time_prefill(ctx, list(range(args.layers)), layers[0].quant_bytes_per_expert, 2048, 2, G=2,
+                             exact=True)
+            print(json.dumps({"config4_prefill_exact": r}), flush=True)
+            return
         r = time_prefill(ctx, list(range(args.layers)), layers[0].quant_bytes_per_expert, 2048,
                          max(4, args.steps // 64))
         print(json.dumps({"config4_prefill": r}), flush=True)
