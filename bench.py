@@ -126,7 +126,7 @@ def cpu_baseline(iters, warmup):
 
 COPY_BYTES = 1 << 30
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gate_up_config1_M1.json")
-GATE_UP_KERNEL = "gu_kernel<3, 1, false, false>"
+GATE_UP_KERNEL = "gu_kernel<3, 1, false>"
 
 
 def pmc_probe(ctx, layers, steps=64, M=1):

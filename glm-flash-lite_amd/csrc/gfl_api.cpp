@@ -259,8 +259,10 @@ int run_forward(gfl_ctx* c, const Layer& L, const Workspace& ws, const uint16_t*
     // each streaming and decoding every rw-th group of 8 tile rows while the column's accumulators pass from wave to
     // wave in tile-row order (chain_relay). With one wave per column such a call leaves most SIMDs idle; rw waves per
     // column put rw times the waves on the chip. Measured on MI355X (config-1 layers, 4 cycled): one expert per call
-    // (192 gate|up columns) 39.2 -> 29.8 us with 4 waves per column. At 8 picks (1,536 columns) the relay launches
-    // were 1-2% slower than the per-slot ones, so they are not used there.
+    // (192 gate|up columns) 39.2 -> 27.7 us with 4 waves per column. At 8 picks (1,536 columns) 2 waves per gate|up
+    // column and 1 per down column measured 57.0 us against 58.3, but they fill every SIMD with 3 waves: a shared
+    // expert on a side stream (k_overlap) then has no room, and routed + shared went from 71.3 to 79.1 us. So the
+    // per-slot launches keep 8 picks and more.
     int rw[2] = { 0, 0 };
     if (!mf && ns == 1)
     {

@@ -515,9 +515,10 @@ __device__ __forceinline__ void chain_dma(const uint8_t* __restrict__ col_base, 
 // wave with relay index r streams and decodes groups r, r + RW, r + 2 RW, ..., and the column's accumulators pass from
 // wave to wave through relay (64 floats in LDS) in group order, so every accumulator is still one chain of fused
 // multiply-adds over the tile rows in the reference's order.
-// Phase ph: each wave decodes and transposes its group ph * RW + r, then RW turns follow, each closed by a workgroup
-// barrier; in turn r this wave reads the accumulators of group g - 1, runs the group's 32 FMAs and writes them back.
-// Every wave of the workgroup runs the same phases and turns (the same barriers), whether or not it has a group left.
+// Phase ph: each wave decodes and transposes its group g = ph * RW + r, waits until the column's turn counter (LDS)
+// reaches g, reads the accumulators of group g - 1, runs the group's 32 FMAs, writes them back and moves the counter
+// to g + 1 (release/acquire at workgroup scope). Only the wave of the next group waits, and each wave decodes its
+// next group before it waits; workgroup barriers coupling all waves at every turn measured 1-7 us slower at M=1..4.
 // The trellis streams through registers: each wave keeps its next PF groups in flight as 16-byte buffer loads (lane l
 // of load i holds byte 16 (64 i + l) of the group: tile (64 i + l) / 2K, bytes 16 ((64 i + l) % 2K) onward) and writes
 // a group into its single LDS slot (8 tiles, tile-major) right before decoding it. LDS operations of one wave complete
@@ -527,9 +528,25 @@ __device__ __forceinline__ void chain_dma(const uint8_t* __restrict__ col_base, 
 // Returns the column results (valid in lanes 0..15 of every relay wave of the column).
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
+// Work item of relay launch block b (a grid of relay_blocks(items, RW) blocks): items are (entry, column block),
+// column blocks fastest, and each run of RW adjacent column blocks (4 tile columns, whole 128-byte lines of every tile
+// row) goes to one XCD (XCD = block index mod 8), the runs dealt round-robin over the 8 XCDs. Blocks past the items
+// return -1. Adjacent column blocks of fewer than 4 tile columns share lines; on different XCDs each L2 would fetch
+// them (measured 1.38x the algorithmic bytes of the gate|up launch with 2 columns per workgroup).
+__device__ __forceinline__ long relay_item(long b, int RW, long items)
+{
+    const long xcd = b % 8, j = b / 8;
+    const long item = ((j / RW) * 8 + xcd) * RW + j % RW;
+    return item < items ? item : -1;
+}
+__host__ __device__ constexpr long relay_blocks(long items, int RW)
+{
+    return (items / RW + 7) / 8 * 8 * RW;
+}
+
 template <int K, int PF, int RW, class PreLoad, class Pre>
 __device__ __forceinline__ float chain_relay(const uint8_t* __restrict__ col_base, size_t gstride, int TK,
-                                             const float* lds_x, uint8_t* slot, float* relay, int r,
+                                             const float* lds_x, uint8_t* slot, float* relay, int* turn, int r,
                                              PreLoad&& pre_load, Pre&& pre)
 {
     constexpr int TB = 32 * K, CH = 2 * K, NCH = 8 * CH, NLD = (NCH + 63) / 64;   // 16-byte chunks
@@ -602,31 +619,44 @@ __device__ __forceinline__ float chain_relay(const uint8_t* __restrict__ col_bas
                 for (int rr = 0; rr < 8; ++rr)
                     xf[rr] = *reinterpret_cast<const float4v*>(lds_x + ((size_t)g * 8 + rr) * 16 + j * 4);
             }
-            if (ph < nph)   // the same for every wave of the workgroup
+            if (mine)
             {
-#pragma unroll
-                for (int turn = 0; turn < RW; ++turn)
+                if (g > 0)
                 {
-                    if (turn == r && mine)
-                    {
-                        if (g > 0) acc = relay[lane];
-#pragma unroll
-                        for (int rr = 0; rr < 8; ++rr)
+                    // the turn of group g: the wave of group g - 1 has written its accumulators (bounded wait: that
+                    // wave is resident and waits only for groups before its own)
+                    if (RW > 1)
+                        for (int spin = 0; spin < (1 << 22); ++spin)
                         {
-                            acc = __builtin_fmaf(cw[rr][0], xf[rr][0], acc);
-                            acc = __builtin_fmaf(cw[rr][1], xf[rr][1], acc);
-                            acc = __builtin_fmaf(cw[rr][2], xf[rr][2], acc);
-                            acc = __builtin_fmaf(cw[rr][3], xf[rr][3], acc);
+                            if (__hip_atomic_load(turn, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= g) break;
+                            __builtin_amdgcn_s_sleep(1);
                         }
-                        relay[lane] = acc;
-                    }
-                    if (RW > 1) lds_barrier();
+                    acc = relay[lane];
                 }
+#pragma unroll
+                for (int rr = 0; rr < 8; ++rr)
+                {
+                    acc = __builtin_fmaf(cw[rr][0], xf[rr][0], acc);
+                    acc = __builtin_fmaf(cw[rr][1], xf[rr][1], acc);
+                    acc = __builtin_fmaf(cw[rr][2], xf[rr][2], acc);
+                    acc = __builtin_fmaf(cw[rr][3], xf[rr][3], acc);
+                }
+                relay[lane] = acc;
+                if (RW > 1) __hip_atomic_store(turn, g + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
             }
         }
     }
     wait_vmcnt<0>();   // the padding's clamped prefetches
-    if (RW > 1) acc = relay[lane];   // the last group's accumulators (its turn ended with a barrier)
+    if (RW > 1)
+    {
+        // the last group's accumulators
+        for (int spin = 0; spin < (1 << 22); ++spin)
+        {
+            if (__hip_atomic_load(turn, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= ngroups) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        acc = relay[lane];
+    }
     const float a1 = __shfl(acc, n + 16), a2 = __shfl(acc, n + 32), a3 = __shfl(acc, n + 48);
     return (acc + a1) + (a2 + a3);
 }
@@ -733,6 +763,7 @@ struct GuArgs
     int ns_cap;                // slots per pass the LDS allocation holds (<= NS)
     int per_slot;              // workgroups per slot (one pass each) instead of per union entry (NS == 1 only)
     int mf;                    // MFMA-accumulate mode: down inputs written in the MFMA input layout
+    int nmat_launch;           // matrices of this launch (the relay launches' item count)
 };
 
 __device__ __forceinline__ float ld_agent(const float* p)
@@ -980,6 +1011,7 @@ struct DnArgs
     float* out;                // [M][H]
     int ns_cap;                // slots per pass the LDS allocation holds (<= NS)
     int per_slot;              // workgroups per slot (one pass each), as the gate|up launch
+    int pv_picks;              // picks of the call (the relay down launch's item count)
 };
 
 // Grid: umax * H/128. Workgroup = 8 waves = one 128-output block of one routed expert, all its slots (with per_slot:
@@ -1214,6 +1246,8 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
     __shared__ int hdr[4];
     __shared__ int s_last;
     __shared__ float relay[CW][64];
+    __shared__ int relay_turn[CW];
+    if (threadIdx.x < CW) relay_turn[threadIdx.x] = 0;   // ordered before every hand-off by the input barrier
     constexpr int RB = 8 * TB;                                           // one group slot per wave
     uint8_t* rings = lds_raw;                                            // [NW][RB]
     float* lds_x = reinterpret_cast<float*>(lds_raw + NW * RB);          // [H] permuted, fp32
@@ -1226,7 +1260,10 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
         publish_plan_picks(L, hdr, a.P, a.topk, a.w, a.w_half, a.pv, a.out, a.H, a.ptrs);
         return;
     }
-    const int wg = blockIdx.x - 1, per_mat = a.P * ncb;
+    // block 0 publishes the plan, blocks 1..7 have no work (the items start at an XCD-aligned block)
+    const long item = blockIdx.x < 8 ? -1 : relay_item(blockIdx.x - 8, RW, (long)a.nmat_launch * a.P * ncb);
+    if (item < 0) return;
+    const int wg = (int)item, per_mat = a.P * ncb;
     const int p = (wg % per_mat) / ncb, cb = wg % ncb;
     const int64_t e64 = a.sel[p];
     if (e64 < 0 || e64 >= a.E) return;
@@ -1292,8 +1329,8 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
         }
         lds_barrier();   // lds_x complete
     };
-    const float res = chain_relay<K, NGRP - 1, RW>(col, gstride, TK, lds_x, rings + wid * RB, relay[c], r, pre_load,
-                                                   pre);
+    const float res = chain_relay<K, NGRP - 1, RW>(col, gstride, TK, lds_x, rings + wid * RB, relay[c],
+                                                   &relay_turn[c], r, pre_load, pre);
     float* ybase = a.ygu + (size_t)mat * a.pv.cap_slots * a.I;
     if (r == 0 && lane < 16) st_agent(&ybase[(size_t)p * a.I + t * 16 + n], res);
     release_agent();
@@ -1331,11 +1368,15 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
     __shared__ int c_tok, c_npk, c_slot[MAX_TOPK];
     __shared__ float c_w[MAX_TOPK];
     __shared__ float relay[CW][64];
+    __shared__ int relay_turn[CW];
+    if (threadIdx.x < CW) relay_turn[threadIdx.x] = 0;   // ordered before every hand-off by the input barrier
     constexpr int RB = 8 * TB;                                      // one group slot per wave
     uint8_t* rings = lds_raw;                                       // [NW][RB]
     float* lds_x = reinterpret_cast<float*>(lds_raw + NW * RB);     // [I] permuted, fp32
     const int TN = a.H / 16, TK = a.I / 16, ncb = TN / CW;
-    const int p = blockIdx.x / ncb, cb = blockIdx.x % ncb;
+    const long item = relay_item(blockIdx.x, RW, (long)a.pv_picks * ncb);
+    if (item < 0) return;
+    const int p = (int)(item / ncb), cb = (int)(item % ncb);
     const int blk = cb / NQ;
     const uint8_t* tr = reinterpret_cast<const uint8_t*>(a.pv.uptr[2 * p]);
     const gptr<uint16_t> svh = gaddr<uint16_t>(a.pv.uptr[2 * p + 1]);
@@ -1389,8 +1430,8 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
         for (int i = threadIdx.x + 2 * NW * 64; i < nvec; i += NW * 64) put(i, xsrc[i]);
         lds_barrier();   // lds_x complete
     };
-    const float res = chain_relay<K, NGRP - 1, RW>(col, gstride, TK, lds_x, rings + wid * RB, relay[c], r, pre_load,
-                                                   pre);
+    const float res = chain_relay<K, NGRP - 1, RW>(col, gstride, TK, lds_x, rings + wid * RB, relay[c],
+                                                   &relay_turn[c], r, pre_load, pre);
     if (r == 0 && lane < 16) st_agent(&a.yd[(size_t)p * a.H + t * 16 + n], res);
     if (ck < a.topk)
     {
@@ -1549,7 +1590,9 @@ static void gu_relay_launch(const GuArgs& a, int nmat, hipStream_t st)
     (void)opened;
     const long nwg = (long)a.P * (a.I / (16 * CW)) * nmat;   // GEMV workgroups (plus the publishing one)
     const size_t lds = balanced_lds(gu_relay_lds<K>(a.H, a.P, a.E), nwg);
-    timed_launch(kern, dim3(1 + nwg), dim3(GU_NW * 64), lds, st, a);
+    GuArgs b = a;
+    b.nmat_launch = nmat;
+    timed_launch(kern, dim3(8 + relay_blocks(nwg, RW)), dim3(GU_NW * 64), lds, st, b);
 }
 
 template <int K, int RW>
@@ -1561,7 +1604,9 @@ static void dn_relay_launch(const DnArgs& a, int P, hipStream_t st)
     (void)opened;
     const long nwg = (long)P * (a.H / (16 * CW));
     const size_t lds = balanced_lds(dn_relay_lds<K>(a.I), nwg);
-    timed_launch(kern, dim3(nwg), dim3(GU_NW * 64), lds, st, a);
+    DnArgs b = a;
+    b.pv_picks = P;
+    timed_launch(kern, dim3(relay_blocks(nwg, RW)), dim3(GU_NW * 64), lds, st, b);
 }
 
 // relay width: 1, 2 or 4 waves per tile column
