@@ -126,7 +126,9 @@ def cpu_baseline(iters, warmup):
 
 COPY_BYTES = 1 << 30
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gate_up_config1_M1.json")
-GATE_UP_KERNEL = "gu_kernel<3, 1, false>"
+# the gate|up launch of a config-1 M=1 call: 8 picks (1,536 gate|up tile columns) run the relay launches, 2 waves per
+# column (gfl_moe_forward's launch choice)
+GATE_UP_KERNEL = "gu_relay_kernel<3, 2>"
 
 
 def pmc_probe(ctx, layers, steps=64, M=1):
@@ -502,8 +504,8 @@ def time_router(M, reps=8, G=32):
 
 def time_prefill(ctx, layer_ids, bytes_per_expert, M, reps, G=4, exact=False):
     """Config 4 prefill: M tokens, uniform top-8 routing, through gfl_grouped_forward (MFMA grouped GEMMs), or with
-    exact=True through gfl_moe_forward in EXACT mode (the decode kernels driven by the grouped plan, bit-identical to
-    the reference's EXACT mode). G layer calls (layers cycled) are captured in one HIP graph and replayed `reps` times.
+    exact=True through gfl_moe_forward in EXACT mode (above 1,024 picks the accumulator-chain GEMMs on the grouped
+    plan, bit-identical to the reference's EXACT mode). G layer calls (layers cycled) are captured in one HIP graph and replayed `reps` times.
     Algorithmic work per call: 2 * picks * 3 * H * I flops (gate, up, down GEMMs) and the union's quantized expert
     bytes."""
     import numpy as np

@@ -15,7 +15,8 @@ SYMBOLS = ("gfl_last_error", "gfl_version", "gfl_ctx_create", "gfl_ctx_destroy",
            "gfl_moe_forward", "gfl_grouped_forward", "gfl_dequant", "gfl_split", "gfl_combine", "gfl_grouped_rows",
            "gfl_synth_trellis", "gfl_route",
            "gfl_stats", "gfl_profile_enable", "gfl_profile_read", "gfl_exp_table", "gfl_silu_table",
-           "gfl_grouped_plan", "gfl_grouped_reserve", "gfl_layer_info", "gfl_route_split", "gfl_moe_forward_noalloc")
+           "gfl_grouped_plan", "gfl_grouped_reserve", "gfl_layer_info", "gfl_route_split", "gfl_moe_forward_noalloc",
+           "gfl_ctx_set_shared")
 
 # layout limits of gfl_moe_forward_noalloc's static scratch array (GFL_NOALLOC_MAX_* in include/gfl_moe.h)
 NOALLOC_MAX_PICKS, NOALLOC_MAX_H, NOALLOC_MAX_I = 64, 8192, 4096
@@ -68,6 +69,7 @@ def load(path=LIB_PATH):
     L.gfl_route.argtypes = [_P, C.c_int, C.c_int, C.c_int, _P, _P, _P]
     L.gfl_stats.argtypes = [_P, _P, C.c_int]
     L.gfl_profile_enable.argtypes = [_P, C.c_int]
+    L.gfl_ctx_set_shared.argtypes = [_P, C.c_int]
     L.gfl_profile_read.argtypes = [_P, _P, _P]
     L.gfl_exp_table.argtypes = [_P, C.c_int]
     L.gfl_silu_table.argtypes = [_P, C.c_int]
@@ -217,6 +219,11 @@ class Context:
         return r
 
     STAGES = ("plan", "gate_up", "grouped", "down", "combine")
+
+    def set_shared(self, shared):
+        """Tell the context whether other GPU work runs beside its decode calls (gfl_ctx_set_shared): with shared set,
+        calls of up to 1,536 gate|up tile columns keep the per-slot launches, which leave SIMDs free."""
+        check(load().gfl_ctx_set_shared(self.h, int(bool(shared))))
 
     def profile(self, enable):
         check(load().gfl_profile_enable(self.h, int(bool(enable))))

@@ -68,6 +68,9 @@ struct gfl_ctx
     // relay widths of the one-slot-per-pass EXACT launches forced by GFL_RELAY="g,d" (gate|up, down; 1, 2 or 4), or
     // "0" for the per-slot launches without relay; -1 = chosen from the call's size
     int rw_override[2] = { -1, -1 };
+    // other GPU work runs beside this context's decode calls (gfl_ctx_set_shared): keep calls of 769..1536 gate|up
+    // tile columns on the per-slot launches, which leave SIMDs free
+    int shared = 0;
     // workspace of the prefill path (gfl_grouped_forward / gfl_grouped_reserve), grown on demand outside captures
     void* gws = nullptr;
     size_t gws_bytes = 0;
@@ -259,10 +262,11 @@ int run_forward(gfl_ctx* c, const Layer& L, const Workspace& ws, const uint16_t*
     // each streaming and decoding every rw-th group of 8 tile rows while the column's accumulators pass from wave to
     // wave in tile-row order (chain_relay). With one wave per column such a call leaves most SIMDs idle; rw waves per
     // column put rw times the waves on the chip. Measured on MI355X (config-1 layers, 4 cycled): one expert per call
-    // (192 gate|up columns) 39.2 -> 27.7 us with 4 waves per column. At 8 picks (1,536 columns) 2 waves per gate|up
-    // column and 1 per down column measured 57.0 us against 58.3, but they fill every SIMD with 3 waves: a shared
-    // expert on a side stream (k_overlap) then has no room, and routed + shared went from 71.3 to 79.1 us. So the
-    // per-slot launches keep 8 picks and more.
+    // (192 gate|up columns) 39.2 -> 27.5 us with 4 waves per column; 8 picks (1,536 columns) 58.4 -> 56.4 us with 2
+    // waves per gate|up column and 1 per down column; 16 picks and more are 7-11% slower than the per-slot launches.
+    // The relay launches at 8 picks fill every SIMD with 3 waves, so a shared expert on a side stream (k_overlap)
+    // then waits (routed + shared 71.3 -> 79.1 us): a context told that other work runs beside it (gfl_ctx_set_shared)
+    // keeps those calls on the per-slot launches.
     int rw[2] = { 0, 0 };
     if (!mf && ns == 1)
     {
@@ -271,6 +275,11 @@ int run_forward(gfl_ctx* c, const Layer& L, const Workspace& ws, const uint16_t*
         {
             rw[0] = 4;
             rw[1] = cdn <= 768 ? 4 : cdn <= 1536 ? 2 : 1;
+        }
+        else if (cgu <= 1536 && !c->shared)
+        {
+            rw[0] = 2;
+            rw[1] = 1;
         }
         if (c->rw_override[0] >= 0) { rw[0] = c->rw_override[0]; rw[1] = c->rw_override[1]; }
     }
@@ -841,6 +850,14 @@ int gfl_synth_trellis(void* dst, size_t nbytes, uint64_t seed, gfl_stream stream
     if (!dst) return fail(GFL_EINVAL, "gfl_synth_trellis: NULL destination");
     gfl::launch_synth(static_cast<uint8_t*>(dst), nbytes, seed, reinterpret_cast<hipStream_t>(stream));
     GFL_HIP(hipGetLastError());
+    return GFL_OK;
+}
+
+int gfl_ctx_set_shared(gfl_ctx* c, int shared)
+{
+    if (!c) return fail(GFL_EINVAL, "gfl_ctx_set_shared: NULL context");
+    std::lock_guard<std::mutex> g(c->mu);
+    c->shared = shared != 0;
     return GFL_OK;
 }
 

@@ -592,12 +592,12 @@ __device__ __forceinline__ float chain_relay(const uint8_t* __restrict__ col_bas
             const int g = ph * RW + r;
             const bool mine = ph < nph && g < ngroups;
             float4v cw[8], xf[8];
-            if (mine)
-            {
+            // written in every phase, padding ones included (the slot is this wave's own and only its own decode
+            // reads it): with the write under the phase's branch, the compiler's wait before it also covered the
+            // younger of the groups in flight
 #pragma unroll
-                for (int i = 0; i < NLD; ++i)
-                    if (64 * i + lane < NCH) *reinterpret_cast<u32x4*>(slot + (64 * i + lane) * 16) = buf[k][i];
-            }
+            for (int i = 0; i < NLD; ++i)
+                if (64 * i + lane < NCH) *reinterpret_cast<u32x4*>(slot + (64 * i + lane) * 16) = buf[k][i];
             load(buf[k], ph + PF);
             if (mine)
             {

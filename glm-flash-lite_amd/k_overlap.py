@@ -9,7 +9,8 @@ add, so the result equals routed + shared computed one after the other, bit for 
 captures into HIP graphs (events are created once, up front).
 
 At decode sizes the routed launches leave compute units idle (1,536 gate|up column-waves on 1,024 SIMDs at M=1), which
-is the room the shared expert's 48 + 40 workgroups run in.
+is the room the shared expert's 48 + 40 workgroups run in. The routed context is told so for the overlapped call
+(gfl_ctx_set_shared): on its own it runs such calls with launches that fill every SIMD.
 """
 import torch
 
@@ -61,7 +62,12 @@ class SharedOverlap:
         with torch.cuda.stream(self.side):
             self.ctx.moe_forward(li, x, s1, w1, y)
             self.join.record(self.side)
-        routed.moe_forward(li, x, sel, w, out)
+        # the routed call keeps launch shapes that leave SIMDs free for the side stream (same results)
+        routed.set_shared(True)
+        try:
+            routed.moe_forward(li, x, sel, w, out)
+        finally:
+            routed.set_shared(False)
         main.wait_event(self.join)
         out.add_(y)
         self.overlapped += 1

@@ -472,3 +472,26 @@ def test_relay_launches_full_shape_bitexact(gpu, oracle, relay):
         mx, rms, nbad = _report(f"relay {relay} full shape M={M}", got, want)
         assert mx <= TOL * rms
         assert nbad == 0
+
+
+@pytest.mark.gpu
+def test_shared_context_launch_choice_bitexact(gpu, oracle):
+    """At 8 picks of the config-1 shape the default context runs the relay launches and a context told that other GPU
+    work runs beside it (gfl_ctx_set_shared) keeps the per-slot launches: both bit-exact against the oracle, on the
+    same inputs, and the flag can be switched between calls."""
+    import synth
+    import _native
+    ctx = _native.Context(0)
+    H, I, E = 5120, 1536, 10
+    L = _layer(ctx, 52, E, H, I)
+    ex = _host_experts(oracle, L)
+    rng = np.random.default_rng(5200)
+    x16 = rng.standard_normal((1, H)).astype(np.float16)
+    (sel, w16), _ = synth.route_uniform(1, E, 8, rng)
+    want = oracle.moe_forward(ex, x16.astype(np.float32), sel, w16.astype(np.float32), mode=1)
+    for shared in (False, True, False):
+        ctx.set_shared(shared)
+        got = _forward(ctx, 52, x16, sel, w16)
+        _, _, nbad = _report(f"shared={shared} 8 picks", got, want)
+        assert nbad == 0
+    ctx.set_shared(False)
