@@ -668,23 +668,29 @@ __global__ __launch_bounds__(GP_NW * 64) void gp_gemm_kernel(GemmArgs a)
 // The reference's EXACT sum (tile_accum<M,EXACT>, ft_core.h:313-345) gives every output column n four fp32
 // accumulators; accumulator j takes, in each tile row tk, the products of rows 2q + {0, 1, 8, 9}[j] for q = 0..3, in
 // that order, tile rows ascending, and the four are reduced (a0 + a1) + (a2 + a3) (gemv_block, ft_core.h:377-386).
-// Here wave j of a workgroup runs chain j for 64 output columns (lane = column) and for every slot of the pass (one
-// accumulator per slot), so:
-//   - a lane decodes exactly the four weights its chain needs from each tile (stream indices 32 (n % 8) + 4 (n / 8)
-//     + j + 8q of the tile's stream, a3/PERM), and each decoded weight serves all the pass's slots;
-//   - the inputs a chain multiplies them with are the same in every lane: x[slot][tk * 16 + 2q + off_j] for q = 0..3
-//     (the input layout of xg_store_row). Lane k of each 16-lane row reads slot k's four with one ds_read_b128, and
-//     v_fmac_f32_dpp broadcasts them across the row (xg_fma16): one LDS read per 64 FMAs of a wave.
-// Every accumulator is one chain of fused multiply-adds in the reference's order, so the results are bit-identical to
-// the decode path's, while the decode is amortised over the pass (it is about a tenth of the work; the fp32 FMAs are
-// the rest).
+// Here each chain step runs on the matrix cores. v_mfma_f32_16x16x1_4b_f32 computes four independent 16x16 rank-1
+// updates D_b = C_b + A_b B_b^T with K = 1. Per element that is one product added to one accumulator, and both
+// operands are fp16 values, so the product is exact in fp32 and D = RN(C + A B) = fmaf(A, B, C), the reference's
+// chain step. A probe on MI355X matched fmaf bit for bit on 4,096,000 elements (zeros, signed zeros and near-cancelling
+// sums included). Block b is chain j = b:
+//   - B: lane 16j + n holds chain j's weight of column n at step q. A lane decodes exactly the four weights its chain
+//     needs from each tile (stream indices 32 (n % 8) + 4 (n / 8) + j + 8q of the tile's stream, a3/PERM), and each
+//     decoded weight serves all the pass's slots.
+//   - A: lane 16j + m holds slot m's input for chain j at step q, x[slot][tk * 16 + 2q + off_j] (the input layout of
+//     xg_store_row): one ds_read_b128 per lane gives q = 0..3.
+//   - D: chain j of (slot 4 (l / 16) + i, column l % 16) sits in register 4j + i of lane l. The reduction
+//     (a0 + a1) + (a2 + a3) is then four registers of one lane.
+// A wave takes one tile column (16 outputs) with its 4 chains for every slot of the pass, in blocks of 16 slots (one
+// MFMA per block and step). Every accumulator is one chain of fused multiply-adds in the reference's order, so the
+// results are bit-identical to the decode path's.
 
-constexpr int XG_COLS = 64;                 // output columns per workgroup (lane = column)
+constexpr int XG_COLS = 64;                 // output columns per workgroup (a tile column per wave)
 constexpr int XG_TC = XG_COLS / 16;         // tile columns per workgroup
 constexpr int XG_MS = 64;                   // slots per pass
 constexpr int XG_NG = 2;                    // ring depth (groups of 8 tile rows)
 constexpr int XG_XROW = 8 * 16 * 4;         // input bytes of one slot per group: 8 tile rows x 16 rows x fp32
 constexpr int XG_XGB = XG_MS * XG_XROW;     // input bytes per group (32 KB)
+typedef float xg_acc __attribute__((ext_vector_type(16)));   // one 16-slot block of a wave's 4 x 16 x 16 accumulators
 
 struct XgArgs
 {
@@ -713,31 +719,11 @@ __device__ __forceinline__ StateDec state_dec(int t, int K)
     return d;
 }
 
-// acc[k] = fma(w_q, x_q of lane k of the row, acc[k]) for k = 0..15 and q = 0..3 (q outer, so 16 independent FMAs
-// lie between dependent ones): lane k of every 16-lane row holds slot k's four inputs, and v_fmac_f32_dpp with
-// row_newbcast:k hands them to the whole row. One asm block, so nothing the compiler schedules can write a DPP source
-// between the leading s_nop (the VALU-write -> DPP-read hazard) and the reads.
-#define XG_F(K, XQ, WQ) "v_fmac_f32_dpp %" #K ", %" XQ ", %" WQ " row_newbcast:" #K " row_mask:0xf bank_mask:0xf\n\t"
-#define XG_Q(XQ, WQ)                                                                                                   \
-    XG_F(0, XQ, WQ) XG_F(1, XQ, WQ) XG_F(2, XQ, WQ) XG_F(3, XQ, WQ) XG_F(4, XQ, WQ) XG_F(5, XQ, WQ) XG_F(6, XQ, WQ)    \
-    XG_F(7, XQ, WQ) XG_F(8, XQ, WQ) XG_F(9, XQ, WQ) XG_F(10, XQ, WQ) XG_F(11, XQ, WQ) XG_F(12, XQ, WQ)                \
-    XG_F(13, XQ, WQ) XG_F(14, XQ, WQ) XG_F(15, XQ, WQ)
 
-__device__ __forceinline__ void xg_fma16(float* acc, const float4& x, float w0, float w1, float w2, float w3)
-{
-    asm("s_nop 1\n\t" XG_Q("16", "20") XG_Q("17", "21") XG_Q("18", "22") XG_Q("19", "23")
-        : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]), "+v"(acc[4]), "+v"(acc[5]), "+v"(acc[6]),
-          "+v"(acc[7]), "+v"(acc[8]), "+v"(acc[9]), "+v"(acc[10]), "+v"(acc[11]), "+v"(acc[12]), "+v"(acc[13]),
-          "+v"(acc[14]), "+v"(acc[15])
-        : "v"(x.x), "v"(x.y), "v"(x.z), "v"(x.w), "v"(w0), "v"(w1), "v"(w2), "v"(w3));
-}
-#undef XG_Q
-#undef XG_F
-
-// Grid: 8 * ceil(E / 8) * (ndim / 64) * matrices, XCD-major as the MFMA GEMM. Workgroup = 4 waves (the 4 chains) x
-// 64 columns of one matrix of one expert; the expert's slots go through in passes of XG_MS. Per group of 8 tile rows
-// the trellis of the 4 tile columns and the pass's inputs arrive by LDS-direct loads one group ahead (one workgroup
-// barrier per group); at the end of a pass the 4 chains meet in LDS and are reduced per output.
+// Grid: 8 * ceil(E / 8) * (ndim / 64) * matrices, XCD-major as the MFMA GEMM. Workgroup = 4 waves x 16 columns (a
+// tile column each, all 4 chains) of one matrix of one expert; the expert's slots go through in passes of XG_MS. Per
+// group of 8 tile rows the trellis of the 4 tile columns and the pass's inputs arrive by LDS-direct loads one group
+// ahead (one workgroup barrier per group); at the end of a pass each lane reduces its outputs' 4 chains.
 template <int K>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void xg_gemm_kernel(XgArgs a)
 {
@@ -775,8 +761,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void x
         const_cast<uint8_t*>(uniform_ptr(reinterpret_cast<const uint8_t*>(xin))), (short)0,
         (int)((size_t)a.cap * a.kdim * 4), 0x00020000);
     uint16_t* yout = a.yout + (size_t)(mat - a.mat_base) * a.cap * a.ndim;
-    // this lane's column and the stream windows of its chain's four weights in each tile
-    const int j = wave, tcl = lane >> 4, n = lane & 15;
+    // this lane's chain and column, and the stream windows of the chain's four weights in each tile
+    const int j = lane >> 4, tcl = wave, n = lane & 15;
     StateDec sd[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) sd[q] = state_dec(32 * (n & 7) + 4 * (n >> 3) + j + 8 * q, K);
@@ -808,10 +794,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void x
             }
         };
         auto pass = [&](auto nsl_c) {
-            constexpr int NSL = decltype(nsl_c)::value;
-            float acc[NSL];
+            constexpr int NSL = decltype(nsl_c)::value, NB = NSL / 16;
+            xg_acc acc[NB];
 #pragma unroll
-            for (int s = 0; s < NSL; ++s) acc[s] = 0.f;
+            for (int b = 0; b < NB; ++b)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[b][r] = 0.f;
             __syncthreads();   // the previous pass is done with the rings
             issue(0, NSL);
             for (int g = 0; g < ngroups; ++g)
@@ -820,7 +808,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void x
                 gp_barrier();   // group g landed for every wave; every wave is done with group g - 1
                 if (g + 1 < ngroups) issue(g + 1, NSL);
                 const uint8_t* tl = tring + (g % NG) * GB + tcl * TB;
-                const uint8_t* xl = xring + (g % NG) * XG_XGB + j * 16;
+                // lane (j, m) reads slot 16 b + m's inputs of chain j
+                const uint8_t* xl = xring + (g % NG) * XG_XGB + n * XG_XROW + j * 16;
 #pragma unroll
                 for (int t8 = 0; t8 < 8; ++t8)
                 {
@@ -834,29 +823,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void x
                         st[q] = __builtin_amdgcn_alignbit(hi, lo, sd[q].sh) & 0xFFFFu;
                     }
                     const half4 wh = codebook4(st[0], st[1], st[2], st[3]);
-                    const float w0 = (float)wh[0], w1 = (float)wh[1], w2 = (float)wh[2], w3 = (float)wh[3];
+                    const float w[4] = { (float)wh[0], (float)wh[1], (float)wh[2], (float)wh[3] };
+                    float4 xv[NB];
 #pragma unroll
-                    for (int b16 = 0; b16 < NSL / 16; ++b16)
-                    {
-                        const float4 xv =
-                            *reinterpret_cast<const float4*>(xl + (b16 * 16 + n) * XG_XROW + t8 * 64);
-                        xg_fma16(acc + b16 * 16, xv, w0, w1, w2, w3);
-                    }
+                    for (int b = 0; b < NB; ++b)
+                        xv[b] = *reinterpret_cast<const float4*>(xl + b * 16 * XG_XROW + t8 * 64);
+                    // steps q = 0..3 of the tile row; the blocks' chains are independent between dependent steps
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) acc[b] = __builtin_amdgcn_mfma_f32_16x16x1f32(xv[b].x, w[0], acc[b], 0, 0, 0);
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) acc[b] = __builtin_amdgcn_mfma_f32_16x16x1f32(xv[b].y, w[1], acc[b], 0, 0, 0);
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) acc[b] = __builtin_amdgcn_mfma_f32_16x16x1f32(xv[b].z, w[2], acc[b], 0, 0, 0);
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) acc[b] = __builtin_amdgcn_mfma_f32_16x16x1f32(xv[b].w, w[3], acc[b], 0, 0, 0);
                 }
             }
-            // the 4 chains of every output meet in LDS (the input ring, free once every wave is past the last group)
-            __syncthreads();
-            float* red = reinterpret_cast<float*>(xring);   // [4 chains][NSL slots][64 columns]
+            // chain c of (slot 16 b + 4 (lane / 16) + i, column lane % 16) is register 4c + i of acc[b]: the
+            // reference's (a0 + a1) + (a2 + a3), rounded to fp16 (out_block's leading r16)
+            const int col = col0 + tcl * 16 + n;
 #pragma unroll
-            for (int s = 0; s < NSL; ++s) red[(j * NSL + s) * XG_COLS + lane] = acc[s];
-            __syncthreads();
-            const int colw = threadIdx.x & 63;
-            for (int s = threadIdx.x >> 6; s < T; s += 4)
-            {
-                const float r0 = red[(0 * NSL + s) * XG_COLS + colw], r1 = red[(1 * NSL + s) * XG_COLS + colw];
-                const float r2 = red[(2 * NSL + s) * XG_COLS + colw], r3 = red[(3 * NSL + s) * XG_COLS + colw];
-                yout[(size_t)(c0 + s) * a.ndim + col0 + colw] = (uint16_t)f2h_bits((r0 + r1) + (r2 + r3));
-            }
+            for (int b = 0; b < NB; ++b)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                {
+                    const int s = 16 * b + 4 * j + i;
+                    const float y = (acc[b][i] + acc[b][4 + i]) + (acc[b][8 + i] + acc[b][12 + i]);
+                    if (s < T) yout[(size_t)(c0 + s) * a.ndim + col] = (uint16_t)f2h_bits(y);
+                }
         };
         switch ((T + 15) / 16)
         {
