@@ -684,7 +684,11 @@ __global__ __launch_bounds__(GP_NW * 64) void gp_gemm_kernel(GemmArgs a)
 // MFMA per block and step). Every accumulator is one chain of fused multiply-adds in the reference's order, so the
 // results are bit-identical to the decode path's.
 
-constexpr int XG_COLS = 64;                 // output columns per workgroup (a tile column per wave)
+// Waves per workgroup: 8 tile columns share one input ring. With the rings (76 KB of LDS at K=3) two workgroups fit
+// a CU, 4 waves per SIMD, which needs at most 128 VGPRs. Against 4-wave workgroups at 2 waves per SIMD this measured
+// 9.7 against 10.6 ms per config-4 layer.
+constexpr int XG_NW = 8;
+constexpr int XG_COLS = 16 * XG_NW;         // output columns per workgroup (a tile column per wave)
 constexpr int XG_TC = XG_COLS / 16;         // tile columns per workgroup
 constexpr int XG_MS = 64;                   // slots per pass
 constexpr int XG_NG = 2;                    // ring depth (groups of 8 tile rows)
@@ -720,16 +724,17 @@ __device__ __forceinline__ StateDec state_dec(int t, int K)
 }
 
 
-// Grid: 8 * ceil(E / 8) * (ndim / 64) * matrices, XCD-major as the MFMA GEMM. Workgroup = 4 waves x 16 columns (a
-// tile column each, all 4 chains) of one matrix of one expert; the expert's slots go through in passes of XG_MS. Per
-// group of 8 tile rows the trellis of the 4 tile columns and the pass's inputs arrive by LDS-direct loads one group
-// ahead (one workgroup barrier per group); at the end of a pass each lane reduces its outputs' 4 chains.
+// Grid: 8 * ceil(E / 8) * (ndim / XG_COLS) * matrices, XCD-major as the MFMA GEMM. Workgroup = XG_NW waves x 16
+// columns (a tile column each, all 4 chains) of one matrix of one expert; the expert's slots go through in passes of
+// XG_MS. Per group of 8 tile rows the trellis of the XG_TC tile columns and the pass's inputs arrive by LDS-direct
+// loads one group ahead (one workgroup barrier per group); at the end of a pass each lane reduces its outputs' 4
+// chains.
 template <int K>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void xg_gemm_kernel(XgArgs a)
+__global__ __launch_bounds__(XG_NW * 64) __attribute__((amdgpu_waves_per_eu(4))) void xg_gemm_kernel(XgArgs a)
 {
     constexpr int TB = 32 * K, RB = XG_TC * TB, GB = 8 * RB, NG = XG_NG;
-    constexpr int NLD = GB / 256 / 4;          // trellis dword loads per lane per group (the 4 waves share a group)
-    static_assert(GB % 1024 == 0, "a group of tiles splits into whole loads of the 4 waves");
+    constexpr int NLD = GB / 256 / XG_NW;      // trellis dword loads per lane per group (the waves share a group)
+    static_assert(GB % (256 * XG_NW) == 0, "a group of tiles splits into whole loads of the waves");
     extern __shared__ __align__(16) uint8_t xg_lds[];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int nch = a.ndim / XG_COLS, per = nch * a.nmat;
@@ -777,14 +782,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void x
             for (int i = 0; i < NLD; ++i)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (gp_lds_void*)(dst + (wave * NLD + i) * 256), 4, voff[i],
                                                          g * 8 * gs, 0, 0);
-            // this wave's 16 slot rows of the group (rows of slots past the pass repeat its last slot)
+            // this wave's RPW slot rows of the group (rows of slots past the pass repeat its last slot)
+            constexpr int RPW = XG_MS / XG_NW;
             uint8_t* xd = xring + (g % NG) * XG_XGB;
-            if (wave * 16 < nsl)
+            if (wave * RPW < nsl)
             {
 #pragma unroll
-                for (int r = 0; r < 16; ++r)
+                for (int r = 0; r < RPW; ++r)
                 {
-                    const int sl = wave * 16 + r;
+                    const int sl = wave * RPW + r;
                     const int srow = (c0 + min(sl, T - 1)) * a.kdim * 4 + g * XG_XROW;
 #pragma unroll
                     for (int h = 0; h < XG_XROW / 256; ++h)
@@ -915,7 +921,7 @@ static int xg_gemm_launch(const XgArgs& a, int nmat, hipStream_t st)
     XgArgs b = a;
     b.nmat = nmat;
     const unsigned grid = (unsigned)(((a.E + 7) / 8) * 8 * (a.ndim / XG_COLS) * nmat);
-    hipLaunchKernelGGL(xg_gemm_kernel<K>, dim3(grid), dim3(256), lds, st, b);
+    hipLaunchKernelGGL(xg_gemm_kernel<K>, dim3(grid), dim3(XG_NW * 64), lds, st, b);
     return 0;
 }
 
