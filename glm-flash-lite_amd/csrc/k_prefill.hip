@@ -836,13 +836,17 @@ __global__ __launch_bounds__(XG_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
                         xv[b] = *reinterpret_cast<const float4*>(xl + b * 16 * XG_XROW + t8 * 64);
                     // steps q = 0..3 of the tile row; the blocks' chains are independent between dependent steps
 #pragma unroll
-                    for (int b = 0; b < NB; ++b) acc[b] = __builtin_amdgcn_mfma_f32_16x16x1f32(xv[b].x, w[0], acc[b], 0, 0, 0);
+                    for (int b = 0; b < NB; ++b)
+                        acc[b] = __builtin_amdgcn_mfma_f32_16x16x1f32(xv[b].x, w[0], acc[b], 0, 0, 0);
 #pragma unroll
-                    for (int b = 0; b < NB; ++b) acc[b] = __builtin_amdgcn_mfma_f32_16x16x1f32(xv[b].y, w[1], acc[b], 0, 0, 0);
+                    for (int b = 0; b < NB; ++b)
+                        acc[b] = __builtin_amdgcn_mfma_f32_16x16x1f32(xv[b].y, w[1], acc[b], 0, 0, 0);
 #pragma unroll
-                    for (int b = 0; b < NB; ++b) acc[b] = __builtin_amdgcn_mfma_f32_16x16x1f32(xv[b].z, w[2], acc[b], 0, 0, 0);
+                    for (int b = 0; b < NB; ++b)
+                        acc[b] = __builtin_amdgcn_mfma_f32_16x16x1f32(xv[b].z, w[2], acc[b], 0, 0, 0);
 #pragma unroll
-                    for (int b = 0; b < NB; ++b) acc[b] = __builtin_amdgcn_mfma_f32_16x16x1f32(xv[b].w, w[3], acc[b], 0, 0, 0);
+                    for (int b = 0; b < NB; ++b)
+                        acc[b] = __builtin_amdgcn_mfma_f32_16x16x1f32(xv[b].w, w[3], acc[b], 0, 0, 0);
                 }
             }
             // chain c of (slot 16 b + 4 (lane / 16) + i, column lane % 16) is register 4c + i of acc[b]: the

@@ -63,7 +63,8 @@ int gfl_ctx_destroy(gfl_ctx* ctx);
  * stream. No counterpart in the reference: it selects launch shapes only, never results (every shape is bit-exact).
  * With shared = 0 (the default) a call of 769..1536 gate|up tile columns (8 picks at I = 1536) runs the relay
  * launches, which put 3 waves on every SIMD; with shared != 0 it keeps the per-slot launches, which leave SIMDs free
- * for the other work. Read at each gfl_moe_forward / gfl_moe_forward_noalloc call (and so fixed in a captured graph). */
+ * for the other work. Read at each gfl_moe_forward / gfl_moe_forward_noalloc call (and so fixed in a captured
+ * graph). */
 int gfl_ctx_set_shared(gfl_ctx* ctx, int shared);
 
 /* Register layer `li`: E experts of a SwiGLU MLP, hidden H, intermediate I (multiples of 256); gate/up are [H->I],
