@@ -92,11 +92,11 @@ int gfl_layer_info(gfl_ctx* ctx, int li, int* info);
  * x: fp16 [M, H]; sel: int64 [M, topk]; w: [M, topk] fp16 (w_is_half=1) or fp32; out: fp32 [M, H].
  * act_limit: SwiGLU clamp (tier_set_act_limit, ft_tier_ext.cpp:629-636), 0 = off. topk <= 16; x 16-byte aligned.
  * M*topk <= 1024: the decode launches (routing plan built in every workgroup). 1024 < M*topk <= 65536 (EXACT modes
- * only; MFMA is refused there): the grouped plan of the prefill path, then the reference's accumulator chains with
- * each weight decoded once per pass of up to 64 of an expert's slots, bit-identical to the reference's EXACT mode at
- * any batch size; there out must be 16-byte aligned too and M*topk*max(H, I) < 2^29. That path uses the prefill
- * workspace (gfl_grouped_reserve sizes it ahead of graph capture; otherwise the first call of a larger size grows
- * it). */
+ * only; MFMA is refused there): the grouped plan of the prefill path, then the reference's accumulator chains (each
+ * chain step one element of a K=1 fp32 MFMA, i.e. an fmaf), each weight decoded once per pass of up to 64 of an
+ * expert's slots, bit-identical to the reference's EXACT mode at any batch size; there out must be 16-byte aligned
+ * too and M*topk*max(H, I) < 2^29. That path uses the prefill workspace (gfl_grouped_reserve sizes it ahead of graph
+ * capture; otherwise the first call of a larger size grows it). */
 int gfl_moe_forward(gfl_ctx* ctx, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half, int M,
                     int topk, float* out, int mode, float act_limit, gfl_stream stream);
 
