@@ -57,6 +57,8 @@ def test_argument_checks_without_device(lib):
     assert lib.gfl_combine(None, 0, 1, None, None, None, None, 0, None) == 1
     with pytest.raises(_native.NativeError):
         _native.check(lib.gfl_stats(None, None, 0))
+    assert lib.gfl_ctx_set_shared(None, 1) == 1
+    assert b"gfl_ctx_set_shared" in lib.gfl_last_error()
 
 
 def test_grouped_rows_host_matches_oracle(oracle):
