@@ -222,7 +222,8 @@ int check_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, con
 {
     const std::string f(who);
     if (!c || !x || !sel || !w || !out) return fail(GFL_EINVAL, f + ": NULL argument");
-    if (li < 0 || li >= (int)c->layers.size() || !c->layers[li].dptrs) return fail(GFL_EINVAL, f + ": layer not registered");
+    if (li < 0 || li >= (int)c->layers.size() || !c->layers[li].dptrs)
+        return fail(GFL_EINVAL, f + ": layer not registered");
     // AFFINE (0) and I16 (2) name the reference CPU engine's speed modes; the device computes EXACT for them, which
     // lies closer to the fp64 expert than either of them does
     if (mode < GFL_MODE_AUTO || mode > GFL_MODE_MFMA)
@@ -422,7 +423,8 @@ int gfl_ctx_create(int device, gfl_ctx** out)
     std::vector<float> tab(65536);
     build_silu_table(tab.data());
     float* dtab = nullptr;
-    if (hipMalloc(&dtab, tab.size() * sizeof(float)) != hipSuccess) return fail(GFL_ENOMEM, "gfl_ctx_create: silu table");
+    if (hipMalloc(&dtab, tab.size() * sizeof(float)) != hipSuccess)
+        return fail(GFL_ENOMEM, "gfl_ctx_create: silu table");
     const hipError_t e = hipMemcpy(dtab, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice);
     if (e != hipSuccess)
     {
@@ -735,7 +737,8 @@ int gfl_split(const int64_t* sel, const uint16_t* w, const uint16_t* z, int bsz,
               int32_t* hpicks, int64_t seq, int li, int keep_ids, int64_t* sel_out, uint16_t* w_out, int64_t* dflag,
               int64_t* stats, const int32_t* rres, gfl_stream stream)
 {
-    if (!sel || !w || !z || !slotof || !score || !pol || !ctrl || !hx || !hpicks || !sel_out || !w_out || !dflag || !stats)
+    if (!sel || !w || !z || !slotof || !score || !pol || !ctrl || !hx || !hpicks || !sel_out || !w_out || !dflag ||
+        !stats)
         return fail(GFL_EINVAL, "gfl_split: NULL argument");
     if (bsz < 1 || n < 1 || n % bsz) return fail(GFL_EINVAL, "gfl_split: n must be a positive multiple of bsz");
     if (n > gfl::MAX_PICKS) return fail(GFL_EINVAL, "gfl_split: n <= 1024");

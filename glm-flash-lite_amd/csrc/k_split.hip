@@ -366,7 +366,8 @@ __global__ __launch_bounds__(1024) void combine_kernel(void* out, int is_half, i
 // The router feeding ft_split (cpu_tier.py:305-307 calls the model's routing_fn, exllamav3's, which returns sel int64
 // [bsz, 8] and w fp16 [bsz, 8]). One wave per token. The score is s = 1 / (1 + e) in fp32 with e = exp(-x) rounded once
 // to fp32 (evaluated in double, so it is the correctly rounded value). k rounds of a wave arg-max over the unused
-// experts, ordered by (score descending, index ascending); the picks' scores are summed in pick order and w_j = s_j / sum
+// experts, ordered by (score descending, index ascending); the picks' scores are summed in pick order and
+// w_j = s_j / sum
 // is rounded to fp16 (round to nearest even). Logits must be finite.
 // one butterfly step of the (score descending, index ascending) arg-max: combine with lane ^ W
 template <int W>

@@ -180,7 +180,8 @@ torch::Tensor tier_forward(int64_t li, torch::Tensor x, torch::Tensor sel, torch
     const c10::DeviceGuard g(dev);
     auto xd = x.to(dev);
     auto x16 = xd.to(torch::kHalf).contiguous();
-    TORCH_CHECK(torch::equal(x16.to(torch::kFloat), xd), "tier_forward: x must be fp16-valued (the expert input is fp16)");
+    TORCH_CHECK(torch::equal(x16.to(torch::kFloat), xd),
+                "tier_forward: x must be fp16-valued (the expert input is fp16)");
     const int E = T->layers[size_t(li)].E;
     TORCH_CHECK(sel.lt(E).all().item<bool>(), "tier_forward: expert id out of range");
     auto seld = sel.to(dev).to(torch::kLong);
