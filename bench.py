@@ -17,11 +17,13 @@ roofline     = the gate|up GEMV kernel (the dominant one) at M=1: algorithmic qu
                the runtime stamps on each launch's own dispatch (hipExtLaunchKernelGGL, through gfl_profile_*) during
                an eager pass on the launch stream; peak = 8 TB/s HBM; traffic = HBM bytes per launch from the
                FETCH_SIZE/WRITE_SIZE counter file (--pmc-probe / --pmc-digest).
+per_M_end_to_end = the decode step a routing_fn caller pays at M=1..4, from router logits to the layer output:
+               gfl_route_split + gfl_moe_forward + gfl_combine in one captured step (128 steps, same protocol).
 configs      = BASELINE configs 0 (one expert per call), 2 (mixed bitrates, Zipf routing), 3 (M=16/32/64) and 4 (42
-               resident layers decoded at M=1; prefill of M=2048 tokens through the MFMA grouped path, as TFLOP/s
-               against 2.5 PF dense fp16, and through the EXACT path); the router (gfl_route) per call; routed layer +
-               shared expert, sequential vs overlapped on a side stream; config 1 in mode MFMA (MFMA-accumulate GEMVs,
-               outside the 2e-3 bar, so never the headline).
+               resident layers decoded at M=1; prefill of M=2048 tokens through the EXACT path, as TFLOP/s against
+               the 157.3 TF dense fp32 MFMA peak its chain steps run on, and through the MFMA grouped path, against
+               2.5 PF dense fp16); the router (gfl_route) per call; routed layer + shared expert, sequential vs
+               overlapped on a side stream.
 cpu_baseline = the reference's own AVX2 expert engine (kernels/cpu_avx2/ft_core.h, built into oracle/_ref) timed on
                this host: decode calls of M tokens x 8 experts cycling a DRAM-cold pool of 288 experts; value = I16
                at M=1; EXACT at M=1..4, AFFINE at M=2..4 and the single expert of config 0 beside it, with the CPU
@@ -40,6 +42,7 @@ METRIC = "MoE-layer decode µs/token at M=1..4 + % HBM roofline on quantized byt
 HBM_PEAK_GBPS = 8000.0
 MODE = 1   # decode mode of every gfl_moe_forward call (1 EXACT, 3 MFMA-accumulate GEMVs); set by --mode
 MFMA_PEAK_TFLOPS = 2500.0   # dense fp16 MFMA
+MFMA_FP32_PEAK_TFLOPS = 157.3   # dense fp32 MFMA
 H, I, E, TOPK, KBITS = 5120, 1536, 288, 8, 3
 XSTEPS = 128   # steps per line of the configs beside the headline
 
@@ -266,24 +269,13 @@ def _dist(ms_per_step, M):
             "p90": round(float(np.percentile(a, 90)), 3)}
 
 
-def time_layer_steps(ctx, layer_ids, routes, M, steps, G, warmup, bytes_per_expert, per_step=1, ngraphs=8):
-    """Graph-timed decode steps. A step is `per_step` consecutive layer calls (call c = s * per_step + i of step s runs
-    layer layer_ids[c % len] with routing c % len(routes)). Up to `ngraphs` graphs of G consecutive steps each are
-    captured (graph j holds steps jG .. jG+G-1) and replayed round-robin, steps / G replays in all, so exactly
-    `steps` steps are timed and a graph comes back only after the others' layers have streamed through (far more bytes
-    than the 256 MB Infinity Cache). Per-step times come from device events between replays: the headline is their
-    median; p10/p90 and the mean over the whole timed region are reported beside it."""
-    import numpy as np
+def graph_time(step, out, steps, G, warmup, ngraphs=8):
+    """Graph-timed steps: step(s) enqueues step s on the current stream. Up to `ngraphs` graphs of G consecutive steps
+    each are captured (graph j holds steps jG .. jG+G-1) and replayed round-robin, steps / G replays in all, so exactly
+    `steps` steps are timed and a graph comes back only after the others' steps have streamed through. Returns
+    (per-step ms from device events between replays, ms over the whole timed region, graphs, whether the last graph's
+    final step replayed equals the same step run eagerly, compared on `out`)."""
     import torch
-    out = torch.empty((M, H), dtype=torch.float32, device="cuda")
-    NR, NL = len(routes), len(layer_ids)
-
-    def step(s_):
-        for i in range(per_step):
-            c = s_ * per_step + i
-            x, sel, w, _ = routes[c % NR]
-            ctx.moe_forward(layer_ids[c % NL], x, sel, w, out, mode=MODE)
-
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
@@ -306,7 +298,6 @@ def time_layer_steps(ctx, layer_ids, routes, M, steps, G, warmup, bytes_per_expe
         g.replay()
     torch.cuda.synchronize()
     samples, total_ms = replay_samples(graphs, reps)
-    # the last graph's final step, replayed and then run eagerly: same output
     graphs[-1].replay()
     torch.cuda.synchronize()
     got = out.clone()
@@ -314,7 +305,26 @@ def time_layer_steps(ctx, layer_ids, routes, M, steps, G, warmup, bytes_per_expe
     torch.cuda.synchronize()
     graph_ok = bool(torch.equal(got, out))
     del graphs
-    per_step_ms = [t / G for t in samples]
+    return [t / G for t in samples], total_ms, ng, graph_ok
+
+
+def time_layer_steps(ctx, layer_ids, routes, M, steps, G, warmup, bytes_per_expert, per_step=1, ngraphs=8):
+    """Graph-timed decode steps (graph_time). A step is `per_step` consecutive layer calls (call c = s * per_step + i
+    of step s runs layer layer_ids[c % len] with routing c % len(routes)); with many layers cycled a graph comes back
+    only after far more bytes than the 256 MB Infinity Cache. The headline is the median of the per-step times;
+    p10/p90 and the mean over the whole timed region are reported beside it."""
+    import numpy as np
+    import torch
+    out = torch.empty((M, H), dtype=torch.float32, device="cuda")
+    NR, NL = len(routes), len(layer_ids)
+
+    def step(s_):
+        for i in range(per_step):
+            c = s_ * per_step + i
+            x, sel, w, _ = routes[c % NR]
+            ctx.moe_forward(layer_ids[c % NL], x, sel, w, out, mode=MODE)
+
+    per_step_ms, total_ms, ng, graph_ok = graph_time(step, out, steps, G, warmup, ngraphs)
     ms = float(np.median(per_step_ms))
     calls = [(s_ * per_step + i) for s_ in range(ng * G) for i in range(per_step)]
     step_bytes = (sum(routes[c % NR][3] * bytes_per_expert(layer_ids[c % NL]) for c in calls) / (ng * G)
@@ -325,6 +335,61 @@ def time_layer_steps(ctx, layer_ids, routes, M, steps, G, warmup, bytes_per_expe
             "steps": steps, "graph_steps": G, "graphs": ng,
             "union_experts": round(float(np.mean([r[3] for r in routes])), 2), "GBps": round(gbps, 1),
             "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "graph_replay_matches_eager": graph_ok}
+
+
+def time_e2e_steps(ctx, layer_ids, M, steps, G, warmup, bytes_per_expert):
+    """The decode step a routing_fn caller pays, from the router's logits to the layer output: one step is
+    gfl_route_split (sigmoid top-8 of fp32 N(0,1) logits [M, 288] and ft_split at full residency, which publishes
+    nothing), gfl_moe_forward on the split's selection, and gfl_combine (no job: it returns without waiting). The
+    router's projection z @ W^T, a plain library GEMM, is outside it. Graph-timed as the headline (graph_time), with
+    32 routings and the layers cycled."""
+    import numpy as np
+    import torch
+    import _native
+    import synth
+    rng = np.random.default_rng(9000 + M)
+    routes = []
+    for _ in range(32):
+        x = rng.standard_normal((M, H)).astype(np.float16)
+        lg = rng.standard_normal((M, E)).astype(np.float32)
+        routes.append((torch.from_numpy(x.view(np.int16)).view(torch.float16).cuda(), torch.from_numpy(lg).cuda(),
+                       len(np.unique(synth.route(lg, TOPK)[0]))))
+    dev = "cuda"
+    n = M * TOPK
+    sel = torch.empty((M, TOPK), dtype=torch.int64, device=dev)
+    w = torch.empty((M, TOPK), dtype=torch.float16, device=dev)
+    so = torch.empty(n, dtype=torch.int64, device=dev)
+    wo = torch.empty(n, dtype=torch.float16, device=dev)
+    ctrl = torch.zeros(16, dtype=torch.int64, device=dev)
+    hx = torch.zeros(n * H, dtype=torch.float16, device=dev)
+    picks = torch.zeros(n * 3, dtype=torch.int32, device=dev)
+    hout = torch.zeros(M * H, dtype=torch.float32, device=dev)
+    dflag = torch.zeros(1, dtype=torch.int64, device=dev)
+    stats = torch.zeros(8, dtype=torch.int64, device=dev)
+    slotof = torch.arange(E, dtype=torch.int32, device=dev)
+    score = torch.zeros(E, dtype=torch.float32, device=dev)
+    pol = torch.tensor([0.4, 0.023, 0.11, 0.104, 0.2, 32, -1, 0] + [0.0] * 12, dtype=torch.float32, device=dev)
+    out = torch.empty((M, H), dtype=torch.float32, device=dev)
+    NR, NL = len(routes), len(layer_ids)
+
+    def step(s_):
+        x, lg, _ = routes[s_ % NR]
+        li = layer_ids[s_ % NL]
+        _native.route_split(lg, TOPK, x, E, 0, slotof, score, pol, ctrl.data_ptr(), hx.data_ptr(), picks.data_ptr(),
+                            s_ + 1, li, 0, sel, w, so, wo, dflag, stats, None)
+        ctx.moe_forward(li, x, so.view(M, TOPK), wo.view(M, TOPK), out, mode=MODE)
+        _native.combine(out, dflag, ctrl.data_ptr(), hout.data_ptr(), stats, 2_000_000_000)
+
+    per_step_ms, total_ms, ng, graph_ok = graph_time(step, out, steps, G, warmup)
+    ms = float(np.median(per_step_ms))
+    union = float(np.mean([r[2] for r in routes]))
+    gbps = (union * bytes_per_expert + M * H * 6) / (ms * 1e-3) / 1e9
+    return {"us_per_token": round(ms * 1e3 / M, 3), "ms_per_step": round(ms, 5),
+            "us_per_token_dist": _dist(per_step_ms, M), "us_per_token_mean": round(total_ms / steps * 1e3 / M, 3),
+            "steps": steps, "graph_steps": G, "graphs": ng, "union_experts": round(union, 2), "GBps": round(gbps, 1),
+            "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "graph_replay_matches_eager": graph_ok,
+            "combine_timeouts": int(stats[6].item()), "split_calls": int(stats[3].item()),
+            "experts_sent_to_host": int(stats[2].item())}
 
 
 def extra_configs(ctx, layers, args):
@@ -354,19 +419,6 @@ def extra_configs(ctx, layers, args):
             per[str(M)] = time_layer_steps(ctx, ids, routes, M, XSTEPS, 4, 8, lambda li, b=bpe: b)
         res["config2_" + name] = per
         print(f"bench: config 2 {name} done ({time.time() - t0:.0f} s)", file=sys.stderr, flush=True)
-    # config 1 in mode MFMA (MFMA-accumulate GEMVs: outside the 2e-3 bar that the EXACT headline meets bit-for-bit;
-    # within the prefill path's bars), on the headline's routings
-    global MODE
-    import _native
-    saved, MODE = MODE, _native.MODE_MFMA
-    per = {}
-    for M in (1, 2, 3, 4):
-        routes = make_routes(M, np.random.default_rng(1000 + M), 32, "uniform")
-        per[str(M)] = time_layer_steps(ctx, list(range(args.layers)), routes, M, XSTEPS, 4, 8,
-                                       lambda li: layers[0].quant_bytes_per_expert)
-    MODE = saved
-    res["config1_mode_mfma"] = per
-    print(f"bench: config 1 in mode MFMA done ({time.time() - t0:.0f} s)", file=sys.stderr, flush=True)
     # config 3: batched decode across conversations on the config-1 layers
     per = {}
     for M in (16, 32, 64):
@@ -547,11 +599,15 @@ def time_prefill(ctx, layer_ids, bytes_per_expert, M, reps, G=4, exact=False):
     tflops = flops / (ms * 1e-3) / 1e12
     union = float(np.mean([r[3] for r in routes]))
     gbps = (union * bytes_per_expert + M * H * 6) / (ms * 1e-3) / 1e9
+    # the EXACT chains run on fp32 MFMAs (v_mfma_f32_16x16x1_4b_f32, each element an fmaf), the grouped GEMMs on
+    # fp16 MFMAs (v_mfma_f32_16x16x32_f16): each is priced against its own dense peak
+    peak = MFMA_FP32_PEAK_TFLOPS if exact else MFMA_PEAK_TFLOPS
     return {"path": "EXACT (gfl_moe_forward)" if exact else "MFMA grouped (gfl_grouped_forward)",
             "tokens": M, "ms_per_layer": round(ms, 4), "us_per_token": round(ms * 1e3 / M, 4),
             "ms_per_layer_replays": [round(t / G, 4) for t in samples],
-            "TFLOPs": round(tflops, 1), "mfma_peak_TFLOPs": MFMA_PEAK_TFLOPS,
-            "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "GBps": round(gbps, 1), "union_experts": union,
+            "TFLOPs": round(tflops, 1), "mfma_peak_TFLOPs": peak,
+            "mfma_peak_kind": "fp32 MFMA (dense)" if exact else "fp16 MFMA (dense)",
+            "mfma_frac": round(tflops / peak, 4), "GBps": round(gbps, 1), "union_experts": union,
             "graph_replay_matches_eager": graph_ok}
 
 
@@ -627,7 +683,7 @@ def main():
     gu_per_expert = layers[0].tbytes[0] + layers[0].tbytes[1] + 2 * 2 * (H + I)
     steps = max(1, args.steps)
     G = graph_size(steps, args.graph_steps)
-    per_M = {}
+    per_M, e2e = {}, {}
     roof = None
     for M in [int(m) for m in args.Ms.split(",")]:
         rng = np.random.default_rng(1000 + M)
@@ -635,6 +691,8 @@ def main():
         r = time_layer_steps(ctx, list(range(args.layers)), routes, M, steps, G, args.warmup,
                              lambda li: layers[li].quant_bytes_per_expert)
         per_M[str(M)] = r
+        e2e[str(M)] = time_e2e_steps(ctx, list(range(args.layers)), M, min(steps, XSTEPS),
+                                     graph_size(min(steps, XSTEPS), args.graph_steps), 8, per_expert)
         if M == 1:
             # live per-kernel timing of the dominant kernel (gate|up GEMV): start/stop events on every launch's dispatch
             out = torch.empty((1, H), dtype=torch.float32, device="cuda")
@@ -670,7 +728,7 @@ def main():
             "config": {"workload": "config1: one 288-expert top-8 MoE layer decode, M=1, H=5120 I=1536 K=3 bpw",
                        "experts": E, "topk": TOPK, "hidden": H, "intermediate": I, "bits": KBITS,
                        "layers_cycled": args.layers, "graph_steps": G},
-            "per_M": per_M, "configs": configs, "roofline": roof, "cpu_baseline": cpu, "setup_s": round(setup_s, 1)}
+            "per_M": per_M, "per_M_end_to_end": e2e, "configs": configs, "roofline": roof, "cpu_baseline": cpu, "setup_s": round(setup_s, 1)}
     print(json.dumps(line), flush=True)
 
 

@@ -16,7 +16,7 @@ SYMBOLS = ("gfl_last_error", "gfl_version", "gfl_ctx_create", "gfl_ctx_destroy",
            "gfl_synth_trellis", "gfl_route",
            "gfl_stats", "gfl_profile_enable", "gfl_profile_read", "gfl_exp_table", "gfl_silu_table",
            "gfl_grouped_plan", "gfl_grouped_reserve", "gfl_layer_info", "gfl_route_split", "gfl_moe_forward_noalloc",
-           "gfl_ctx_set_shared")
+           "gfl_ctx_set_shared", "gfl_ctx_check", "gfl_ingress_serve")
 
 # layout limits of gfl_moe_forward_noalloc's static scratch array (GFL_NOALLOC_MAX_* in include/gfl_moe.h)
 NOALLOC_MAX_PICKS, NOALLOC_MAX_H, NOALLOC_MAX_I = 64, 8192, 4096
@@ -70,6 +70,8 @@ def load(path=LIB_PATH):
     L.gfl_stats.argtypes = [_P, _P, C.c_int]
     L.gfl_profile_enable.argtypes = [_P, C.c_int]
     L.gfl_ctx_set_shared.argtypes = [_P, C.c_int]
+    L.gfl_ctx_check.argtypes = [_P]
+    L.gfl_ingress_serve.argtypes = [_P, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, C.c_int, C.c_float, _P]
     L.gfl_profile_read.argtypes = [_P, _P, _P]
     L.gfl_exp_table.argtypes = [_P, C.c_int]
     L.gfl_silu_table.argtypes = [_P, C.c_int]
@@ -224,6 +226,24 @@ class Context:
         """Tell the context whether other GPU work runs beside its decode calls (gfl_ctx_set_shared): with shared set,
         calls of up to 1,536 gate|up tile columns keep the per-slot launches, which leave SIMDs free."""
         check(load().gfl_ctx_set_shared(self.h, int(bool(shared))))
+        self._shared = bool(shared)
+
+    @property
+    def shared(self):
+        """The flag set_shared last set on this context (False until then)."""
+        return getattr(self, "_shared", False)
+
+    def check(self):
+        """Synchronise the device and raise NativeError when a device-side condition was counted since the last check
+        (an expired relay hand-off wait, a published job the device worker refused): gfl_ctx_check."""
+        check(load().gfl_ctx_check(self.h))
+
+    def ingress_serve(self, li, bsz, topk, ctrl, hx, hpicks, hout, mode=MODE_AUTO, act_limit=0.0):
+        """The device worker (gfl_ingress_serve): compute the job the split published to ctrl / hx / hpicks (integer
+        addresses, as the split takes them) into hout and answer it, on the current stream."""
+        check(load().gfl_ingress_serve(self.h, int(li), int(bsz), int(topk), C.c_void_p(int(ctrl)),
+                                       C.c_void_p(int(hx)), C.c_void_p(int(hpicks)), C.c_void_p(int(hout)), int(mode),
+                                       float(act_limit), _stream()))
 
     def profile(self, enable):
         check(load().gfl_profile_enable(self.h, int(bool(enable))))

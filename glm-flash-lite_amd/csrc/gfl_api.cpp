@@ -77,6 +77,15 @@ struct gfl_ctx
     // superseded workspaces: a graph captured before a workspace grew still holds their addresses, so they stay
     // allocated until gfl_ctx_destroy
     std::vector<void*> retired;
+    // device memory allocated once by gfl_ctx_create: the status words (gfl::GFL_STATUS_*, sticky until
+    // gfl_ctx_check), then the device worker's job state and its picks in selection form (gfl_ingress_serve)
+    void* aux = nullptr;
+    int* status = nullptr;           // [GFL_STATUS_WORDS]
+    int64_t* ing_state = nullptr;    // [4] {job pending and accepted, its sequence number, 0, 0}
+    int64_t* ing_sel = nullptr;      // [MAX_PICKS]
+    float* ing_w = nullptr;          // [MAX_PICKS]
+    // polls of a relay turn wait (GFL_RELAY_SPIN_LIMIT overrides it; 0 makes every wait expire, for tests)
+    int spin_max = gfl::RELAY_SPIN_DEFAULT;
 };
 
 namespace {
@@ -292,16 +301,19 @@ int run_forward(gfl_ctx* c, const Layer& L, const Workspace& ws, const uint16_t*
     auto gate_up = [&] {
         if (L.K[0] == L.K[1])
             return gfl::launch_gate_up(L.K[0], ns, L.dptrs, 0, 2, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                       ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], st);
+                                       ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], c->status,
+                                       c->spin_max, st);
         if (gfl::launch_gate_up(L.K[0], ns, L.dptrs, 0, 1, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], st))
+                                ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], c->status,
+                                c->spin_max, st))
             return -1;
         return gfl::launch_gate_up(L.K[1], ns, L.dptrs, 1, 1, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                   ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], st);
+                                   ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], c->status,
+                                   c->spin_max, st);
     };
     auto down = [&] {
         return gfl::launch_down(L.K[2], ns, L.dptrs, topk, L.H, L.I, umax, P, ws.pv, ws.xtd, ws.yd, ws.out_cnt,
-                                ws.blk_cnt, out, mf, rw[1], st);
+                                ws.blk_cnt, out, mf, rw[1], c->status, c->spin_max, st);
     };
     int r = prof ? staged(c, 1, st, gate_up) : gate_up();
     if (!r) r = prof ? staged(c, 3, st, down) : down();
@@ -335,13 +347,25 @@ __global__ void zero_words(int* p, size_t n)
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
+// per device: the last enqueued no-allocation call's completion. Every eager call waits for it on its own stream and
+// records it again (under g_scratch_mu), so calls from different contexts and streams run one after another on the
+// device's one array. Created by gfl_ctx_create, so the no-allocation calls create nothing.
+hipEvent_t g_scratch_ev[kMaxDevices] = {};
 
-// This device's scratch address (device current). On the first call for the device: look the address up and clear
-// the counter region on `st` (the kernels leave every counter at zero when they finish, so once is enough).
+int scratch_event_for_device(int device)
+{
+    if (device < 0 || device >= kMaxDevices) return GFL_OK;   // gfl_moe_forward_noalloc refuses such a device
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (!g_scratch_ev[device]) GFL_HIP(hipEventCreateWithFlags(&g_scratch_ev[device], hipEventDisableTiming));
+    return GFL_OK;
+}
+
+// This device's scratch address (device current, g_scratch_mu held). On the first call for the device: look the
+// address up and clear the counter region on `st` (the kernels leave every counter at zero when they finish, so once
+// is enough).
 int scratch_for_device(int device, hipStream_t st, void** out)
 {
     if (device < 0 || device >= kMaxDevices) return fail(GFL_EINVAL, "gfl_moe_forward_noalloc: device index too large");
-    std::lock_guard<std::mutex> g(g_scratch_mu);
     if (!g_scratch_ptr[device])
     {
         void* p = nullptr;
@@ -363,7 +387,7 @@ extern "C" {
 
 const char* gfl_last_error(void) { return g_err.c_str(); }
 
-int gfl_version(void) { return 100; }
+int gfl_version(void) { return 101; }
 
 // The SwiGLU gate of the reference is silu(g) = g / (1 + std::exp(-g)) in fp32 (ft_core.h:123), i.e. the host C
 // library's expf. g is always fp16-valued (out_block rounds it, ft_core.h:109), so the exponential the device needs
@@ -431,9 +455,40 @@ int gfl_ctx_create(int device, gfl_ctx** out)
         hipFree(dtab);
         return fail(GFL_ERUNTIME, std::string("gfl_ctx_create: ") + hipGetErrorString(e));
     }
+    // status words, the device worker's job state and picks: one allocation, zeroed
+    const size_t aux_bytes = 256 + 256 + sizeof(int64_t) * gfl::MAX_PICKS + sizeof(float) * gfl::MAX_PICKS;
+    void* aux = nullptr;
+    if (hipMalloc(&aux, aux_bytes) != hipSuccess)
+    {
+        hipFree(dtab);
+        return fail(GFL_ENOMEM, "gfl_ctx_create: status words");
+    }
+    if (hipMemset(aux, 0, aux_bytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+    {
+        hipFree(aux);
+        hipFree(dtab);
+        return fail(GFL_ERUNTIME, "gfl_ctx_create: clearing the status words failed");
+    }
     gfl_ctx* c = new gfl_ctx();
     c->device = device;
     c->silu_tab = dtab;
+    c->aux = aux;
+    c->status = static_cast<int*>(aux);
+    c->ing_state = reinterpret_cast<int64_t*>(static_cast<char*>(aux) + 256);
+    c->ing_sel = reinterpret_cast<int64_t*>(static_cast<char*>(aux) + 512);
+    c->ing_w = reinterpret_cast<float*>(c->ing_sel + gfl::MAX_PICKS);
+    if (const int r = scratch_event_for_device(device))
+    {
+        hipFree(aux);
+        hipFree(dtab);
+        delete c;
+        return r;
+    }
+    if (const char* e = std::getenv("GFL_RELAY_SPIN_LIMIT"))
+    {
+        const long v = std::atol(e);
+        if (v >= 0 && v <= gfl::RELAY_SPIN_DEFAULT) c->spin_max = (int)v;
+    }
     if (const char* e = std::getenv("GFL_SLOTS_PER_PASS"))
     {
         const int v = std::atoi(e);
@@ -464,6 +519,7 @@ int gfl_ctx_destroy(gfl_ctx* c)
     if (c->gws) hipFree(c->gws);
     for (void* p : c->retired) hipFree(p);
     if (c->silu_tab) hipFree(c->silu_tab);
+    if (c->aux) hipFree(c->aux);
     delete c;
     return GFL_OK;
 }
@@ -530,11 +586,21 @@ int gfl_moe_forward_noalloc(gfl_ctx* c, int li, const uint16_t* x, const int64_t
                                     std::to_string(GFL_NOALLOC_MAX_I) + " (the static scratch array's layout)");
     GFL_HIP(hipSetDevice(c->device));
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    std::lock_guard<std::mutex> gs(g_scratch_mu);
     void* base = nullptr;
     if (const int r = scratch_for_device(c->device, st, &base)) return r;
+    hipEvent_t ev = g_scratch_ev[c->device];
+    if (!ev) return fail(GFL_ERUNTIME, std::string(who) + ": no ordering event for this device");
+    // eager calls are ordered through the device's event; a captured call is ordered only within its graph (its
+    // replays must not overlap other calls on the device)
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const bool capturing = hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+    if (!capturing) GFL_HIP(hipStreamWaitEvent(st, ev, 0));
     Workspace ws;
     carve_at(base, GFL_NOALLOC_MAX_PICKS, GFL_NOALLOC_MAX_H, GFL_NOALLOC_MAX_I, L.H, L.I, ws);
-    return run_forward(c, L, ws, x, sel, w, w_is_half, M, topk, out, mode, act_limit, st, false);
+    const int r = run_forward(c, L, ws, x, sel, w, w_is_half, M, topk, out, mode, act_limit, st, false);
+    if (!capturing) GFL_HIP(hipEventRecord(ev, st));
+    return r;
 }
 
 // The prefill workspace of a context, grown on demand (never inside a graph capture). Layout: the grouped plan's ints,
@@ -854,6 +920,54 @@ int gfl_synth_trellis(void* dst, size_t nbytes, uint64_t seed, gfl_stream stream
     gfl::launch_synth(static_cast<uint8_t*>(dst), nbytes, seed, reinterpret_cast<hipStream_t>(stream));
     GFL_HIP(hipGetLastError());
     return GFL_OK;
+}
+
+int gfl_ingress_serve(gfl_ctx* c, int li, int bsz, int topk, int64_t* ctrl, const uint16_t* hx, const int32_t* hpicks,
+                      float* hout, int mode, float act_limit, gfl_stream stream)
+{
+    const char* who = "gfl_ingress_serve";
+    if (!c || !ctrl || !hx || !hpicks || !hout) return fail(GFL_EINVAL, std::string(who) + ": NULL argument");
+    if (mode < GFL_MODE_AUTO || mode > GFL_MODE_I16)
+        return fail(GFL_EINVAL, std::string(who) + ": mode must be -1 (auto), 0 (affine), 1 (exact) or 2 (i16)");
+    if (const int r = check_forward(c, li, hx, c->ing_sel, c->ing_w, bsz, topk, hout, mode, act_limit, who,
+                                    gfl::MAX_PICKS))
+        return r;
+    std::lock_guard<std::mutex> g(c->mu);
+    const Layer& L = c->layers[li];
+    GFL_HIP(hipSetDevice(c->device));
+    if (!c->ws || L.H > c->ws_H || L.I > c->ws_I) return fail(GFL_ERUNTIME, std::string(who) + ": workspace not reserved");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    gfl::launch_ingress_take(ctrl, hpicks, li, bsz, topk, L.E, c->ing_sel, c->ing_w, c->ing_state, c->status, st);
+    GFL_HIP(hipGetLastError());
+    Workspace ws;
+    carve_ws(c, L.H, L.I, ws);
+    if (const int r = run_forward(c, L, ws, hx, c->ing_sel, c->ing_w, 0, bsz, topk, hout, mode, act_limit, st, true))
+        return r;
+    gfl::launch_ingress_answer(ctrl, c->ing_state, st);
+    GFL_HIP(hipGetLastError());
+    return GFL_OK;
+}
+
+int gfl_ctx_check(gfl_ctx* c)
+{
+    if (!c) return fail(GFL_EINVAL, "gfl_ctx_check: NULL context");
+    std::lock_guard<std::mutex> g(c->mu);
+    GFL_HIP(hipSetDevice(c->device));
+    GFL_HIP(hipDeviceSynchronize());
+    int w[gfl::GFL_STATUS_WORDS] = {};
+    GFL_HIP(hipMemcpy(w, c->status, sizeof(w), hipMemcpyDeviceToHost));
+    if (!w[gfl::GFL_STATUS_RELAY_EXPIRED] && !w[gfl::GFL_STATUS_INGRESS_REJECTED]) return GFL_OK;
+    GFL_HIP(hipMemset(c->status, 0, sizeof(w)));
+    GFL_HIP(hipDeviceSynchronize());
+    std::string m = "gfl_ctx_check:";
+    if (w[gfl::GFL_STATUS_RELAY_EXPIRED])
+        m += " " + std::to_string(w[gfl::GFL_STATUS_RELAY_EXPIRED]) +
+             " relay hand-off wait(s) expired (the outputs of the calls concerned are wrong);";
+    if (w[gfl::GFL_STATUS_INGRESS_REJECTED])
+        m += " " + std::to_string(w[gfl::GFL_STATUS_INGRESS_REJECTED]) +
+             " published job(s) refused by the device worker (layer, token count, pick count, token or expert out of "
+             "range; left unanswered);";
+    return fail(GFL_ERUNTIME, m);
 }
 
 int gfl_ctx_set_shared(gfl_ctx* c, int shared)

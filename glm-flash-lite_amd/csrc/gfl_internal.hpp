@@ -42,6 +42,15 @@ constexpr int MAX_TOPK = 16;
 constexpr int MAX_GROUPED_PICKS = 65536;  // tokens * topk per prefill (grouped) call
 constexpr int LDS_LIMIT = 163840;         // bytes of LDS one workgroup may use on gfx950
 
+// Status words of a context (device int32 array, sticky until gfl_ctx_check reads and clears them).
+enum
+{
+    GFL_STATUS_RELAY_EXPIRED = 0,   // relay turn waits (decode relay launches) that ran out of their bound
+    GFL_STATUS_INGRESS_REJECTED = 1,   // published jobs the device worker refused (bad layer, token, expert or weight)
+    GFL_STATUS_WORDS = 4,
+};
+constexpr int RELAY_SPIN_DEFAULT = 1 << 22;   // polls of a relay turn wait (s_sleep 1 between polls: ~0.1 s)
+
 // Device-side routing plan of one forward call (all arrays in device memory, capacity cap_slots picks).
 struct PlanView
 {
@@ -68,12 +77,13 @@ struct PlanView
 int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, const int64_t* sel, const void* w,
                    int w_half, int P, int topk, int E, int H, int I, int umax, const uint16_t* x, float* ygu,
                    uint16_t* xtd, int* act_cnt, const float* silu_tab, float act_limit, const PlanView& pv, float* out,
-                   int mf, int rw, hipStream_t st);
+                   int mf, int rw, int* status, int spin_max, hipStream_t st);
 // down launch: down GEMV + out_block, weighted combine per (token, 128-block) by the token's last expert; mf and ns
 // as for launch_gate_up (the same values for both launches of a call). blk_cnt: [cap][H/128] half-block counters of
 // the one-slot-per-pass EXACT launch (zero between calls). rw as for launch_gate_up (the same value for both).
 int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int umax, int P, const PlanView& pv,
-                const uint16_t* xtd, float* yd, int* out_cnt, int* blk_cnt, float* out, int mf, int rw, hipStream_t st);
+                const uint16_t* xtd, float* yd, int* out_cnt, int* blk_cnt, float* out, int mf, int rw, int* status,
+                int spin_max, hipStream_t st);
 size_t gate_up_lds_bytes(int K, int ns, int H, int P, int E, int mf, int rw);
 size_t down_lds_bytes(int K, int ns, int I, int mf, int rw);
 int launch_dequant(const uint8_t* tr, int k, int n, int K, uint16_t* W, hipStream_t st);
@@ -126,6 +136,11 @@ int launch_split(const int64_t* sel, const uint16_t* w, const uint16_t* z, int n
 void launch_combine(void* out, int is_half, int n, const int64_t* dflag, const int64_t* ctrl, const float* hout,
                     int64_t* stats, int64_t timeout_ns, hipStream_t st);
 void launch_synth(uint8_t* dst, size_t nbytes, uint64_t seed, hipStream_t st);
+// device worker (k_split.hip): the published job as a selection sel [bsz][topk] / w fp32 (state = {accepted, seq}),
+// and the done word once the forward on it has written hout
+void launch_ingress_take(const int64_t* ctrl, const int32_t* hpicks, int li, int bsz, int topk, int E, int64_t* sel,
+                         float* w, int64_t* state, int* status, hipStream_t st);
+void launch_ingress_answer(int64_t* ctrl, const int64_t* state, hipStream_t st);
 int launch_route(const float* logits, int M, int E, int topk, int64_t* sel, uint16_t* w, hipStream_t st);
 int launch_route_split(const float* logits, int M, int ER, int topk, int64_t* sel, uint16_t* w, const uint16_t* z,
                        int H, int E, int first, const int32_t* slotof, const float* score, const float* pol,

@@ -544,10 +544,29 @@ __host__ __device__ constexpr long relay_blocks(long items, int RW)
     return (items / RW + 7) / 8 * 8 * RW;
 }
 
+// Bounded wait for a relay turn: polls `turn` (workgroup-scope acquire) at most spin_max times until it reaches g.
+// Returns false when the bound ran out first; the caller then counts the expiry in the context's status word, which
+// the host reads with gfl_ctx_check (the call's outputs are then wrong, and reported as such). spin_max = 0 polls
+// never and always expires: the host sets it only to test that reporting path.
+__device__ __forceinline__ bool wait_turn(const int* turn, int g, int spin_max)
+{
+    for (int spin = 0; spin < spin_max; ++spin)
+    {
+        if (__hip_atomic_load(turn, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= g) return true;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return false;
+}
+
+__device__ __forceinline__ void count_expiry(int* status)
+{
+    __hip_atomic_fetch_add(&status[GFL_STATUS_RELAY_EXPIRED], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int K, int PF, int RW, class PreLoad, class Pre>
 __device__ __forceinline__ float chain_relay(const uint8_t* __restrict__ col_base, size_t gstride, int TK,
                                              const float* lds_x, uint8_t* slot, float* relay, int* turn, int r,
-                                             PreLoad&& pre_load, Pre&& pre)
+                                             int* status, int spin_max, PreLoad&& pre_load, Pre&& pre)
 {
     constexpr int TB = 32 * K, CH = 2 * K, NCH = 8 * CH, NLD = (NCH + 63) / 64;   // 16-byte chunks
     const int lane = threadIdx.x & 63;
@@ -625,12 +644,7 @@ __device__ __forceinline__ float chain_relay(const uint8_t* __restrict__ col_bas
                 {
                     // the turn of group g: the wave of group g - 1 has written its accumulators (bounded wait: that
                     // wave is resident and waits only for groups before its own)
-                    if (RW > 1)
-                        for (int spin = 0; spin < (1 << 22); ++spin)
-                        {
-                            if (__hip_atomic_load(turn, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= g) break;
-                            __builtin_amdgcn_s_sleep(1);
-                        }
+                    if (RW > 1 && !wait_turn(turn, g, spin_max) && lane == 0) count_expiry(status);
                     acc = relay[lane];
                 }
 #pragma unroll
@@ -650,11 +664,7 @@ __device__ __forceinline__ float chain_relay(const uint8_t* __restrict__ col_bas
     if (RW > 1)
     {
         // the last group's accumulators
-        for (int spin = 0; spin < (1 << 22); ++spin)
-        {
-            if (__hip_atomic_load(turn, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= ngroups) break;
-            __builtin_amdgcn_s_sleep(1);
-        }
+        if (!wait_turn(turn, ngroups, spin_max) && lane == 0) count_expiry(status);
         acc = relay[lane];
     }
     const float a1 = __shfl(acc, n + 16), a2 = __shfl(acc, n + 32), a3 = __shfl(acc, n + 48);
@@ -764,6 +774,8 @@ struct GuArgs
     int per_slot;              // workgroups per slot (one pass each) instead of per union entry (NS == 1 only)
     int mf;                    // MFMA-accumulate mode: down inputs written in the MFMA input layout
     int nmat_launch;           // matrices of this launch (the relay launches' item count)
+    int* status;               // the context's status words (relay waits that expired)
+    int spin_max;              // bound of a relay turn wait, in polls
 };
 
 __device__ __forceinline__ float ld_agent(const float* p)
@@ -1012,6 +1024,8 @@ struct DnArgs
     int ns_cap;                // slots per pass the LDS allocation holds (<= NS)
     int per_slot;              // workgroups per slot (one pass each), as the gate|up launch
     int pv_picks;              // picks of the call (the relay down launch's item count)
+    int* status;               // the context's status words (relay waits that expired)
+    int spin_max;              // bound of a relay turn wait, in polls
 };
 
 // Grid: umax * H/128. Workgroup = 8 waves = one 128-output block of one routed expert, all its slots (with per_slot:
@@ -1330,7 +1344,7 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
         lds_barrier();   // lds_x complete
     };
     const float res = chain_relay<K, NGRP - 1, RW>(col, gstride, TK, lds_x, rings + wid * RB, relay[c],
-                                                   &relay_turn[c], r, pre_load, pre);
+                                                   &relay_turn[c], r, a.status, a.spin_max, pre_load, pre);
     float* ybase = a.ygu + (size_t)mat * a.pv.cap_slots * a.I;
     if (r == 0 && lane < 16) st_agent(&ybase[(size_t)p * a.I + t * 16 + n], res);
     release_agent();
@@ -1431,7 +1445,7 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
         lds_barrier();   // lds_x complete
     };
     const float res = chain_relay<K, NGRP - 1, RW>(col, gstride, TK, lds_x, rings + wid * RB, relay[c],
-                                                   &relay_turn[c], r, pre_load, pre);
+                                                   &relay_turn[c], r, a.status, a.spin_max, pre_load, pre);
     if (r == 0 && lane < 16) st_agent(&a.yd[(size_t)p * a.H + t * 16 + n], res);
     if (ck < a.topk)
     {
@@ -1657,9 +1671,10 @@ size_t down_lds_bytes(int K, int ns, int I, int mf, int rw)
 int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, const int64_t* sel, const void* w,
                    int w_half, int P, int topk, int E, int H, int I, int umax, const uint16_t* x, float* ygu,
                    uint16_t* xtd, int* act_cnt, const float* silu_tab, float act_limit, const PlanView& pv, float* out,
-                   int mf, int rw, hipStream_t st)
+                   int mf, int rw, int* status, int spin_max, hipStream_t st)
 {
     GuArgs a;
+    a.status = status; a.spin_max = spin_max; a.nmat_launch = nmat;
     a.ptrs = ptrs; a.sel = sel; a.w = w; a.w_half = w_half; a.P = P; a.topk = topk; a.E = E; a.H = H; a.I = I;
     a.mat_base = mat_base; a.x = x; a.ygu = ygu; a.xtd = xtd; a.act_cnt = act_cnt; a.silu_tab = silu_tab;
     a.act_limit = act_limit; a.pv = pv; a.out = out;
@@ -1688,9 +1703,11 @@ int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, 
 }
 
 int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int umax, int P, const PlanView& pv,
-                const uint16_t* xtd, float* yd, int* out_cnt, int* blk_cnt, float* out, int mf, int rw, hipStream_t st)
+                const uint16_t* xtd, float* yd, int* out_cnt, int* blk_cnt, float* out, int mf, int rw, int* status,
+                int spin_max, hipStream_t st)
 {
     DnArgs a;
+    a.status = status; a.spin_max = spin_max; a.pv_picks = P;
     a.ptrs = ptrs; a.topk = topk; a.H = H; a.I = I; a.pv = pv; a.xtd = xtd; a.yd = yd; a.out_cnt = out_cnt;
     a.blk_cnt = blk_cnt;
     a.out = out;

@@ -283,9 +283,6 @@ __device__ void split_body(SplitLds& S, const int64_t* __restrict__ sel, const u
             ctrl[4] = npk;
             __threadfence_system();
             __hip_atomic_store(&ctrl[0], seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
-            // a job without picks has a zero partial: it is answered here, as the reference's worker answers every
-            // job it receives (ft_tier_ext.cpp:781-802), and ft_combine adds nothing for it
-            if (npk == 0) __hip_atomic_store(&ctrl[1], seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
             __threadfence_system();
             dflag[0] = seq;
         }
@@ -309,18 +306,15 @@ __global__ __launch_bounds__(SP_T) void split_kernel(const int64_t* __restrict__
 // timeout window can be added by some blocks and dropped by others; its LUT build already moved the decision into a
 // single block (ft_tier_cu.cu:162-201). Same counters: stats[4] waited ns, [5] waits, [6] timeouts, [7] already done.
 // timeout_ticks: bounded wait in wall-clock ticks (the caller converts ns with the device's wall clock rate).
-// A job with no picks (ctrl[4] == 0, answered by the split itself) has a zero partial: +0 is added instead of hout,
-// the sum the reference's worker produces by zeroing hout for an empty route (ft_tier_ext.cpp:384).
 __global__ __launch_bounds__(1024) void combine_kernel(void* out, int is_half, int n, const int64_t* __restrict__ dflag,
                                                        const int64_t* ctrl, const float* hout, int64_t* stats,
                                                        int64_t timeout_ticks, int64_t ns_per_tick_q16)
 {
-    __shared__ int go, empty;
+    __shared__ int go;
     if (threadIdx.x == 0)
     {
         const int64_t s = dflag[0];
         go = s != 0;
-        empty = 0;
         if (go)
         {
             const int64_t* done = ctrl + 1;
@@ -338,7 +332,6 @@ __global__ __launch_bounds__(1024) void combine_kernel(void* out, int is_half, i
                     break;
                 }
             }
-            if (go) empty = __hip_atomic_load(ctrl + 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) == 0;
             const unsigned long long waited = (unsigned long long)(((t1 - t0) * (uint64_t)ns_per_tick_q16) >> 16);
             atomicAdd(reinterpret_cast<unsigned long long*>(&stats[4]), waited);
             atomicAdd(reinterpret_cast<unsigned long long*>(&stats[5]), 1ull);
@@ -346,10 +339,9 @@ __global__ __launch_bounds__(1024) void combine_kernel(void* out, int is_half, i
     }
     __syncthreads();
     if (!go) return;
-    const bool zero = empty;
     for (int i = threadIdx.x; i < n; i += blockDim.x)
     {
-        const float v = zero ? 0.0f : __hip_atomic_load(&hout[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        const float v = __hip_atomic_load(&hout[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         if (is_half)
         {
             uint16_t* o = reinterpret_cast<uint16_t*>(out);
@@ -357,6 +349,105 @@ __global__ __launch_bounds__(1024) void combine_kernel(void* out, int is_half, i
         }
         else reinterpret_cast<float*>(out)[i] += v;
     }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// device worker: the consumer of a published job (run_job + worker_main, ft_tier_ext.cpp:400-627, 781-802)
+// ---------------------------------------------------------------------------------------------------------------
+
+// The worker's read of a published job. A job is pending when ctrl[0] (the split's sequence number) differs from
+// ctrl[1] (the last one answered). It is accepted when it names layer li, ntok = ctrl[3] <= bsz tokens and
+// np = ctrl[4] <= ntok * topk picks, each pick (token, expert, weight bits) with a token in [0, ntok), an expert in
+// [0, E) and at most topk picks per token (run_job indexes its route and the layer with them unchecked). Its picks
+// are laid out as a selection sel int64 [bsz][topk] / w fp32 [bsz][topk]: token t's picks in pick order, then -1 / 0.
+// That is run_job's route[t] (picks pushed in pick order), which moe_forward walks token-major, so the forward on
+// this selection builds the reference's jobs in the reference's order. No pending job, or a refused one: the
+// selection stays empty (a refused job counts in status[GFL_STATUS_INGRESS_REJECTED] and is never answered, so the
+// combine waits out its timeout and counts it). state = {1 if accepted, the job's sequence number}.
+__global__ __launch_bounds__(256) void ingress_take_kernel(const int64_t* ctrl, const int32_t* hpicks, int li, int bsz,
+                                                           int topk, int E, int64_t* sel, float* w, int64_t* state,
+                                                           int* status)
+{
+    __shared__ int s_job, s_ntok, s_np, s_bad;
+    __shared__ int64_t s_seq;
+    __shared__ int pt[MAX_PICKS], pe[MAX_PICKS], pw[MAX_PICKS], cnt[MAX_PICKS];
+    const int t = threadIdx.x, nt = blockDim.x, n = bsz * topk;
+    for (int i = t; i < n; i += nt) { sel[i] = -1; w[i] = 0.0f; }
+    for (int i = t; i < bsz; i += nt) cnt[i] = 0;
+    if (t == 0)
+    {
+        const int64_t seq = __hip_atomic_load(&ctrl[0], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+        const int64_t done = __hip_atomic_load(&ctrl[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        const int64_t jl = __hip_atomic_load(&ctrl[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        const int64_t jt = __hip_atomic_load(&ctrl[3], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        const int64_t jp = __hip_atomic_load(&ctrl[4], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        const bool pending = seq != done;
+        const bool ok = jl == li && jt >= 0 && jt <= bsz && jp >= 0 && jp <= jt * topk;
+        s_job = !pending ? 0 : ok ? 1 : -1;
+        s_seq = seq;
+        s_ntok = ok ? (int)jt : 0;
+        s_np = ok ? (int)jp : 0;
+        s_bad = 0;
+    }
+    __syncthreads();
+    const int np = s_np, ntok = s_ntok;
+    if (s_job == 1)
+    {
+        for (int k = t; k < np; k += nt)
+        {
+            const int tk = hpicks[3 * k], e = hpicks[3 * k + 1];
+            pt[k] = tk;
+            pe[k] = e;
+            pw[k] = hpicks[3 * k + 2];
+            if (tk < 0 || tk >= ntok || e < 0 || e >= E) s_bad = 1;
+            else if (atomicAdd(&cnt[tk], 1) >= topk) s_bad = 1;
+        }
+        __syncthreads();
+        if (!s_bad)
+            for (int tk = t; tk < ntok; tk += nt)
+            {
+                int c = 0;
+                for (int k = 0; k < np; ++k)
+                    if (pt[k] == tk)
+                    {
+                        sel[tk * topk + c] = pe[k];
+                        w[tk * topk + c] = __int_as_float(pw[k]);
+                        ++c;
+                    }
+            }
+    }
+    if (t == 0)
+    {
+        const bool accepted = s_job == 1 && !s_bad;
+        state[0] = accepted ? 1 : 0;
+        state[1] = s_seq;
+        if (s_job == -1 || (s_job == 1 && s_bad))
+            __hip_atomic_fetch_add(&status[GFL_STATUS_INGRESS_REJECTED], 1, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// The worker's answer (worker_main, ft_tier_ext.cpp:797-799): after the forward has written hout, the done word
+// ctrl[1] = the job's sequence number, released at system scope (hout first).
+__global__ void ingress_answer_kernel(int64_t* ctrl, const int64_t* state)
+{
+    if (threadIdx.x == 0 && state[0] == 1)
+    {
+        __threadfence_system();
+        __hip_atomic_store(&ctrl[1], state[1], __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
+void launch_ingress_take(const int64_t* ctrl, const int32_t* hpicks, int li, int bsz, int topk, int E, int64_t* sel,
+                         float* w, int64_t* state, int* status, hipStream_t st)
+{
+    hipLaunchKernelGGL(ingress_take_kernel, dim3(1), dim3(256), 0, st, ctrl, hpicks, li, bsz, topk, E, sel, w, state,
+                       status);
+}
+
+void launch_ingress_answer(int64_t* ctrl, const int64_t* state, hipStream_t st)
+{
+    hipLaunchKernelGGL(ingress_answer_kernel, dim3(1), dim3(64), 0, st, ctrl, state);
 }
 
 // ---------------------------------------------------------------------------------------------------------------

@@ -4,8 +4,11 @@
 // cpu_tier's `_H` and `_CU` handles can be this one module.
 //
 // With every expert resident in HBM there is no host worker pool: tier_forward runs the layer on the GPU through
-// gfl_moe_forward / gfl_grouped_forward, and the split / combine pair runs gfl_split / gfl_combine. Work goes to the
-// current HIP stream of the tensors' device. threads / cpus / swz are recorded, nothing more.
+// gfl_moe_forward, and the split / combine pair runs gfl_split / gfl_combine. The worker that tier_start starts is the
+// device worker: while it runs, a job that ft_split publishes to the tier's ingress buffers is computed and answered
+// on the split's stream right after the split (gfl_ingress_serve), as the reference's worker thread computes and
+// answers every job it finds (ft_tier_ext.cpp:781-802). Work goes to the current HIP stream of the tensors' device.
+// threads / cpus / swz are recorded, nothing more.
 #include <torch/extension.h>
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
@@ -147,6 +150,8 @@ void tier_add_layer(int64_t li, torch::Tensor ptrs, torch::Tensor suh_g, torch::
     T->layers[size_t(li)] = std::move(L);
 }
 
+// Starts the device worker (the reference pins a worker thread to cpu0, ft_tier_ext.cpp:781-802; here the jobs are
+// served on the device, so cpu0 is recorded only).
 void tier_start(int64_t cpu0)
 {
     TORCH_CHECK(T && !T->running, "init first / already running");
@@ -160,9 +165,10 @@ void tier_stop()
     T->running = false;
 }
 
-// Every mode number of the reference is accepted. Mode 1 (EXACT) is bit-identical to the reference's EXACT mode at
-// every size up to 65,536 picks; modes -1, 0 and 2 (the reference CPU engine's speed choices, ft_tier_ext.cpp:900)
-// compute EXACT too up to 1,024 picks and take the MFMA grouped path above that.
+// Every mode number of the reference is accepted, and every one computes EXACT, bit-identical to the reference's
+// EXACT mode at every size up to 65,536 picks (as gfl_moe_forward does for them): the reference CPU engine's speed
+// modes (-1 auto, 0 AFFINE, 2 I16, ft_tier_ext.cpp:396) trade accuracy for CPU time, and EXACT lies closer to the fp64
+// expert than either. The MFMA grouped path (gfl_grouped_forward) is not reached from here.
 torch::Tensor tier_forward(int64_t li, torch::Tensor x, torch::Tensor sel, torch::Tensor w, int64_t mode)
 {
     TORCH_CHECK(T && !T->running, "tier_forward: worker running");
@@ -189,15 +195,8 @@ torch::Tensor tier_forward(int64_t li, torch::Tensor x, torch::Tensor sel, torch
     auto wd = w.to(dev).contiguous();
     auto out = torch::empty({ m, int64_t(T->H) }, torch::dtype(torch::kFloat).device(dev));
     const hipStream_t st = cur_stream(dev);
-    const bool grouped = m * k > 1024 && mode != 1;
-    if (grouped)
-        check_rc(gfl_grouped_forward(T->ctx, int(li), static_cast<const uint16_t*>(x16.data_ptr()),
-                                     seld.data_ptr<int64_t>(), wd.data_ptr(), 0, int(m), int(k), out.data_ptr<float>(),
-                                     g_act_limit, st));
-    else
-        check_rc(gfl_moe_forward(T->ctx, int(li), static_cast<const uint16_t*>(x16.data_ptr()),
-                                 seld.data_ptr<int64_t>(), wd.data_ptr(), 0, int(m), int(k), out.data_ptr<float>(),
-                                 GFL_MODE_EXACT, g_act_limit, st));
+    check_rc(gfl_moe_forward(T->ctx, int(li), static_cast<const uint16_t*>(x16.data_ptr()), seld.data_ptr<int64_t>(),
+                             wd.data_ptr(), 0, int(m), int(k), out.data_ptr<float>(), int(mode), g_act_limit, st));
     const int64_t valid = sel.ge(0).sum().item<int64_t>();
     T->jobs += 1;
     T->experts += valid;
@@ -299,6 +298,18 @@ void ft_split(torch::Tensor sel, torch::Tensor w, torch::Tensor z, int64_t E, in
                        reinterpret_cast<int32_t*>(hpicks), seq, int(li), int(keep_ids), sel_out.data_ptr<int64_t>(),
                        static_cast<uint16_t*>(w_out.data_ptr()), dflag.data_ptr<int64_t>(), stats.data_ptr<int64_t>(),
                        rres.numel() ? rres.data_ptr<int32_t>() : nullptr, cur_stream(sel.device())));
+    // the device worker serves the tier's own ingress buffers while it runs (a split on other buffers is left to
+    // whoever consumes them)
+    if (T && T->running && ctrl == reinterpret_cast<int64_t>(T->ingress[0].data_ptr()))
+    {
+        const int li_ = int(li);
+        TORCH_CHECK(li_ >= 0 && li_ < int(T->layers.size()) && T->layers[size_t(li_)].E > 0,
+                    "ft_split: the tier's worker has no layer ", li_);
+        check_rc(gfl_ingress_serve(T->ctx, li_, bsz, n / bsz, reinterpret_cast<int64_t*>(ctrl),
+                                   reinterpret_cast<const uint16_t*>(hx), reinterpret_cast<const int32_t*>(hpicks),
+                                   static_cast<float*>(T->ingress[3].data_ptr()), T->mode, g_act_limit,
+                                   cur_stream(sel.device())));
+    }
 }
 
 void ft_combine(torch::Tensor out, torch::Tensor dflag, int64_t ctrl, int64_t hout, torch::Tensor stats,

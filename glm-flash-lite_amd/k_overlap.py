@@ -62,12 +62,14 @@ class SharedOverlap:
         with torch.cuda.stream(self.side):
             self.ctx.moe_forward(li, x, s1, w1, y)
             self.join.record(self.side)
-        # the routed call keeps launch shapes that leave SIMDs free for the side stream (same results)
+        # the routed call keeps launch shapes that leave SIMDs free for the side stream (same results); the caller's
+        # own setting is restored afterwards
+        prev = routed.shared
         routed.set_shared(True)
         try:
             routed.moe_forward(li, x, sel, w, out)
         finally:
-            routed.set_shared(False)
+            routed.set_shared(prev)
         main.wait_event(self.join)
         out.add_(y)
         self.overlapped += 1

@@ -67,6 +67,16 @@ int gfl_ctx_destroy(gfl_ctx* ctx);
  * graph). */
 int gfl_ctx_set_shared(gfl_ctx* ctx, int shared);
 
+/* Synchronises the context's device, then reads and clears its status words, which count since the last check:
+ * relay hand-off waits of the decode launches that ran out of their bound (the outputs of the calls concerned are
+ * wrong), and published jobs that gfl_ingress_serve refused. Returns GFL_ERUNTIME with the counts in
+ * gfl_last_error() when either is nonzero, else GFL_OK. The reference's counterpart of a worker failure is an
+ * exception out of tier_forward or the LUT worker's failed word ctrl[7] (kernels/cpu_avx2/ft_tier_ext.cpp:744-775);
+ * these conditions arise on the device, so they are collected there and surfaced here. The relay wait's bound is
+ * 2^22 polls (about 0.1 s); the environment variable GFL_RELAY_SPIN_LIMIT, read by gfl_ctx_create, lowers it (0 makes
+ * every wait expire: only for testing this report). */
+int gfl_ctx_check(gfl_ctx* ctx);
+
 /* Register layer `li`: E experts of a SwiGLU MLP, hidden H, intermediate I (multiples of 256); gate/up are [H->I],
  * down [I->H], each an EXL3 trellis of K bits per weight (k_gate/k_up/k_down in 2..5) in 16x16 tiles stored
  * row-major [k/16][n/16].
@@ -107,8 +117,10 @@ int gfl_moe_forward(gfl_ctx* ctx, int li, const uint16_t* x, const int64_t* sel,
  * everything it needs was allocated by gfl_ctx_create and gfl_register_layer. Same arguments and results as
  * gfl_moe_forward (bit-identical), within the array's layout: M*topk <= GFL_NOALLOC_MAX_PICKS, the layer's
  * H <= GFL_NOALLOC_MAX_H and I <= GFL_NOALLOC_MAX_I, else GFL_EINVAL. All calls on one device share the array (its
- * counters are cleared on the device's first call and left at zero by every call): calls that overlap on one device,
- * from any context or stream, race. */
+ * counters are cleared on the device's first call and left at zero by every call). Eager calls from any context or
+ * stream on one device are ordered through a per-device event (each waits for the previous call and records its own
+ * end), so they run one after another. A call captured into a HIP graph is ordered only inside that graph: replays
+ * of it that overlap other calls on the device, eager or replayed, race. */
 #define GFL_NOALLOC_MAX_PICKS 64
 #define GFL_NOALLOC_MAX_H 8192
 #define GFL_NOALLOC_MAX_I 4096
@@ -158,10 +170,10 @@ int gfl_dequant(const void* trellis, int k, int n, int K, uint16_t* out, gfl_str
  * tensors as pointers: sel int64 [n], w fp16 [n], z fp16 [bsz, H], slotof int32 [E], score fp32 [E], pol fp32 [20],
  * ctrl int64 [>=5] / hx fp16 [bsz*H] / hpicks int32 [n*3] (host-mapped or device memory), sel_out int64 [n],
  * w_out fp16 [n], dflag int64 [1], stats int64 [8], rres int32 [E] or NULL. n = bsz*topk <= 1024, E <= 1024.
- * Outputs are the reference's bit for bit; in addition a published job without picks (the handshake policy pol[7]
- * with nothing for the host) is answered here (ctrl[1] = seq), as the reference's worker answers every job, so that
- * gfl_combine does not wait for a host that has nothing to do. Scores must be finite (the reference's two split
- * kernels order NaN scores differently from each other). */
+ * Outputs are the reference's bit for bit, including its handshake: a published job (ctrl[0] = seq, dflag = seq) is
+ * answered by its consumer, a reference host worker (worker_main, ft_tier_ext.cpp:781-802) or the device worker
+ * gfl_ingress_serve, never by the split itself. Scores must be finite (the reference's two split kernels order NaN
+ * scores differently from each other). */
 int gfl_split(const int64_t* sel, const uint16_t* w, const uint16_t* z, int bsz, int n, int H, int E, int first,
               const int32_t* slotof, const float* score, const float* pol, int64_t* ctrl, uint16_t* hx,
               int32_t* hpicks, int64_t seq, int li, int keep_ids, int64_t* sel_out, uint16_t* w_out, int64_t* dflag,
@@ -177,10 +189,24 @@ int gfl_route_split(const float* logits, int M, int E_route, int topk, int64_t* 
                     uint16_t* w_out, int64_t* dflag, int64_t* stats, const int32_t* rres, gfl_stream stream);
 
 /* ft_combine (kernels/cpu_avx2/ft_tier_cu.cu:273-294): when dflag != 0 wait (at most timeout_ns) for the done word
- * ctrl[1] >= dflag, then out += hout (+0 for a job without picks, ctrl[4] == 0, which gfl_split answers itself). out fp32 or fp16 (out_is_half) [n]; stats as ft_split's (4 wait ns, 5 waits,
+ * ctrl[1] >= dflag, then out += hout. out fp32 or fp16 (out_is_half) [n]; stats as ft_split's (4 wait ns, 5 waits,
  * 6 timeouts, 7 already done). */
 int gfl_combine(void* out, int out_is_half, int n, const int64_t* dflag, const int64_t* ctrl, const float* hout,
                 int64_t* stats, int64_t timeout_ns, gfl_stream stream);
+
+/* The device worker: run_job + worker_main's answer (kernels/cpu_avx2/ft_tier_ext.cpp:400-627, 781-802) on the
+ * device, stream-ordered after the split that published the job. When a job is pending (ctrl[0] != ctrl[1]):
+ * hout[t] = sum over its ctrl[4] picks (token, expert, fp32 weight bits, in hpicks) of w * expert(hx[t]) for layer li,
+ * in the reference's job order, rows of tokens without picks zeroed (run_job zeroes hout for an empty job), then the
+ * done word ctrl[1] = ctrl[0] (system-scope release after hout). Every expert is resident, so every job is computed.
+ * The job must name layer li (ctrl[2]), ntok = ctrl[3] <= bsz tokens and at most topk picks per token, with tokens and
+ * experts in range; a job that does not is left unanswered (gfl_combine then times out and counts it) and counted in
+ * the status words (gfl_ctx_check). No pending job: hout's bsz rows are zeroed and nothing is answered.
+ * hx fp16 [bsz, H] (16-byte aligned), hpicks int32 [bsz*topk][3], hout fp32 [bsz, H], ctrl int64 [>= 5]: the
+ * buffers gfl_split published to (host-mapped or device memory). bsz*topk <= 1024; mode -1..2 (computed EXACT, as
+ * gfl_moe_forward). Only one consumer may serve a ctrl block: do not run a host worker on the same ctrl. */
+int gfl_ingress_serve(gfl_ctx* ctx, int li, int bsz, int topk, int64_t* ctrl, const uint16_t* hx,
+                      const int32_t* hpicks, float* hout, int mode, float act_limit, gfl_stream stream);
 
 /* Expert-major routing rows (tier_lut_build_grouped_rows, ft_tier_ext.cpp:1047-1097), HOST arrays:
  * sel int64 [T*K], w fp32 [T*K], take uint8 [E] -> experts [<=E], offsets [<=E+1], row_token / row_weight [<=T*K].

@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_version_and_error_string(lib):
-    assert lib.gfl_version() == 100
+    assert lib.gfl_version() == 101
     assert isinstance(lib.gfl_last_error(), bytes)
 
 
@@ -59,6 +59,8 @@ def test_argument_checks_without_device(lib):
         _native.check(lib.gfl_stats(None, None, 0))
     assert lib.gfl_ctx_set_shared(None, 1) == 1
     assert b"gfl_ctx_set_shared" in lib.gfl_last_error()
+    assert lib.gfl_ctx_check(None) == 1 and b"NULL" in lib.gfl_last_error()
+    assert lib.gfl_ingress_serve(None, 0, 1, 8, None, None, None, None, -1, 0.0, None) == 1
 
 
 def test_grouped_rows_host_matches_oracle(oracle):

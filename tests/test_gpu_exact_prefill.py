@@ -105,7 +105,9 @@ def test_exact_at_the_pick_maximum_rows_bitexact(gpu, oracle):
 @pytest.mark.gpu
 def test_exact_large_graph_replay(gpu):
     """Workspace reserved up front (gfl_grouped_reserve), then an M=300 top-8 EXACT call captured in a HIP graph and
-    replayed three times with eager calls between: every replay equals the eager result."""
+    replayed three times with eager calls between: a decode-sized one, one above 1,024 picks within the reserve, and
+    one above the reserved 4,096 picks, which grows the prefill workspace (the captured graph keeps the retired
+    buffer's addresses). Every replay equals the eager result."""
     import torch
     H, I, E, li = 512, 256, 16, 62
     _layer(gpu, li, E, H, I)
@@ -133,3 +135,16 @@ def test_exact_large_graph_replay(gpu):
         assert torch.equal(out, ref)
         gpu.moe_forward(li, x[:50], sel[:50], w[:50], other[:50])   # an eager call in between (other sizes)
         torch.cuda.synchronize()
+    # eager calls of the prefill path between replays: 1,600 picks inside the reserve, then 4,800 beyond it
+    xb = torch.from_numpy((rng.standard_normal((600, H)) * 0.4).astype(np.float16)).cuda()
+    sb = torch.from_numpy(_route("zipf", 600, 8, E, rng)).cuda()
+    wb = torch.from_numpy(rng.random((600, 8)).astype(np.float32)).cuda()
+    big = torch.empty((600, H), dtype=torch.float32, device="cuda")
+    for m in (200, 600):
+        gpu.moe_forward(li, xb[:m], sb[:m], wb[:m], big[:m])
+        torch.cuda.synchronize()
+        assert torch.all(torch.isfinite(big[:m]))
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay after an eager call of {m * 8} picks"

@@ -1,18 +1,21 @@
-"""Prefill path (gfl_grouped_forward: MFMA grouped GEMMs) against the reference's EXACT mode and its fp64 expert.
+"""Prefill path (gfl_grouped_forward: MFMA grouped GEMMs, an explicit opt-in outside the north-star bar) against the
+reference's EXACT mode and its fp64 expert.
 
 The grouped path keeps the bit-exact fp16 weights and every fp16 rounding point of the reference's transforms but
-forms the hidden-dimension sums in MFMA order, so it differs from EXACT by fp32 accumulation rounding. Bars, taken from
-how far the reference's own fp64 expert (ref_expert) lies from EXACT on config-0 experts (max-abs 2.9e-3..3.3e-3 of the
-output RMS, RMS difference ~3.5e-4 of it):
-  * RMS of the difference <= 1e-3 of the output RMS;
-  * max-abs difference <= 1e-2 of the output RMS;
+forms the hidden-dimension sums in MFMA order, so it differs from EXACT by fp32 accumulation rounding, about as far as
+the reference's own fp64 expert (ref_expert) lies from EXACT on config-0 experts (max-abs 2.9e-3..3.3e-3 of the output
+RMS). It misses the 2e-3 max-abs bar that EXACT meets, so no reference mode number routes to it (tier_forward and
+gfl_moe_forward compute EXACT at every size). Bars, set to what the path measures on these cases (max-abs 1.5e-3 to
+3.6e-3 of the output RMS, rel-RMS 1.6e-4 to 3.6e-4; config 4: 2.93e-3 and 3.6e-4):
+  * RMS of the difference <= 5e-4 of the output RMS;
+  * max-abs difference <= 4e-3 of the output RMS;
   * for one expert, the distance to the fp64 reference is within 2x of EXACT's own distance to it.
 """
 import numpy as np
 import pytest
 
-REL_RMS = 1e-3
-MAX_ABS = 1e-2
+REL_RMS = 5e-4
+MAX_ABS = 4e-3
 
 
 def _layer(gpu, li, E, H, I, Ks=(3, 3, 3)):

@@ -63,6 +63,11 @@ def test_overlap_equals_routed_plus_shared(gpu, oracle, setup, M):
     setup["so"].forward(gpu, setup["li"], xd, seld, wd, seq, overlap=False)
     torch.cuda.synchronize()
     assert np.array_equal(seq.cpu().numpy(), got)
+    # the routed context's own shared flag survives the overlapped call, whichever it was
+    for flag in (True, False):
+        gpu.set_shared(flag)
+        setup["so"].forward(gpu, setup["li"], xd, seld, wd, out)
+        assert gpu.shared is flag
 
 
 def test_overlap_graph_replays(gpu, setup):

@@ -302,6 +302,45 @@ def test_config2_full_shape_bitexact(gpu, oracle, layer_kind, M):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("M", [16, 32, 64])
+def test_config3_full_shape_bitexact(gpu, oracle, M):
+    """Config 3 at its shape: M = 16, 32 and 64 tokens, each routed top-8 over 288 experts with uniform N(0,1) logits,
+    H=5120, I=1536, 3 bpw, through the default launch choice (above 8 tokens: a workgroup per routed expert taking
+    its slots two per pass, gu_kernel / down_kernel with NS = 2). The layer holds the routed union (up to 240
+    experts, 2.1 GB); the oracle evaluates rows 0, M/2 and M-1 with the whole call's jobs (moe_forward_rows), so each
+    checked row's combine order is the full batch's."""
+    import synth
+    from oracle import Mat
+    H, I, E = 5120, 1536, 288
+    rng = np.random.default_rng(3000 + M)
+    (sel, w16), _ = synth.route_uniform(M, E, 8, rng)
+    L, sel2 = _union_layer(gpu, 40 + M, sel, H, I, (3, 3, 3))
+    x16 = rng.standard_normal((M, H)).astype(np.float16)
+    got = _forward(gpu, 40 + M, x16, sel2, w16)
+    rows = [0, M // 2, M - 1]
+    need = {int(e) for r in rows for e in sel2[r] if e >= 0}
+    dummy = None
+    ex = []
+    for e in range(L.E):
+        if e in need or dummy is None:
+            mats = []
+            for p in range(3):
+                tr, suh, svh = L.matrix(e, p)
+                k, n = (H, I) if p < 2 else (I, H)
+                mats.append(Mat(tr, suh, svh, k, n, 3))
+            ex.append(tuple(mats))
+            if dummy is None:
+                dummy = ex[-1]
+        else:
+            ex.append(dummy)       # never read: no checked row picks it
+    want = oracle.moe_forward_rows(ex, x16.astype(np.float32), sel2, w16.astype(np.float32), rows, mode=1)
+    mx, rms, nbad = _report(f"config3 M={M} union={L.E} rows {rows}", got[rows], want)
+    assert mx <= TOL * rms
+    assert nbad == 0
+    assert np.all(np.isfinite(got)) and float(np.sqrt(np.mean(got.astype(np.float64) ** 2))) > 0
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("mode", [1, 0, 2, -1])
 def test_every_mode_number_computes_exact(gpu, oracle, mode):
     """tier_forward's mode numbers (-1 auto, 0 AFFINE, 1 EXACT, 2 I16; ft_tier_ext.cpp:865-904) all compute EXACT

@@ -64,8 +64,9 @@ def test_route_empty_and_errors(gpu):
 def test_routing_hook_decode_layer(gpu, oracle, handshake):
     """routing.RoutingHook: routing_fn(bsz, cfg, z, params) -> the split's selection from one fused router+split
     launch, equal to the router's picks (every expert resident); the layer on that selection is the oracle's EXACT
-    layer on the router's closed-form picks; the combine hook leaves it unchanged (with the handshake policy the
-    split publishes an empty job and answers it itself, so the combine does not wait: stats[6] stays 0)."""
+    layer on the router's closed-form picks; the combine hook leaves its values unchanged (with the handshake policy
+    the split publishes an empty job, which the hook's device worker answers, so the combine does not wait: stats[6]
+    stays 0)."""
     import torch
     import _native
     import routing
@@ -78,7 +79,7 @@ def test_routing_hook_decode_layer(gpu, oracle, handshake):
     z = torch.from_numpy(rng.standard_normal((bsz, H)).astype(np.float16)).cuda()
     ing = routing.Ingress(H, max_bsz=4, topk=8)
     pol = torch.tensor([0.4, 0.023, 0.11, 0.104, 0.2, 32, -1, float(handshake)] + [0.0] * 12, device="cuda")
-    hook = routing.RoutingHook(W, E, 8, li, torch.arange(E, dtype=torch.int32, device="cuda"), pol, ing)
+    hook = routing.RoutingHook(W, E, 8, li, torch.arange(E, dtype=torch.int32, device="cuda"), pol, ing, ctx=gpu)
     sel, w = hook.routing_fn(bsz, None, z, {})
     out = torch.empty((bsz, H), dtype=torch.float32, device="cuda")
     gpu.moe_forward(li, z, sel, w, out)

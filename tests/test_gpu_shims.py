@@ -27,7 +27,7 @@ def tier(gpu):
     hout = torch.zeros(4 * H, dtype=torch.float32, device="cuda")
     ft_tier.tier_init(1, [0], ctrl, hx, picks, hout, -1, H, I, len(mods), 0)
     ft_tier.add_pool_layers(pool, bits=[L.Ks for L in layers])
-    yield dict(pool=pool, layers=layers, mods=mods, H=H, I=I, E=E)
+    yield dict(pool=pool, layers=layers, mods=mods, H=H, I=I, E=E, ctrl=ctrl, hx=hx, picks=picks, hout=hout)
     ft_tier.tier_set_act_limit(0.0)
     ft_tier.tier_shutdown()
 
@@ -62,21 +62,21 @@ def test_tier_forward_reference_signature_bitexact(tier, oracle, li):
     assert len(st) == 12 and st[0] >= 1
 
 
-def test_tier_forward_auto_prefill_takes_grouped_path(tier, oracle):
-    """m * k > 1024 in auto mode: the MFMA grouped path, within its bars of the oracle's EXACT result (RMS of the
-    difference <= 1e-3, max-abs <= 1e-2 of the output RMS)."""
+@pytest.mark.parametrize("mode", [-1, 0, 2])
+def test_tier_forward_prefill_sizes_every_mode_exact(tier, oracle, mode):
+    """m * k > 1024 in the reference's auto, AFFINE and I16 modes: the EXACT layer, bit for bit (one policy for every
+    mode number at every size, as gfl_moe_forward; the MFMA grouped path is only reached through
+    gfl_grouped_forward)."""
     import ft_tier
-    rng = np.random.default_rng(70)
+    rng = np.random.default_rng(70 + mode)
     m = 300
     x = torch.from_numpy((rng.standard_normal((m, tier["H"])) * 0.5).astype(np.float16).astype(np.float32))
     sel = torch.from_numpy(np.stack([rng.choice(tier["E"], 4, replace=False) for _ in range(m)]).astype(np.int32))
     sel[7, 1] = -1
     w = torch.from_numpy(rng.random((m, 4)).astype(np.float32))
-    got = ft_tier.tier_forward(1, x, sel, w, -1).numpy().astype(np.float64)
+    got = ft_tier.tier_forward(1, x, sel, w, mode).numpy()
     want = oracle.moe_forward(_experts(oracle, tier["layers"][1]), x.numpy(), sel.numpy(), w.numpy(), mode=1)
-    rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
-    d = got - want
-    assert float(np.sqrt(np.mean(d ** 2))) <= 1e-3 * rms and float(np.abs(d).max()) <= 1e-2 * rms
+    assert np.array_equal(got, want)
 
 
 def test_tier_forward_exact_prefill_bitexact(tier, oracle):
@@ -193,36 +193,107 @@ def test_serve_stats_after_forward(tier):
     assert all(p["bad_slots"] == 0 and p["bad_tables"] == 0 for p in v)
 
 
-def test_handshake_layer_through_the_extension(tier, oracle):
-    """cpu_tier's decode sequence through the extension's own entry points (ft_split, tier_forward, ft_combine) with
-    the handshake policy (pol[7] = 1, GLM53_CT_HANDSHAKE): every layer publishes an empty job, which the split answers
-    itself, so ft_combine returns without waiting out its timeout (stats[6] == 0) and leaves the layer output (the
-    EXACT layer, bit for bit) as it was."""
+GPU_LI = 200   # the tier's layers li in the session context (ids no other test module registers)
+
+
+@pytest.fixture
+def worker(tier, gpu):
+    """tier_start: the extension's device worker serves the jobs ft_split publishes to the tier's ingress buffers.
+    The device share of each layer runs on a second context holding the same layers (tier_forward is refused while
+    the worker runs, as in the reference)."""
     import ft_tier
-    H, E = tier["H"], tier["E"]
+    for li, L in enumerate(tier["layers"]):
+        L.register(gpu, GPU_LI + li)
+    tier["ctrl"].zero_()
+    ft_tier.tier_start(0)
+    try:
+        yield tier
+    finally:
+        ft_tier.tier_stop()
+
+
+def _split_on_tier(t, sel, w, z, slotof, pol, seq, li):
+    import ft_tier
+    n = sel.numel()
+    so, wo = torch.empty(n, dtype=torch.int64, device="cuda"), torch.empty(n, dtype=torch.float16, device="cuda")
+    dflag, stats = torch.zeros(1, dtype=torch.int64, device="cuda"), torch.zeros(8, dtype=torch.int64, device="cuda")
+    ft_tier.ft_split(sel, w, z, t["E"], 0, slotof, torch.zeros(t["E"], device="cuda"), pol, t["ctrl"].data_ptr(),
+                     t["hx"].data_ptr(), t["picks"].data_ptr(), seq, li, 0, so, wo, dflag, stats,
+                     torch.empty(0, dtype=torch.int32, device="cuda"))
+    return so, wo, dflag, stats
+
+
+def test_handshake_layer_through_the_extension(worker, gpu, oracle):
+    """cpu_tier's decode sequence through the extension's own entry points (ft_split, ft_combine) with the handshake
+    policy (pol[7] = 1, GLM53_CT_HANDSHAKE): every layer publishes an empty job, which the worker started by
+    tier_start answers on the device (hout zeroed, as run_job does), so ft_combine returns without waiting out its
+    timeout (stats[6] == 0) and leaves the values of the layer output (the EXACT layer, bit for bit) as they were."""
+    import ft_tier
+    t = worker
+    H, E = t["H"], t["E"]
     rng = np.random.default_rng(88)
     x = torch.from_numpy((rng.standard_normal((1, H)) * 0.5).astype(np.float16)).cuda()
     sel = torch.from_numpy(rng.choice(E, 4, replace=False).astype(np.int64)).cuda()
     w = torch.from_numpy(rng.random(4).astype(np.float16)).cuda()
-    ctrl = torch.zeros(16, dtype=torch.int64, device="cuda")
-    hx = torch.zeros(H, dtype=torch.float16, device="cuda")
-    hp = torch.zeros(4 * 3, dtype=torch.int32, device="cuda")
-    hout = torch.full((H,), 7.0, dtype=torch.float32, device="cuda")
-    so, wo = torch.empty(4, dtype=torch.int64, device="cuda"), torch.empty(4, dtype=torch.float16, device="cuda")
-    dflag, stats = torch.zeros(1, dtype=torch.int64, device="cuda"), torch.zeros(8, dtype=torch.int64, device="cuda")
+    t["hout"].fill_(7.0)
     pol = torch.tensor([0.4, 0.023, 0.11, 0.104, 0.2, 32, -1, 1] + [0.0] * 12, device="cuda")
-    pool = tier["pool"]
-    want = oracle.moe_forward(_experts(oracle, tier["layers"][0]), x.float().cpu().numpy(),
+    pool = t["pool"]
+    want = oracle.moe_forward(_experts(oracle, t["layers"][0]), x.float().cpu().numpy(),
                               sel.cpu().numpy().reshape(1, 4), w.float().cpu().numpy().reshape(1, 4), mode=1)
     for seq in (1, 2, 3):
-        ft_tier.ft_split(sel, w, x, E, pool.first, pool.slotof[0], torch.zeros(E, device="cuda"), pol,
-                         ctrl.data_ptr(), hx.data_ptr(), hp.data_ptr(), seq, 0, 0, so, wo, dflag, stats,
-                         torch.empty(0, dtype=torch.int32, device="cuda"))
-        out = ft_tier.tier_forward(0, x.float(), so.view(1, 4), wo.float().view(1, 4), 1)
-        before = out.clone()
-        ft_tier.ft_combine(out, dflag, ctrl.data_ptr(), hout.data_ptr(), stats, 2_000_000_000)
+        so, wo, dflag, stats = _split_on_tier(t, sel, w, x, pool.slotof[0], pol, seq, 0)
+        out = torch.empty((1, H), dtype=torch.float32, device="cuda")
+        gpu.moe_forward(GPU_LI, x, so.view(1, 4), wo.view(1, 4), out)
         torch.cuda.synchronize()
-        assert int(dflag.item()) == seq and int(ctrl[1].item()) == seq
+        before = out.clone()
+        ft_tier.ft_combine(out, dflag, t["ctrl"].data_ptr(), t["hout"].data_ptr(), stats, 2_000_000_000)
+        torch.cuda.synchronize()
+        assert int(dflag.item()) == seq and int(t["ctrl"][1].item()) == seq
+        assert not torch.any(t["hout"][:H])
         assert torch.equal(out, before) and np.array_equal(out.cpu().numpy(), want)
-    st = stats.tolist()
-    assert st[6] == 0 and st[5] == 3 and st[7] == 3
+        st = stats.tolist()
+        assert st[6] == 0 and st[5] == 1 and st[7] == 1
+
+
+@pytest.mark.parametrize("li", [0, 1])
+def test_extension_worker_computes_published_picks(worker, gpu, oracle, li):
+    """A residency row with misses (experts 3..5) and the policy forcing every miss to the host lane: ft_split
+    publishes those picks to the tier, the device worker computes them into hout (the reference's job order) and
+    answers, ft_combine adds them to the device share: the layer is the reference's composition, bit for bit, and
+    no pick is lost."""
+    import ft_tier
+    t = worker
+    H, E, bsz = t["H"], t["E"], 3
+    rng = np.random.default_rng(120 + li)
+    x = torch.from_numpy((rng.standard_normal((bsz, H)) * 0.5).astype(np.float16)).cuda()
+    sel = torch.from_numpy(np.stack([rng.choice(E, 4, replace=False) for _ in range(bsz)]).astype(np.int64)).cuda()
+    w = torch.from_numpy((rng.random((bsz, 4)) + 0.1).astype(np.float16)).cuda()
+    slotof = torch.tensor([0, 1, 2, -1, -1, -1], dtype=torch.int32, device="cuda")
+    pol = torch.tensor([0.4, 0.023, 0.11, 0.104, 0.2, 32, 100, 0] + [0.0] * 12, device="cuda")
+    so, wo, dflag, stats = _split_on_tier(t, sel.view(-1), w.view(-1), x, slotof, pol, 1, li)
+    out = torch.empty((bsz, H), dtype=torch.float32, device="cuda")
+    gpu.moe_forward(GPU_LI + li, x, so.view(bsz, 4), wo.view(bsz, 4), out)
+    ft_tier.ft_combine(out, dflag, t["ctrl"].data_ptr(), t["hout"].data_ptr(), stats, 500_000_000)
+    torch.cuda.synchronize()
+    ctrl = t["ctrl"].cpu().numpy()
+    np_ = int(ctrl[4])
+    assert int(dflag.item()) == 1 and ctrl[0] == 1 and ctrl[1] == 1 and np_ > 0 and stats.tolist()[6] == 0
+    picks = t["picks"].cpu().numpy()[:3 * np_].reshape(-1, 3)
+    hs = np.full((bsz, 4), -1, np.int64)
+    hw = np.zeros((bsz, 4), np.float32)
+    cnt = [0] * bsz
+    for tk, e, wb in picks:
+        hs[tk, cnt[tk]] = e
+        hw[tk, cnt[tk]] = np.array([wb], np.int32).view(np.float32)[0]
+        cnt[tk] += 1
+    ds = so.view(bsz, 4).cpu().numpy()
+    for tk in range(bsz):
+        assert sorted([int(e) for e in ds[tk] if e >= 0] + [int(e) for e in hs[tk] if e >= 0]) == \
+            sorted(int(e) for e in sel[tk].cpu().numpy())
+    ex = _experts(oracle, t["layers"][li])
+    xf = x.float().cpu().numpy()
+    want = (oracle.moe_forward(ex, xf, ds, wo.view(bsz, 4).float().cpu().numpy(), mode=1)
+            + oracle.moe_forward(ex, xf, hs, hw, mode=1)).astype(np.float32)
+    assert np.array_equal(out.cpu().numpy(), want)
+    with pytest.raises(RuntimeError, match="worker running"):
+        ft_tier.tier_forward(li, x.float().cpu(), sel.int().cpu(), w.float().cpu(), 1)

@@ -92,8 +92,8 @@ def _check(oracle, c, tag):
         assert np.array_equal(g["ctrl"][2:5], r["ctrl"][2:5]), tag
         assert np.array_equal(g["hpicks"][:3 * npk].reshape(-1, 3), r["hpicks"]), tag
         assert np.array_equal(g["hx"], c["z"].reshape(-1)), tag
-        # a job without picks is answered on the device (the reference's worker answers every job it receives)
-        assert g["ctrl"][1] == (c["seq"] if npk == 0 else 0), tag
+        # the split never answers a job itself (its consumer, a host or the device worker, writes ctrl[1])
+        assert g["ctrl"][1] == 0, tag
     else:
         assert not g["ctrl"].any(), tag
         assert (g["hpicks"] == -7).all(), tag
@@ -182,16 +182,19 @@ def test_combine_timeout_drops_partial(gpu):
     assert 15_000 <= st[4] <= 50_000_000     # waited about the timeout (wall-clock ticks converted to ns)
 
 
-def test_combine_empty_job_adds_zero(gpu):
-    """A job without picks (ctrl[4] == 0) has a zero partial, whatever hout holds: out + 0 (the reference's worker
-    zeroes hout for an empty route, ft_tier_ext.cpp:384), including -0 + 0 = +0."""
+def test_combine_adds_hout_of_an_empty_job(gpu):
+    """A job without picks (ctrl[4] == 0) is combined like any other: out += hout, which its worker zeroed (run_job,
+    ft_tier_ext.cpp:431-435), so -0 + 0 = +0; the combine itself does not look at ctrl[4] (ft_tier_cu.cu:205-235)."""
     n = 5120
     out0 = np.random.default_rng(40).standard_normal(n).astype(np.float32)
     out0[:3] = [-0.0, 0.0, -1.5]
     ctrl = np.zeros(16, np.int64); ctrl[0] = ctrl[1] = 9
-    got, st = _combine_gpu(out0.copy(), 9, ctrl, np.full(n, 123.0, np.float32), np.zeros(8, np.int64), 10**9)
+    got, st = _combine_gpu(out0.copy(), 9, ctrl, np.zeros(n, np.float32), np.zeros(8, np.int64), 10**9)
     assert np.array_equal(got, out0 + np.float32(0.0)) and np.signbit(got[0]) == False
     assert list(st[5:8]) == [1, 0, 1]
+    hout = np.full(n, 123.0, np.float32)
+    got, st = _combine_gpu(out0.copy(), 9, ctrl, hout, np.zeros(8, np.int64), 10**9)
+    assert np.array_equal(got, (out0 + hout).astype(np.float32))
 
 
 def _route_split_gpu(logits, topk, c):
@@ -248,8 +251,10 @@ def test_route_split_matches_router_then_split(gpu, oracle, kind):
 
 def test_handshake_layer_does_not_wait(gpu):
     """cpu_tier's decode sequence at full residency with the handshake policy (pol[7] = 1, GLM53_CT_HANDSHAKE):
-    ft_split publishes an empty job every layer, the layer runs on the device, ft_combine returns without waiting
-    out its timeout (stats[6] == 0) and leaves the layer output as it was."""
+    ft_split publishes an empty job every layer and leaves it unanswered (the reference's handshake); the device
+    worker (gfl_ingress_serve) answers it as the reference's worker does, zeroing hout; the layer runs on the device
+    and ft_combine returns without waiting out its timeout (stats[6] == 0) and leaves the layer output's values as
+    they were."""
     import torch
     import _native
     import synth
@@ -273,8 +278,12 @@ def test_handshake_layer_does_not_wait(gpu):
         _native.split(sel_d.view(-1), w_d.view(-1), x, E, 0, torch.arange(E, dtype=torch.int32, device="cuda"),
                       torch.zeros(E, device="cuda"), pol, ctrl.data_ptr(), hx.data_ptr(), hp.data_ptr(), seq, 60, 0,
                       so, wo, dflag, stats, None)
+        torch.cuda.synchronize()
+        assert int(ctrl[0].item()) == seq and int(ctrl[1].item()) == seq - 1   # published, not answered by the split
+        gpu.ingress_serve(60, 1, 8, ctrl.data_ptr(), hx.data_ptr(), hp.data_ptr(), hout.data_ptr())
         gpu.moe_forward(60, x, so.view(1, 8), wo.view(1, 8), out)
         torch.cuda.synchronize()
+        assert not torch.any(hout)
         before = out.clone()
         _native.combine(out, dflag, ctrl.data_ptr(), hout.data_ptr(), stats, 2_000_000_000)
         torch.cuda.synchronize()

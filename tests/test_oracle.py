@@ -380,16 +380,54 @@ def test_grouped_rows_brute_force(oracle):
         oracle.grouped_rows(sel, badw, np.ones(E, np.uint8), E)
 
 
-def test_router_closed_form(oracle):
+def _round_fraction(q, p):
+    """The binary float with p significand bits nearest to the positive Fraction q (ties to even), as a Fraction;
+    normal range only (the values below are far from both ends of fp16 and fp32)."""
+    from fractions import Fraction
+    e = q.numerator.bit_length() - q.denominator.bit_length()
+    if Fraction(2) ** e > q:
+        e -= 1
+    ulp = Fraction(2) ** (e - p + 1)                # q in [2^e, 2^(e+1))
+    n, r = divmod(q, ulp)
+    n = int(n)
+    if r * 2 > ulp or (r * 2 == ulp and n % 2 == 1):
+        n += 1
+    return n * ulp
+
+
+def test_router_weights_exact_rounding(oracle):
+    """The router's picks and fp16 weights pinned bit for bit by exact rational arithmetic with explicit
+    round-to-nearest-even at each of the closed form's rounding points: e = exp(-x) rounded to fp32, s = 1 / (1 + e)
+    (the add and the division each rounded to fp32), top-k by (score descending, index ascending), the picked scores
+    summed in pick order with each add rounded to fp32, and w = s / sum rounded to fp32 and then to fp16.
+    The final fp16 rounding hides most one-ulp differences of the fp32 sum, so besides random rows the cases include
+    rows of a 60,000-row N(0,1) draw (seed 2024) on which a plausible mistake flips fp16 bits: summing in reverse pick
+    order (rows 1464, 4784, 4950, 12179), an exactly rounded sum (831, 6281, 8226) or a single rounding of s / sum
+    straight to fp16 (881, 2333, 3122)."""
+    import math
+    from fractions import Fraction
+    f32 = lambda q: _round_fraction(q, 24)
     rng = np.random.default_rng(9)
-    logits = rng.standard_normal((6, 288)).astype(np.float32)
-    sel, w = oracle.route(logits, 8)
-    s = 1.0 / (1.0 + np.exp(-logits.astype(np.float64)))
-    for m in range(6):
-        assert list(sel[m]) == list(np.argsort(-s[m], kind="stable")[:8])
-        ww = w[m].view(np.float16).astype(np.float64)
-        assert abs(ww.sum() - 1.0) < 4e-3
-        assert np.allclose(ww, s[m][sel[m]] / s[m][sel[m]].sum(), atol=5e-4)
+    draw = np.random.default_rng(2024).standard_normal((60000, 288)).astype(np.float32)
+    near = draw[[1464, 4784, 4950, 12179, 831, 6281, 8226, 881, 2333, 3122]]
+    cases = [((rng.standard_normal((M, E)) * scale).astype(np.float32), topk)
+             for M, E, topk, scale in [(6, 288, 8, 1.0), (4, 288, 8, 3.0), (3, 64, 16, 0.5)]] + [(near, 8)]
+    for logits, topk in cases:
+        M, E = logits.shape
+        sel, w = oracle.route(logits, topk)
+        for m in range(M):
+            s = []
+            for x in logits[m]:
+                ex = f32(Fraction(math.exp(-float(x))))
+                s.append(f32(1 / f32(1 + ex)))
+            order = sorted(range(E), key=lambda i: (-s[i], i))[:topk]
+            assert list(sel[m]) == order, (M, m)
+            tot = Fraction(0)
+            for i in order:
+                tot = f32(tot + s[i])
+            want = [_round_fraction(f32(s[i] / tot), 11) for i in order]
+            got = [Fraction(float(v)) for v in w[m].view(np.float16)]
+            assert got == want, (M, m)
 
 
 def test_package_synth_matches_checker(oracle):

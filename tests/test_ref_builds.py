@@ -53,3 +53,14 @@ def test_server_build_distance(oracle, ref, ref_server):
     r = _rel(b, a)
     print(f"EXACT server build vs A/B build: max-abs/RMS {r:.2e}, differing {int(np.count_nonzero(a != b))}/{a.size}")
     assert r <= 2e-3
+
+
+@pytest.mark.parametrize("limit", [0.05, 0.5])
+def test_swiglu_clamp_equals_the_reference_engine(oracle, ref, limit):
+    """The oracle's act_mul clamp (exllamav3's semantics: u clipped to [-L, L], silu(g) capped at L; ft_core.h:123-132)
+    against the reference engine's own ACT_LIMIT path, bit for bit, at limits where the clamp changes the layer."""
+    ex, x, sel, w = _case(oracle, 512, 256, 6, 9, 4, 11)
+    x = (x * 4).astype(np.float16).astype(np.float32)
+    got = oracle.moe_forward(ex, x, sel, w, mode=1, act_limit=limit)
+    assert not np.array_equal(got, oracle.moe_forward(ex, x, sel, w, mode=1))
+    assert np.array_equal(got, ref.moe_forward(ex, x, sel, w, mode=1, act_limit=limit))

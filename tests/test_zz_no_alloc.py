@@ -64,3 +64,43 @@ def test_noalloc_small_shape_and_limits(gpu):
     out = torch.empty(x.shape, dtype=torch.float32, device="cuda")
     with pytest.raises(_native.NativeError, match="M\\*topk <= 64"):
         gpu.moe_forward_noalloc(li, x, sel, w, out)
+
+
+@pytest.mark.gpu
+def test_noalloc_graph_replays(gpu):
+    """A no-allocation call captured into a HIP graph (torch.cuda.graph) replays to the eager result, with eager
+    no-allocation calls of other sizes and a gfl_moe_forward call run between the replays."""
+    import torch
+    import synth
+    H, I, E, li = 512, 256, 6, 952
+    synth.SynthLayer(li, E, H, I, (3, 3, 3)).register(gpu, li)
+    rng = np.random.default_rng(123)
+    x, sel, w = _inputs(rng, 2, 4, E, H)
+    want = torch.empty(x.shape, dtype=torch.float32, device="cuda")
+    gpu.moe_forward(li, x, sel, w, want)
+    out = torch.full(x.shape, float("nan"), dtype=torch.float32, device="cuda")
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        gpu.moe_forward_noalloc(li, x, sel, w, out)       # warm-up on a side stream, as torch's graph recipe does
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    assert torch.equal(out, want)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        gpu.moe_forward_noalloc(li, x, sel, w, out)
+    others = [_inputs(rng, M, 4, E, H) for M in (9, 1)]
+    for rep in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {rep}"
+        xo, so, wo = others[rep % 2]
+        a = torch.empty(xo.shape, dtype=torch.float32, device="cuda")
+        b = torch.empty(xo.shape, dtype=torch.float32, device="cuda")
+        gpu.moe_forward_noalloc(li, xo, so, wo, a)          # eager work between the replays
+        gpu.moe_forward(li, xo, so, wo, b)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b)
+    del g
