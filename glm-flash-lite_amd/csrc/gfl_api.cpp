@@ -529,8 +529,9 @@ int gfl_register_layer(gfl_ctx* c, int li, int E, int H, int I, int k_gate, int 
     if (!c || !ptrs) return fail(GFL_EINVAL, "gfl_register_layer: NULL argument");
     if (li < 0 || li > 4096) return fail(GFL_EINVAL, "gfl_register_layer: layer index out of range");
     if (E < 1 || E > gfl::MAX_EXPERTS) return fail(GFL_EINVAL, "gfl_register_layer: E must be 1..1024");
-    if (H < 256 || I < 256 || H % 256 || I % 256)
-        return fail(GFL_EINVAL, "gfl_register_layer: H and I must be multiples of 256");
+    if (H < 256 || I < 256 || H % 256 || I % 256 || H > GFL_MAX_DIM || I > GFL_MAX_DIM)
+        return fail(GFL_EINVAL, "gfl_register_layer: H and I must be multiples of 256 up to " +
+                                    std::to_string(GFL_MAX_DIM));
     if (!k_ok(k_gate) || !k_ok(k_up) || !k_ok(k_down)) return fail(GFL_EINVAL, "gfl_register_layer: K must be 2..5");
     // trellis words are read 4 bytes at a time, suh/svh 16 bytes at a time
     for (int i = 0; i < E * 9; ++i)
@@ -715,6 +716,9 @@ int gfl_grouped_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* se
     std::lock_guard<std::mutex> g(c->mu);
     const Layer& L = c->layers[li];
     if (L.H % 256 || L.I % 256) return fail(GFL_EINVAL, "gfl_grouped_forward: H and I must be multiples of 256");
+    // the GEMMs address their fp16 inputs [picks][max(H, I)] through 32-bit buffer offsets
+    if ((size_t)M * topk * (size_t)std::max(L.H, L.I) * 2 > (size_t)0x7fffffff)
+        return fail(GFL_EINVAL, "gfl_grouped_forward: M*topk*max(H, I) must stay below 2^30");
     GFL_HIP(hipSetDevice(c->device));
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const int P = M * topk, E = L.E, H = L.H, I = L.I;

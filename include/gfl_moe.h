@@ -77,9 +77,13 @@ int gfl_ctx_set_shared(gfl_ctx* ctx, int shared);
  * every wait expire: only for testing this report). */
 int gfl_ctx_check(gfl_ctx* ctx);
 
-/* Register layer `li`: E experts of a SwiGLU MLP, hidden H, intermediate I (multiples of 256); gate/up are [H->I],
- * down [I->H], each an EXL3 trellis of K bits per weight (k_gate/k_up/k_down in 2..5) in 16x16 tiles stored
- * row-major [k/16][n/16].
+/* Largest hidden or intermediate size a layer may have: every trellis matrix then stays below 2^31 bytes (at most
+ * 32768 x 32768 x 5/8), so the kernels' 32-bit buffer offsets cannot wrap. */
+#define GFL_MAX_DIM 32768
+
+/* Register layer `li`: E experts of a SwiGLU MLP, hidden H, intermediate I (multiples of 256 up to GFL_MAX_DIM);
+ * gate/up are [H->I], down [I->H], each an EXL3 trellis of K bits per weight (k_gate/k_up/k_down in 2..5) in 16x16
+ * tiles stored row-major [k/16][n/16].
  * ptrs: HOST array [E][9] of DEVICE addresses per expert:
  *   trellis gate, up, down; suh_gate, svh_gate, suh_up, svh_up, suh_down, svh_down (fp16 sign/scale vectors).
  * Trellis addresses must be 4-byte aligned, suh/svh addresses 16-byte aligned (both hold for torch allocations).
@@ -135,13 +139,14 @@ int gfl_moe_forward_noalloc(gfl_ctx* ctx, int li, const uint16_t* x, const int64
 
 /* Routed-expert forward of one layer for prefill-sized M (the north star's MFMA grouped GEMM), same arguments and
  * result layout as gfl_moe_forward: x fp16 [M, H], sel int64 [M, topk] (ids outside [0, E) skipped), w fp16 or fp32
- * [M, topk], out fp32 [M, H]; M*topk <= 65536; x and out 16-byte aligned. Rows are grouped expert-major
- * (tier_lut_build_grouped_rows, kernels/cpu_avx2/ft_tier_ext.cpp:1047-1097), gate|up and down run as
- * v_mfma_f32_16x16x32_f16 grouped GEMMs on the
- * bit-exact dequantized fp16 weights, the transforms keep the reference's fp16 rounding points and the combine its job
- * order (kernels/cpu_avx2/ft_core.h:933-1033). The hidden-dimension sums are formed in MFMA order, so results differ
- * from the EXACT mode of gfl_moe_forward by fp32 accumulation rounding (as the reference's own fp64 expert,
- * ref_expert, ft_core.h:1674-1691, does). Profiling stage 2. */
+ * [M, topk], out fp32 [M, H]; M*topk <= 65536 and M*topk*max(H, I) < 2^30; x and out 16-byte aligned. Rows are
+ * grouped expert-major (tier_lut_build_grouped_rows, kernels/cpu_avx2/ft_tier_ext.cpp:1047-1097), gate|up and down
+ * run as v_mfma_f32_16x16x32_f16 grouped GEMMs on the bit-exact dequantized fp16 weights, the transforms keep the
+ * reference's fp16 rounding points and the combine its job order (kernels/cpu_avx2/ft_core.h:933-1033). The
+ * hidden-dimension sums are formed in MFMA order, so results differ from the EXACT mode of gfl_moe_forward by fp32
+ * accumulation rounding (max-abs up to about 3.6e-3 of the output RMS, as far as the reference's own fp64 expert,
+ * ref_expert, ft_core.h:1674-1691, lies from EXACT): outside the 2e-3 bar, so this is an explicit opt-in that no
+ * reference mode number reaches (tier_forward and gfl_moe_forward compute EXACT at every size). Profiling stage 2. */
 int gfl_grouped_forward(gfl_ctx* ctx, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half,
                         int M, int topk, float* out, float act_limit, gfl_stream stream);
 
