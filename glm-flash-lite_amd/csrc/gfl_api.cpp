@@ -295,7 +295,7 @@ int run_forward(gfl_ctx* c, const Layer& L, const Workspace& ws, const uint16_t*
     }
     if (gfl::gate_up_lds_bytes(L.K[0], ns, L.H, P, L.E, mf, rw[0]) > gfl::LDS_LIMIT ||
         gfl::gate_up_lds_bytes(L.K[1], ns, L.H, P, L.E, mf, rw[0]) > gfl::LDS_LIMIT ||
-        gfl::down_lds_bytes(L.K[2], ns, L.I, mf, rw[1]) > gfl::LDS_LIMIT)
+        gfl::down_lds_bytes(L.K[2], ns, L.I, P, L.E, mf, rw[1]) > gfl::LDS_LIMIT)
         return fail(GFL_EINVAL, "gfl_moe_forward: shape needs more than 160 KB of LDS per workgroup");
     const int wh = w_is_half ? 1 : 0;
     auto gate_up = [&] {
@@ -312,8 +312,8 @@ int run_forward(gfl_ctx* c, const Layer& L, const Workspace& ws, const uint16_t*
                                    c->spin_max, st);
     };
     auto down = [&] {
-        return gfl::launch_down(L.K[2], ns, L.dptrs, topk, L.H, L.I, umax, P, ws.pv, ws.xtd, ws.yd, ws.out_cnt,
-                                ws.blk_cnt, out, mf, rw[1], c->status, c->spin_max, st);
+        return gfl::launch_down(L.K[2], ns, L.dptrs, topk, L.H, L.I, umax, P, L.E, sel, w, wh, ws.pv, ws.xtd, ws.yd,
+                                ws.out_cnt, ws.blk_cnt, out, mf, rw[1], c->status, c->spin_max, st);
     };
     int r = prof ? staged(c, 1, st, gate_up) : gate_up();
     if (!r) r = prof ? staged(c, 3, st, down) : down();

@@ -81,11 +81,11 @@ int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, 
 // down launch: down GEMV + out_block, weighted combine per (token, 128-block) by the token's last expert; mf and ns
 // as for launch_gate_up (the same values for both launches of a call). blk_cnt: [cap][H/128] half-block counters of
 // the one-slot-per-pass EXACT launch (zero between calls). rw as for launch_gate_up (the same value for both).
-int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int umax, int P, const PlanView& pv,
-                const uint16_t* xtd, float* yd, int* out_cnt, int* blk_cnt, float* out, int mf, int rw, int* status,
-                int spin_max, hipStream_t st);
+int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int umax, int P, int E, const int64_t* sel,
+                const void* w, int w_half, const PlanView& pv, const uint16_t* xtd, float* yd, int* out_cnt,
+                int* blk_cnt, float* out, int mf, int rw, int* status, int spin_max, hipStream_t st);
 size_t gate_up_lds_bytes(int K, int ns, int H, int P, int E, int mf, int rw);
-size_t down_lds_bytes(int K, int ns, int I, int mf, int rw);
+size_t down_lds_bytes(int K, int ns, int I, int P, int E, int mf, int rw);
 int launch_dequant(const uint8_t* tr, int k, int n, int K, uint16_t* W, hipStream_t st);
 
 // Grouped-rows plan of the prefill path (device arrays; P picks, E experts, M tokens).

@@ -168,12 +168,13 @@ __device__ void build_plan(const int64_t* __restrict__ sel, int P, int E, const 
 // The same plan for P <= 64 picks from one wave, without LDS atomics or intermediate barriers (the decode case):
 // lane p holds pick p; all derived quantities are ballot/prefix arithmetic over the wave. first[] is written only for
 // the experts present (the only entries read).
-__device__ void build_plan_wave(const int64_t* __restrict__ sel, int P, int E, const LPlan& L, int* hdr)
+// e64_lane: lane p's pick sel[p] (-1 for lanes >= P), already in a register of wave 0
+__device__ void build_plan_wave_from(int64_t e64_lane, int P, int E, const LPlan& L, int* hdr)
 {
     const int lane = threadIdx.x & 63;
     if (threadIdx.x < 64)
     {
-        const int64_t e64 = lane < P ? sel[lane] : -1;
+        const int64_t e64 = lane < P ? e64_lane : -1;
         const bool ok = e64 >= 0 && e64 < E;
         const int e = ok ? (int)e64 : -1;
         const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
@@ -226,6 +227,12 @@ __device__ void build_plan_wave(const int64_t* __restrict__ sel, int P, int E, c
         }
     }
     __syncthreads();
+}
+
+__device__ void build_plan_wave(const int64_t* __restrict__ sel, int P, int E, const LPlan& L, int* hdr)
+{
+    const int lane = threadIdx.x & 63;
+    build_plan_wave_from(threadIdx.x < 64 && lane < P ? sel[lane] : -1, P, E, L, hdr);
 }
 
 // union entry of pick p's expert and its job index (the job's first pick is the slot 8*floor(c/8) of the entry)
@@ -300,53 +307,86 @@ __device__ void publish_plan(const LPlan& L, const int* hdr, int P, int topk, co
     }
 }
 
-// publish_plan for the relay launches, where the slot of pick p is p itself (its workgroups read sel directly and need
-// no plan): the down launch's address table is indexed by pick, with 0 for skipped picks (their workgroups return),
-// and each token's picks in (job, pick) order come from the same job rule.
-__device__ void publish_plan_picks(const LPlan& L, const int* hdr, int P, int topk, const void* w, int w_half,
-                                   const PlanView& pv, float* out, int H, const uint64_t* ptrs)
+// The relay launches need no published plan: their workgroups read sel directly, each pick's gate|up workgroup of
+// tile-column block 0 publishes the pick's down addresses, and the down launch's combining workgroups form each
+// token's job order themselves (relay_combine_list). What is left for the plan block is what no GEMV workgroup
+// covers: the address entries of skipped picks (null, so that their down workgroups return) and the output rows of
+// tokens without a valid pick (the reference's sum over an empty route is 0).
+__device__ void relay_plan_block(const int64_t* __restrict__ sel, int P, int topk, int E, float* out, int H,
+                                 uint64_t* uptr, int* flags)
 {
-    const int t = threadIdx.x, nt = blockDim.x;
-    const int U = hdr[0];
-    if (t < 3) pv.hdr[t] = t == 1 ? P : hdr[t];
-    for (int u = t; u < U; u += nt) pv.uexp[u] = L.uexp[u];
+    const int t = threadIdx.x, nt = blockDim.x, M = P / topk;
     for (int p = t; p < P; p += nt)
     {
-        const int e = L.e[p];
-        pv.uptr[2 * p] = e < 0 ? 0 : ptrs[(size_t)e * 9 + 2];
-        pv.uptr[2 * p + 1] = e < 0 ? 0 : ptrs[(size_t)e * 9 + 8];
-        pv.slot_pick[p] = p;
-        pv.pick_slot[p] = e < 0 ? -1 : p;
-        pv.pick_job[p] = e < 0 ? 0x7fffffff : plan_job(L, p);
-        if (e >= 0) pv.slot_u[p] = plan_u(L, p);
+        const int64_t e = sel[p];
+        if (e < 0 || e >= E) { uptr[2 * p] = 0; uptr[2 * p + 1] = 0; }
     }
-    const int M = P / topk;
     for (int tk = t; tk < M; tk += nt)
     {
-        int ord[MAX_TOPK], job[MAX_TOPK];
-        int n = 0;
+        bool any = false;
         for (int k = 0; k < topk; ++k)
         {
-            const int p = tk * topk + k;
-            if (L.e[p] < 0) continue;
-            const int jb = plan_job(L, p);
-            int b = n++;
-            while (b > 0 && job[b - 1] > jb) { ord[b] = ord[b - 1]; job[b] = job[b - 1]; --b; }
-            ord[b] = p;
-            job[b] = jb;
+            const int64_t e = sel[(size_t)tk * topk + k];
+            any = any || (e >= 0 && e < E);
         }
-        for (int k = 0; k < topk; ++k)
-        {
-            const int p = k < n ? ord[k] : -1;
-            pv.tok_slot[tk * topk + k] = p;
-            pv.tok_w[tk * topk + k] = p < 0 ? 0.f
-                                    : (w_half ? h2f_bits(reinterpret_cast<const uint16_t*>(w)[p])
-                                              : reinterpret_cast<const float*>(w)[p]);
-        }
-        pv.tok_npk[tk] = n;
-        if (n == 0)
-            for (int i = 0; i < H; ++i) out[(size_t)tk * H + i] = 0.f;
+        flags[tk] = any ? 0 : 1;
     }
+    __syncthreads();
+    for (int tk = 0; tk < M; ++tk)
+        if (flags[tk])
+            for (int i = t; i < H; i += nt) out[(size_t)tk * H + i] = 0.f;
+}
+
+// The combine list of token tk for a relay down workgroup: the token's valid picks in (job, pick) order, the
+// reference's combine order (moe_forward's jobs, ft_core.h:1343-1349 and 1020-1033), as pick indices (the relay's
+// slots) with their fp32 weights and svh_down addresses. Jobs are those of build_plan: an expert's picks in pick order,
+// a new job at every 8th of them, jobs numbered in the order of their first picks. Wave 0 computes it in registers
+// (lane = pick, P <= 64): e64_lane the pick's id, w_lane its weight, svh_lane its expert's svh_down address. Whole
+// workgroup (ends with a barrier); writes slot[k], wt[k], sv[k] for k < *npk.
+__device__ void relay_combine_list(int64_t e64_lane, float w_lane, uint64_t svh_lane, int P, int E, int topk, int tk,
+                                   int* slot, float* wt, uint64_t* sv, int* npk)
+{
+    if (threadIdx.x < 64)
+    {
+        const int lane = threadIdx.x;
+        const bool ok = lane < P && e64_lane >= 0 && e64_lane < E;
+        const int e = ok ? (int)e64_lane : -1;
+        // lanes of the same expert: ten ballots on the id bits (E <= 1024)
+        uint64_t eq = __ballot(ok);
+#pragma unroll
+        for (int b = 0; b < 10; ++b)
+        {
+            const bool bit = ok && ((e >> b) & 1);
+            const uint64_t m = __ballot(bit);
+            eq &= bit ? m : ~m;
+        }
+        const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+        const int c = __popcll(eq & below);                 // occurrence of the pick among its expert's picks
+        const uint64_t mc = __ballot(ok && (c & 7) == 0);  // picks that open a job
+        const int crank = __popcll(mc & below);            // job number, at a job's opening pick
+        uint64_t m = eq;
+        for (int k = 0; k < (c & ~7); ++k) m &= m - 1;      // the opening pick of this pick's job: set bit c & ~7
+        const int opener = ok ? __builtin_ctzll(m) : lane;
+        const int job = __shfl(crank, opener);
+        const bool mine = ok && lane / topk == tk;
+        int rank = 0;
+        for (int k = 0; k < topk; ++k)
+        {
+            const int lk = tk * topk + k;
+            const int jk = __shfl(job, lk);
+            const bool okk = __shfl((int)(ok ? 1 : 0), lk) != 0;
+            rank += (okk && (jk < job || (jk == job && lk < lane))) ? 1 : 0;
+        }
+        if (mine)
+        {
+            slot[rank] = lane;
+            wt[rank] = w_lane;
+            sv[rank] = svh_lane;
+        }
+        const uint64_t mm = __ballot(mine);
+        if (lane == 0) *npk = __popcll(mm);
+    }
+    __syncthreads();
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -1026,6 +1066,9 @@ struct DnArgs
     int pv_picks;              // picks of the call (the relay down launch's item count)
     int* status;               // the context's status words (relay waits that expired)
     int spin_max;              // bound of a relay turn wait, in polls
+    const int64_t* sel;        // [P] picks (relay launches: slot = pick)
+    const void* w;             // [P] routing weights, fp16 (w_half) or fp32
+    int w_half, E;
 };
 
 // Grid: umax * H/128. Workgroup = 8 waves = one 128-output block of one routed expert, all its slots (with per_slot:
@@ -1246,10 +1289,11 @@ __host__ __device__ constexpr size_t gu_relay_lds(int H, int P, int E)
     return (size_t)GU_NW * 8 * 32 * K + (x > plan ? x : plan);
 }
 
-// Grid: 1 + nmat * P * I / (16 * CW), CW = GU_NW / RW tile columns per workgroup. Workgroup 1 + (m * P + p) *
+// Grid: 8 + relay_blocks(nmat * P * I / (16 * CW)), CW = GU_NW / RW tile columns per workgroup. Item (m * P + p) *
 // (I / (16 CW)) + cb: pick p's 16 CW outputs [cb * 16 CW, (cb + 1) * 16 CW) of matrix mat_base + m, RW waves per column
-// (chain_relay); a skipped pick's workgroups return at once. Workgroup 0 (dispatched first, so that it never waits
-// for a GEMV workgroup's slot) builds the plan and publishes it for the down launch (slots = picks).
+// (chain_relay); a skipped pick's workgroups return at once. Workgroup 0 marks skipped picks for the down launch and
+// zeroes the output rows of tokens without a valid pick (slots are picks; the down launch forms each token's combine
+// order itself).
 // The last of the workgroups covering a 128-block of a pick (gate and up) runs its SwiGLU stage, as in gu_kernel.
 template <int K, int RW>
 __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3))) void gu_relay_kernel(GuArgs a)
@@ -1268,13 +1312,12 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
     const int TN = a.I / 16, TK = a.H / 16, ncb = TN / CW;
     if (blockIdx.x == 0)
     {
-        const LPlan L = lplan_carve(reinterpret_cast<int*>(lds_x), a.P, a.E);
-        if (a.P <= 64) build_plan_wave(a.sel, a.P, a.E, L, hdr);
-        else build_plan(a.sel, a.P, a.E, L, hdr);
-        publish_plan_picks(L, hdr, a.P, a.topk, a.w, a.w_half, a.pv, a.out, a.H, a.ptrs);
+        relay_plan_block(a.sel, a.P, a.topk, a.E, a.out, a.H, a.pv.uptr, reinterpret_cast<int*>(lds_x));
         return;
     }
-    // block 0 publishes the plan, blocks 1..7 have no work (the items start at an XCD-aligned block)
+    // block 0 marks skipped picks and zeroes the rows of tokens without picks, blocks 1..7 have no work (the items
+    // start at an XCD-aligned block); all of them end within a load's latency, so every GEMV workgroup finds a free
+    // slot in the first dispatch round
     const long item = blockIdx.x < 8 ? -1 : relay_item(blockIdx.x - 8, RW, (long)a.nmat_launch * a.P * ncb);
     if (item < 0) return;
     const int wg = (int)item, per_mat = a.P * ncb;
@@ -1288,6 +1331,9 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
     const int c = wid / RW, r = wid % RW;
     const uint8_t* tr = reinterpret_cast<const uint8_t*>(a.ptrs[(size_t)e * 9 + mat]);
     const gptr<uint16_t> suh = gaddr<uint16_t>(a.ptrs[(size_t)e * 9 + 3 + 2 * mat]);
+    // the pick's down trellis and svh_down addresses for the down launch, from the workgroup of the gate matrix's
+    // first column block
+    if (mat == 0 && cb == 0 && threadIdx.x < 2) a.pv.uptr[2 * p + threadIdx.x] = a.ptrs[(size_t)e * 9 + 2 + 6 * threadIdx.x];
     const size_t gstride = (size_t)TN * TB;
     const int t = cb * CW + c;   // this wave's tile column
     const uint8_t* col = tr + (size_t)t * TB;
@@ -1372,15 +1418,18 @@ __host__ __device__ constexpr size_t dn_relay_lds(int I)
 
 // Grid: P * H / (16 * CW). Workgroup (p, cb): the raw down sums [cb * 16 CW, (cb + 1) * 16 CW) of pick p (slot p)
 // into yd, RW waves per column; the last of the NQ * npk workgroups that cover a token's 128-output block (NQ quarters
-// of each of its npk picks) runs out_block on every pick's block and the token's weighted sum of the block.
+// of each of its npk picks) runs out_block on every pick's block and the token's weighted sum of the block, in the
+// job order it forms itself from sel (relay_combine_list; wave 0 loads the call's picks, weights and svh_down
+// addresses into registers before the GEMV, so none of their latency falls on that tail).
 template <int K, int RW>
 __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3))) void dn_relay_kernel(DnArgs a)
 {
     constexpr int NW = GU_NW, CW = NW / RW, TB = 32 * K, NQ = 128 / (16 * CW);
     extern __shared__ __align__(16) uint8_t lds_raw[];
     __shared__ int s_last;
-    __shared__ int c_tok, c_npk, c_slot[MAX_TOPK];
+    __shared__ int c_npk, c_slot[MAX_TOPK];
     __shared__ float c_w[MAX_TOPK];
+    __shared__ uint64_t c_svh[MAX_TOPK];
     __shared__ float relay[CW][64];
     __shared__ int relay_turn[CW];
     if (threadIdx.x < CW) relay_turn[threadIdx.x] = 0;   // ordered before every hand-off by the input barrier
@@ -1388,7 +1437,8 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
     uint8_t* rings = lds_raw;                                       // [NW][RB]
     float* lds_x = reinterpret_cast<float*>(lds_raw + NW * RB);     // [I] permuted, fp32
     const int TN = a.H / 16, TK = a.I / 16, ncb = TN / CW;
-    const long item = relay_item(blockIdx.x, RW, (long)a.pv_picks * ncb);
+    const int P = a.pv_picks;
+    const long item = relay_item(blockIdx.x, RW, (long)P * ncb);
     if (item < 0) return;
     const int p = (int)(item / ncb), cb = (int)(item % ncb);
     const int blk = cb / NQ;
@@ -1396,23 +1446,23 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
     const gptr<uint16_t> svh = gaddr<uint16_t>(a.pv.uptr[2 * p + 1]);
     if (tr == nullptr) return;   // skipped pick
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15;
+    // wave 0: the call's picks, weights and svh_down addresses (lane = pick), for the combine list at the end
+    int64_t e_l = -1;
+    float w_l = 0.f;
+    uint64_t svh_l = 0;
+    if (wave == 0 && lane < P)
+    {
+        e_l = a.sel[lane];
+        w_l = a.w_half ? h2f_bits(reinterpret_cast<const uint16_t*>(a.w)[lane]) : reinterpret_cast<const float*>(a.w)[lane];
+        svh_l = a.pv.uptr[2 * lane + 1];
+    }
     const int wid = __builtin_amdgcn_readfirstlane(wave);
     const int c = wid / RW, r = wid % RW;
     const size_t gstride = (size_t)TN * TB;
     const int t = cb * CW + c;
     const uint8_t* col = tr + (size_t)t * TB;
     const int nbh = a.H / 128;
-    // the token's combine list (slots in job order and weights): loads issued before the GEMV, written to LDS after
-    const int ck = threadIdx.x;
-    int q_tok = 0, q_slot = -1, q_npk = 0;
-    float q_w = 0.f;
-    if (ck < a.topk)
-    {
-        q_tok = p / a.topk;
-        q_slot = a.pv.tok_slot[q_tok * a.topk + ck];
-        q_w = a.pv.tok_w[q_tok * a.topk + ck];
-        q_npk = a.pv.tok_npk[q_tok];
-    }
+    const int tok = p / a.topk;
     // the slot's down input (I fp16) into LDS as fp32; each thread's first two 16-byte loads are issued before the
     // trellis groups are requested
     const int nvec = a.I / 8;
@@ -1447,11 +1497,12 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
     const float res = chain_relay<K, NGRP - 1, RW>(col, gstride, TK, lds_x, rings + wid * RB, relay[c],
                                                    &relay_turn[c], r, a.status, a.spin_max, pre_load, pre);
     if (r == 0 && lane < 16) st_agent(&a.yd[(size_t)p * a.H + t * 16 + n], res);
-    if (ck < a.topk)
+    // the number of valid picks of the token (its combine's arrival count), from the registers of wave 0
+    if (wave == 0)
     {
-        c_slot[ck] = q_slot;
-        c_w[ck] = q_w;
-        if (ck == 0) { c_tok = q_tok; c_npk = q_npk; }
+        const bool mine = lane < P && lane / a.topk == tok && e_l >= 0 && e_l < a.E;
+        const uint64_t m = __ballot(mine);
+        if (lane == 0) c_npk = __popcll(m);
     }
     release_agent();
     __syncthreads();
@@ -1460,7 +1511,7 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
     // (ft_core.h:1020-1033): o = 0, then o += w * y
     if (threadIdx.x == 0)
     {
-        int* ctr = a.out_cnt + (size_t)c_tok * nbh + blk;
+        int* ctr = a.out_cnt + (size_t)tok * nbh + blk;
         const int need = NQ * c_npk;
         const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = old == need - 1;
@@ -1468,13 +1519,14 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
     }
     __syncthreads();
     if (!s_last) return;
-    const int npk = c_npk;
     float* ylds = lds_x;   // [npk][128] the picks' blocks after out_block (the GEMV inputs are no longer needed)
+    relay_combine_list(e_l, w_l, svh_l, P, a.E, a.topk, tok, c_slot, c_w, c_svh, &c_npk);
+    const int npk = c_npk;
     for (int k = wave; k < npk; k += NW)
     {
         const int sl = c_slot[k];
         const float* y = a.yd + (size_t)sl * a.H + blk * 128;
-        const gptr<uint16_t> sv = gaddr<uint16_t>(a.pv.uptr[2 * sl + 1]);
+        const gptr<uint16_t> sv = gaddr<uint16_t>(c_svh[k]);
         float v0 = ld_agent(&y[lane]), v1 = ld_agent(&y[lane + 64]);
         out_block_wave(v0, v1, h2f_bits(sv[blk * 128 + lane]), h2f_bits(sv[blk * 128 + lane + 64]));
         ylds[k * 128 + lane] = v0;
@@ -1488,8 +1540,8 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
         o0 = o0 + c_w[k] * ylds[k * 128 + lane];
         o1 = o1 + c_w[k] * ylds[k * 128 + lane + 64];
     }
-    a.out[(size_t)c_tok * a.H + blk * 128 + lane] = o0;
-    a.out[(size_t)c_tok * a.H + blk * 128 + lane + 64] = o1;
+    a.out[(size_t)tok * a.H + blk * 128 + lane] = o0;
+    a.out[(size_t)tok * a.H + blk * 128 + lane + 64] = o1;
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -1657,7 +1709,7 @@ size_t gate_up_lds_bytes(int K, int ns, int H, int P, int E, int mf, int rw)
     return r;
 }
 
-size_t down_lds_bytes(int K, int ns, int I, int mf, int rw)
+size_t down_lds_bytes(int K, int ns, int I, int P, int E, int mf, int rw)
 {
     size_t r = 0;
     auto f = [&]() -> int {
@@ -1702,12 +1754,13 @@ int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, 
     return 0;
 }
 
-int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int umax, int P, const PlanView& pv,
-                const uint16_t* xtd, float* yd, int* out_cnt, int* blk_cnt, float* out, int mf, int rw, int* status,
-                int spin_max, hipStream_t st)
+int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int umax, int P, int E, const int64_t* sel,
+                const void* w, int w_half, const PlanView& pv, const uint16_t* xtd, float* yd, int* out_cnt,
+                int* blk_cnt, float* out, int mf, int rw, int* status, int spin_max, hipStream_t st)
 {
     DnArgs a;
     a.status = status; a.spin_max = spin_max; a.pv_picks = P;
+    a.sel = sel; a.w = w; a.w_half = w_half; a.E = E;
     a.ptrs = ptrs; a.topk = topk; a.H = H; a.I = I; a.pv = pv; a.xtd = xtd; a.yd = yd; a.out_cnt = out_cnt;
     a.blk_cnt = blk_cnt;
     a.out = out;
