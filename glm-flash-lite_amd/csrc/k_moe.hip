@@ -584,16 +584,22 @@ __host__ __device__ constexpr long relay_blocks(long items, int RW)
     return (items / RW + 7) / 8 * 8 * RW;
 }
 
-// Bounded wait for a relay turn: polls `turn` (workgroup-scope acquire) at most spin_max times until it reaches g.
-// Returns false when the bound ran out first; the caller then counts the expiry in the context's status word, which
-// the host reads with gfl_ctx_check (the call's outputs are then wrong, and reported as such). spin_max = 0 polls
-// never and always expires: the host sets it only to test that reporting path.
+// Bounded wait for a relay turn: polls `turn` (workgroup-scope acquire) until it reaches g, at most spin_max polls
+// rounded up to a multiple of 8. Returns false when the bound ran out first; the caller then counts the expiry in the
+// context's status word, which the host reads with gfl_ctx_check (the call's outputs are then wrong, and reported as
+// such). spin_max = 0 polls never and always expires: the host sets it only to test that reporting path.
 __device__ __forceinline__ bool wait_turn(const int* turn, int g, int spin_max)
 {
-    for (int spin = 0; spin < spin_max; ++spin)
+    // polls in runs of 8 with the bound checked once per run: a hand-off is seen within a poll's LDS read and one
+    // s_sleep, with no loop bookkeeping between polls (the relay's serial chain waits on every group's turn)
+    for (int spin = 0; spin < spin_max; spin += 8)
     {
-        if (__hip_atomic_load(turn, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= g) return true;
-        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+        {
+            if (__hip_atomic_load(turn, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= g) return true;
+            __builtin_amdgcn_s_sleep(1);
+        }
     }
     return false;
 }
@@ -641,6 +647,9 @@ __device__ __forceinline__ float chain_relay(const uint8_t* __restrict__ col_bas
 #pragma unroll
     for (int k = 0; k < PF; ++k) load(buf[k], k);
     float acc = 0.f;
+    // every turn wait ended in time; an expiry is counted once, after the loop, so the hand-off path of each group
+    // carries no branch around the status word's atomic
+    bool waits_ok = true;
     const int nphp = (nph + PF - 1) / PF * PF;   // phases padded to whole rounds of PF (the padding has no work)
     for (int ph0 = 0; ph0 < nphp; ph0 += PF)
     {
@@ -684,7 +693,7 @@ __device__ __forceinline__ float chain_relay(const uint8_t* __restrict__ col_bas
                 {
                     // the turn of group g: the wave of group g - 1 has written its accumulators (bounded wait: that
                     // wave is resident and waits only for groups before its own)
-                    if (RW > 1 && !wait_turn(turn, g, spin_max) && lane == 0) count_expiry(status);
+                    if (RW > 1) waits_ok &= wait_turn(turn, g, spin_max);
                     acc = relay[lane];
                 }
 #pragma unroll
@@ -704,8 +713,9 @@ __device__ __forceinline__ float chain_relay(const uint8_t* __restrict__ col_bas
     if (RW > 1)
     {
         // the last group's accumulators
-        if (!wait_turn(turn, ngroups, spin_max) && lane == 0) count_expiry(status);
+        waits_ok &= wait_turn(turn, ngroups, spin_max);
         acc = relay[lane];
+        if (!waits_ok && lane == 0) count_expiry(status);
     }
     const float a1 = __shfl(acc, n + 16), a2 = __shfl(acc, n + 32), a3 = __shfl(acc, n + 48);
     return (acc + a1) + (a2 + a3);
