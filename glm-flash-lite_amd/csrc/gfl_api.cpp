@@ -118,7 +118,7 @@ constexpr WsSizes ws_sizes(int cap, int H, int I)
     z.ygu = align256(sizeof(float) * 4 * (size_t)cap * I);
     z.xtd = align256(sizeof(uint16_t) * (size_t)cap * I);
     z.yd = align256(sizeof(float) * (size_t)cap * H);
-    z.cnt = align256(sizeof(int) * (size_t)cap * (I / 128 + 2 * (H / 128)));
+    z.cnt = align256(sizeof(int) * (size_t)cap * (I / 128 + 2 * (H / 128)) * gfl::CNT_STRIDE);
     return z;
 }
 
@@ -171,8 +171,8 @@ void carve_at(void* base, int cap, int wH, int wI, int H, int I, Workspace& w)
     w.xtd = reinterpret_cast<uint16_t*>(b + z.ints + z.ygu);
     w.yd = reinterpret_cast<float*>(b + z.ints + z.ygu + z.xtd);
     w.act_cnt = reinterpret_cast<int*>(b + z.data());
-    w.out_cnt = w.act_cnt + (size_t)cap * (I / 128);
-    w.blk_cnt = w.out_cnt + (size_t)cap * (H / 128);
+    w.out_cnt = w.act_cnt + (size_t)cap * (I / 128) * gfl::CNT_STRIDE;
+    w.blk_cnt = w.out_cnt + (size_t)cap * (H / 128) * gfl::CNT_STRIDE;
 }
 
 // the context's reserved workspace: MAX_PICKS slots at the largest registered H and I

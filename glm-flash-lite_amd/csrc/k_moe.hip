@@ -1047,7 +1047,7 @@ gu_kernel(GuArgs a)
     const int blk = (cb * NW * 16) / 128;
     if (threadIdx.x == 0)
     {
-        int* ctr = a.act_cnt + (size_t)ent * (a.I / 128) + blk;
+        int* ctr = a.act_cnt + ((size_t)ent * (a.I / 128) + blk) * CNT_STRIDE;
         const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = old == a.nmat_total - 1;
         if (s_last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1213,7 +1213,7 @@ __attribute__((amdgpu_waves_per_eu(K == 5 || NS == 8 ? 3 : 4))) void down_kernel
             // the second half to finish runs out_block (ft_core.h:1016) on the whole 128-block, in place
             if (threadIdx.x == 0)
             {
-                int* ctr = a.blk_cnt + (size_t)c0 * nbh + blk;
+                int* ctr = a.blk_cnt + ((size_t)c0 * nbh + blk) * CNT_STRIDE;
                 const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 s_last[0] = old == 1;
                 if (old == 1) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1247,7 +1247,7 @@ __attribute__((amdgpu_waves_per_eu(K == 5 || NS == 8 ? 3 : 4))) void down_kernel
         {
             const int s = threadIdx.x;
             const int tok = c_tok[s], npk = c_npk[s];
-            int* ctr = a.out_cnt + (size_t)tok * nbh + blk;
+            int* ctr = a.out_cnt + ((size_t)tok * nbh + blk) * CNT_STRIDE;
             const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             s_last[s] = old == npk - 1 ? tok : -1;
             if (old == npk - 1) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1408,7 +1408,7 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
     const int blk = (cb * CW * 16) / 128;
     if (threadIdx.x == 0)
     {
-        int* ctr = a.act_cnt + (size_t)p * (a.I / 128) + blk;
+        int* ctr = a.act_cnt + ((size_t)p * (a.I / 128) + blk) * CNT_STRIDE;
         const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = old == a.nmat_total - 1;
         if (s_last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1521,7 +1521,7 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
     // (ft_core.h:1020-1033): o = 0, then o += w * y
     if (threadIdx.x == 0)
     {
-        int* ctr = a.out_cnt + (size_t)tok * nbh + blk;
+        int* ctr = a.out_cnt + ((size_t)tok * nbh + blk) * CNT_STRIDE;
         const int need = NQ * c_npk;
         const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = old == need - 1;

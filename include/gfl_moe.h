@@ -115,7 +115,7 @@ int gfl_moe_forward(gfl_ctx* ctx, int li, const uint16_t* x, const int64_t* sel,
                     int topk, float* out, int mode, float act_limit, gfl_stream stream);
 
 /* No counterpart in the reference. gfl_moe_forward with the per-call workspace in a file-scope device array of the
- * library (about 6.5 MiB per device, held until the process ends) instead of the context's reserved workspace: for
+ * library (about 7.8 MiB per device, held until the process ends) instead of the context's reserved workspace: for
  * callers that cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc). It calls no hipMalloc, hipFree or other allocating routine (and records no profiling events);
  * everything it needs was allocated by gfl_ctx_create and gfl_register_layer. Same arguments and results as
