@@ -564,7 +564,7 @@ __device__ __forceinline__ void chain_dma(const uint8_t* __restrict__ col_base, 
 // a group into its single LDS slot (8 tiles, tile-major) right before decoding it. LDS operations of one wave complete
 // in issue order, so the slot is rewritten only after the previous group's reads; the waits for the loads are the
 // compiler's own (registers it tracks). lds_x: the slot's transformed inputs as fp32 in the permuted [tk][j][q] order,
-// filled by pre() (which ends with a workgroup barrier) after the first group's decode, which does not need them.
+// filled by pre() (which ends with a workgroup barrier) while the first groups are in flight.
 // Returns the column results (valid in lanes 0..15 of every relay wave of the column).
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
@@ -660,6 +660,11 @@ __device__ __forceinline__ float chain_relay(const uint8_t* __restrict__ col_bas
             const int g = ph * RW + r;
             const bool mine = ph < nph && g < ngroups;
             float4v cw[8], xf[8];
+            // the input transform (ending with a workgroup barrier) first: at the launch's start every workgroup's
+            // first trellis groups queue behind one another in HBM, and the inputs (x from L2, suh shared by the
+            // expert's workgroups) land sooner, so the transform fills that wait (before the first group's decode it
+            // measured 1.1 us faster at config 1 M=1 than after it)
+            if (ph == 0) pre();
             // written in every phase, padding ones included (the slot is this wave's own and only its own decode
             // reads it): with the write under the phase's branch, the compiler's wait before it also covered the
             // younger of the groups in flight
@@ -678,9 +683,6 @@ __device__ __forceinline__ float chain_relay(const uint8_t* __restrict__ col_bas
                     cw[rr] = __builtin_amdgcn_mfma_f32_16x16x16f16(Pm, decode4<K>(hi, lo, d.sh), zero, 0, 0, 0);
                 }
             }
-            // the input transform (ending with a workgroup barrier) after the first group's decode, which does not
-            // need the inputs: that decode overlaps the transform's loads
-            if (ph == 0) pre();
             if (mine)
             {
 #pragma unroll
