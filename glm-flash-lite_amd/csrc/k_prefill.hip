@@ -694,6 +694,11 @@ constexpr int XG_MS = 64;                   // slots per pass
 constexpr int XG_NG = 2;                    // ring depth (groups of 8 tile rows)
 constexpr int XG_XROW = 8 * 16 * 4;         // input bytes of one slot per group: 8 tile rows x 16 rows x fp32
 constexpr int XG_XGB = XG_MS * XG_XROW;     // input bytes per group (32 KB)
+// Slots past a pass's whole blocks of 16 run as VALU chains when there are at most XG_REM of them, else as one more
+// MFMA block. A VALU chain slot costs a 16-byte LDS read and 4 v_fmac_f32 per tile row against a padded block's 4
+// MFMAs; at config 4 (about 57 slots per expert) thresholds 4, 6 and 8 measured 8.61, 8.60 and 8.70 ms per layer
+// against 8.95 ms with padding only.
+constexpr int XG_REM = 6;
 typedef float xg_acc __attribute__((ext_vector_type(16)));   // one 16-slot block of a wave's 4 x 16 x 16 accumulators
 
 struct XgArgs
@@ -799,23 +804,31 @@ __global__ __launch_bounds__(XG_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
                 }
             }
         };
-        auto pass = [&](auto nsl_c) {
+        // NSL slots in blocks of 16 on the matrix cores, then R <= XG_REM slots past them as VALU chains: lane
+        // (j, n) runs slot m's chain j of column n as v_fmac_f32 steps, fmaf(x, w, acc) as each K=1 MFMA step is, in
+        // the same step order, on the weights the lane decoded for the MFMAs
+        auto pass = [&](auto nsl_c, int R) {
             constexpr int NSL = decltype(nsl_c)::value, NB = NSL / 16;
-            xg_acc acc[NB];
+            xg_acc acc[NB > 0 ? NB : 1];
 #pragma unroll
             for (int b = 0; b < NB; ++b)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[b][r] = 0.f;
+            float racc[XG_REM];
+#pragma unroll
+            for (int m = 0; m < XG_REM; ++m) racc[m] = 0.f;
             __syncthreads();   // the previous pass is done with the rings
-            issue(0, NSL);
+            issue(0, NSL + R);
             for (int g = 0; g < ngroups; ++g)
             {
                 gp_wait_vmcnt<0>();
                 gp_barrier();   // group g landed for every wave; every wave is done with group g - 1
-                if (g + 1 < ngroups) issue(g + 1, NSL);
+                if (g + 1 < ngroups) issue(g + 1, NSL + R);
                 const uint8_t* tl = tring + (g % NG) * GB + tcl * TB;
                 // lane (j, m) reads slot 16 b + m's inputs of chain j
                 const uint8_t* xl = xring + (g % NG) * XG_XGB + n * XG_XROW + j * 16;
+                // lane (j, n) reads remainder slot NSL + m's inputs of chain j (the same 16 bytes for all n)
+                const uint8_t* xr = xring + (g % NG) * XG_XGB + NSL * XG_XROW + j * 16;
 #pragma unroll
                 for (int t8 = 0; t8 < 8; ++t8)
                 {
@@ -830,7 +843,7 @@ __global__ __launch_bounds__(XG_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
                     }
                     const half4 wh = codebook4(st[0], st[1], st[2], st[3]);
                     const float w[4] = { (float)wh[0], (float)wh[1], (float)wh[2], (float)wh[3] };
-                    float4 xv[NB];
+                    float4 xv[NB > 0 ? NB : 1];
 #pragma unroll
                     for (int b = 0; b < NB; ++b)
                         xv[b] = *reinterpret_cast<const float4*>(xl + b * 16 * XG_XROW + t8 * 64);
@@ -847,6 +860,19 @@ __global__ __launch_bounds__(XG_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
 #pragma unroll
                     for (int b = 0; b < NB; ++b)
                         acc[b] = __builtin_amdgcn_mfma_f32_16x16x1f32(xv[b].w, w[3], acc[b], 0, 0, 0);
+                    if (R > 0)
+                    {
+#pragma unroll
+                        for (int m = 0; m < XG_REM; ++m)
+                            if (m < R)
+                            {
+                                const float4 x4 = *reinterpret_cast<const float4*>(xr + m * XG_XROW + t8 * 64);
+                                racc[m] = __builtin_fmaf(x4.x, w[0], racc[m]);
+                                racc[m] = __builtin_fmaf(x4.y, w[1], racc[m]);
+                                racc[m] = __builtin_fmaf(x4.z, w[2], racc[m]);
+                                racc[m] = __builtin_fmaf(x4.w, w[3], racc[m]);
+                            }
+                    }
                 }
             }
             // chain c of (slot 16 b + 4 (lane / 16) + i, column lane % 16) is register 4c + i of acc[b]: the
@@ -861,13 +887,29 @@ __global__ __launch_bounds__(XG_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
                     const float y = (acc[b][i] + acc[b][4 + i]) + (acc[b][8 + i] + acc[b][12 + i]);
                     if (s < T) yout[(size_t)(c0 + s) * a.ndim + col] = (uint16_t)f2h_bits(y);
                 }
+            // remainder slots: chain j of (slot, column n) is racc in lane 16 j + n
+            if (R > 0)
+            {
+#pragma unroll
+                for (int m = 0; m < XG_REM; ++m)
+                    if (m < R)
+                    {
+                        const float a1 = __shfl(racc[m], n + 16), a2 = __shfl(racc[m], n + 32),
+                                    a3 = __shfl(racc[m], n + 48);
+                        const float y = (racc[m] + a1) + (a2 + a3);
+                        if (j == 0) yout[(size_t)(c0 + NSL + m) * a.ndim + col] = (uint16_t)f2h_bits(y);
+                    }
+            }
         };
-        switch ((T + 15) / 16)
+        // slots past the last whole block of 16: up to XG_REM of them as VALU chains, more as one more MFMA block
+        const int R = T % 16 <= XG_REM ? T % 16 : 0;
+        switch ((T - R + 15) / 16)
         {
-            case 1: pass(std::integral_constant<int, 16>{}); break;
-            case 2: pass(std::integral_constant<int, 32>{}); break;
-            case 3: pass(std::integral_constant<int, 48>{}); break;
-            default: pass(std::integral_constant<int, 64>{}); break;
+            case 0: pass(std::integral_constant<int, 0>{}, R); break;
+            case 1: pass(std::integral_constant<int, 16>{}, R); break;
+            case 2: pass(std::integral_constant<int, 32>{}, R); break;
+            case 3: pass(std::integral_constant<int, 48>{}, R); break;
+            default: pass(std::integral_constant<int, 64>{}, 0); break;
         }
     }
 }
