@@ -27,6 +27,10 @@ struct SplitLds
     int nu, nh, nm, nr, best, bestr, publish, npk;
     int wsum[SP_T / 64];
     float pol[20];
+    int slot[MAX_EXPERTS];          // the layer's residency row (slotof), loaded before the routed experts are known
+    long long st[4];                // stats[0..3] before this call
+    long long rsel[MAX_PICKS];      // the picks as the fused router wrote them (route_split_kernel)
+    unsigned short rw[MAX_PICKS];
 };
 
 // Ascending order of finite floats as unsigned integers (+0 and -0 compare equal, as the reference's float compare
@@ -98,6 +102,9 @@ __device__ void split_cost(const SplitLds& S, const int* miss, const int* rmiss,
 
 // The split of one call (whole workgroup). sel/w are read from global memory (the caller's selection, or the router
 // output written by this workgroup before a barrier).
+// PRE: the fused router already put the picks (S.rsel, S.rw), the residency row (S.slot), the policy (S.pol) and
+// stats[0..3] (S.st) in LDS; else they are loaded here, all in one round trip.
+template <bool PRE>
 __device__ void split_body(SplitLds& S, const int64_t* __restrict__ sel, const uint16_t* __restrict__ w,
                            const uint16_t* __restrict__ z, int n, int bsz, int topk, int H, int E, int first,
                            const int32_t* __restrict__ slotof, const float* __restrict__ score,
@@ -108,14 +115,25 @@ __device__ void split_body(SplitLds& S, const int64_t* __restrict__ sel, const u
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
     // 1. per-pick classification
+    if (!PRE)
+    {
+        for (int q = t; q < n; q += SP_T)
+        {
+            S.rsel[q] = sel[q];
+            S.rw[q] = w[q];
+        }
+        for (int e = t; e < E; e += SP_T) S.slot[e] = slotof[e];
+        if (t < 4) S.st[t] = stats[t];
+        if (t < 20) S.pol[t] = pol[t];
+        __syncthreads();
+    }
     for (int q = t; q < n; q += SP_T)
     {
-        const int64_t e = sel[q] - first;
+        const int64_t e = S.rsel[q] - first;
         S.le[q] = (e >= 0 && e < E) ? (short)e : (short)-1;
-        S.nz[q] = (w[q] & 0x7FFFu) != 0;
+        S.nz[q] = (S.rw[q] & 0x7FFFu) != 0;
     }
     for (int e = t; e < E; e += SP_T) { S.seen[e] = 0; S.take[e] = 0; }
-    if (t < 20) S.pol[t] = pol[t];
     if (t == 0) { S.nh = 0; S.nm = 0; S.nr = 0; }
     __syncthreads();
     // 2. routed experts in first-appearance order, and their nonzero-pick counts (wave 0)
@@ -157,7 +175,7 @@ __device__ void split_body(SplitLds& S, const int64_t* __restrict__ sel, const u
     {
         const int e = S.ulist[i];
         unsigned long long k = ~0ull;
-        if (slotof[e] >= 0) ++h;
+        if (S.slot[e] >= 0) ++h;
         else
         {
             const bool remote = tri && rres[e];
@@ -221,10 +239,10 @@ __device__ void split_body(SplitLds& S, const int64_t* __restrict__ sel, const u
         S.best = best;
         S.bestr = bestr;
         S.publish = best + bestr > 0 || S.pol[7] > 0.5f;
-        stats[0] += nh;
-        stats[1] += nm + nr;
-        stats[2] += best + bestr;
-        stats[3] += 1;
+        stats[0] = S.st[0] + nh;
+        stats[1] = S.st[1] + nm + nr;
+        stats[2] = S.st[2] + best + bestr;
+        stats[3] = S.st[3] + 1;
     }
     __syncthreads();
     const bool publish = S.publish, any_taken = S.best + S.bestr > 0;
@@ -234,8 +252,8 @@ __device__ void split_body(SplitLds& S, const int64_t* __restrict__ sel, const u
     {
         const int e = S.le[q];
         const bool c = e >= 0 && S.take[e];
-        sel_out[q] = (c && !keep_ids) ? -1 : sel[q];
-        w_out[q] = c ? (uint16_t)0 : w[q];
+        sel_out[q] = (c && !keep_ids) ? -1 : S.rsel[q];
+        w_out[q] = c ? (uint16_t)0 : S.rw[q];
     }
     if (publish)
     {
@@ -266,7 +284,7 @@ __device__ void split_body(SplitLds& S, const int64_t* __restrict__ sel, const u
             {
                 hpicks[base * 3] = q / topk;
                 hpicks[base * 3 + 1] = S.le[q];
-                hpicks[base * 3 + 2] = (int32_t)__float_as_uint(h2f_bits(w[q]));
+                hpicks[base * 3 + 2] = (int32_t)__float_as_uint(h2f_bits(S.rw[q]));
                 ++base;
             }
         }
@@ -297,8 +315,8 @@ __global__ __launch_bounds__(SP_T) void split_kernel(const int64_t* __restrict__
     int64_t* dflag, int64_t* stats, const int32_t* __restrict__ rres)
 {
     __shared__ SplitLds S;
-    split_body(S, sel, w, z, n, bsz, topk, H, E, first, slotof, score, pol, ctrl, hx, hpicks, seq, li, keep_ids,
-               sel_out, w_out, dflag, stats, rres);
+    split_body<false>(S, sel, w, z, n, bsz, topk, H, E, first, slotof, score, pol, ctrl, hx, hpicks, seq, li,
+                      keep_ids, sel_out, w_out, dflag, stats, rres);
 }
 
 // One workgroup decides once, for every output element, whether the host partial is added: the trellis build of the
@@ -460,16 +478,17 @@ void launch_ingress_answer(int64_t* ctrl, const int64_t* state, hipStream_t st)
 // experts, ordered by (score descending, index ascending); the picks' scores are summed in pick order and
 // w_j = s_j / sum
 // is rounded to fp16 (round to nearest even). Logits must be finite.
-// one butterfly step of the (score descending, index ascending) arg-max: combine with lane ^ W
+// One butterfly step of the wave arg-max on 64-bit keys (order-preserving score bits above the complemented index, so
+// the larger key is the higher score and, on a tie, the lower index; 0 = no candidate): combine with lane ^ W.
 template <int W>
-__device__ __forceinline__ void route_argmax_step(float& bv, int& bi)
+__device__ __forceinline__ void route_argmax_step(uint32_t& hi, uint32_t& lo)
 {
-    const float ov = lane_xor<W>(bv);
-    const int oi = __float_as_int(lane_xor<W>(__int_as_float(bi)));
-    if (oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi)))
+    const uint32_t ohi = __float_as_uint(lane_xor<W>(__uint_as_float(hi)));
+    const uint32_t olo = __float_as_uint(lane_xor<W>(__uint_as_float(lo)));
+    if ((((uint64_t)ohi << 32) | olo) > (((uint64_t)hi << 32) | lo))
     {
-        bv = ov;
-        bi = oi;
+        hi = ohi;
+        lo = olo;
     }
 }
 
@@ -480,7 +499,7 @@ constexpr int ROUTE_MAXE = 1024;   // experts per token: up to 16 per lane
 // compile-time count so that the per-lane loops hold only live experts.
 template <int NI>
 __device__ __forceinline__ void route_token(const float* __restrict__ lg, int E, int topk, int64_t* sel_row,
-                                            uint16_t* w_row)
+                                            uint16_t* w_row, long long* lsel = nullptr, unsigned short* lw = nullptr)
 {
     const int lane = threadIdx.x & 63;
     // every load first (uniform guards, clamped addresses), so the token's logits arrive in one round trip
@@ -493,32 +512,41 @@ __device__ __forceinline__ void route_token(const float* __restrict__ lg, int E,
         const float ex = (float)exp(-(double)sc[i]);
         sc[i] = lane + 64 * i < E ? 1.0f / (1.0f + ex) : -INFINITY;
     }
-    uint32_t used = 0;
+    // each candidate as a 64-bit key: the score's order-preserving bits above the complemented expert index, so that
+    // the largest key is the highest score and, among equal scores, the lowest index (the reference's first strict
+    // maximum in index order); a picked or absent candidate is key 0
+    uint32_t khi[NI], klo[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+    {
+        const int e = lane + 64 * i;
+        khi[i] = e < E ? float_order_key(sc[i]) : 0u;
+        klo[i] = e < E ? ~(uint32_t)e : 0u;
+    }
     float tot = 0.0f, mine = 0.0f;
     int myidx = 0;
     for (int j = 0; j < topk; ++j)
     {
-        // this lane's best unused (score descending, index ascending: the first strict maximum in index order)
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
+        // this lane's best remaining candidate, then the wave's, through DPP / permlane exchanges
+        uint32_t hi = khi[0], lo = klo[0];
+#pragma unroll
+        for (int i = 1; i < NI; ++i)
+            if ((((uint64_t)khi[i] << 32) | klo[i]) > (((uint64_t)hi << 32) | lo))
+            {
+                hi = khi[i];
+                lo = klo[i];
+            }
+        route_argmax_step<1>(hi, lo);
+        route_argmax_step<2>(hi, lo);
+        route_argmax_step<4>(hi, lo);
+        route_argmax_step<8>(hi, lo);
+        route_argmax_step<16>(hi, lo);
+        route_argmax_step<32>(hi, lo);
+        const int bi = (int)~lo;
+        const float bv = __uint_as_float((hi & 0x80000000u) ? (hi & 0x7FFFFFFFu) : ~hi);
 #pragma unroll
         for (int i = 0; i < NI; ++i)
-        {
-            const int e = lane + 64 * i;
-            if (e < E && !((used >> i) & 1) && (sc[i] > bv || bi == 0x7fffffff))
-            {
-                bv = sc[i];
-                bi = e;
-            }
-        }
-        // wave arg-max with the same order, through DPP / permlane exchanges (no LDS round trips)
-        route_argmax_step<1>(bv, bi);
-        route_argmax_step<2>(bv, bi);
-        route_argmax_step<4>(bv, bi);
-        route_argmax_step<8>(bv, bi);
-        route_argmax_step<16>(bv, bi);
-        route_argmax_step<32>(bv, bi);
-        if ((bi & 63) == lane) used |= 1u << (bi >> 6);
+            if (bi == lane + 64 * i) khi[i] = klo[i] = 0u;
         tot = tot + bv;               // pick order, as the reference's renormalisation loop
         if (lane == j)
         {
@@ -528,8 +556,14 @@ __device__ __forceinline__ void route_token(const float* __restrict__ lg, int E,
     }
     if (lane < topk)
     {
+        const uint16_t wb = (uint16_t)f2h_bits(mine / tot);
         sel_row[lane] = myidx;
-        w_row[lane] = (uint16_t)f2h_bits(mine / tot);
+        w_row[lane] = wb;
+        if (lsel)
+        {
+            lsel[lane] = myidx;
+            lw[lane] = wb;
+        }
     }
 }
 
@@ -553,11 +587,26 @@ __global__ __launch_bounds__(SP_T) void route_split_kernel(const float* __restri
     int64_t* dflag, int64_t* stats, const int32_t* __restrict__ rres)
 {
     __shared__ SplitLds S;
-    for (int m = threadIdx.x >> 6; m < M; m += SP_T / 64)
-        route_token<NI>(logits + (size_t)m * ER, ER, topk, sel + (size_t)m * topk, w + (size_t)m * topk);
-    __syncthreads();   // the routed picks (global writes of this workgroup) are visible to all of its threads
-    split_body(S, sel, w, z, M * topk, M, topk, H, E, first, slotof, score, pol, ctrl, hx, hpicks, seq, li, keep_ids,
-               sel_out, w_out, dflag, stats, rres);
+    const int t = threadIdx.x;
+    // the split's inputs that do not depend on the routing, loaded first so that their round trip overlaps the
+    // logits'; the routed picks go to the split through LDS
+    constexpr int SLOT_PER = (MAX_EXPERTS + SP_T - 1) / SP_T;
+    int32_t slot_r[SLOT_PER];
+#pragma unroll
+    for (int i = 0; i < SLOT_PER; ++i) slot_r[i] = t + i * SP_T < E ? slotof[t + i * SP_T] : 0;
+    const long long st_r = t < 4 ? (long long)stats[t] : 0;
+    const float pol_r = t < 20 ? pol[t] : 0.f;
+    for (int m = t >> 6; m < M; m += SP_T / 64)
+        route_token<NI>(logits + (size_t)m * ER, ER, topk, sel + (size_t)m * topk, w + (size_t)m * topk,
+                        S.rsel + (size_t)m * topk, S.rw + (size_t)m * topk);
+#pragma unroll
+    for (int i = 0; i < SLOT_PER; ++i)
+        if (t + i * SP_T < E) S.slot[t + i * SP_T] = slot_r[i];
+    if (t < 4) S.st[t] = st_r;
+    if (t < 20) S.pol[t] = pol_r;
+    __syncthreads();
+    split_body<true>(S, sel, w, z, M * topk, M, topk, H, E, first, slotof, score, pol, ctrl, hx, hpicks, seq, li,
+                     keep_ids, sel_out, w_out, dflag, stats, rres);
 }
 
 int launch_route(const float* logits, int M, int E, int topk, int64_t* sel, uint16_t* w, hipStream_t st)
