@@ -224,7 +224,7 @@ class Context:
 
     def set_shared(self, shared):
         """Tell the context whether other GPU work runs beside its decode calls (gfl_ctx_set_shared): with shared set,
-        calls of up to 1,536 gate|up tile columns keep the per-slot launches, which leave SIMDs free."""
+        calls of 769..1,536 gate|up tile columns keep the per-slot launches, which leave SIMDs free."""
         check(load().gfl_ctx_set_shared(self.h, int(bool(shared))))
         self._shared = bool(shared)
 

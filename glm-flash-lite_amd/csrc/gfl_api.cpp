@@ -268,15 +268,18 @@ int run_forward(gfl_ctx* c, const Layer& L, const Workspace& ws, const uint16_t*
     const int mf = mode == GFL_MODE_MFMA ? 1 : 0;
     int ns = mf ? std::min(M, 4) : M <= 8 ? 1 : 2;
     if (c->ns_override > 0) ns = std::min(c->ns_override, mf ? std::min(M, 16) : M);
-    // Calls with few tile columns run the relay launches: a workgroup per (pick, tile columns), rw waves per column,
-    // each streaming and decoding every rw-th group of 8 tile rows while the column's accumulators pass from wave to
-    // wave in tile-row order (chain_relay). With one wave per column such a call leaves most SIMDs idle; rw waves per
-    // column put rw times the waves on the chip. Measured on MI355X (config-1 layers, 4 cycled): one expert per call
-    // (192 gate|up columns) 39.2 -> 27.5 us with 4 waves per column; 8 picks (1,536 columns) 58.4 -> 56.4 us with 2
-    // waves per gate|up column and 1 per down column; 16 picks and more are 7-11% slower than the per-slot launches.
+    // With one slot per pass the calls run the relay launches: a workgroup per (pick, tile columns), rw waves per
+    // column, each streaming and decoding every rw-th group of 8 tile rows while the column's accumulators pass from
+    // wave to wave in tile-row order (chain_relay). With one wave per column a call of few columns leaves most SIMDs
+    // idle; rw waves per column put rw times the waves on the chip. Measured on MI355X (config-1 layers, 4 cycled):
+    // one expert per call (192 gate|up columns) 39.2 -> 27.5 us with 4 waves per column; 8 picks (1,536 columns)
+    // 58.4 -> 56.4 us with 2 waves per gate|up column and 1 per down column. From 16 picks on, one wave per column
+    // beats the per-slot launches (gu_kernel / dn_kernel) by 2-5% on uniform routing (us per token at M = 2, 3, 4, 6,
+    // 8: 39.7 -> 38.8, 36.8 -> 35.1, 33.2 -> 31.6, 31.5 -> 30.1, 30.5 -> 29.5) and matches them on Zipf routing.
     // The relay launches at 8 picks fill every SIMD with 3 waves, so a shared expert on a side stream (k_overlap)
     // then waits (routed + shared 71.3 -> 79.1 us): a context told that other work runs beside it (gfl_ctx_set_shared)
-    // keeps those calls on the per-slot launches.
+    // keeps those calls on the per-slot launches. From 16 picks on the one-wave relay launches stay (routed + shared
+    // at M = 4 overlapped: 43.2 us per token with the per-slot launches, 41.5 with them).
     int rw[2] = { 0, 0 };
     if (!mf && ns == 1)
     {
@@ -286,7 +289,12 @@ int run_forward(gfl_ctx* c, const Layer& L, const Workspace& ws, const uint16_t*
             rw[0] = 4;
             rw[1] = cdn <= 768 ? 4 : cdn <= 1536 ? 2 : 1;
         }
-        else if (cgu <= 1536 && !c->shared)
+        else if (cgu > 1536)
+        {
+            rw[0] = 1;
+            rw[1] = 1;
+        }
+        else if (!c->shared)
         {
             rw[0] = 2;
             rw[1] = 1;

@@ -486,7 +486,7 @@ def test_relay_launches_bitexact(gpu, oracle, relay):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("relay", ["4,4", "2,1", "2,2"])
+@pytest.mark.parametrize("relay", ["4,4", "2,1", "2,2", "1,1"])
 def test_relay_launches_full_shape_bitexact(gpu, oracle, relay):
     """The relay launches at the config-1 shape (H=5120, I=1536, K=3): one expert (config 0) and top-8 of a
     10-expert layer at M = 1 and 3."""

@@ -35,17 +35,23 @@ def test_noalloc_matches_forward_two_calls(gpu, mode):
     H, I, E, topk, li = 5120, 1536, 96, 8, 950
     synth.SynthLayer(li, E, H, I, (4, 4, 3)).register(gpu, li)
     rng = np.random.default_rng(4242 + mode)
-    # 64 picks (the maximum), then fewer: 24 (per-slot launches) and 8 (relay launches in EXACT mode)
-    cases = [_inputs(rng, M, topk, E, H) for M in (8, 3, 1)]
+    # 64 picks (the maximum), then fewer: 24 and 8 (in EXACT mode the relay launches with one and two waves per
+    # gate|up column), then 8 again on the context told that it shares the GPU (the per-slot launches)
+    cases = [_inputs(rng, M, topk, E, H) for M in (8, 3, 1, 1)]
     _pair(gpu, li, *cases[0], mode)                         # kernels loaded, output tensors cached by torch
     torch.cuda.synchronize()
     free0 = torch.cuda.mem_get_info()[0]
-    for i, (x, sel, w) in enumerate(cases):
-        print(f"noalloc mode={mode} call {i}: M={x.shape[0]} topk={topk} H={H} I={I}", flush=True)
-        got, want = _pair(gpu, li, x, sel, w, mode)
-        nbad = int(np.count_nonzero(got != want))
-        print(f"  mismatched {nbad}/{want.size}, max-abs {float(np.abs(got - want).max()):.3e}", flush=True)
-        assert np.all(np.isfinite(want)) and nbad == 0
+    try:
+        for i, (x, sel, w) in enumerate(cases):
+            shared = i == len(cases) - 1
+            gpu.set_shared(shared)
+            print(f"noalloc mode={mode} call {i}: M={x.shape[0]} topk={topk} H={H} I={I} shared={shared}", flush=True)
+            got, want = _pair(gpu, li, x, sel, w, mode)
+            nbad = int(np.count_nonzero(got != want))
+            print(f"  mismatched {nbad}/{want.size}, max-abs {float(np.abs(got - want).max()):.3e}", flush=True)
+            assert np.all(np.isfinite(want)) and nbad == 0
+    finally:
+        gpu.set_shared(False)
     assert torch.cuda.mem_get_info()[0] == free0
 
 
