@@ -691,11 +691,12 @@ __device__ __forceinline__ float chain_relay(const uint8_t* __restrict__ col_bas
             }
             if (mine)
             {
-                if (g > 0)
+                if (RW > 1 && g > 0)
                 {
                     // the turn of group g: the wave of group g - 1 has written its accumulators (bounded wait: that
-                    // wave is resident and waits only for groups before its own)
-                    if (RW > 1) waits_ok &= wait_turn(turn, g, spin_max);
+                    // wave is resident and waits only for groups before its own). With one wave per column the
+                    // accumulators stay in registers.
+                    waits_ok &= wait_turn(turn, g, spin_max);
                     acc = relay[lane];
                 }
 #pragma unroll
@@ -706,8 +707,11 @@ __device__ __forceinline__ float chain_relay(const uint8_t* __restrict__ col_bas
                     acc = __builtin_fmaf(cw[rr][2], xf[rr][2], acc);
                     acc = __builtin_fmaf(cw[rr][3], xf[rr][3], acc);
                 }
-                relay[lane] = acc;
-                if (RW > 1) __hip_atomic_store(turn, g + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+                if (RW > 1)
+                {
+                    relay[lane] = acc;
+                    __hip_atomic_store(turn, g + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+                }
             }
         }
     }
@@ -1259,23 +1263,23 @@ __attribute__((amdgpu_waves_per_eu(K == 5 || NS == 8 ? 3 : 4))) void down_kernel
         {
             const int tok = s_last[s];
             if (tok < 0) continue;
-            // weighted sum in (job, pick) order (ft_core.h:1020-1033): o = 0, then o += w * y; four experts' blocks
-            // are loaded at a time (independent loads), then added in order
+            // weighted sum in (job, pick) order (ft_core.h:1020-1033): o = 0, then o += w * y; eight experts' blocks
+            // are loaded at a time, unconditionally (past the token's picks its last pick again, never used), so
+            // the loads do not wait for one another: one memory round trip at top-8. Then they are added in order.
             const int npk = c_npk[s];
             float o0 = 0.f, o1 = 0.f;
-            for (int k0 = 0; k0 < npk; k0 += 4)
+            for (int k0 = 0; k0 < npk; k0 += 8)
             {
-                float y0[4], y1[4];
+                float y0[8], y1[8];
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    if (k0 + i < npk)
-                    {
-                        const float* y = a.yd + (size_t)c_slot[s][k0 + i] * a.H + blk * 128;
-                        y0[i] = ld_agent(&y[lane]);
-                        y1[i] = ld_agent(&y[lane + 64]);
-                    }
+                for (int i = 0; i < 8; ++i)
+                {
+                    const float* y = a.yd + (size_t)c_slot[s][min(k0 + i, npk - 1)] * a.H + blk * 128;
+                    y0[i] = ld_agent(&y[lane]);
+                    y1[i] = ld_agent(&y[lane + 64]);
+                }
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < 8; ++i)
                     if (k0 + i < npk)
                     {
                         o0 = o0 + c_w[s][k0 + i] * y0[i];
@@ -1534,15 +1538,36 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
     float* ylds = lds_x;   // [npk][128] the picks' blocks after out_block (the GEMV inputs are no longer needed)
     relay_combine_list(e_l, w_l, svh_l, P, a.E, a.topk, tok, c_slot, c_w, c_svh, &c_npk);
     const int npk = c_npk;
-    for (int k = wave; k < npk; k += NW)
+    // wave w takes picks w, w + NW, ...: every load of its picks is issued before the first out_block, so the wave
+    // waits one memory round trip, not one per pick. The loads run unconditionally (past the token's picks on its
+    // last pick again, loaded and never used): under a branch each would be waited for before the next was issued.
+    constexpr int KPW = (MAX_TOPK + NW - 1) / NW;
+    if (wave < npk)
     {
-        const int sl = c_slot[k];
-        const float* y = a.yd + (size_t)sl * a.H + blk * 128;
-        const gptr<uint16_t> sv = gaddr<uint16_t>(c_svh[k]);
-        float v0 = ld_agent(&y[lane]), v1 = ld_agent(&y[lane + 64]);
-        out_block_wave(v0, v1, h2f_bits(sv[blk * 128 + lane]), h2f_bits(sv[blk * 128 + lane + 64]));
-        ylds[k * 128 + lane] = v0;
-        ylds[k * 128 + lane + 64] = v1;
+        float v0[KPW], v1[KPW];
+        uint32_t s0[KPW], s1[KPW];
+#pragma unroll
+        for (int i = 0; i < KPW; ++i)
+        {
+            const int k = min(wave + i * NW, npk - 1);
+            const float* y = a.yd + (size_t)c_slot[k] * a.H + blk * 128;
+            const gptr<uint16_t> sv = gaddr<uint16_t>(c_svh[k]);
+            v0[i] = ld_agent(&y[lane]);
+            v1[i] = ld_agent(&y[lane + 64]);
+            s0[i] = sv[blk * 128 + lane];
+            s1[i] = sv[blk * 128 + lane + 64];
+        }
+#pragma unroll
+        for (int i = 0; i < KPW; ++i)
+        {
+            const int k = wave + i * NW;
+            if (k < npk)
+            {
+                out_block_wave(v0[i], v1[i], h2f_bits((uint16_t)s0[i]), h2f_bits((uint16_t)s1[i]));
+                ylds[k * 128 + lane] = v0[i];
+                ylds[k * 128 + lane + 64] = v1[i];
+            }
+        }
     }
     __syncthreads();
     if (wave != 0) return;
