@@ -230,19 +230,21 @@ int check_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, con
                   const float* out, int mode, float act_limit, const char* who, int max_picks)
 {
     const std::string f(who);
-    if (!c || !x || !sel || !w || !out) return fail(GFL_EINVAL, f + ": NULL argument");
+    if (!c) return fail(GFL_EINVAL, f + ": NULL argument");
     if (li < 0 || li >= (int)c->layers.size() || !c->layers[li].dptrs)
         return fail(GFL_EINVAL, f + ": layer not registered");
     // AFFINE (0) and I16 (2) name the reference CPU engine's speed modes; the device computes EXACT for them, which
     // lies closer to the fp64 expert than either of them does
     if (mode < GFL_MODE_AUTO || mode > GFL_MODE_MFMA)
         return fail(GFL_EINVAL, f + ": mode must be -1 (auto), 0 (affine), 1 (exact), 2 (i16) or 3 (mfma)");
-    if (M < 1 || topk < 1 || topk > gfl::MAX_TOPK || (int64_t)M * topk > max_picks)
-        return fail(GFL_EINVAL, f + ": need 1 <= topk <= 16 and M*topk <= " + std::to_string(max_picks));
+    if (M < 0 || topk < 0 || topk > gfl::MAX_TOPK || (int64_t)M * topk > max_picks)
+        return fail(GFL_EINVAL, f + ": need M >= 0, 0 <= topk <= 16 and M*topk <= " + std::to_string(max_picks));
     if ((int64_t)M * topk > gfl::MAX_PICKS && mode == GFL_MODE_MFMA)
         return fail(GFL_EINVAL, f + ": mode MFMA takes M*topk <= 1024 (gfl_grouped_forward is the MFMA path for "
                                     "more)");
     if (!std::isfinite(act_limit) || act_limit < 0) return fail(GFL_EINVAL, f + ": act_limit must be >= 0");
+    // an empty batch touches no buffer (they may be NULL); without picks only x and out are used
+    if (M > 0 && (!x || !out || (topk > 0 && (!sel || !w)))) return fail(GFL_EINVAL, f + ": NULL argument");
     if (reinterpret_cast<uintptr_t>(x) & 15) return fail(GFL_EINVAL, f + ": x must be 16-byte aligned");
     return GFL_OK;
 }
@@ -350,6 +352,16 @@ __global__ void zero_words(int* p, size_t n)
 {
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
         p[i] = 0;
+}
+
+// The result of a call without picks (topk = 0, as the reference's tier_forward returns for sel [m, 0]): M rows of
+// zeros, written by a fill kernel (capture-safe, no allocation).
+int forward_without_picks(gfl_ctx* c, const Layer& L, int M, float* out, hipStream_t st)
+{
+    GFL_HIP(hipSetDevice(c->device));
+    hipLaunchKernelGGL(zero_words, dim3(64), dim3(256), 0, st, reinterpret_cast<int*>(out), (size_t)M * L.H);
+    GFL_HIP(hipGetLastError());
+    return GFL_OK;
 }
 
 constexpr int kMaxDevices = 64;
@@ -568,8 +580,10 @@ int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, c
     if (const int r = check_forward(c, li, x, sel, w, M, topk, out, mode, act_limit, "gfl_moe_forward",
                                     gfl::MAX_GROUPED_PICKS))
         return r;
+    if (M == 0) return GFL_OK;   // an empty batch: nothing to compute
     std::lock_guard<std::mutex> g(c->mu);
     const Layer& L = c->layers[li];
+    if (topk == 0) return forward_without_picks(c, L, M, out, reinterpret_cast<hipStream_t>(stream));
     GFL_HIP(hipSetDevice(c->device));
     if (M * topk > gfl::MAX_PICKS)
         return run_forward_grouped_plan(c, L, x, sel, w, w_is_half, M, topk, out, act_limit,
@@ -587,8 +601,10 @@ int gfl_moe_forward_noalloc(gfl_ctx* c, int li, const uint16_t* x, const int64_t
     const char* who = "gfl_moe_forward_noalloc";
     if (const int r = check_forward(c, li, x, sel, w, M, topk, out, mode, act_limit, who, GFL_NOALLOC_MAX_PICKS))
         return r;
+    if (M == 0) return GFL_OK;   // an empty batch: nothing to compute
     std::lock_guard<std::mutex> g(c->mu);
     const Layer& L = c->layers[li];
+    if (topk == 0) return forward_without_picks(c, L, M, out, reinterpret_cast<hipStream_t>(stream));
     if ((int64_t)M * topk > GFL_NOALLOC_MAX_PICKS || L.H > GFL_NOALLOC_MAX_H || L.I > GFL_NOALLOC_MAX_I)
         return fail(GFL_EINVAL, std::string(who) + ": needs M*topk <= " + std::to_string(GFL_NOALLOC_MAX_PICKS) +
                                     ", H <= " + std::to_string(GFL_NOALLOC_MAX_H) + " and I <= " +
@@ -712,17 +728,20 @@ static int run_forward_grouped_plan(gfl_ctx* c, const Layer& L, const uint16_t* 
 int gfl_grouped_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half,
                         int M, int topk, float* out, float act_limit, gfl_stream stream)
 {
-    if (!c || !x || !sel || !w || !out) return fail(GFL_EINVAL, "gfl_grouped_forward: NULL argument");
+    if (!c) return fail(GFL_EINVAL, "gfl_grouped_forward: NULL argument");
     if (li < 0 || li >= (int)c->layers.size() || !c->layers[li].dptrs)
         return fail(GFL_EINVAL, "gfl_grouped_forward: layer not registered");
-    if (M < 1 || topk < 1 || topk > gfl::MAX_TOPK || (int64_t)M * topk > gfl::MAX_GROUPED_PICKS)
-        return fail(GFL_EINVAL, "gfl_grouped_forward: need 1 <= topk <= 16 and M*topk <= 65536");
+    if (M < 0 || topk < 0 || topk > gfl::MAX_TOPK || (int64_t)M * topk > gfl::MAX_GROUPED_PICKS)
+        return fail(GFL_EINVAL, "gfl_grouped_forward: need M >= 0, 0 <= topk <= 16 and M*topk <= 65536");
     if (!std::isfinite(act_limit) || act_limit < 0)
         return fail(GFL_EINVAL, "gfl_grouped_forward: act_limit must be >= 0");
+    if (M == 0) return GFL_OK;   // an empty batch: nothing to compute (its buffers may be NULL)
+    if (!x || !out || (topk > 0 && (!sel || !w))) return fail(GFL_EINVAL, "gfl_grouped_forward: NULL argument");
     if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out)) & 15)
         return fail(GFL_EINVAL, "gfl_grouped_forward: x and out must be 16-byte aligned");
     std::lock_guard<std::mutex> g(c->mu);
     const Layer& L = c->layers[li];
+    if (topk == 0) return forward_without_picks(c, L, M, out, reinterpret_cast<hipStream_t>(stream));
     if (L.H % 256 || L.I % 256) return fail(GFL_EINVAL, "gfl_grouped_forward: H and I must be multiples of 256");
     // the GEMMs address their fp16 inputs [picks][max(H, I)] through 32-bit buffer offsets
     if ((size_t)M * topk * (size_t)std::max(L.H, L.I) * 2 > (size_t)0x7fffffff)

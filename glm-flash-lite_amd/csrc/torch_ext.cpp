@@ -181,7 +181,8 @@ torch::Tensor tier_forward(int64_t li, torch::Tensor x, torch::Tensor sel, torch
                 "sel: int32 [m, k]");
     TORCH_CHECK(w.scalar_type() == at::kFloat && w.sizes() == sel.sizes(), "w: float32 [m, k]");
     const int64_t m = x.size(0), k = sel.size(1);
-    TORCH_CHECK(m >= 1 && k >= 1 && k <= 16 && m * k <= 65536, "tier_forward: k <= 16 and m * k <= 65536 picks");
+    // m = 0 gives an empty [0, H] result and k = 0 zeros, as the reference's tier_forward does (ft_tier_ext.cpp:893-903)
+    TORCH_CHECK(k <= 16 && m * k <= 65536, "tier_forward: k <= 16 and m * k <= 65536 picks");
     const torch::Device dev(torch::kCUDA, T->device);
     const c10::DeviceGuard g(dev);
     auto xd = x.to(dev);

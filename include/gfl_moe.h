@@ -105,6 +105,8 @@ int gfl_layer_info(gfl_ctx* ctx, int li, int* info);
  * summed in the reference's job order (moe_forward, kernels/cpu_avx2/ft_core.h:1338-1407).
  * x: fp16 [M, H]; sel: int64 [M, topk]; w: [M, topk] fp16 (w_is_half=1) or fp32; out: fp32 [M, H].
  * act_limit: SwiGLU clamp (tier_set_act_limit, ft_tier_ext.cpp:629-636), 0 = off. topk <= 16; x 16-byte aligned.
+ * Empty calls, as the reference's tier_forward takes them (ft_tier_ext.cpp:893-903): M = 0 does nothing (every
+ * buffer may be NULL); topk = 0 writes M rows of zeros to out (sel and w may be NULL).
  * M*topk <= 1024: the decode launches (routing plan built in every workgroup). 1024 < M*topk <= 65536 (EXACT modes
  * only; MFMA is refused there): the grouped plan of the prefill path, then the reference's accumulator chains (each
  * chain step one element of a K=1 fp32 MFMA, i.e. an fmaf), each weight decoded once per pass of up to 64 of an
@@ -139,7 +141,8 @@ int gfl_moe_forward_noalloc(gfl_ctx* ctx, int li, const uint16_t* x, const int64
 
 /* Routed-expert forward of one layer for prefill-sized M (the north star's MFMA grouped GEMM), same arguments and
  * result layout as gfl_moe_forward: x fp16 [M, H], sel int64 [M, topk] (ids outside [0, E) skipped), w fp16 or fp32
- * [M, topk], out fp32 [M, H]; M*topk <= 65536 and M*topk*max(H, I) < 2^30; x and out 16-byte aligned. Rows are
+ * [M, topk], out fp32 [M, H]; M*topk <= 65536 and M*topk*max(H, I) < 2^30; x and out 16-byte aligned; M = 0 and
+ * topk = 0 as in gfl_moe_forward. Rows are
  * grouped expert-major (tier_lut_build_grouped_rows, kernels/cpu_avx2/ft_tier_ext.cpp:1047-1097), gate|up and down
  * run as v_mfma_f32_16x16x32_f16 grouped GEMMs on the bit-exact dequantized fp16 weights, the transforms keep the
  * reference's fp16 rounding points and the combine its job order (kernels/cpu_avx2/ft_core.h:933-1033). The

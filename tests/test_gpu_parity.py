@@ -205,6 +205,40 @@ def test_alignment_errors(gpu):
 
 
 @pytest.mark.gpu
+def test_empty_calls(gpu, oracle):
+    """Empty calls as the reference's tier_forward takes them (ft_tier_ext.cpp:893-903): no tokens is a no-op, and
+    tokens without picks (sel [M, 0]) give rows of zeros, which the oracle's moe_forward gives too; through the
+    decode, no-allocation and grouped entry points, then a normal call on the same context still bit-exact."""
+    import torch
+    L = _layer(gpu, 8, 4, 512, 256)
+    ex = _host_experts(oracle, L)
+    f16 = dict(dtype=torch.float16, device="cuda")
+    i64 = dict(dtype=torch.int64, device="cuda")
+    f32 = dict(dtype=torch.float32, device="cuda")
+    for fn in (gpu.moe_forward, gpu.moe_forward_noalloc, gpu.grouped_forward):
+        name = fn.__name__
+        print(f"empty calls: {name}", flush=True)
+        out0 = torch.empty((0, 512), **f32)
+        fn(8, torch.empty((0, 512), **f16), torch.empty((0, 8), **i64), torch.empty((0, 8), **f32), out0)
+        x = torch.randn((3, 512), **f32).to(torch.float16)
+        out = torch.full((3, 512), float("nan"), **f32)
+        fn(8, x, torch.empty((3, 0), **i64), torch.empty((3, 0), **f32), out)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        want = oracle.moe_forward(ex, x.float().cpu().numpy(), np.zeros((3, 0), np.int64), np.zeros((3, 0), np.float32),
+                                  mode=1)
+        assert np.array_equal(got, np.zeros((3, 512), np.float32)) and np.array_equal(want, got), name
+        assert not np.signbit(got).any(), name
+    rng = np.random.default_rng(800)
+    x16 = rng.standard_normal((2, 512)).astype(np.float16)
+    sel = np.array([[0, 1], [2, 3]], np.int64)
+    w = rng.random((2, 2)).astype(np.float32)
+    got = _forward(gpu, 8, x16, sel, w)
+    _, _, nbad = _report("after empty calls", got, oracle.moe_forward(ex, x16.astype(np.float32), sel, w, mode=1))
+    assert nbad == 0
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("ns", [1, 2, 4, 8])
 def test_forward_slots_per_pass_bitexact(gpu, oracle, ns):
     """Every slots-per-pass instantiation (GFL_SLOTS_PER_PASS, read at context creation): 12 tokens over 6 experts, so

@@ -141,6 +141,20 @@ def test_tier_forward_argument_errors(tier):
         ft_tier.tier_init(1, [0], e, e, e, e, -1, tier["H"], tier["I"], 1, 0)
 
 
+def test_tier_forward_empty_calls(tier):
+    """m = 0 returns an empty [0, H] result and sel [m, 0] rows of zeros, as the reference's tier_forward builds them
+    (torch::zeros of [m, H], ft_tier_ext.cpp:893-903)."""
+    import ft_tier
+    H = tier["H"]
+    out = ft_tier.tier_forward(0, torch.zeros(0, H), torch.zeros(0, 4, dtype=torch.int32), torch.zeros(0, 4), 1)
+    assert tuple(out.shape) == (0, H) and out.dtype == torch.float32 and not out.is_cuda
+    x = torch.randn(2, H).half().float()
+    out = ft_tier.tier_forward(0, x, torch.zeros(2, 0, dtype=torch.int32), torch.zeros(2, 0), -1)
+    assert tuple(out.shape) == (2, H) and torch.equal(out, torch.zeros(2, H))
+    out = ft_tier.tier_forward(0, x.cuda(), torch.zeros(2, 0, dtype=torch.int32), torch.zeros(2, 0), 1)
+    assert out.is_cuda and torch.equal(out.cpu(), torch.zeros(2, H))
+
+
 def test_pool_on_device_verifies_clean(tier):
     r = tier["pool"].verify()
     assert r["bad_slots"] == 0 and r["bad_tables"] == 0 and r["owned"] == 2 * tier["E"]
