@@ -653,6 +653,16 @@ int launch_route_split(const float* logits, int M, int ER, int topk, int64_t* se
                        hipStream_t st)
 {
     if (ER < 1 || ER > ROUTE_MAXE || topk < 1 || topk > ER || topk > 64 || M * topk > MAX_PICKS) return -1;
+    // one launch while each of its waves routes at most one token. Above that its waves would take their tokens one
+    // after another (one logits round trip and about 2 us of exponentials and argmax rounds each: 17.7 / 32.0 /
+    // 58.9 us at M = 16 / 32 / 64), so the router runs over a grid of its own (a wave per token) and the split follows
+    // as a second launch; both write what the fused launch writes, bit for bit.
+    if (M > SP_T / 64)
+    {
+        if (launch_route(logits, M, ER, topk, sel, w, st)) return -1;
+        return launch_split(sel, w, z, M * topk, M, topk, H, E, first, slotof, score, pol, ctrl, hx, hpicks, seq, li,
+                            keep_ids, sel_out, w_out, dflag, stats, rres, st);
+    }
     switch ((ER + 63) / 64)
     {
 #define GFL_RS_CASE(N)                                                                                             \

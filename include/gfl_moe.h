@@ -187,10 +187,11 @@ int gfl_split(const int64_t* sel, const uint16_t* w, const uint16_t* z, int bsz,
               int32_t* hpicks, int64_t seq, int li, int keep_ids, int64_t* sel_out, uint16_t* w_out, int64_t* dflag,
               int64_t* stats, const int32_t* rres, gfl_stream stream);
 
-/* Router and split in one launch: the routing_fn that cpu_tier.routed wraps (glm53/cpu_tier.py:305-333) followed by
- * ft_split on its output. logits fp32 [M, E_route] -> sel int64 [M, topk] / w fp16 [M, topk] (written: the routing
- * gfl_route computes), then the split of those picks with the remaining arguments as gfl_split's (bsz = M,
- * n = M * topk <= 1024). No counterpart of its own in the reference (it fuses two of its launches). */
+/* Router and split: the routing_fn that cpu_tier.routed wraps (glm53/cpu_tier.py:305-333) followed by ft_split on
+ * its output. logits fp32 [M, E_route] -> sel int64 [M, topk] / w fp16 [M, topk] (written: the routing gfl_route
+ * computes), then the split of those picks with the remaining arguments as gfl_split's (bsz = M,
+ * n = M * topk <= 1024). One launch up to M = 4 (a wave per token); above, gfl_route's launch then gfl_split's, with
+ * the same results. No counterpart of its own in the reference (it fuses two of its launches). */
 int gfl_route_split(const float* logits, int M, int E_route, int topk, int64_t* sel, uint16_t* w, const uint16_t* z,
                     int H, int E, int first, const int32_t* slotof, const float* score, const float* pol,
                     int64_t* ctrl, uint16_t* hx, int32_t* hpicks, int64_t seq, int li, int keep_ids, int64_t* sel_out,

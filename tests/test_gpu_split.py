@@ -228,11 +228,11 @@ def _route_split_gpu(logits, topk, c):
 
 @pytest.mark.parametrize("kind", ["stock", "tri", "lut"])
 def test_route_split_matches_router_then_split(gpu, oracle, kind):
-    """gfl_route_split (router + split in one launch) = the router (closed form, checked against the oracle's) followed
-    by the split (the oracle's), on every output."""
+    """gfl_route_split = the router (closed form, checked against the oracle's) followed by the split (the oracle's),
+    on every output: one launch up to 4 tokens, the router's grid then the split above (5 to 128 tokens)."""
     rng = np.random.default_rng({"stock": 51, "tri": 52, "lut": 53}[kind])
-    for i in range(20):
-        M = int(rng.choice([1, 2, 4, 16]))
+    for i in range(21):
+        M = [1, 2, 4, 5, 16, 64, 128][i % 7]
         E = int(rng.choice([64, 288]))
         logits = rng.standard_normal((M, E)).astype(np.float32)
         c = _case(rng, E, 0, M, 8, float(rng.choice([1.0, 0.5, 0.0])), kind)
