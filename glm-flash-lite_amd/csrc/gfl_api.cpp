@@ -303,22 +303,27 @@ int run_forward(gfl_ctx* c, const Layer& L, const Workspace& ws, const uint16_t*
         }
         if (c->rw_override[0] >= 0) { rw[0] = c->rw_override[0]; rw[1] = c->rw_override[1]; }
     }
-    if (gfl::gate_up_lds_bytes(L.K[0], ns, L.H, P, L.E, mf, rw[0]) > gfl::LDS_LIMIT ||
-        gfl::gate_up_lds_bytes(L.K[1], ns, L.H, P, L.E, mf, rw[0]) > gfl::LDS_LIMIT ||
+    // above 192 picks the launches without relay take the routing plan from a launch of its own (plan_kernel) instead
+    // of every workgroup building it in LDS. Measured on MI355X (config 1, us per token): M = 28 26.4 -> 25.2, M = 32
+    // 25.9 -> 24.5, M = 64 23.3 -> 21.5; even at M = 24, and 2-3% slower at M = 12..20, where the extra launch and the
+    // workgroups' dependent reads of the published plan cost more than the smaller builds they save.
+    const int gplan = !rw[0] && P > 192 ? 1 : 0;
+    if (gfl::gate_up_lds_bytes(L.K[0], ns, L.H, P, L.E, mf, rw[0], gplan) > gfl::LDS_LIMIT ||
+        gfl::gate_up_lds_bytes(L.K[1], ns, L.H, P, L.E, mf, rw[0], gplan) > gfl::LDS_LIMIT ||
         gfl::down_lds_bytes(L.K[2], ns, L.I, P, L.E, mf, rw[1]) > gfl::LDS_LIMIT)
         return fail(GFL_EINVAL, "gfl_moe_forward: shape needs more than 160 KB of LDS per workgroup");
     const int wh = w_is_half ? 1 : 0;
     auto gate_up = [&] {
         if (L.K[0] == L.K[1])
             return gfl::launch_gate_up(L.K[0], ns, L.dptrs, 0, 2, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                       ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], c->status,
+                                       ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], gplan, c->status,
                                        c->spin_max, st);
         if (gfl::launch_gate_up(L.K[0], ns, L.dptrs, 0, 1, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], c->status,
+                                ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], gplan, c->status,
                                 c->spin_max, st))
             return -1;
         return gfl::launch_gate_up(L.K[1], ns, L.dptrs, 1, 1, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                   ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], c->status,
+                                   ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], gplan, c->status,
                                    c->spin_max, st);
     };
     auto down = [&] {

@@ -832,6 +832,8 @@ struct GuArgs
     int nmat_launch;           // matrices of this launch (the relay launches' item count)
     int* status;               // the context's status words (relay waits that expired)
     int spin_max;              // bound of a relay turn wait, in polls
+    int gplan;                 // the routing plan was published to pv by plan_kernel before this launch: workgroups
+                               // read their entries from pv instead of each building the plan in LDS
 };
 
 __device__ __forceinline__ float ld_agent(const float* p)
@@ -888,6 +890,21 @@ __device__ void act_block(const GuArgs& a, int e, int s_begin, int s_end, int b)
     }
 }
 
+// The routing plan of a call, built once and published to pv before the gate|up launch (calls above 192 picks
+// outside the relay launches). Each of the launch's thousands of workgroups building the whole plan itself (one wave
+// scanning every pick with ballots while the others wait) measured 2.6% of the layer at M = 12..16 and 6.4% at
+// M = 32..64 (config 1, a second build per workgroup), and its LDS (17 KB at 512 picks) held the gate|up launch to 3
+// workgroups per CU. One workgroup; dynamic LDS: lplan_ints(P, E) ints.
+__global__ __launch_bounds__(GU_NW * 64) void plan_kernel(GuArgs a)
+{
+    extern __shared__ __align__(16) uint8_t lds_raw[];
+    __shared__ int hdr[4];
+    const LPlan L = lplan_carve(reinterpret_cast<int*>(lds_raw), a.P, a.E);
+    if (a.P <= 64) build_plan_wave(a.sel, a.P, a.E, L, hdr);
+    else build_plan(a.sel, a.P, a.E, L, hdr);
+    publish_plan(L, hdr, a.P, a.topk, a.w, a.w_half, a.pv, a.out, a.H, a.ptrs, a.per_slot);
+}
+
 // Grid: (umax * I/64 + 1, nmat). Workgroup = 4 waves = 64 outputs of one matrix of one routed expert, all its
 // slots; the last workgroup of row 0 publishes the plan. With per_slot the grid is (P * I/64 + 1, nmat) and a
 // workgroup takes one slot: an expert picked by several tokens is streamed once per slot, in parallel, instead of in
@@ -914,28 +931,32 @@ gu_kernel(GuArgs a)
     int* plan_mem = reinterpret_cast<int*>(lds_raw + NW * RB + (size_t)a.ns_cap * a.H * XE / (MF ? 2 : 1));
     const int TN = a.I / 16, TK = a.H / 16, ncb = TN / NW;
     const LPlan L = lplan_carve(plan_mem, a.P, a.E);
-    if (a.P <= 64) build_plan_wave(a.sel, a.P, a.E, L, hdr);
-    else build_plan(a.sel, a.P, a.E, L, hdr);
+    if (!a.gplan)
+    {
+        if (a.P <= 64) build_plan_wave(a.sel, a.P, a.E, L, hdr);
+        else build_plan(a.sel, a.P, a.E, L, hdr);
+    }
     if (blockIdx.x == gridDim.x - 1)
     {
         // the grid's extra workgroup publishes the plan for the down launch (no GEMV work of its own)
-        if (blockIdx.y == 0) publish_plan(L, hdr, a.P, a.topk, a.w, a.w_half, a.pv, a.out, a.H, a.ptrs, a.per_slot);
+        if (blockIdx.y == 0 && !a.gplan)
+            publish_plan(L, hdr, a.P, a.topk, a.w, a.w_half, a.pv, a.out, a.H, a.ptrs, a.per_slot);
         return;
     }
 
     // union entry (or slot with per_slot), column block, and with MF the half of the tile rows (adjacent workgroups)
     const int nper = MF ? 2 * ncb : ncb;
     const int ent = blockIdx.x / nper, cb = (blockIdx.x % nper) / (MF ? 2 : 1), hf = MF ? blockIdx.x & 1 : 0;
-    if (ent >= hdr[a.per_slot ? 1 : 0]) return;
-    const int u = a.per_slot ? plan_u(L, L.spick[ent]) : ent;
+    if (ent >= (a.gplan ? a.pv.hdr[a.per_slot ? 1 : 0] : hdr[a.per_slot ? 1 : 0])) return;
+    const int u = a.per_slot ? (a.gplan ? a.pv.slot_u[ent] : plan_u(L, L.spick[ent])) : ent;
     const int mat = a.mat_base + blockIdx.y;              // 0 gate, 1 up
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15;
     const int wid = __builtin_amdgcn_readfirstlane(wave);
-    const int e = L.uexp[u];
+    const int e = a.gplan ? a.pv.uexp[u] : L.uexp[u];
     const uint8_t* tr = reinterpret_cast<const uint8_t*>(a.ptrs[(size_t)e * 9 + mat]);
     const gptr<uint16_t> suh = gaddr<uint16_t>(a.ptrs[(size_t)e * 9 + 3 + 2 * mat]);
-    const int s_begin = a.per_slot ? ent : L.uoff[u];
-    const int s_end = a.per_slot ? ent + 1 : L.uoff[u + 1];
+    const int s_begin = a.per_slot ? ent : (a.gplan ? a.pv.uoff[u] : L.uoff[u]);
+    const int s_end = a.per_slot ? ent + 1 : (a.gplan ? a.pv.uoff[u + 1] : L.uoff[u + 1]);
     const size_t gstride = (size_t)TN * TB;
     const int t = cb * NW + wave;                         // this wave's tile column
     const uint8_t* col = tr + (size_t)t * TB;
@@ -957,7 +978,7 @@ gu_kernel(GuArgs a)
         auto load_round = [&](int r, int k) {
             const int it = min((r * NW + wave) * 4 + rl, nit - 1);
             const int s = it / nblk, b = g0 + it % nblk;
-            const int pk = L.spick[c0 + s];
+            const int pk = a.gplan ? a.pv.slot_pick[c0 + s] : L.spick[c0 + s];
             xv[k] = *reinterpret_cast<const uint4*>(a.x + (size_t)(pk / a.topk) * a.H + b * 128 + li * 8);
             sv[k] = gld16(suh, b * 128 + li * 8);
         };
@@ -1622,10 +1643,12 @@ static bool open_lds(F kern)
                                LDS_LIMIT - (int)at.sharedSizeBytes) == hipSuccess;
 }
 
+// gplan: the plan comes from pv (plan_kernel), so none is built in LDS
 template <int K>
-static size_t gu_lds(int ns, int H, int P, int E, int mf)
+static size_t gu_lds(int ns, int H, int P, int E, int mf, int gplan)
 {
-    return (size_t)GU_NW * NGRP * 8 * 32 * K + (size_t)ns * H * (mf ? 1 : x_lds_elem(ns)) + lplan_ints(P, E) * 4;
+    return (size_t)GU_NW * NGRP * 8 * 32 * K + (size_t)ns * H * (mf ? 1 : x_lds_elem(ns)) +
+           (gplan ? 0 : lplan_ints(P, E) * 4);
 }
 
 template <int K>
@@ -1638,13 +1661,20 @@ static size_t dn_lds(int ns, int I, int mf)
 template <int K, int NS, bool MF>
 static void gu_launch(const GuArgs& a, int umax, int nmat, hipStream_t st)
 {
-    const size_t lds = gu_lds<K>(a.ns_cap, a.H, a.P, a.E, MF);
+    const size_t lds = gu_lds<K>(a.ns_cap, a.H, a.P, a.E, MF, a.gplan);
     auto kern = gu_kernel<K, NS, MF>;
     static const bool opened = open_lds(kern);
     (void)opened;
     const int ents = a.per_slot ? a.P : umax;
     const int per_ent = (a.I / (16 * GU_NW)) * (MF ? 2 : 1);   // MF: both halves of the tile rows
     timed_launch(kern, dim3(ents * per_ent + 1, nmat), dim3(GU_NW * 64), lds, st, a);
+}
+
+static void plan_launch(const GuArgs& a, hipStream_t st)
+{
+    static const bool opened = open_lds(plan_kernel);
+    (void)opened;
+    timed_launch(plan_kernel, dim3(1), dim3(GU_NW * 64), lplan_ints(a.P, a.E) * 4, st, a);
 }
 
 template <int K, int NS, bool MF>
@@ -1735,11 +1765,11 @@ static void dn_relay_launch(const DnArgs& a, int P, hipStream_t st)
         default: return -1;                                                                                     \
     }
 
-size_t gate_up_lds_bytes(int K, int ns, int H, int P, int E, int mf, int rw)
+size_t gate_up_lds_bytes(int K, int ns, int H, int P, int E, int mf, int rw, int gplan)
 {
     size_t r = 0;
     auto f = [&]() -> int {
-        GFL_K_SWITCH(K, (r = rw ? gu_relay_lds<K_>(H, P, E) : gu_lds<K_>(ns, H, P, E, mf)))
+        GFL_K_SWITCH(K, (r = rw ? gu_relay_lds<K_>(H, P, E) : gu_lds<K_>(ns, H, P, E, mf, gplan)))
         return 0;
     };
     f();
@@ -1760,10 +1790,10 @@ size_t down_lds_bytes(int K, int ns, int I, int P, int E, int mf, int rw)
 int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, const int64_t* sel, const void* w,
                    int w_half, int P, int topk, int E, int H, int I, int umax, const uint16_t* x, float* ygu,
                    uint16_t* xtd, int* act_cnt, const float* silu_tab, float act_limit, const PlanView& pv, float* out,
-                   int mf, int rw, int* status, int spin_max, hipStream_t st)
+                   int mf, int rw, int gplan, int* status, int spin_max, hipStream_t st)
 {
     GuArgs a;
-    a.status = status; a.spin_max = spin_max; a.nmat_launch = nmat;
+    a.status = status; a.spin_max = spin_max; a.nmat_launch = nmat; a.gplan = rw ? 0 : gplan;
     a.ptrs = ptrs; a.sel = sel; a.w = w; a.w_half = w_half; a.P = P; a.topk = topk; a.E = E; a.H = H; a.I = I;
     a.mat_base = mat_base; a.x = x; a.ygu = ygu; a.xtd = xtd; a.act_cnt = act_cnt; a.silu_tab = silu_tab;
     a.act_limit = act_limit; a.pv = pv; a.out = out;
@@ -1774,6 +1804,7 @@ int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, 
         // MFMA-accumulate mode: workgroups per union entry, all its slots in passes of up to ns
         a.nmat_total = 2 * 2 * (128 / (16 * GU_NW));   // gate, up x two halves
         a.per_slot = 0;
+        if (a.gplan && mat_base == 0) plan_launch(a, st);
         GFL_K_SWITCH(K, (gu_launch<K_, 4, true>(a, umax, nmat, st)))
         return 0;
     }
@@ -1787,6 +1818,7 @@ int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, 
     }
     a.nmat_total = 2 * (128 / (16 * GU_NW));
     a.per_slot = ns == 1;
+    if (a.gplan && mat_base == 0) plan_launch(a, st);
     GFL_K_SWITCH(K, GFL_NS_SWITCH(ns, (gu_launch<K_, NS_, false>(a, umax, nmat, st))))
     return 0;
 }
