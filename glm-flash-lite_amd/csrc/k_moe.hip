@@ -281,25 +281,42 @@ __device__ void publish_plan(const LPlan& L, const int* hdr, int P, int topk, co
     const int M = P / topk;
     for (int tk = t; tk < M; tk += nt)
     {
-        int ord[MAX_TOPK], job[MAX_TOPK];
-        int n = 0;
-        for (int k = 0; k < topk; ++k)
+        // the token's picks in (job, pick) order: each valid pick's place is the number of valid picks before it in
+        // that order. Everything is read first and kept in registers (the loads are unconditional, past topk on the
+        // token's last pick again): with the weight loads between the stores below, each would wait for the store
+        // before it, and a sort through indexed arrays would live in scratch memory.
+        int jb[MAX_TOPK], sl[MAX_TOPK];
+        float wt[MAX_TOPK];
+        bool ok[MAX_TOPK];
+#pragma unroll
+        for (int k = 0; k < MAX_TOPK; ++k)
         {
-            const int p = tk * topk + k;
-            if (L.e[p] < 0) continue;
-            const int jb = plan_job(L, p);
-            int b = n++;
-            while (b > 0 && job[b - 1] > jb) { ord[b] = ord[b - 1]; job[b] = job[b - 1]; --b; }
-            ord[b] = p;
-            job[b] = jb;
+            const int p = tk * topk + min(k, topk - 1);
+            ok[k] = k < topk && L.e[p] >= 0;
+            wt[k] = w_half ? h2f_bits(reinterpret_cast<const uint16_t*>(w)[p]) : reinterpret_cast<const float*>(w)[p];
+            jb[k] = ok[k] ? plan_job(L, p) : 0;
+            sl[k] = ok[k] ? L.uoff[plan_u(L, p)] + L.c[p] : -1;
         }
-        for (int k = 0; k < topk; ++k)
+        int n = 0;
+#pragma unroll
+        for (int k = 0; k < MAX_TOPK; ++k) n += ok[k] ? 1 : 0;
+#pragma unroll
+        for (int k = 0; k < MAX_TOPK; ++k)
         {
-            const int p = k < n ? ord[k] : -1;
-            pv.tok_slot[tk * topk + k] = p >= 0 ? L.uoff[plan_u(L, p)] + L.c[p] : -1;
-            pv.tok_w[tk * topk + k] = p < 0 ? 0.f
-                                    : (w_half ? h2f_bits(reinterpret_cast<const uint16_t*>(w)[p])
-                                              : reinterpret_cast<const float*>(w)[p]);
+            int r = 0;
+#pragma unroll
+            for (int k2 = 0; k2 < MAX_TOPK; ++k2)
+                r += (ok[k2] && (jb[k2] < jb[k] || (jb[k2] == jb[k] && k2 < k))) ? 1 : 0;
+            if (ok[k])
+            {
+                pv.tok_slot[tk * topk + r] = sl[k];
+                pv.tok_w[tk * topk + r] = wt[k];
+            }
+        }
+        for (int k = n; k < topk; ++k)
+        {
+            pv.tok_slot[tk * topk + k] = -1;
+            pv.tok_w[tk * topk + k] = 0.f;
         }
         pv.tok_npk[tk] = n;
         if (n == 0)
