@@ -283,7 +283,8 @@ int run_forward(gfl_ctx* c, const Layer& L, const Workspace& ws, const uint16_t*
     // keeps those calls on the per-slot launches. From 16 picks on the one-wave relay launches stay (routed + shared
     // at M = 4 overlapped: 43.2 us per token with the per-slot launches, 41.5 with them).
     int rw[2] = { 0, 0 };
-    if (!mf && ns == 1)
+    // the relay down launch forms each token's combine order from one pick per lane of a wave: at most 64 picks
+    if (!mf && ns == 1 && P <= 64)
     {
         const int64_t cgu = (int64_t)P * 2 * (L.I / 16), cdn = (int64_t)P * (L.H / 16);   // tile columns
         if (cgu <= 768)
@@ -332,7 +333,7 @@ int run_forward(gfl_ctx* c, const Layer& L, const Workspace& ws, const uint16_t*
     };
     int r = prof ? staged(c, 1, st, gate_up) : gate_up();
     if (!r) r = prof ? staged(c, 3, st, down) : down();
-    if (r) return r > 0 ? r : fail(GFL_EINVAL, "gfl_moe_forward: unsupported K");
+    if (r) return r > 0 ? r : fail(GFL_EINVAL, "gfl_moe_forward: unsupported K or launch shape");
     GFL_HIP(hipGetLastError());
     c->calls += 1;
     c->picks += P;
@@ -723,7 +724,7 @@ static int run_forward_grouped_plan(gfl_ctx* c, const Layer& L, const uint16_t* 
                                         L.K[2], x, ws.gp, P, ws.xte, ws.ygue, ws.xde, ws.yre, c->silu_tab, act_limit,
                                         out, st);
     });
-    if (r) return r > 0 ? r : fail(GFL_EINVAL, "gfl_moe_forward: unsupported K");
+    if (r) return r > 0 ? r : fail(GFL_EINVAL, "gfl_moe_forward: unsupported K or launch shape");
     GFL_HIP(hipGetLastError());
     c->calls += 1;
     c->picks += P;

@@ -86,7 +86,8 @@ int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, 
                    int mf, int rw, int gplan, int* status, int spin_max, hipStream_t st);
 // down launch: down GEMV + out_block, weighted combine per (token, 128-block) by the token's last expert; mf and ns
 // as for launch_gate_up (the same values for both launches of a call). blk_cnt: [cap][H/128] half-block counters of
-// the one-slot-per-pass EXACT launch (zero between calls). rw as for launch_gate_up (the same value for both).
+// the one-slot-per-pass EXACT launch (zero between calls). rw as for launch_gate_up (the same value for both; the
+// relay down launch takes at most 64 picks, else -1).
 int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int umax, int P, int E, const int64_t* sel,
                 const void* w, int w_half, const PlanView& pv, const uint16_t* xtd, float* yd, int* out_cnt,
                 int* blk_cnt, float* out, int mf, int rw, int* status, int spin_max, hipStream_t st);

@@ -1859,6 +1859,8 @@ int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int
     }
     if (rw)
     {
+        // relay_combine_list holds the call's picks one per lane of a wave
+        if (P > 64) return -1;
         a.per_slot = 1;
         GFL_K_SWITCH(K, GFL_RW_SWITCH(rw, (dn_relay_launch<K_, RW_>(a, P, st))))
         return 0;

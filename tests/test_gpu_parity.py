@@ -548,6 +548,29 @@ def test_relay_launches_full_shape_bitexact(gpu, oracle, relay):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("relay", [None, "1,1"])
+def test_one_slot_per_pass_above_64_picks_bitexact(gpu, oracle, relay):
+    """Top-16 at M = 5 and 8 (80 and 128 picks, one slot per pass): more picks than the relay down launch's combine
+    list holds (one per lane of a wave), so these calls keep the per-slot launches, under the default launch choice
+    and with the relay forced (GFL_RELAY applies up to 64 picks); every token's row bit-exact, including tokens past
+    the first 64 picks. At 64 picks (M = 4) the relay launches run."""
+    ctx = gpu if relay is None else _ctx_with_env(GFL_RELAY=relay)
+    H, I, E, li = 512, 256, 20, 54 if relay is None else 55
+    L = _layer(ctx, li, E, H, I, (3, 4, 3))
+    ex = _host_experts(oracle, L)
+    for M in (4, 5, 8):
+        rng = np.random.default_rng(5400 + M)
+        x16 = rng.standard_normal((M, H)).astype(np.float16)
+        sel = np.stack([rng.permutation(E)[:16] for _ in range(M)]).astype(np.int64)
+        sel[M - 1, 3] = -1
+        w = rng.random(sel.shape).astype(np.float32)
+        got = _forward(ctx, li, x16, sel, w)
+        want = oracle.moe_forward(ex, x16.astype(np.float32), sel, w, mode=1)
+        _, _, nbad = _report(f"relay {relay} top-16 M={M}", got, want)
+        assert nbad == 0
+
+
+@pytest.mark.gpu
 def test_shared_context_launch_choice_bitexact(gpu, oracle):
     """At 8 picks of the config-1 shape the default context runs the relay launches and a context told that other GPU
     work runs beside it (gfl_ctx_set_shared) keeps the per-slot launches: both bit-exact against the oracle, on the
