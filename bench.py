@@ -5,7 +5,9 @@ Workload: one MoE layer of 288 routed experts, top-8, SwiGLU
 M = 1..4 decode tokens with fp16 N(0,1) activations and sigmoid top-8 routing of N(0,1) fp32 logits. A step is one
 layer call (split -> 8*M expert GEMVs -> weighted combine) through the C ABI. Steps cycle through `--layers` distinct
 288-expert layers (2.56 GB each) and 32 routings, so expert bytes come from HBM, not the 256 MB Infinity Cache.
-Steps are captured in a HIP graph and replayed; the timed region is bracketed by synchronisation.
+Steps are captured in a HIP graph and replayed; the timed region is bracketed by synchronisation. Before it, after
+the --warmup eager steps, the captured graphs are replayed until 30 ms of device time has passed: the device's first
+~10 ms of sustained load run up to 25% slower, which a short timed region (--steps 20) would otherwise measure.
 
 value        = microseconds per token at M=1 (lower is better): the median over exactly --steps timed steps of the
                per-step times (device events between replays of up to 8 captured graphs of up to --graph-steps steps,
@@ -45,6 +47,7 @@ MFMA_PEAK_TFLOPS = 2500.0   # dense fp16 MFMA
 MFMA_FP32_PEAK_TFLOPS = 157.3   # dense fp32 MFMA
 H, I, E, TOPK, KBITS = 5120, 1536, 288, 8, 3
 XSTEPS = 128   # steps per line of the configs beside the headline
+WARM_MS = 30.0   # device time of graph replays before each graph-timed region (graph_time)
 
 
 def physical_cpus(skip=2, cap=16):
@@ -262,6 +265,23 @@ def replay_samples(graphs, reps):
     return [ev[r].elapsed_time(ev[r + 1]) for r in range(reps)], ev[0].elapsed_time(ev[reps])
 
 
+def warm_graphs(graphs):
+    """Replay `graphs` round-robin until WARM_MS of device time has passed (each at least once): the device's first
+    ~10 ms of sustained load run slower (20-step measurements of config 1 M=4 repeated back to back in one process
+    gave 42.1, 41.2, 35.8, 34.6, ... 33.7 us/token), so a timed region right after capture would measure that ramp
+    rather than the kernels."""
+    import torch
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    while True:
+        for g in graphs:
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        if e0.elapsed_time(e1) >= WARM_MS:
+            return
+
+
 def _dist(ms_per_step, M):
     import numpy as np
     a = np.asarray(ms_per_step) * 1e3 / M
@@ -294,9 +314,7 @@ def graph_time(step, out, steps, G, warmup, ngraphs=8):
             for i in range(G):
                 step(j * G + i)
         graphs.append(g)
-    for g in graphs:
-        g.replay()
-    torch.cuda.synchronize()
+    warm_graphs(graphs)
     samples, total_ms = replay_samples(graphs, reps)
     graphs[-1].replay()
     torch.cuda.synchronize()
@@ -511,8 +529,7 @@ def time_shared(ctx, layer_ids, G, reps):
             with torch.cuda.graph(g):
                 for i in range(G):
                     step(i)
-            g.replay()
-            torch.cuda.synchronize()
+            warm_graphs([g])
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
             for _ in range(reps):
@@ -542,8 +559,7 @@ def time_router(M, reps=8, G=32):
     with torch.cuda.graph(g):
         for _ in range(G):
             _native.route(lg, TOPK, sel, w)
-    g.replay()
-    torch.cuda.synchronize()
+    warm_graphs([g])
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(reps):
@@ -591,6 +607,7 @@ def time_prefill(ctx, layer_ids, bytes_per_expert, M, reps, G=4, exact=False):
     call(G - 1)
     torch.cuda.synchronize()
     graph_ok = bool(torch.equal(got, out))
+    warm_graphs([g])
     samples, total = replay_samples([g], reps)
     ms = total / (reps * G)
     del g

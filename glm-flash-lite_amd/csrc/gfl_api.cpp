@@ -69,7 +69,7 @@ struct gfl_ctx
     // "0" for the per-slot launches without relay; -1 = chosen from the call's size
     int rw_override[2] = { -1, -1 };
     // other GPU work runs beside this context's decode calls (gfl_ctx_set_shared): keep calls of 769..1536 gate|up
-    // tile columns on the per-slot launches, which leave SIMDs free
+    // tile columns on the per-slot launches and run calls of up to 768 with 2 waves per column, which leave SIMDs free
     int shared = 0;
     // workspace of the prefill path (gfl_grouped_forward / gfl_grouped_reserve), grown on demand outside captures
     void* gws = nullptr;
@@ -281,13 +281,20 @@ int run_forward(gfl_ctx* c, const Layer& L, const Workspace& ws, const uint16_t*
     // The relay launches at 8 picks fill every SIMD with 3 waves, so a shared expert on a side stream (k_overlap)
     // then waits (routed + shared 71.3 -> 79.1 us): a context told that other work runs beside it (gfl_ctx_set_shared)
     // keeps those calls on the per-slot launches. From 16 picks on the one-wave relay launches stay (routed + shared
-    // at M = 4 overlapped: 43.2 us per token with the per-slot launches, 41.5 with them).
+    // at M = 4 overlapped: 43.2 us per token with the per-slot launches, 41.5 with them). A shared context's calls of
+    // up to 768 columns (a shared expert beside a routed call that fills every SIMD) take 2 waves per gate|up column
+    // and 1 per down column instead of 4: routed + shared at M = 4 overlapped 41.1 -> 38.8 us per token.
     int rw[2] = { 0, 0 };
     // the relay down launch forms each token's combine order from one pick per lane of a wave: at most 64 picks
     if (!mf && ns == 1 && P <= 64)
     {
         const int64_t cgu = (int64_t)P * 2 * (L.I / 16), cdn = (int64_t)P * (L.H / 16);   // tile columns
-        if (cgu <= 768)
+        if (cgu <= 768 && c->shared)
+        {
+            rw[0] = 2;
+            rw[1] = 1;
+        }
+        else if (cgu <= 768)
         {
             rw[0] = 4;
             rw[1] = cdn <= 768 ? 4 : cdn <= 1536 ? 2 : 1;

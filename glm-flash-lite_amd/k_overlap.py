@@ -10,7 +10,8 @@ captures into HIP graphs (events are created once, up front).
 
 At decode sizes the routed launches leave compute units idle (1,536 gate|up column-waves on 1,024 SIMDs at M=1), which
 is the room the shared expert's 48 + 40 workgroups run in. The routed context is told so for the overlapped call
-(gfl_ctx_set_shared): on its own it runs such calls with launches that fill every SIMD.
+(gfl_ctx_set_shared): on its own it runs such calls with launches that fill every SIMD. A larger routed call fills
+every SIMD anyway; beside it the shared expert's own context is told so, and its launches leave SIMDs free instead.
 """
 import torch
 
@@ -29,6 +30,7 @@ class SharedOverlap:
         self._sel = {}
         self._w = {}
         self._y = {}
+        self._I = {}
         self.overlapped = 0
         self.sequential = 0
 
@@ -53,13 +55,21 @@ class SharedOverlap:
         main = torch.cuda.current_stream(self.device)
         if not overlap:
             routed.moe_forward(li, x, sel, w, out)
+            self.ctx.set_shared(False)
             self.ctx.moe_forward(li, x, s1, w1, y)
             out.add_(y)
             self.sequential += 1
             return out
         self.fork.record(main)                   # MoE input ready
         self.side.wait_event(self.fork)
+        # beside a routed call of more than 1,536 gate|up tile columns (it fills every SIMD: 2 or more tokens at
+        # top-8 and I = 1536) the shared expert takes narrower launches that leave SIMDs free (routed + shared at M = 4
+        # 41.1 -> 38.8 us per token); beside a smaller routed call the default launches are faster (69.9 against 72.5
+        # at M = 1)
+        I = self._inter(routed, li)
+        narrow = M * sel.shape[1] * 2 * (I // 16) > 1536
         with torch.cuda.stream(self.side):
+            self.ctx.set_shared(narrow)
             self.ctx.moe_forward(li, x, s1, w1, y)
             self.join.record(self.side)
         # the routed call keeps launch shapes that leave SIMDs free for the side stream (same results); the caller's
@@ -74,6 +84,12 @@ class SharedOverlap:
         out.add_(y)
         self.overlapped += 1
         return out
+
+    def _inter(self, routed, li):
+        """The routed layer's intermediate size (gfl_layer_info), cached per layer."""
+        if li not in self._I:
+            self._I[li] = routed.layer_info(li)[2]
+        return self._I[li]
 
     def summary(self):
         return {"overlapped": self.overlapped, "sequential": self.sequential}

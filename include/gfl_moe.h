@@ -62,8 +62,9 @@ int gfl_ctx_destroy(gfl_ctx* ctx);
 /* Whether other GPU work runs beside this context's decode calls (shared != 0), such as a shared expert on a side
  * stream. No counterpart in the reference: it selects launch shapes only, never results (every shape is bit-exact).
  * With shared = 0 (the default) a call of 769..1536 gate|up tile columns (8 picks at I = 1536) runs the relay
- * launches, which put 3 waves on every SIMD; with shared != 0 it keeps the per-slot launches, which leave SIMDs free
- * for the other work. Read at each gfl_moe_forward / gfl_moe_forward_noalloc call (and so fixed in a captured
+ * launches, which put 3 waves on every SIMD, and a call of up to 768 (e.g. one expert) 4 waves per tile column; with
+ * shared != 0 the first keeps the per-slot launches and the second takes 2 waves per gate|up column and 1 per down
+ * column, which leave SIMDs free for the other work. Read at each gfl_moe_forward / gfl_moe_forward_noalloc call (and so fixed in a captured
  * graph). */
 int gfl_ctx_set_shared(gfl_ctx* ctx, int shared);
 

@@ -46,8 +46,9 @@ def _inputs(rng, M):
     return x16, sel, w, t
 
 
-@pytest.mark.parametrize("M", [1, 4])
+@pytest.mark.parametrize("M", [1, 4, 17])
 def test_overlap_equals_routed_plus_shared(gpu, oracle, setup, M):
+    """M = 17 (1,632 routed gate|up tile columns) also runs the shared expert's narrower launches."""
     import torch
     rng = np.random.default_rng(70 + M)
     x16, sel, w, (xd, seld, wd) = _inputs(rng, M)
