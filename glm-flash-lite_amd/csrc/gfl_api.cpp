@@ -311,11 +311,11 @@ int run_forward(gfl_ctx* c, const Layer& L, const Workspace& ws, const uint16_t*
         }
         if (c->rw_override[0] >= 0) { rw[0] = c->rw_override[0]; rw[1] = c->rw_override[1]; }
     }
-    // above 192 picks the launches without relay take the routing plan from a launch of its own (plan_kernel) instead
-    // of every workgroup building it in LDS. Measured on MI355X (config 1, us per token): M = 28 26.4 -> 25.2, M = 32
-    // 25.9 -> 24.5, M = 64 23.3 -> 21.5; even at M = 24, and 2-3% slower at M = 12..20, where the extra launch and the
-    // workgroups' dependent reads of the published plan cost more than the smaller builds they save.
-    const int gplan = !rw[0] && P > 192 ? 1 : 0;
+    // above 64 picks the launches without relay take the routing plan from a launch of its own (plan_kernel) instead
+    // of every workgroup building it in LDS. Measured on MI355X (config 1, us per token): M = 32 25.9 -> 24.5, M = 64
+    // 23.3 -> 21.5, and with the plan launch at 9-12 us, M = 12..24 0.1-0.4 faster than building it per workgroup.
+    // Up to 64 picks a workgroup builds it from one wave's registers (build_plan_wave), cheaper than a launch.
+    const int gplan = !rw[0] && P > 64 ? 1 : 0;
     if (gfl::gate_up_lds_bytes(L.K[0], ns, L.H, P, L.E, mf, rw[0], gplan) > gfl::LDS_LIMIT ||
         gfl::gate_up_lds_bytes(L.K[1], ns, L.H, P, L.E, mf, rw[0], gplan) > gfl::LDS_LIMIT ||
         gfl::down_lds_bytes(L.K[2], ns, L.I, P, L.E, mf, rw[1]) > gfl::LDS_LIMIT)

@@ -244,12 +244,22 @@ __device__ inline int plan_job(const LPlan& L, int p)
 
 // Publish the plan for the down launch (one workgroup): PlanView arrays plus each token's picks in (job, pick) order
 // with their fp32 weights; rows of tokens without a valid pick are written as zeros here (no down workgroup touches
-// them; the reference's sum over an empty route is 0).
+// them; the reference's sum over an empty route is 0). jscr: LDS scratch of P ints (each pick's job, -1 if skipped).
 __device__ void publish_plan(const LPlan& L, const int* hdr, int P, int topk, const void* w, int w_half,
-                             const PlanView& pv, float* out, int H, const uint64_t* ptrs, int per_slot)
+                             const PlanView& pv, float* out, int H, const uint64_t* ptrs, int per_slot, int* jscr)
 {
     const int t = threadIdx.x, nt = blockDim.x;
     const int U = hdr[0], S = hdr[1];
+    // the weights of this thread's picks first (they are stored only at the end; with the loads between the stores
+    // below, each would wait for the store before it)
+    constexpr int PPT = (MAX_PICKS + 255) / 256;   // picks per thread (both callers run 256 threads)
+    float wr[PPT];
+#pragma unroll
+    for (int i = 0; i < PPT; ++i)
+    {
+        const int p = min(t + i * nt, P - 1);
+        wr[i] = w_half ? h2f_bits(reinterpret_cast<const uint16_t*>(w)[p]) : reinterpret_cast<const float*>(w)[p];
+    }
     if (t < 3) pv.hdr[t] = hdr[t];
     for (int u = t; u < U; u += nt)
     {
@@ -272,55 +282,51 @@ __device__ void publish_plan(const LPlan& L, const int* hdr, int P, int topk, co
     for (int s = t; s < S; s += nt) pv.slot_pick[s] = L.spick[s];
     for (int p = t; p < P; p += nt)
     {
-        if (L.e[p] < 0) { pv.pick_slot[p] = -1; pv.pick_job[p] = 0x7fffffff; continue; }
-        const int u = plan_u(L, p), s = L.uoff[u] + L.c[p];
+        if (L.e[p] < 0)
+        {
+            pv.pick_slot[p] = -1;
+            pv.pick_job[p] = 0x7fffffff;
+            jscr[p] = -1;
+            continue;
+        }
+        const int u = plan_u(L, p), s = L.uoff[u] + L.c[p], jb = plan_job(L, p);
         pv.pick_slot[p] = s;
         pv.slot_u[s] = u;
-        pv.pick_job[p] = plan_job(L, p);
+        pv.pick_job[p] = jb;
+        jscr[p] = jb;
     }
-    const int M = P / topk;
-    for (int tk = t; tk < M; tk += nt)
+    __syncthreads();
+    // each token's picks in (job, pick) order, a thread per pick: a valid pick's place is the number of the token's
+    // valid picks before it in that order; places n..topk-1 of a token with n valid picks are padding
+#pragma unroll
+    for (int i = 0; i < PPT; ++i)
     {
-        // the token's picks in (job, pick) order: each valid pick's place is the number of valid picks before it in
-        // that order. Everything is read first and kept in registers (the loads are unconditional, past topk on the
-        // token's last pick again): with the weight loads between the stores below, each would wait for the store
-        // before it, and a sort through indexed arrays would live in scratch memory.
-        int jb[MAX_TOPK], sl[MAX_TOPK];
-        float wt[MAX_TOPK];
-        bool ok[MAX_TOPK];
-#pragma unroll
-        for (int k = 0; k < MAX_TOPK; ++k)
+        const int p = t + i * nt;
+        if (p >= P) break;
+        const int tk = p / topk, k = p - tk * topk, b = tk * topk, jb = jscr[p];
+        int r = 0, n = 0;
+        for (int k2 = 0; k2 < topk; ++k2)
         {
-            const int p = tk * topk + min(k, topk - 1);
-            ok[k] = k < topk && L.e[p] >= 0;
-            wt[k] = w_half ? h2f_bits(reinterpret_cast<const uint16_t*>(w)[p]) : reinterpret_cast<const float*>(w)[p];
-            jb[k] = ok[k] ? plan_job(L, p) : 0;
-            sl[k] = ok[k] ? L.uoff[plan_u(L, p)] + L.c[p] : -1;
+            const int j2 = jscr[b + k2];
+            n += j2 >= 0 ? 1 : 0;
+            r += (j2 >= 0 && (j2 < jb || (j2 == jb && k2 < k))) ? 1 : 0;
         }
-        int n = 0;
-#pragma unroll
-        for (int k = 0; k < MAX_TOPK; ++k) n += ok[k] ? 1 : 0;
-#pragma unroll
-        for (int k = 0; k < MAX_TOPK; ++k)
+        if (jb >= 0)
         {
-            int r = 0;
-#pragma unroll
-            for (int k2 = 0; k2 < MAX_TOPK; ++k2)
-                r += (ok[k2] && (jb[k2] < jb[k] || (jb[k2] == jb[k] && k2 < k))) ? 1 : 0;
-            if (ok[k])
-            {
-                pv.tok_slot[tk * topk + r] = sl[k];
-                pv.tok_w[tk * topk + r] = wt[k];
-            }
+            pv.tok_slot[b + r] = L.uoff[plan_u(L, p)] + L.c[p];
+            pv.tok_w[b + r] = wr[i];
         }
-        for (int k = n; k < topk; ++k)
+        if (k >= n)
         {
-            pv.tok_slot[tk * topk + k] = -1;
-            pv.tok_w[tk * topk + k] = 0.f;
+            pv.tok_slot[b + k] = -1;
+            pv.tok_w[b + k] = 0.f;
         }
-        pv.tok_npk[tk] = n;
-        if (n == 0)
-            for (int i = 0; i < H; ++i) out[(size_t)tk * H + i] = 0.f;
+        if (k == 0)
+        {
+            pv.tok_npk[tk] = n;
+            if (n == 0)
+                for (int c = 0; c < H; ++c) out[(size_t)tk * H + c] = 0.f;
+        }
     }
 }
 
@@ -907,11 +913,11 @@ __device__ void act_block(const GuArgs& a, int e, int s_begin, int s_end, int b)
     }
 }
 
-// The routing plan of a call, built once and published to pv before the gate|up launch (calls above 192 picks
+// The routing plan of a call, built once and published to pv before the gate|up launch (calls above 64 picks
 // outside the relay launches). Each of the launch's thousands of workgroups building the whole plan itself (one wave
 // scanning every pick with ballots while the others wait) measured 2.6% of the layer at M = 12..16 and 6.4% at
 // M = 32..64 (config 1, a second build per workgroup), and its LDS (17 KB at 512 picks) held the gate|up launch to 3
-// workgroups per CU. One workgroup; dynamic LDS: lplan_ints(P, E) ints.
+// workgroups per CU. One workgroup of 256 threads; dynamic LDS: lplan_ints(P, E) + P ints.
 __global__ __launch_bounds__(GU_NW * 64) void plan_kernel(GuArgs a)
 {
     extern __shared__ __align__(16) uint8_t lds_raw[];
@@ -919,7 +925,8 @@ __global__ __launch_bounds__(GU_NW * 64) void plan_kernel(GuArgs a)
     const LPlan L = lplan_carve(reinterpret_cast<int*>(lds_raw), a.P, a.E);
     if (a.P <= 64) build_plan_wave(a.sel, a.P, a.E, L, hdr);
     else build_plan(a.sel, a.P, a.E, L, hdr);
-    publish_plan(L, hdr, a.P, a.topk, a.w, a.w_half, a.pv, a.out, a.H, a.ptrs, a.per_slot);
+    publish_plan(L, hdr, a.P, a.topk, a.w, a.w_half, a.pv, a.out, a.H, a.ptrs, a.per_slot,
+                 reinterpret_cast<int*>(lds_raw) + lplan_ints(a.P, a.E));
 }
 
 // Grid: (umax * I/64 + 1, nmat). Workgroup = 4 waves = 64 outputs of one matrix of one routed expert, all its
@@ -957,7 +964,8 @@ gu_kernel(GuArgs a)
     {
         // the grid's extra workgroup publishes the plan for the down launch (no GEMV work of its own)
         if (blockIdx.y == 0 && !a.gplan)
-            publish_plan(L, hdr, a.P, a.topk, a.w, a.w_half, a.pv, a.out, a.H, a.ptrs, a.per_slot);
+            publish_plan(L, hdr, a.P, a.topk, a.w, a.w_half, a.pv, a.out, a.H, a.ptrs, a.per_slot,
+                         reinterpret_cast<int*>(rings));   // the rings (>= 8 KB) are free in this workgroup
         return;
     }
 
@@ -1691,7 +1699,7 @@ static void plan_launch(const GuArgs& a, hipStream_t st)
 {
     static const bool opened = open_lds(plan_kernel);
     (void)opened;
-    timed_launch(plan_kernel, dim3(1), dim3(GU_NW * 64), lplan_ints(a.P, a.E) * 4, st, a);
+    timed_launch(plan_kernel, dim3(1), dim3(GU_NW * 64), (lplan_ints(a.P, a.E) + a.P) * 4, st, a);
 }
 
 template <int K, int NS, bool MF>
