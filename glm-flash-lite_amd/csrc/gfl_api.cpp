@@ -276,7 +276,7 @@ int run_forward(gfl_ctx* c, const Layer& L, const Workspace& ws, const uint16_t*
     // idle; rw waves per column put rw times the waves on the chip. Measured on MI355X (config-1 layers, 4 cycled):
     // one expert per call (192 gate|up columns) 39.2 -> 27.5 us with 4 waves per column; 8 picks (1,536 columns)
     // 58.4 -> 56.4 us with 2 waves per gate|up column and 1 per down column. From 16 picks on, one wave per column
-    // beats the per-slot launches (gu_kernel / dn_kernel) by 2-5% on uniform routing (us per token at M = 2, 3, 4, 6,
+    // beats the per-slot launches (gu_kernel / down_kernel) by 2-5% on uniform routing (us per token at M = 2, 3, 4, 6,
     // 8: 39.7 -> 38.8, 36.8 -> 35.1, 33.2 -> 31.6, 31.5 -> 30.1, 30.5 -> 29.5) and matches them on Zipf routing.
     // The relay launches at 8 picks fill every SIMD with 3 waves, so a shared expert on a side stream (k_overlap)
     // then waits (routed + shared 71.3 -> 79.1 us): a context told that other work runs beside it (gfl_ctx_set_shared)
@@ -324,15 +324,15 @@ int run_forward(gfl_ctx* c, const Layer& L, const Workspace& ws, const uint16_t*
     auto gate_up = [&] {
         if (L.K[0] == L.K[1])
             return gfl::launch_gate_up(L.K[0], ns, L.dptrs, 0, 2, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                       ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], gplan, c->status,
-                                       c->spin_max, st);
+                                       ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], gplan,
+                                       c->status, c->spin_max, st);
         if (gfl::launch_gate_up(L.K[0], ns, L.dptrs, 0, 1, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], gplan, c->status,
-                                c->spin_max, st))
+                                ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], gplan,
+                                c->status, c->spin_max, st))
             return -1;
         return gfl::launch_gate_up(L.K[1], ns, L.dptrs, 1, 1, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                   ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], gplan, c->status,
-                                   c->spin_max, st);
+                                   ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], gplan,
+                                   c->status, c->spin_max, st);
     };
     auto down = [&] {
         return gfl::launch_down(L.K[2], ns, L.dptrs, topk, L.H, L.I, umax, P, L.E, sel, w, wh, ws.pv, ws.xtd, ws.yd,
