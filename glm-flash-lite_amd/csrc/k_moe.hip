@@ -297,12 +297,18 @@ __device__ void publish_plan(const LPlan& L, const int* hdr, int P, int topk, co
     }
     __syncthreads();
     // each token's picks in (job, pick) order, a thread per pick: a valid pick's place is the number of the token's
-    // valid picks before it in that order; places n..topk-1 of a token with n valid picks are padding
-#pragma unroll
-    for (int i = 0; i < PPT; ++i)
+    // valid picks before it in that order; places n..topk-1 of a token with n valid picks are padding (picks past
+    // PPT * nt, with fewer than 256 threads, load their weight here)
+    for (int i = 0;; ++i)
     {
         const int p = t + i * nt;
         if (p >= P) break;
+        float wp = 0.f;
+#pragma unroll
+        for (int i2 = 0; i2 < PPT; ++i2)
+            if (i2 == i) wp = wr[i2];
+        if (i >= PPT)
+            wp = w_half ? h2f_bits(reinterpret_cast<const uint16_t*>(w)[p]) : reinterpret_cast<const float*>(w)[p];
         const int tk = p / topk, k = p - tk * topk, b = tk * topk, jb = jscr[p];
         int r = 0, n = 0;
         for (int k2 = 0; k2 < topk; ++k2)
@@ -314,7 +320,7 @@ __device__ void publish_plan(const LPlan& L, const int* hdr, int P, int topk, co
         if (jb >= 0)
         {
             pv.tok_slot[b + r] = L.uoff[plan_u(L, p)] + L.c[p];
-            pv.tok_w[b + r] = wr[i];
+            pv.tok_w[b + r] = wp;
         }
         if (k >= n)
         {
