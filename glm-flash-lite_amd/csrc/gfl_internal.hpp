@@ -109,7 +109,7 @@ struct GPlan
     int* tok_slot;   // [M][topk] slots of each token in combine order
     float* tok_w;    // [M][topk] their routing weights (fp32)
     int* tok_npk;    // [M] valid picks of each token
-    int* eord;       // [E] experts in GEMM dispatch order: most passes first, then ascending id
+    int* eord;       // [E] experts in GEMM dispatch order: most slots first, then ascending id
     int* ccnt;       // [chunks][E + 1] picks of each expert per chunk of GP_PLAN_CHUNK picks, other ids at [E]
 };
 

@@ -110,7 +110,7 @@ __global__ __launch_bounds__(GP_PLAN_THREADS) void gp_place_kernel(const int64_t
 {
     __shared__ int s_base[MAX_EXPERTS];
     __shared__ int s_off[MAX_EXPERTS];
-    __shared__ __align__(16) int s_pass[MAX_EXPERTS];
+    __shared__ __align__(16) int s_nsl[MAX_EXPERTS];
     __shared__ int s_wtot[GP_PLAN_WAVES], s_wjob[GP_PLAN_WAVES], s_wop[GP_PLAN_WAVES];
     __shared__ int s_bad;
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
@@ -166,18 +166,18 @@ __global__ __launch_bounds__(GP_PLAN_THREADS) void gp_place_kernel(const int64_t
     __syncthreads();
     if (c == 0)
     {
-        // experts by descending GEMM passes of GP_MT slots, ties by ascending id: the GEMM dispatches the longest
-        // workgroups first, so the short ones fill the end of the launch
+        // experts by descending slot count, ties by ascending id: a GEMM workgroup's time grows with its expert's
+        // slots (passes, and the blocks of the last pass), so the longest workgroups go first and the short ones
+        // fill the end of the launch
         if (t == 0) g.hdr[1] = s_bad;
-        const int pe = (tot + GP_MT - 1) / GP_MT;
-        s_pass[t] = t < E ? pe : -1;
+        s_nsl[t] = t < E ? tot : -1;
         __syncthreads();
         int rk = 0;
         for (int k = 0; k < E; k += 4)   // 16-byte broadcast reads; entries past E are -1
         {
-            const int4 pk = *reinterpret_cast<const int4*>(&s_pass[k]);
-            rk += (pk.x > pe || (pk.x == pe && k < t)) + (pk.y > pe || (pk.y == pe && k + 1 < t)) +
-                  (pk.z > pe || (pk.z == pe && k + 2 < t)) + (pk.w > pe || (pk.w == pe && k + 3 < t));
+            const int4 pk = *reinterpret_cast<const int4*>(&s_nsl[k]);
+            rk += (pk.x > tot || (pk.x == tot && k < t)) + (pk.y > tot || (pk.y == tot && k + 1 < t)) +
+                  (pk.z > tot || (pk.z == tot && k + 2 < t)) + (pk.w > tot || (pk.w == tot && k + 3 < t));
         }
         if (t < E) g.eord[rk] = t;
     }
@@ -525,7 +525,7 @@ __global__ __launch_bounds__(GP_NW * 64) void gp_gemm_kernel(GemmArgs a)
     const int xcd = blockIdx.x % 8, j = blockIdx.x / 8;
     const int ei = (j / per) * 8 + xcd, rr0 = j % per;
     if (ei >= a.E) return;
-    const int e = a.g.eord[ei];   // experts with the most passes first
+    const int e = a.g.eord[ei];   // experts with the most slots first
     const int nc = rr0 % nch;
     const int mat = a.mat_base + rr0 / nch;
     const int s_begin = a.g.off[e], s_end = a.g.off[e + 1];
