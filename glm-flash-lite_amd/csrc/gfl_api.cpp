@@ -68,6 +68,9 @@ struct gfl_ctx
     // relay widths of the one-slot-per-pass EXACT launches forced by GFL_RELAY="g,d" (gate|up, down; 1, 2 or 4), or
     // "0" for the per-slot launches without relay; -1 = chosen from the call's size
     int rw_override[2] = { -1, -1 };
+    // progress priority of the relay launches forced by GFL_RELAY_PRIO="g,d" (gate|up, down; 0 or 1); -1 = chosen
+    // from the launch's waves per SIMD
+    int prio_override[2] = { -1, -1 };
     // other GPU work runs beside this context's decode calls (gfl_ctx_set_shared): keep calls of 769..1536 gate|up
     // tile columns on the per-slot launches and run calls of up to 768 with 2 waves per column, which leave SIMDs free
     int shared = 0;
@@ -311,6 +314,8 @@ int run_forward(gfl_ctx* c, const Layer& L, const Workspace& ws, const uint16_t*
         }
         if (c->rw_override[0] >= 0) { rw[0] = c->rw_override[0]; rw[1] = c->rw_override[1]; }
     }
+    // progress priority of the relay launches: -1 = chosen by each launch from its waves per SIMD
+    const int prio[2] = { c->prio_override[0], c->prio_override[1] };
     // above 64 picks the launches without relay take the routing plan from a launch of its own (plan_kernel) instead
     // of every workgroup building it in LDS. Measured on MI355X (config 1, us per token): M = 32 25.9 -> 24.5, M = 64
     // 23.3 -> 21.5, and with the plan launch at 9-12 us, M = 12..24 0.1-0.4 faster than building it per workgroup.
@@ -324,19 +329,19 @@ int run_forward(gfl_ctx* c, const Layer& L, const Workspace& ws, const uint16_t*
     auto gate_up = [&] {
         if (L.K[0] == L.K[1])
             return gfl::launch_gate_up(L.K[0], ns, L.dptrs, 0, 2, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                       ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], gplan,
+                                       ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], prio[0], gplan,
                                        c->status, c->spin_max, st);
         if (gfl::launch_gate_up(L.K[0], ns, L.dptrs, 0, 1, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], gplan,
+                                ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], prio[0], gplan,
                                 c->status, c->spin_max, st))
             return -1;
         return gfl::launch_gate_up(L.K[1], ns, L.dptrs, 1, 1, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                   ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], gplan,
+                                   ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], prio[0], gplan,
                                    c->status, c->spin_max, st);
     };
     auto down = [&] {
         return gfl::launch_down(L.K[2], ns, L.dptrs, topk, L.H, L.I, umax, P, L.E, sel, w, wh, ws.pv, ws.xtd, ws.yd,
-                                ws.out_cnt, ws.blk_cnt, out, mf, rw[1], c->status, c->spin_max, st);
+                                ws.out_cnt, ws.blk_cnt, out, mf, rw[1], prio[1], c->status, c->spin_max, st);
     };
     int r = prof ? staged(c, 1, st, gate_up) : gate_up();
     if (!r) r = prof ? staged(c, 3, st, down) : down();
@@ -534,6 +539,15 @@ int gfl_ctx_create(int device, gfl_ctx** out)
         auto ok = [](int v) { return v == 0 || v == 1 || v == 2 || v == 4; };
         if (n == 1 && g == 0) c->rw_override[0] = c->rw_override[1] = 0;
         else if (n == 2 && ok(g) && ok(d) && g > 0 && d > 0) { c->rw_override[0] = g; c->rw_override[1] = d; }
+    }
+    if (const char* e = std::getenv("GFL_RELAY_PRIO"))
+    {
+        int g = -1, d = -1;
+        if (std::sscanf(e, "%d,%d", &g, &d) == 2 && (g == 0 || g == 1) && (d == 0 || d == 1))
+        {
+            c->prio_override[0] = g;
+            c->prio_override[1] = d;
+        }
     }
 
     *out = c;

@@ -641,7 +641,7 @@ __device__ __forceinline__ void count_expiry(int* status)
 template <int K, int PF, int RW, class PreLoad, class Pre>
 __device__ __forceinline__ float chain_relay(const uint8_t* __restrict__ col_base, size_t gstride, int TK,
                                              const float* lds_x, uint8_t* slot, float* relay, int* turn, int r,
-                                             int* status, int spin_max, PreLoad&& pre_load, Pre&& pre)
+                                             int* status, int spin_max, int prio, PreLoad&& pre_load, Pre&& pre)
 {
     constexpr int TB = 32 * K, CH = 2 * K, NCH = 8 * CH, NLD = (NCH + 63) / 64;   // 16-byte chunks
     const int lane = threadIdx.x & 63;
@@ -682,6 +682,18 @@ __device__ __forceinline__ float chain_relay(const uint8_t* __restrict__ col_bas
     const int nphp = (nph + PF - 1) / PF * PF;   // phases padded to whole rounds of PF (the padding has no work)
     for (int ph0 = 0; ph0 < nphp; ph0 += PF)
     {
+        // prio: the wave's issue priority falls from 3 to 0 over the quarters of its phases. A SIMD issues its
+        // oldest ready wave first; with 2 or 3 waves per SIMD the oldest then finish early and the youngest runs its
+        // last stretch alone, at about half the rate of two waves sharing the SIMD. Waves that are ahead yield to
+        // those behind, so the waves of a SIMD end together.
+        if (prio)
+        {
+            const int q4 = (4 * ph0) / nphp;
+            if (q4 == 0) __builtin_amdgcn_s_setprio(3);
+            else if (q4 == 1) __builtin_amdgcn_s_setprio(2);
+            else if (q4 == 2) __builtin_amdgcn_s_setprio(1);
+            else __builtin_amdgcn_s_setprio(0);
+        }
 #pragma unroll
         for (int k = 0; k < PF; ++k)
         {
@@ -744,6 +756,7 @@ __device__ __forceinline__ float chain_relay(const uint8_t* __restrict__ col_bas
             }
         }
     }
+    if (prio) __builtin_amdgcn_s_setprio(0);
     wait_vmcnt<0>();   // the padding's clamped prefetches
     if (RW > 1)
     {
@@ -861,6 +874,7 @@ struct GuArgs
     int nmat_launch;           // matrices of this launch (the relay launches' item count)
     int* status;               // the context's status words (relay waits that expired)
     int spin_max;              // bound of a relay turn wait, in polls
+    int prio;                  // relay launches: waves lower their issue priority as they progress (chain_relay)
     int gplan;                 // the routing plan was published to pv by plan_kernel before this launch: workgroups
                                // read their entries from pv instead of each building the plan in LDS
 };
@@ -1134,6 +1148,7 @@ struct DnArgs
     int pv_picks;              // picks of the call (the relay down launch's item count)
     int* status;               // the context's status words (relay waits that expired)
     int spin_max;              // bound of a relay turn wait, in polls
+    int prio;                  // relay launches: waves lower their issue priority as they progress (chain_relay)
     const int64_t* sel;        // [P] picks (relay launches: slot = pick)
     const void* w;             // [P] routing weights, fp16 (w_half) or fp32
     int w_half, E;
@@ -1458,7 +1473,7 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
         lds_barrier();   // lds_x complete
     };
     const float res = chain_relay<K, NGRP - 1, RW>(col, gstride, TK, lds_x, rings + wid * RB, relay[c],
-                                                   &relay_turn[c], r, a.status, a.spin_max, pre_load, pre);
+                                                   &relay_turn[c], r, a.status, a.spin_max, a.prio, pre_load, pre);
     float* ybase = a.ygu + (size_t)mat * a.pv.cap_slots * a.I;
     if (r == 0 && lane < 16) st_agent(&ybase[(size_t)p * a.I + t * 16 + n], res);
     release_agent();
@@ -1563,7 +1578,7 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
         lds_barrier();   // lds_x complete
     };
     const float res = chain_relay<K, NGRP - 1, RW>(col, gstride, TK, lds_x, rings + wid * RB, relay[c],
-                                                   &relay_turn[c], r, a.status, a.spin_max, pre_load, pre);
+                                                   &relay_turn[c], r, a.status, a.spin_max, a.prio, pre_load, pre);
     if (r == 0 && lane < 16) st_agent(&a.yd[(size_t)p * a.H + t * 16 + n], res);
     // the number of valid picks of the token (its combine's arrival count), from the registers of wave 0
     if (wave == 0)
@@ -1745,6 +1760,17 @@ static size_t balanced_lds(size_t need, long nwg)
     return cap > need && cap <= (size_t)LDS_LIMIT ? cap : need;
 }
 
+// Progress priority of a relay launch (chain_relay's prio): on when the launch puts more than one and at most three
+// waves on a SIMD, where a SIMD's last wave would otherwise run alone. Measured on MI355X (config 1, us per token):
+// M = 1 (gate|up 3 waves per SIMD, down 2.5) 48.9 -> 45.8; M = 2 with it on gate|up (3 per SIMD) 36.6 -> 34.9, and
+// 0.4 slower with it on down as well (5 per SIMD). prio >= 0 (GFL_RELAY_PRIO) forces it.
+static int relay_prio(int prio, long waves)
+{
+    if (prio >= 0) return prio;
+    const long simds = 4L * device_cus();
+    return waves > simds && waves <= 3 * simds ? 1 : 0;
+}
+
 template <int K, int RW>
 static void gu_relay_launch(const GuArgs& a, int nmat, hipStream_t st)
 {
@@ -1756,6 +1782,7 @@ static void gu_relay_launch(const GuArgs& a, int nmat, hipStream_t st)
     const size_t lds = balanced_lds(gu_relay_lds<K>(a.H, a.P, a.E), nwg);
     GuArgs b = a;
     b.nmat_launch = nmat;
+    b.prio = relay_prio(a.prio, nwg * GU_NW);
     timed_launch(kern, dim3(8 + relay_blocks(nwg, RW)), dim3(GU_NW * 64), lds, st, b);
 }
 
@@ -1770,6 +1797,7 @@ static void dn_relay_launch(const DnArgs& a, int P, hipStream_t st)
     const size_t lds = balanced_lds(dn_relay_lds<K>(a.I), nwg);
     DnArgs b = a;
     b.pv_picks = P;
+    b.prio = relay_prio(a.prio, nwg * GU_NW);
     timed_launch(kern, dim3(relay_blocks(nwg, RW)), dim3(GU_NW * 64), lds, st, b);
 }
 
@@ -1821,10 +1849,11 @@ size_t down_lds_bytes(int K, int ns, int I, int P, int E, int mf, int rw)
 int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, const int64_t* sel, const void* w,
                    int w_half, int P, int topk, int E, int H, int I, int umax, const uint16_t* x, float* ygu,
                    uint16_t* xtd, int* act_cnt, const float* silu_tab, float act_limit, const PlanView& pv, float* out,
-                   int mf, int rw, int gplan, int* status, int spin_max, hipStream_t st)
+                   int mf, int rw, int prio, int gplan, int* status, int spin_max, hipStream_t st)
 {
     GuArgs a;
     a.status = status; a.spin_max = spin_max; a.nmat_launch = nmat; a.gplan = rw ? 0 : gplan;
+    a.prio = rw ? prio : 0;
     a.ptrs = ptrs; a.sel = sel; a.w = w; a.w_half = w_half; a.P = P; a.topk = topk; a.E = E; a.H = H; a.I = I;
     a.mat_base = mat_base; a.x = x; a.ygu = ygu; a.xtd = xtd; a.act_cnt = act_cnt; a.silu_tab = silu_tab;
     a.act_limit = act_limit; a.pv = pv; a.out = out;
@@ -1856,10 +1885,11 @@ int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, 
 
 int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int umax, int P, int E, const int64_t* sel,
                 const void* w, int w_half, const PlanView& pv, const uint16_t* xtd, float* yd, int* out_cnt,
-                int* blk_cnt, float* out, int mf, int rw, int* status, int spin_max, hipStream_t st)
+                int* blk_cnt, float* out, int mf, int rw, int prio, int* status, int spin_max, hipStream_t st)
 {
     DnArgs a;
     a.status = status; a.spin_max = spin_max; a.pv_picks = P;
+    a.prio = rw ? prio : 0;
     a.sel = sel; a.w = w; a.w_half = w_half; a.E = E;
     a.ptrs = ptrs; a.topk = topk; a.H = H; a.I = I; a.pv = pv; a.xtd = xtd; a.yd = yd; a.out_cnt = out_cnt;
     a.blk_cnt = blk_cnt;

@@ -494,13 +494,19 @@ def _ctx_with_env(**env):
                 os.environ[k] = v
 
 
+def _relay_env(relay, prio):
+    return dict(GFL_RELAY=relay, **({"GFL_RELAY_PRIO": prio} if prio else {}))
+
+
 @pytest.mark.gpu
+@pytest.mark.parametrize("prio", [None, "1,1"])
 @pytest.mark.parametrize("relay", ["0", "1,1", "2,2", "4,4", "2,1", "4,2", "1,4"])
-def test_relay_launches_bitexact(gpu, oracle, relay):
+def test_relay_launches_bitexact(gpu, oracle, relay, prio):
     """Every decode launch family of one slot per pass (GFL_RELAY, read at context creation): without relay ("0"), and
     the relay launches with 1, 2 or 4 waves per tile column for gate|up and down; mixed K (2..5), skipped picks, a token
-    picking one expert twice, and 1, 2 and 5 tokens."""
-    ctx = _ctx_with_env(GFL_RELAY=relay)
+    picking one expert twice, and 1, 2 and 5 tokens. With prio "1,1" (GFL_RELAY_PRIO) the relay waves lower their issue
+    priority as they progress, which these small launches would not choose by themselves."""
+    ctx = _ctx_with_env(**_relay_env(relay, prio))
     H, I = 512, 256
     for li, Ks in enumerate([(3, 3, 3), (2, 5, 4), (4, 4, 3), (5, 2, 5)]):
         L = _layer(ctx, 40 + li, 6, H, I, Ks)
@@ -520,12 +526,14 @@ def test_relay_launches_bitexact(gpu, oracle, relay):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("relay", ["4,4", "2,1", "2,2", "1,1"])
-def test_relay_launches_full_shape_bitexact(gpu, oracle, relay):
+@pytest.mark.parametrize("relay,prio", [("4,4", None), ("2,1", None), ("2,1", "0,0"), ("2,2", None), ("1,1", None),
+                                        ("1,1", "1,1")])
+def test_relay_launches_full_shape_bitexact(gpu, oracle, relay, prio):
     """The relay launches at the config-1 shape (H=5120, I=1536, K=3): one expert (config 0) and top-8 of a
-    10-expert layer at M = 1 and 3."""
+    10-expert layer at M = 1 and 3; the progress priority as each launch chooses it (on at M = 1 for "2,1"), or forced
+    off / on (GFL_RELAY_PRIO)."""
     import synth
-    ctx = _ctx_with_env(GFL_RELAY=relay)
+    ctx = _ctx_with_env(**_relay_env(relay, prio))
     H, I, E = 5120, 1536, 10
     L = _layer(ctx, 50, E, H, I)
     ex = _host_experts(oracle, L)
