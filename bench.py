@@ -493,8 +493,9 @@ def time_config0(ctx, layer_ids, bytes_per_expert, steps=XSTEPS):
 
 def time_shared(ctx, layer_ids, G, reps):
     """Routed layer + the layer's shared expert (one more config-0-shaped expert at 3 bpw), per token: the shared
-    expert after the routed call on one stream ("sequential", the stock order) and on a side stream overlapped with
-    it (k_overlap.SharedOverlap, "overlapped"). Graph-timed like the decode steps."""
+    expert after the routed call on one stream ("sequential", the stock order) and through k_overlap.SharedOverlap
+    with overlap requested ("overlapped": on a side stream, except at M = 1 where SharedOverlap keeps the stock order).
+    Graph-timed like the decode steps."""
     import numpy as np
     import torch
     import k_overlap
@@ -506,7 +507,7 @@ def time_shared(ctx, layer_ids, G, reps):
         so.register(li, H, I, S.Ks, S.ptr_table, keep=S)
         keep.append(S)
     res = {}
-    for M in (1, 4):
+    for M in (1, 2, 4):
         routes = make_routes(M, np.random.default_rng(7000 + M), 32, "uniform")
         out = torch.empty((M, H), dtype=torch.float32, device="cuda")
         r = {}

@@ -8,10 +8,16 @@ on a side stream at the default priority. The routed layer call stays on the cal
 add, so the result equals routed + shared computed one after the other, bit for bit. All work is stream-ordered and
 captures into HIP graphs (events are created once, up front).
 
-At decode sizes the routed launches leave compute units idle (1,536 gate|up column-waves on 1,024 SIMDs at M=1), which
-is the room the shared expert's 48 + 40 workgroups run in. The routed context is told so for the overlapped call
-(gfl_ctx_set_shared): on its own it runs such calls with launches that fill every SIMD. A larger routed call fills
-every SIMD anyway; beside it the shared expert's own context is told so, and its launches leave SIMDs free instead.
+Whether the overlap pays depends on how the routed call fills the GPU (measured on MI355X, config 1 routed + one
+config-0-shaped shared expert, us per token; gate|up tile columns = tokens x top-k x 2 x I / 16):
+- up to 1,536 routed gate|up columns (M = 1 at top-8) the routed relay launches fill every SIMD with waves that yield
+  to each other as they progress, and any overlapped form was slower than the stock order (69.6 sequential; 71.7
+  with the routed call on narrower launches beside the shared expert, 73.1 with both on their own launches): such
+  calls run in the stock order;
+- up to 3,072 (M = 2) both run on their own launches, overlapped: 44.2 against 48.2 sequential (52.2 with the shared
+  expert on narrow launches);
+- above that the routed call fills every SIMD for longer, and the shared expert's context is told so
+  (gfl_ctx_set_shared), so that its launches leave SIMDs free: 40.0 against 40.5 sequential at M = 4.
 """
 import torch
 
@@ -49,11 +55,13 @@ class SharedOverlap:
     def forward(self, routed, li, x, sel, w, out, overlap=True):
         """out = routed layer li (context `routed`, picks sel / w) + shared expert of layer li, for x fp16 [M, H].
         overlap=False runs the shared expert after the routed call on the caller's stream (the reference's stock
-        order), for comparison."""
+        order), for comparison; so does a routed call of at most 1,536 gate|up tile columns, where the overlap measured
+        slower. Both orders give the same bits."""
         M, H = x.shape
         s1, w1, y = self._bufs(M, H)
         main = torch.cuda.current_stream(self.device)
-        if not overlap:
+        cols = M * sel.shape[1] * 2 * (self._inter(routed, li) // 16)   # the routed call's gate|up tile columns
+        if not overlap or cols <= 1536:
             routed.moe_forward(li, x, sel, w, out)
             self.ctx.set_shared(False)
             self.ctx.moe_forward(li, x, s1, w1, y)
@@ -62,18 +70,16 @@ class SharedOverlap:
             return out
         self.fork.record(main)                   # MoE input ready
         self.side.wait_event(self.fork)
-        # beside a routed call of more than 1,536 gate|up tile columns (it fills every SIMD: 2 or more tokens at
-        # top-8 and I = 1536) the shared expert takes narrower launches that leave SIMDs free (routed + shared at M = 4
-        # 41.1 -> 38.8 us per token); beside a smaller routed call the default launches are faster (69.9 against 72.5
-        # at M = 1)
-        I = self._inter(routed, li)
-        narrow = M * sel.shape[1] * 2 * (I // 16) > 1536
+        # beside a routed call of more than 3,072 gate|up tile columns the shared expert takes narrower launches
+        # that leave SIMDs free (M = 4: 40.0 against 40.5 us per token with its own launches); beside a smaller one its
+        # own launches are faster (M = 2: 44.2 against 52.2)
+        narrow = cols > 3072
         with torch.cuda.stream(self.side):
             self.ctx.set_shared(narrow)
             self.ctx.moe_forward(li, x, s1, w1, y)
             self.join.record(self.side)
-        # the routed call keeps launch shapes that leave SIMDs free for the side stream (same results); the caller's
-        # own setting is restored afterwards
+        # the routed call is told that the side stream runs beside it (above 1,536 gate|up columns this changes no
+        # launch shape, and results never change); the caller's own setting is restored afterwards
         prev = routed.shared
         routed.set_shared(True)
         try:

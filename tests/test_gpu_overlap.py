@@ -46,15 +46,21 @@ def _inputs(rng, M):
     return x16, sel, w, t
 
 
-@pytest.mark.parametrize("M", [1, 4, 17])
+@pytest.mark.parametrize("M", [1, 17, 33])
 def test_overlap_equals_routed_plus_shared(gpu, oracle, setup, M):
-    """M = 17 (1,632 routed gate|up tile columns) also runs the shared expert's narrower launches."""
+    """The three orders SharedOverlap takes (96 routed gate|up tile columns per token here): M = 1 runs in the stock
+    order (at most 1,536 columns), M = 17 (1,632) overlaps the shared expert on its own launches, M = 33 (3,168) on
+    its narrower ones."""
     import torch
     rng = np.random.default_rng(70 + M)
     x16, sel, w, (xd, seld, wd) = _inputs(rng, M)
     out = torch.empty((M, H), dtype=torch.float32, device="cuda")
+    before = setup["so"].summary()
     setup["so"].forward(gpu, setup["li"], xd, seld, wd, out)
     torch.cuda.synchronize()
+    after = setup["so"].summary()
+    took = "sequential" if M == 1 else "overlapped"
+    assert after[took] == before[took] + 1
     got = out.cpu().numpy()
     routed = oracle.moe_forward(_experts(setup["routed"]), x16.astype(np.float32), sel, w, mode=1)
     shared = oracle.expert_forward(_experts(setup["shared"])[0], x16.astype(np.float32), mode=1)
@@ -72,9 +78,10 @@ def test_overlap_equals_routed_plus_shared(gpu, oracle, setup, M):
 
 
 def test_overlap_graph_replays(gpu, setup):
+    """M = 17: the overlapped order (fork, side stream, join) inside a captured graph."""
     import torch
     rng = np.random.default_rng(80)
-    M = 2
+    M = 17
     ins = [_inputs(rng, M)[3] for _ in range(3)]
     outs = [torch.empty((M, H), dtype=torch.float32, device="cuda") for _ in range(3)]
     for (xd, seld, wd), o in zip(ins, outs):
