@@ -493,30 +493,34 @@ def time_config0(ctx, layer_ids, bytes_per_expert, steps=XSTEPS):
 
 def time_shared(ctx, layer_ids, G, reps):
     """Routed layer + the layer's shared expert (one more config-0-shaped expert at 3 bpw), per token: the shared
-    expert after the routed call on one stream ("sequential", the stock order) and through k_overlap.SharedOverlap
-    with overlap requested ("overlapped": on a side stream, except at M = 1 where SharedOverlap keeps the stock order).
-    Graph-timed like the decode steps."""
+    expert after the routed call on one stream ("sequential", the stock order); through k_overlap.SharedOverlap with
+    overlap requested and the shared expert in its own context only ("overlapped": on a side stream, except at M = 1
+    where SharedOverlap keeps the stock order); and with the routed context holding the shared expert too ("fused":
+    both in the routed call's launches, gfl_moe_forward_shared). Graph-timed like the decode steps."""
     import numpy as np
     import torch
     import k_overlap
     import synth
     so = k_overlap.SharedOverlap(0)
+    sof = k_overlap.SharedOverlap(0)
     keep = []
     for li in layer_ids:
         S = synth.SynthLayer(300 + li, 1, H, I, (KBITS,) * 3)
         so.register(li, H, I, S.Ks, S.ptr_table, keep=S)
+        sof.register(li, H, I, S.Ks, S.ptr_table, keep=S, routed=ctx)
         keep.append(S)
     res = {}
     for M in (1, 2, 4):
         routes = make_routes(M, np.random.default_rng(7000 + M), 32, "uniform")
         out = torch.empty((M, H), dtype=torch.float32, device="cuda")
         r = {}
-        for mode in ("sequential", "overlapped"):
-            ov = mode == "overlapped"
+        for mode in ("sequential", "overlapped", "fused"):
+            ov = mode != "sequential"
+            obj = sof if mode == "fused" else so
 
             def step(i):
                 x, sel, w, _ = routes[i % len(routes)]
-                so.forward(ctx, layer_ids[i % len(layer_ids)], x, sel, w, out, overlap=ov)
+                obj.forward(ctx, layer_ids[i % len(layer_ids)], x, sel, w, out, overlap=ov)
 
             for i in range(8):
                 step(i)
@@ -540,6 +544,7 @@ def time_shared(ctx, layer_ids, G, reps):
             del g
             r[mode] = round(e0.elapsed_time(e1) * 1e3 / (reps * G) / M, 3)
         r["overlap_gain"] = round(r["sequential"] / r["overlapped"], 3)
+        r["fused_gain"] = round(r["sequential"] / r["fused"], 3)
         res[f"M{M}_us_per_token"] = r
     return res
 

@@ -16,7 +16,10 @@ SYMBOLS = ("gfl_last_error", "gfl_version", "gfl_ctx_create", "gfl_ctx_destroy",
            "gfl_synth_trellis", "gfl_route",
            "gfl_stats", "gfl_profile_enable", "gfl_profile_read", "gfl_exp_table", "gfl_silu_table",
            "gfl_grouped_plan", "gfl_grouped_reserve", "gfl_layer_info", "gfl_route_split", "gfl_moe_forward_noalloc",
-           "gfl_ctx_set_shared", "gfl_ctx_check", "gfl_ingress_serve")
+           "gfl_ctx_set_shared", "gfl_ctx_check", "gfl_ingress_serve", "gfl_register_shared",
+           "gfl_moe_forward_shared")
+
+EUNSUPPORTED = 4   # GFL_EUNSUPPORTED: gfl_moe_forward_shared cannot fuse this call (nothing was launched)
 
 # layout limits of gfl_moe_forward_noalloc's static scratch array (GFL_NOALLOC_MAX_* in include/gfl_moe.h)
 NOALLOC_MAX_PICKS, NOALLOC_MAX_H, NOALLOC_MAX_I = 64, 8192, 4096
@@ -54,6 +57,8 @@ def load(path=LIB_PATH):
     L.gfl_register_layer.argtypes = [_P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _P]
     L.gfl_moe_forward.argtypes = [_P, C.c_int, _P, _P, _P, C.c_int, C.c_int, C.c_int, _P, C.c_int, C.c_float, _P]
     L.gfl_moe_forward_noalloc.argtypes = L.gfl_moe_forward.argtypes
+    L.gfl_moe_forward_shared.argtypes = L.gfl_moe_forward.argtypes
+    L.gfl_register_shared.argtypes = [_P, C.c_int, C.c_int, C.c_int, C.c_int, _P]
     L.gfl_grouped_forward.argtypes = [_P, C.c_int, _P, _P, _P, C.c_int, C.c_int, C.c_int, _P, C.c_float, _P]
     L.gfl_grouped_reserve.argtypes = [_P, C.c_int]
     L.gfl_layer_info.argtypes = [_P, C.c_int, _P]
@@ -127,6 +132,13 @@ class Context:
         if keep is not None:
             self._keep[li] = keep
 
+    def register_shared(self, li, ks, ptr_row, keep=None):
+        """The shared expert of registered layer li: ptr_row = its 9 device addresses (gfl_register_shared)."""
+        arr = (C.c_uint64 * 9)(*[int(p) for p in ptr_row])
+        check(load().gfl_register_shared(self.h, int(li), int(ks[0]), int(ks[1]), int(ks[2]), arr))
+        if keep is not None:
+            self._keep[("shared", li)] = keep
+
     def layer_info(self, li):
         """(E, H, I, k_gate, k_up, k_down) of a registered layer (gfl_layer_info)."""
         info = (C.c_int * 6)()
@@ -148,11 +160,17 @@ class Context:
         """x fp16 [M,H], sel int64 [M,topk], w fp16|fp32 [M,topk], out fp32 [M,H] (all on the context device)."""
         return self._decode_forward(load().gfl_moe_forward, li, x, sel, w, out, mode, act_limit)
 
+    def moe_forward_shared(self, li, x, sel, w, out, mode=MODE_EXACT, act_limit=0.0):
+        """out = routed layer li + its shared expert in the routed call's own launches (gfl_moe_forward_shared).
+        Returns False, with nothing launched, when the call cannot take that form (GFL_EUNSUPPORTED)."""
+        return self._decode_forward(load().gfl_moe_forward_shared, li, x, sel, w, out, mode, act_limit,
+                                    allow=(EUNSUPPORTED,)) is not None
+
     def moe_forward_noalloc(self, li, x, sel, w, out, mode=MODE_EXACT, act_limit=0.0):
         """moe_forward on the library's static scratch array: allocates nothing (M*topk <= NOALLOC_MAX_PICKS)."""
         return self._decode_forward(load().gfl_moe_forward_noalloc, li, x, sel, w, out, mode, act_limit)
 
-    def _decode_forward(self, fn, li, x, sel, w, out, mode, act_limit):
+    def _decode_forward(self, fn, li, x, sel, w, out, mode, act_limit, allow=()):
         import torch
         if sel.dim() != 2:
             raise ValueError("sel must be int64 [M, topk]")
@@ -169,8 +187,11 @@ class Context:
             if not (t.is_cuda and t.device.index == self.device):
                 raise ValueError(f"all tensors must be on cuda:{self.device}")
         self._check_width(li, x)
-        check(fn(self.h, li, ptr(x), ptr(sel), ptr(w), int(w.dtype == torch.float16), M, topk, ptr(out), int(mode),
-                 float(act_limit), _stream()))
+        rc = fn(self.h, li, ptr(x), ptr(sel), ptr(w), int(w.dtype == torch.float16), M, topk, ptr(out), int(mode),
+                float(act_limit), _stream())
+        if rc in allow:
+            return None
+        check(rc)
         return out
 
     def grouped_forward(self, li, x, sel, w, out, act_limit=0.0):

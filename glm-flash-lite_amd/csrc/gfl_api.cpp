@@ -40,7 +40,9 @@ int hip_fail(hipError_t e, const char* what)
 struct Layer
 {
     int E = 0, H = 0, I = 0, K[3] = { 0, 0, 0 };
-    uint64_t* dptrs = nullptr;  // device copy of the [E][9] table
+    uint64_t* dptrs = nullptr;  // device copy of the [E][9] table, [E + 1][9] with the shared expert as row E
+    int shared = 0;             // gfl_register_shared gave the layer a shared expert (row E) of bit widths shK
+    int shK[3] = { 0, 0, 0 };
 };
 
 }  // namespace
@@ -254,9 +256,11 @@ int check_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, con
 
 // The decode forward on workspace ws (caller holds c->mu, device set). prof: bracket the stages with the context's
 // profiling events when profiling is on (the no-allocation entry point does not: event creation is left out of it).
+// nsh = M: the layer's shared expert rides on the relay launches as one more pick per token (gfl_moe_forward_shared);
+// a call that does not take them then returns GFL_EUNSUPPORTED before anything is launched.
 int run_forward(gfl_ctx* c, const Layer& L, const Workspace& ws, const uint16_t* x, const int64_t* sel,
                 const void* w, int w_is_half, int M, int topk, float* out, int mode, float act_limit, hipStream_t st,
-                bool prof)
+                bool prof, int nsh = 0)
 {
     const int P = M * topk;
     const int umax = P < L.E ? P : L.E;
@@ -291,7 +295,7 @@ int run_forward(gfl_ctx* c, const Layer& L, const Workspace& ws, const uint16_t*
     // the relay down launch forms each token's combine order from one pick per lane of a wave: at most 64 picks
     if (!mf && ns == 1 && P <= 64)
     {
-        const int64_t cgu = (int64_t)P * 2 * (L.I / 16), cdn = (int64_t)P * (L.H / 16);   // tile columns
+        const int64_t cgu = (int64_t)(P + nsh) * 2 * (L.I / 16), cdn = (int64_t)(P + nsh) * (L.H / 16);   // columns
         if (cgu <= 768 && c->shared)
         {
             rw[0] = 2;
@@ -316,6 +320,9 @@ int run_forward(gfl_ctx* c, const Layer& L, const Workspace& ws, const uint16_t*
     }
     // progress priority of the relay launches: -1 = chosen by each launch from its waves per SIMD
     const int prio[2] = { c->prio_override[0], c->prio_override[1] };
+    if (nsh && !rw[0])
+        return fail(GFL_EUNSUPPORTED, "gfl_moe_forward_shared: this call does not take the relay launches (more than 64 "
+                                      "picks, mode MFMA, or a context set shared at 769..1536 columns)");
     // above 64 picks the launches without relay take the routing plan from a launch of its own (plan_kernel) instead
     // of every workgroup building it in LDS. Measured on MI355X (config 1, us per token): M = 32 25.9 -> 24.5, M = 64
     // 23.3 -> 21.5, and with the plan launch at 9-12 us, M = 12..24 0.1-0.4 faster than building it per workgroup.
@@ -329,19 +336,19 @@ int run_forward(gfl_ctx* c, const Layer& L, const Workspace& ws, const uint16_t*
     auto gate_up = [&] {
         if (L.K[0] == L.K[1])
             return gfl::launch_gate_up(L.K[0], ns, L.dptrs, 0, 2, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                       ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], prio[0], gplan,
+                                       ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], prio[0], nsh, gplan,
                                        c->status, c->spin_max, st);
         if (gfl::launch_gate_up(L.K[0], ns, L.dptrs, 0, 1, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], prio[0], gplan,
+                                ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], prio[0], nsh, gplan,
                                 c->status, c->spin_max, st))
             return -1;
         return gfl::launch_gate_up(L.K[1], ns, L.dptrs, 1, 1, sel, w, wh, P, topk, L.E, L.H, L.I, umax, x, ws.ygu,
-                                   ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], prio[0], gplan,
+                                   ws.xtd, ws.act_cnt, c->silu_tab, act_limit, ws.pv, out, mf, rw[0], prio[0], nsh, gplan,
                                    c->status, c->spin_max, st);
     };
     auto down = [&] {
         return gfl::launch_down(L.K[2], ns, L.dptrs, topk, L.H, L.I, umax, P, L.E, sel, w, wh, ws.pv, ws.xtd, ws.yd,
-                                ws.out_cnt, ws.blk_cnt, out, mf, rw[1], prio[1], c->status, c->spin_max, st);
+                                ws.out_cnt, ws.blk_cnt, out, mf, rw[1], prio[1], nsh, c->status, c->spin_max, st);
     };
     int r = prof ? staged(c, 1, st, gate_up) : gate_up();
     if (!r) r = prof ? staged(c, 3, st, down) : down();
@@ -594,8 +601,39 @@ int gfl_register_layer(gfl_ctx* c, int li, int E, int H, int I, int k_gate, int 
     GFL_HIP(hipMalloc(&L.dptrs, sizeof(uint64_t) * 9 * (size_t)E));
     GFL_HIP(hipMemcpy(L.dptrs, ptrs, sizeof(uint64_t) * 9 * (size_t)E, hipMemcpyHostToDevice));
     L.E = E; L.H = H; L.I = I; L.K[0] = k_gate; L.K[1] = k_up; L.K[2] = k_down;
+    L.shared = 0;
     // the decode workspace for this shape, reserved now so that no forward call allocates
     return reserve_ws(c, H, I);
+}
+
+int gfl_register_shared(gfl_ctx* c, int li, int k_gate, int k_up, int k_down, const uint64_t* ptr_row)
+{
+    if (!c || !ptr_row) return fail(GFL_EINVAL, "gfl_register_shared: NULL argument");
+    if (li < 0 || li >= (int)c->layers.size() || !c->layers[li].dptrs)
+        return fail(GFL_EINVAL, "gfl_register_shared: layer not registered");
+    if (!k_ok(k_gate) || !k_ok(k_up) || !k_ok(k_down)) return fail(GFL_EINVAL, "gfl_register_shared: K must be 2..5");
+    for (int i = 0; i < 9; ++i)
+        if (ptr_row[i] == 0 || (ptr_row[i] & (i < 3 ? 3 : 15)))
+            return fail(GFL_EINVAL, "gfl_register_shared: NULL or misaligned device pointer (trellis 4-byte, suh/svh "
+                                    "16-byte alignment)");
+    std::lock_guard<std::mutex> g(c->mu);
+    GFL_HIP(hipSetDevice(c->device));
+    Layer& L = c->layers[li];
+    // the routed table with the shared expert as row E
+    uint64_t* t = nullptr;
+    GFL_HIP(hipMalloc(&t, sizeof(uint64_t) * 9 * (size_t)(L.E + 1)));
+    hipError_t e = hipMemcpy(t, L.dptrs, sizeof(uint64_t) * 9 * (size_t)L.E, hipMemcpyDeviceToDevice);
+    if (e == hipSuccess) e = hipMemcpy(t + 9 * (size_t)L.E, ptr_row, sizeof(uint64_t) * 9, hipMemcpyHostToDevice);
+    if (e != hipSuccess)
+    {
+        hipFree(t);
+        return hip_fail(e, "gfl_register_shared");
+    }
+    GFL_HIP(hipFree(L.dptrs));
+    L.dptrs = t;
+    L.shared = 1;
+    L.shK[0] = k_gate; L.shK[1] = k_up; L.shK[2] = k_down;
+    return GFL_OK;
 }
 
 static int run_forward_grouped_plan(gfl_ctx* c, const Layer& L, const uint16_t* x, const int64_t* sel, const void* w,
@@ -620,6 +658,29 @@ int gfl_moe_forward(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, c
     carve_ws(c, L.H, L.I, ws);
     return run_forward(c, L, ws, x, sel, w, w_is_half, M, topk, out, mode, act_limit,
                        reinterpret_cast<hipStream_t>(stream), true);
+}
+
+int gfl_moe_forward_shared(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half,
+                           int M, int topk, float* out, int mode, float act_limit, gfl_stream stream)
+{
+    const char* who = "gfl_moe_forward_shared";
+    if (const int r = check_forward(c, li, x, sel, w, M, topk, out, mode, act_limit, who, gfl::MAX_GROUPED_PICKS))
+        return r;
+    std::lock_guard<std::mutex> g(c->mu);
+    const Layer& L = c->layers[li];
+    if (!L.shared) return fail(GFL_EINVAL, std::string(who) + ": the layer has no shared expert (gfl_register_shared)");
+    if (M == 0) return GFL_OK;   // an empty batch: nothing to compute
+    // the shared expert's picks run in the routed launches' kernels, instantiated for the layer's bit widths
+    if (topk == 0 || L.shK[0] != L.K[0] || L.shK[1] != L.K[1] || L.shK[2] != L.K[2] || (int64_t)M * (topk + 1) >
+        gfl::MAX_PICKS)
+        return fail(GFL_EUNSUPPORTED, std::string(who) + ": needs topk >= 1, M*(topk+1) <= 1024 and the shared "
+                                                         "expert's bit widths equal to the layer's");
+    GFL_HIP(hipSetDevice(c->device));
+    if (!c->ws || L.H > c->ws_H || L.I > c->ws_I) return fail(GFL_ERUNTIME, std::string(who) + ": workspace not reserved");
+    Workspace ws;
+    carve_ws(c, L.H, L.I, ws);
+    return run_forward(c, L, ws, x, sel, w, w_is_half, M, topk, out, mode, act_limit,
+                       reinterpret_cast<hipStream_t>(stream), true, M);
 }
 
 int gfl_moe_forward_noalloc(gfl_ctx* c, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half,

@@ -79,20 +79,23 @@ struct PlanView
 // (EXACT, one slot per pass): the relay launches, a workgroup per (pick, 64 / rw outputs) with rw waves per tile
 // column, slot = pick; rw = 0: the per-slot or per-union-entry launches. prio (relay launches only): 1 = each wave
 // lowers its issue priority as it progresses, so the waves sharing a SIMD end together; 0 = off; -1 = chosen from the
-// launch's waves per SIMD. gplan (rw = 0 only): the routing plan is
+// launch's waves per SIMD. nsh (relay launches only, else -1 is returned): M shared-expert picks P .. P + M - 1 after
+// the routed ones (token p - P, expert row E of ptrs, weight 1), whose down output the combine adds after the token's
+// routed sum. gplan (rw = 0 only): the routing plan is
 // built once by its own one-workgroup launch before the launch of matrix 0 and read from pv by every workgroup,
 // instead of each workgroup building it in LDS.
 int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, const int64_t* sel, const void* w,
                    int w_half, int P, int topk, int E, int H, int I, int umax, const uint16_t* x, float* ygu,
                    uint16_t* xtd, int* act_cnt, const float* silu_tab, float act_limit, const PlanView& pv, float* out,
-                   int mf, int rw, int prio, int gplan, int* status, int spin_max, hipStream_t st);
+                   int mf, int rw, int prio, int nsh, int gplan, int* status, int spin_max, hipStream_t st);
 // down launch: down GEMV + out_block, weighted combine per (token, 128-block) by the token's last expert; mf and ns
 // as for launch_gate_up (the same values for both launches of a call). blk_cnt: [cap][H/128] half-block counters of
-// the one-slot-per-pass EXACT launch (zero between calls). rw and prio as for launch_gate_up (rw the same value for
-// both; the relay down launch takes at most 64 picks, else -1).
+// the one-slot-per-pass EXACT launch (zero between calls). rw, prio and nsh as for launch_gate_up (rw and nsh the same
+// values for both; the relay down launch takes at most 64 routed picks, else -1).
 int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int umax, int P, int E, const int64_t* sel,
                 const void* w, int w_half, const PlanView& pv, const uint16_t* xtd, float* yd, int* out_cnt,
-                int* blk_cnt, float* out, int mf, int rw, int prio, int* status, int spin_max, hipStream_t st);
+                int* blk_cnt, float* out, int mf, int rw, int prio, int nsh, int* status, int spin_max,
+                hipStream_t st);
 size_t gate_up_lds_bytes(int K, int ns, int H, int P, int E, int mf, int rw, int gplan);
 size_t down_lds_bytes(int K, int ns, int I, int P, int E, int mf, int rw);
 int launch_dequant(const uint8_t* tr, int k, int n, int K, uint16_t* W, hipStream_t st);

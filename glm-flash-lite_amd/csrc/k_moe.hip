@@ -875,6 +875,8 @@ struct GuArgs
     int* status;               // the context's status words (relay waits that expired)
     int spin_max;              // bound of a relay turn wait, in polls
     int prio;                  // relay launches: waves lower their issue priority as they progress (chain_relay)
+    int nsh;                   // relay launches: shared-expert picks P .. P + nsh - 1 (token p - P, expert row E,
+                               // weight 1), one per token, or 0
     int gplan;                 // the routing plan was published to pv by plan_kernel before this launch: workgroups
                                // read their entries from pv instead of each building the plan in LDS
 };
@@ -1149,6 +1151,7 @@ struct DnArgs
     int* status;               // the context's status words (relay waits that expired)
     int spin_max;              // bound of a relay turn wait, in polls
     int prio;                  // relay launches: waves lower their issue priority as they progress (chain_relay)
+    int nsh;                   // relay launches: shared-expert picks after the routed ones, as in GuArgs
     const int64_t* sel;        // [P] picks (relay launches: slot = pick)
     const void* w;             // [P] routing weights, fp16 (w_half) or fp32
     int w_half, E;
@@ -1401,13 +1404,15 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
     // block 0 marks skipped picks and zeroes the rows of tokens without picks, blocks 1..7 have no work (the items
     // start at an XCD-aligned block); all of them end within a load's latency, so every GEMV workgroup finds a free
     // slot in the first dispatch round
-    const long item = blockIdx.x < 8 ? -1 : relay_item(blockIdx.x - 8, RW, (long)a.nmat_launch * a.P * ncb);
+    const int PT = a.P + a.nsh;   // routed picks, then the shared expert's (one per token)
+    const long item = blockIdx.x < 8 ? -1 : relay_item(blockIdx.x - 8, RW, (long)a.nmat_launch * PT * ncb);
     if (item < 0) return;
-    const int wg = (int)item, per_mat = a.P * ncb;
+    const int wg = (int)item, per_mat = PT * ncb;
     const int p = (wg % per_mat) / ncb, cb = wg % ncb;
-    const int64_t e64 = a.sel[p];
-    if (e64 < 0 || e64 >= a.E) return;
+    const int64_t e64 = p < a.P ? a.sel[p] : a.E;   // the shared expert is row E of the table
+    if (e64 < 0 || e64 > a.E || (e64 == a.E && p < a.P)) return;
     const int e = (int)e64;
+    const int tok = p < a.P ? p / a.topk : p - a.P;
     const int mat = a.mat_base + wg / per_mat;   // 0 gate, 1 up
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15;
     const int wid = __builtin_amdgcn_readfirstlane(wave);
@@ -1420,7 +1425,7 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
     const size_t gstride = (size_t)TN * TB;
     const int t = cb * CW + c;   // this wave's tile column
     const uint8_t* col = tr + (size_t)t * TB;
-    const uint16_t* xrow = a.x + (size_t)(p / a.topk) * a.H;
+    const uint16_t* xrow = a.x + (size_t)tok * a.H;
 
     // input transform (prep_block, ft_core.h:97-102) into LDS: each 16-lane row takes one 128-block, 8 elements per
     // lane; the first GU_PR rounds of blocks are loaded before the trellis groups are requested
@@ -1491,11 +1496,11 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
 }
 
 // LDS of the relay down launch: the waves' rings plus the slot's fp32 inputs, or the combining workgroup's blocks of
-// up to MAX_TOPK picks where that is larger
+// up to MAX_TOPK picks and the shared expert's where that is larger
 template <int K>
 __host__ __device__ constexpr size_t dn_relay_lds(int I)
 {
-    const size_t x = (size_t)I * 4, comb = (size_t)MAX_TOPK * 128 * 4;
+    const size_t x = (size_t)I * 4, comb = (size_t)(MAX_TOPK + 1) * 128 * 4;
     return (size_t)GU_NW * 8 * 32 * K + (x > comb ? x : comb);
 }
 
@@ -1510,9 +1515,9 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
     constexpr int NW = GU_NW, CW = NW / RW, TB = 32 * K, NQ = 128 / (16 * CW);
     extern __shared__ __align__(16) uint8_t lds_raw[];
     __shared__ int s_last;
-    __shared__ int c_npk, c_slot[MAX_TOPK];
-    __shared__ float c_w[MAX_TOPK];
-    __shared__ uint64_t c_svh[MAX_TOPK];
+    __shared__ int c_npk, c_slot[MAX_TOPK + 1];   // the token's picks in combine order, then its shared-expert pick
+    __shared__ float c_w[MAX_TOPK + 1];
+    __shared__ uint64_t c_svh[MAX_TOPK + 1];
     __shared__ float relay[CW][64];
     __shared__ int relay_turn[CW];
     if (threadIdx.x < CW) relay_turn[threadIdx.x] = 0;   // ordered before every hand-off by the input barrier
@@ -1520,8 +1525,8 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
     uint8_t* rings = lds_raw;                                       // [NW][RB]
     float* lds_x = reinterpret_cast<float*>(lds_raw + NW * RB);     // [I] permuted, fp32
     const int TN = a.H / 16, TK = a.I / 16, ncb = TN / CW;
-    const int P = a.pv_picks;
-    const long item = relay_item(blockIdx.x, RW, (long)P * ncb);
+    const int P = a.pv_picks, PT = P + a.nsh;   // routed picks, then the shared expert's (one per token)
+    const long item = relay_item(blockIdx.x, RW, (long)PT * ncb);
     if (item < 0) return;
     const int p = (int)(item / ncb), cb = (int)(item % ncb);
     const int blk = cb / NQ;
@@ -1545,7 +1550,7 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
     const int t = cb * CW + c;
     const uint8_t* col = tr + (size_t)t * TB;
     const int nbh = a.H / 128;
-    const int tok = p / a.topk;
+    const int tok = p < P ? p / a.topk : p - P;
     // the slot's down input (I fp16) into LDS as fp32; each thread's first two 16-byte loads are issued before the
     // trellis groups are requested
     const int nvec = a.I / 8;
@@ -1595,7 +1600,7 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
     if (threadIdx.x == 0)
     {
         int* ctr = a.out_cnt + ((size_t)tok * nbh + blk) * CNT_STRIDE;
-        const int need = NQ * c_npk;
+        const int need = NQ * (c_npk + (a.nsh ? 1 : 0));
         const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = old == need - 1;
         if (old == need - 1) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1604,11 +1609,19 @@ __global__ __launch_bounds__(GU_NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
     if (!s_last) return;
     float* ylds = lds_x;   // [npk][128] the picks' blocks after out_block (the GEMV inputs are no longer needed)
     relay_combine_list(e_l, w_l, svh_l, P, a.E, a.topk, tok, c_slot, c_w, c_svh, &c_npk);
-    const int npk = c_npk;
+    // the shared expert last, weight 1: o + 1 * y = o + y, the join of routed + shared (k_overlap's fp32 add)
+    if (a.nsh && threadIdx.x == 0)
+    {
+        c_slot[c_npk] = P + tok;
+        c_w[c_npk] = 1.0f;
+        c_svh[c_npk] = a.pv.uptr[2 * (P + tok) + 1];
+    }
+    __syncthreads();
+    const int npk = c_npk + (a.nsh ? 1 : 0);
     // wave w takes picks w, w + NW, ...: every load of its picks is issued before the first out_block, so the wave
     // waits one memory round trip, not one per pick. The loads run unconditionally (past the token's picks on its
     // last pick again, loaded and never used): under a branch each would be waited for before the next was issued.
-    constexpr int KPW = (MAX_TOPK + NW - 1) / NW;
+    constexpr int KPW = (MAX_TOPK + 1 + NW - 1) / NW;
     if (wave < npk)
     {
         float v0[KPW], v1[KPW];
@@ -1778,7 +1791,7 @@ static void gu_relay_launch(const GuArgs& a, int nmat, hipStream_t st)
     auto kern = gu_relay_kernel<K, RW>;
     static const bool opened = open_lds(kern);
     (void)opened;
-    const long nwg = (long)a.P * (a.I / (16 * CW)) * nmat;   // GEMV workgroups (plus the publishing one)
+    const long nwg = (long)(a.P + a.nsh) * (a.I / (16 * CW)) * nmat;   // GEMV workgroups (plus the publishing one)
     const size_t lds = balanced_lds(gu_relay_lds<K>(a.H, a.P, a.E), nwg);
     GuArgs b = a;
     b.nmat_launch = nmat;
@@ -1793,7 +1806,7 @@ static void dn_relay_launch(const DnArgs& a, int P, hipStream_t st)
     auto kern = dn_relay_kernel<K, RW>;
     static const bool opened = open_lds(kern);
     (void)opened;
-    const long nwg = (long)P * (a.H / (16 * CW));
+    const long nwg = (long)(P + a.nsh) * (a.H / (16 * CW));
     const size_t lds = balanced_lds(dn_relay_lds<K>(a.I), nwg);
     DnArgs b = a;
     b.pv_picks = P;
@@ -1849,11 +1862,13 @@ size_t down_lds_bytes(int K, int ns, int I, int P, int E, int mf, int rw)
 int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, const int64_t* sel, const void* w,
                    int w_half, int P, int topk, int E, int H, int I, int umax, const uint16_t* x, float* ygu,
                    uint16_t* xtd, int* act_cnt, const float* silu_tab, float act_limit, const PlanView& pv, float* out,
-                   int mf, int rw, int prio, int gplan, int* status, int spin_max, hipStream_t st)
+                   int mf, int rw, int prio, int nsh, int gplan, int* status, int spin_max, hipStream_t st)
 {
+    if (nsh && (!rw || mf)) return -1;   // shared-expert picks ride on the relay launches only
     GuArgs a;
     a.status = status; a.spin_max = spin_max; a.nmat_launch = nmat; a.gplan = rw ? 0 : gplan;
     a.prio = rw ? prio : 0;
+    a.nsh = nsh;
     a.ptrs = ptrs; a.sel = sel; a.w = w; a.w_half = w_half; a.P = P; a.topk = topk; a.E = E; a.H = H; a.I = I;
     a.mat_base = mat_base; a.x = x; a.ygu = ygu; a.xtd = xtd; a.act_cnt = act_cnt; a.silu_tab = silu_tab;
     a.act_limit = act_limit; a.pv = pv; a.out = out;
@@ -1885,11 +1900,14 @@ int launch_gate_up(int K, int ns, const uint64_t* ptrs, int mat_base, int nmat, 
 
 int launch_down(int K, int ns, const uint64_t* ptrs, int topk, int H, int I, int umax, int P, int E, const int64_t* sel,
                 const void* w, int w_half, const PlanView& pv, const uint16_t* xtd, float* yd, int* out_cnt,
-                int* blk_cnt, float* out, int mf, int rw, int prio, int* status, int spin_max, hipStream_t st)
+                int* blk_cnt, float* out, int mf, int rw, int prio, int nsh, int* status, int spin_max,
+                hipStream_t st)
 {
+    if (nsh && (!rw || mf)) return -1;
     DnArgs a;
     a.status = status; a.spin_max = spin_max; a.pv_picks = P;
     a.prio = rw ? prio : 0;
+    a.nsh = nsh;
     a.sel = sel; a.w = w; a.w_half = w_half; a.E = E;
     a.ptrs = ptrs; a.topk = topk; a.H = H; a.I = I; a.pv = pv; a.xtd = xtd; a.yd = yd; a.out_cnt = out_cnt;
     a.blk_cnt = blk_cnt;

@@ -28,6 +28,8 @@ enum
     GFL_EINVAL = 1,   /* bad argument (shape, dtype code, unregistered layer, unsupported K) */
     GFL_ERUNTIME = 2, /* HIP runtime error */
     GFL_ENOMEM = 3,   /* device allocation failed */
+    GFL_EUNSUPPORTED = 4, /* gfl_moe_forward_shared: this call cannot run the shared expert in the routed launches;
+                           * nothing was launched (the caller runs the two calls itself) */
 };
 
 /* Expert arithmetic modes, numbered as tier_forward's `mode` (kernels/cpu_avx2/ft_tier_ext.cpp:865-904).
@@ -116,6 +118,22 @@ int gfl_layer_info(gfl_ctx* ctx, int li, int* info);
  * capture; otherwise the first call of a larger size grows it). */
 int gfl_moe_forward(gfl_ctx* ctx, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half, int M,
                     int topk, float* out, int mode, float act_limit, gfl_stream stream);
+
+/* The shared expert of layer li, for gfl_moe_forward_shared: ptr_row = its 9 device addresses, as one row of
+ * gfl_register_layer's table; k_*: its bit widths. Replaces an earlier one; gfl_register_layer for li drops it. The
+ * reference runs the shared GatedMLP beside the routed experts on a side stream (glm53/k_overlap.py:61-90); this has
+ * no counterpart of its own there. Like gfl_register_layer, not to be called while a graph that runs li is captured
+ * or replayed (the layer's table moves). */
+int gfl_register_shared(gfl_ctx* ctx, int li, int k_gate, int k_up, int k_down, const uint64_t* ptr_row);
+
+/* out[t] = routed layer li (as gfl_moe_forward) + its shared expert for x[t] (weight 1), added in fp32 after the
+ * routed sum: bit-identical to gfl_moe_forward into out followed by out += shared(x), the join of glm53/k_overlap.py.
+ * The shared expert rides on the routed call's two launches as one more pick per token, so the pair costs about one
+ * routed call of M*(topk+1) picks. That needs the relay launches (EXACT modes, M*topk <= 64, topk >= 1, a context
+ * not set shared at 769..1536 gate|up columns) and the shared expert's bit widths equal to the layer's; any other
+ * call returns GFL_EUNSUPPORTED with nothing launched. GFL_EINVAL if the layer has no shared expert. */
+int gfl_moe_forward_shared(gfl_ctx* ctx, int li, const uint16_t* x, const int64_t* sel, const void* w, int w_is_half,
+                           int M, int topk, float* out, int mode, float act_limit, gfl_stream stream);
 
 /* No counterpart in the reference. gfl_moe_forward with the per-call workspace in a file-scope device array of the
  * library (about 7.8 MiB per device, held until the process ends) instead of the context's reserved workspace: for
