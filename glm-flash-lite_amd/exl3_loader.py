@@ -182,7 +182,8 @@ def _copy_expert(res, i, who, spec, handles):
 
 def load(paths, ctx, layers=None, device=0, shared=None):
     """Copy the routed experts of `layers` (default: all layers found) into HBM and register each as context layer
-    index L. With `shared` (a k_overlap.SharedOverlap), shared experts are registered there under the same index.
+    index L. With `shared` (a k_overlap.SharedOverlap), shared experts are registered there under the same index,
+    and with the routed layer in ctx too (gfl_register_shared), so that both can run in one call's launches.
     Returns {L: ResidentLayer}."""
     import torch
     from safetensors import safe_open
@@ -209,7 +210,7 @@ def load(paths, ctx, layers=None, device=0, shared=None):
                 _copy_expert(sh, 0, -1, sp, handles)
                 res.shared = sh
                 if shared is not None:
-                    shared.register(L, sp.H, sp.I, sp.Ks, sh.ptr_table, keep=sh)
+                    shared.register(L, sp.H, sp.I, sp.Ks, sh.ptr_table, keep=sh, routed=ctx)
             out[L] = res
     finally:
         for h in handles.values():
