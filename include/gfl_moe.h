@@ -128,6 +128,7 @@ int gfl_register_shared(gfl_ctx* ctx, int li, int k_gate, int k_up, int k_down, 
 
 /* out[t] = routed layer li (as gfl_moe_forward) + its shared expert for x[t] (weight 1), added in fp32 after the
  * routed sum: bit-identical to gfl_moe_forward into out followed by out += shared(x), the join of glm53/k_overlap.py.
+ * act_limit clamps the shared expert's SwiGLU as it does the routed experts'.
  * The shared expert rides on the routed call's two launches as one more pick per token, so the pair costs about one
  * routed call of M*(topk+1) picks. That needs the relay launches (EXACT modes, M*topk <= 64, topk >= 1, a context
  * not set shared at 769..1536 gate|up columns) and the shared expert's bit widths equal to the layer's; any other

@@ -162,6 +162,27 @@ def test_fused_shared_bitexact(gpu, oracle, relay):
         assert np.array_equal(out.cpu().numpy(), _want(oracle, routed, shared, x16, sel, w)), f"M={M}"
 
 
+def test_fused_shared_act_limit(gpu, oracle):
+    """The SwiGLU clamp reaches the shared expert too: the fused call with act_limit equals the routed layer and the
+    shared expert each computed with that clamp, added after the routed sum."""
+    import torch
+    import synth
+    li = 72
+    routed = synth.SynthLayer(li, E, H, I, (3, 3, 3))
+    routed.register(gpu, li)
+    shared = synth.SynthLayer(73, 1, H, I, (3, 3, 3))
+    gpu.register_shared(li, shared.Ks, shared.ptr_table, keep=shared)
+    lim = 0.05
+    rng = np.random.default_rng(97)
+    x16, sel, w, (xd, seld, wd) = _inputs(rng, 3)
+    out = torch.full((3, H), float("nan"), dtype=torch.float32, device="cuda")
+    assert gpu.moe_forward_shared(li, xd, seld, wd, out, act_limit=lim)
+    torch.cuda.synchronize()
+    r = oracle.moe_forward(_experts(routed), x16.astype(np.float32), sel, w, mode=1, act_limit=lim)
+    sh = oracle.expert_forward(_experts(shared)[0], x16.astype(np.float32), mode=1, act_limit=lim)
+    assert np.array_equal(out.cpu().numpy(), (r.astype(np.float32) + sh.astype(np.float32)).astype(np.float32))
+
+
 def test_fused_shared_declines(gpu):
     """gfl_moe_forward_shared launches nothing and says so (False) for calls it cannot fuse: the shared expert's bit
     widths differ from the layer's, mode MFMA, more than 64 routed picks; a layer without a shared expert is an error."""
