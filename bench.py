@@ -654,6 +654,8 @@ def main():
                     help="only the config-4 prefill measurement (M=2048 through the grouped path), one JSON line")
     ap.add_argument("--prefill-exact", action="store_true",
                     help="with --prefill-only: the EXACT path (gfl_moe_forward, accumulator chains) instead")
+    ap.add_argument("--shared-only", action="store_true",
+                    help="only the routed + shared expert measurement (stock order, overlapped, fused), one JSON line")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="counter run: the calibration copy, then eager M=1 steps (run under rocprofv3 --pmc)")
     ap.add_argument("--probe-M", type=int, default=1, help="tokens per layer call of --pmc-probe")
@@ -691,6 +693,9 @@ def main():
     setup_s = time.time() - t0
     if args.pmc_probe:
         pmc_probe(ctx, layers, M=args.probe_M)
+        return
+    if args.shared_only:
+        print(json.dumps({"shared_overlap": time_shared(ctx, list(range(args.layers)), 32, 4)}), flush=True)
         return
     if args.prefill_only:
         if args.prefill_exact:
