@@ -1773,15 +1773,27 @@ static size_t balanced_lds(size_t need, long nwg)
     return cap > need && cap <= (size_t)LDS_LIMIT ? cap : need;
 }
 
-// Progress priority of a relay launch (chain_relay's prio): on when the launch puts more than one and at most three
-// waves on a SIMD, where a SIMD's last wave would otherwise run alone. Measured on MI355X (config 1, us per token):
-// M = 1 (gate|up 3 waves per SIMD, down 2.5) 48.9 -> 45.8; M = 2 with it on gate|up (3 per SIMD) 36.6 -> 34.9, and
-// 0.4 slower with it on down as well (5 per SIMD). prio >= 0 (GFL_RELAY_PRIO) forces it.
-static int relay_prio(int prio, long waves)
+// Waves of a kernel that one SIMD holds at once, from its register count (512 VGPRs per lane, allocated in blocks of
+// 8; at most 8 waves).
+static int resident_waves(const void* kern)
+{
+    hipFuncAttributes at{};
+    if (hipFuncGetAttributes(&at, kern) != hipSuccess || at.numRegs <= 0) return 3;
+    const int regs = (at.numRegs + 7) / 8 * 8;
+    return std::min(8, 512 / regs);
+}
+
+// Progress priority of a relay launch (chain_relay's prio): on when the launch puts more than one wave on a SIMD and
+// all of them fit at once (cap: resident_waves), so that a SIMD's last wave would otherwise run its last stretch
+// alone. Measured on MI355X (config 1, us per token): M = 1 (gate|up 3 waves per SIMD of 3, down 2.5 of 4) 48.9 ->
+// 45.8; M = 2 with it on gate|up (3 of 4) 36.6 -> 34.9, while on down as well (5 waves per SIMD, two rounds) 0.4
+// slower; routed + shared expert in one call at M = 2 (gate|up 3.4 of 4) 42.4 -> 40.0. prio >= 0 (GFL_RELAY_PRIO)
+// forces it.
+static int relay_prio(int prio, long waves, int cap)
 {
     if (prio >= 0) return prio;
     const long simds = 4L * device_cus();
-    return waves > simds && waves <= 3 * simds ? 1 : 0;
+    return waves > simds && waves <= cap * simds ? 1 : 0;
 }
 
 template <int K, int RW>
@@ -1795,7 +1807,8 @@ static void gu_relay_launch(const GuArgs& a, int nmat, hipStream_t st)
     const size_t lds = balanced_lds(gu_relay_lds<K>(a.H, a.P, a.E), nwg);
     GuArgs b = a;
     b.nmat_launch = nmat;
-    b.prio = relay_prio(a.prio, nwg * GU_NW);
+    static const int cap = resident_waves(reinterpret_cast<const void*>(kern));
+    b.prio = relay_prio(a.prio, nwg * GU_NW, cap);
     timed_launch(kern, dim3(8 + relay_blocks(nwg, RW)), dim3(GU_NW * 64), lds, st, b);
 }
 
@@ -1810,7 +1823,8 @@ static void dn_relay_launch(const DnArgs& a, int P, hipStream_t st)
     const size_t lds = balanced_lds(dn_relay_lds<K>(a.I), nwg);
     DnArgs b = a;
     b.pv_picks = P;
-    b.prio = relay_prio(a.prio, nwg * GU_NW);
+    static const int cap = resident_waves(reinterpret_cast<const void*>(kern));
+    b.prio = relay_prio(a.prio, nwg * GU_NW, cap);
     timed_launch(kern, dim3(relay_blocks(nwg, RW)), dim3(GU_NW * 64), lds, st, b);
 }
 
