@@ -61,6 +61,8 @@ def test_argument_checks_without_device(lib):
     assert b"gfl_ctx_set_shared" in lib.gfl_last_error()
     assert lib.gfl_ctx_check(None) == 1 and b"NULL" in lib.gfl_last_error()
     assert lib.gfl_ingress_serve(None, 0, 1, 8, None, None, None, None, -1, 0.0, None) == 1
+    assert lib.gfl_register_shared(None, 0, 3, 3, 3, None) == 1 and b"NULL" in lib.gfl_last_error()
+    assert lib.gfl_moe_forward_shared(None, 0, None, None, None, 0, 1, 8, None, 1, 0.0, None) == 1
 
 
 def test_grouped_rows_host_matches_oracle(oracle):
