@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Routed-MoE decode benchmark on one MI355X.
 
-Workload: one MoE layer of 288 routed experts, top-8, SwiGLU H=5120 I=1536, EXL3 3 bits/weight,
+Workload (benchmark config 1): one MoE layer of 288 routed experts, top-8, SwiGLU H=5120 I=1536, EXL3 3 bits/weight,
 M = 1..4 decode tokens with fp16 N(0,1) activations and sigmoid top-8 routing of N(0,1) fp32 logits. A step is one
 layer call (split -> 8*M expert GEMVs -> weighted combine) through the C ABI. Steps cycle through `--layers` distinct
 288-expert layers (2.56 GB each) and 32 routings, so expert bytes come from HBM, not the 256 MB Infinity Cache.
@@ -21,7 +21,7 @@ roofline     = the gate|up GEMV kernel (the dominant one) at M=1: algorithmic qu
                FETCH_SIZE/WRITE_SIZE counter file (--pmc-probe / --pmc-digest).
 per_M_end_to_end = the decode step a routing_fn caller pays at M=1..4, from router logits to the layer output:
                gfl_route_split + gfl_moe_forward + gfl_combine in one captured step (128 steps, same protocol).
-configs      = BASELINE configs 0 (one expert per call), 2 (mixed bitrates, Zipf routing), 3 (M=16/32/64) and 4 (42
+configs      = benchmark configs 0 (one expert per call), 2 (mixed bitrates, Zipf routing), 3 (M=16/32/64) and 4 (42
                resident layers decoded at M=1; prefill of M=2048 tokens through the EXACT path, as TFLOP/s against
                the 157.3 TF dense fp32 MFMA peak its chain steps run on, and through the MFMA grouped path, against
                2.5 PF dense fp16); the router (gfl_route) per call; routed layer + shared expert, sequential vs
@@ -411,7 +411,7 @@ def time_e2e_steps(ctx, layer_ids, M, steps, G, warmup, bytes_per_expert):
 
 
 def extra_configs(ctx, layers, args):
-    """BASELINE configs 0, 2, 3 and 4 (42-layer resident stack, prefill through both paths), timed like config 1:
+    """Benchmark configs 0, 2, 3 and 4 (42-layer resident stack, prefill through both paths), timed like config 1:
     XSTEPS steps per line (fewer for the long ones), graphs of 4 steps."""
     import numpy as np
     import synth
