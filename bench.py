@@ -24,8 +24,8 @@ per_M_end_to_end = the decode step a routing_fn caller pays at M=1..4, from rout
 configs      = benchmark configs 0 (one expert per call), 2 (mixed bitrates, Zipf routing), 3 (M=16/32/64) and 4 (42
                resident layers decoded at M=1; prefill of M=2048 tokens through the EXACT path, as TFLOP/s against
                the 157.3 TF dense fp32 MFMA peak its chain steps run on, and through the MFMA grouped path, against
-               2.5 PF dense fp16); the router (gfl_route) per call; routed layer + shared expert, sequential vs
-               overlapped on a side stream.
+               2.5 PF dense fp16); the router (gfl_route) per call; routed layer + shared expert: sequential,
+               overlapped on a side stream, and fused into the routed call's launches (gfl_moe_forward_shared).
 cpu_baseline = the reference's own AVX2 expert engine (kernels/cpu_avx2/ft_core.h, built into oracle/_ref) timed on
                this host: decode calls of M tokens x 8 experts cycling a DRAM-cold pool of 288 experts; value = I16
                at M=1; EXACT at M=1..4, AFFINE at M=2..4 and the single expert of config 0 beside it, with the CPU
